@@ -1,0 +1,189 @@
+/*
+ * pkv.h — C ABI of the MI355X-native quantized KV-cache library (libpkv.so).
+ *
+ * Drop-in boundary for paramecia-model's full-attention KV-cache path. Each entry
+ * point names the reference item it replaces (paths relative to the reference root,
+ * mostly paramecia-model/src/qwen3_next.rs, "qn" below).
+ *
+ * Conventions
+ *   - All tensor arguments are DEVICE pointers (hipMalloc'd or torch CUDA tensors),
+ *     plain C types only. Host-side bookkeeping (lengths, tokens) is plain values.
+ *   - Every call returns an int status (pkv_status); on failure
+ *     pkv_last_error() returns a thread-local message. Nothing is partially
+ *     written on a returned error (the reference's bail! semantics).
+ *   - A cache handle owns its K/V buffers and a stream (hipStream_t passed as
+ *     void*; NULL = the default stream). Work is enqueued on that stream and
+ *     returns without synchronising. A handle is not re-entrant (the reference
+ *     holds the cache behind &mut self); different handles are independent.
+ *   - Layout in HBM is the reference's seq-major row layout (qn:465-504): row
+ *     r = (t*batch + b)*n_kv_heads + h, row r at byte r*bytes_per_row in the K and
+ *     in the V buffer. One row = one head of one token = padded_head_dim elements
+ *     in GGML blocks (Q4K: 144 B per 256, Q8_0: 34 B per 32) or f16/bf16.
+ */
+#ifndef PKV_H
+#define PKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct pkv_cache pkv_cache;   /* PreallocatedQuantizedKvCache (qn:343-380) */
+typedef struct pkv_prefix pkv_prefix; /* PrefixCache (qn:856-864) */
+typedef void *pkv_stream;             /* hipStream_t */
+
+/* KvCacheQuantization (qn:88-106). NONE is the deprecated alias of F16. */
+enum {
+  PKV_QUANT_NONE = 0,
+  PKV_QUANT_F16 = 1,
+  PKV_QUANT_BF16 = 2,
+  PKV_QUANT_Q8_0 = 3,
+  PKV_QUANT_Q4K = 4
+};
+
+enum {
+  PKV_OK = 0,
+  PKV_ERR_OVERFLOW = 1,   /* "Quantized KV cache overflow" (qn:435-441) */
+  PKV_ERR_OFFSET = 2,     /* "KV cache offset mismatch" (qn:2430-2440) */
+  PKV_ERR_ARG = 3,        /* bad argument / shape */
+  PKV_ERR_HIP = 4,        /* HIP runtime error */
+  PKV_ERR_EMPTY = 5,      /* "Cannot get storage from empty cache" (qn:583-585) */
+  PKV_ERR_LAYERS = 6,     /* "Prefix cache layer count mismatch" (qn:5727-5733) */
+  PKV_ERR_LAYOUT = 7,     /* snapshot does not fit the cache (quant/heads/dims) */
+  PKV_ERR_UNSUPPORTED = 8 /* combination with no kernel (e.g. head_dim > 512) */
+};
+
+/* Entry kinds of a prefix cache layer (PrefixCacheEntry, qn:834-854). */
+enum { PKV_ENTRY_EMPTY = 0, PKV_ENTRY_FULL = 1, PKV_ENTRY_LINEAR = 2 };
+
+/* Restore modes for pkv_prefix_restore. BYTES copies the packed blocks (bit-exact);
+ * REQUANTIZE reproduces the reference's clear()+append(dequantized) (qn:2843-2847). */
+enum { PKV_RESTORE_BYTES = 0, PKV_RESTORE_REQUANTIZE = 1 };
+
+const char *pkv_last_error(void);
+const char *pkv_version(void);
+
+/* ---- KvCacheQuantization helpers (qn:107-166) ---- */
+/* from_str: f16|fp16, bf16|bfloat16, q8|q8_0, q4|q4k|q4_k, none (case-insensitive). */
+int pkv_quant_parse(const char *s, int *quant_out);
+int pkv_quant_default(void);                  /* impl Default -> Q4K (qn:107-111) */
+int pkv_quant_block_size(int quant);          /* block_size() (qn:123-130) */
+int pkv_quant_is_ggml(int quant);             /* to_ggml_dtype().is_some() (qn:114-121) */
+size_t pkv_bytes_per_row(int quant, int head_dim); /* qn:393-402 */
+
+/* ---- cache lifecycle (qn:384-423, 620-642) ---- */
+int pkv_create(int quant, int batch, int n_kv_heads, int head_dim, int64_t max_seq_len,
+               pkv_stream stream, pkv_cache **out);
+int pkv_destroy(pkv_cache *h);
+int pkv_set_stream(pkv_cache *h, pkv_stream stream);
+int64_t pkv_len(const pkv_cache *h);            /* seq_len */
+int64_t pkv_capacity(const pkv_cache *h);       /* max_seq_len */
+int pkv_geometry(const pkv_cache *h, int *quant, int *batch, int *n_kv_heads, int *head_dim,
+                 size_t *bytes_per_row);
+int pkv_truncate(pkv_cache *h, int64_t new_len); /* truncate(): min(new_len, len) */
+int pkv_clear(pkv_cache *h);                     /* clear() */
+int pkv_resize_batch(pkv_cache *h, int batch);   /* resize_batch(): realloc + reset if changed */
+
+/* ---- append (append_quantized qn:431-509 + FullAttention offset rule qn:2430-2440) ----
+ * k, v: device f32 [batch, n_kv_heads, n, head_dim]. offset < len truncates first,
+ * offset > len -> PKV_ERR_OFFSET, len+n > capacity -> PKV_ERR_OVERFLOW. Pass
+ * offset = -1 to append at the current length. */
+int pkv_append(pkv_cache *h, const float *k, const float *v, int64_t n, int64_t offset);
+
+/* ---- attention over the cache (CPU SDPA qn:2580-2605, flash_attn_q8 role qn:2531-2561) ----
+ * q, out: device f32 [batch, l, num_heads, head_dim]. Query head g reads KV head
+ * g / (num_heads / n_kv_heads) (repeat_kv, utils.rs:71-83). Key j is visible to query
+ * i iff !causal or j <= i + q_offset; scores are scaled, clamped to [-100, 100] and
+ * soft-maxed. For the model path q_offset = len - l and causal = 1 (qn:2538-2542). */
+int pkv_attend(pkv_cache *h, const float *q, int l, int num_heads, float scale,
+               int64_t q_offset, int causal, float *out);
+
+/* One decode step of one full-attention layer: append one token (offset rule as
+ * pkv_append) then attend over all len+1 keys, in a single launch.
+ * k, v: [batch, n_kv_heads, 1, head_dim]; q, out: [batch, 1, num_heads, head_dim]. */
+int pkv_append_attend(pkv_cache *h, const float *k, const float *v, const float *q,
+                      int num_heads, float scale, int64_t offset, float *out);
+
+/* get_kv (qn:520-575): dequantize rows [0, len) into device f32
+ * [batch, n_kv_heads, len, head_dim] (padding trimmed). */
+int pkv_get_kv(pkv_cache *h, float *k_out, float *v_out);
+
+/* get_kv_storage (qn:582-617): device pointers to the packed K/V bytes, the valid
+ * byte count, and the byte strides of the [batch, seq, head, d] view
+ * (stride_b, stride_seq, stride_h, stride_d). Empty cache -> PKV_ERR_EMPTY. */
+int pkv_kv_storage(const pkv_cache *h, const void **k_bytes, const void **v_bytes,
+                   size_t *valid_bytes, int64_t strides[4]);
+
+/* flash_attn_q8 (paramecia-model/src/ops.rs:756-792), stateless, any of the four
+ * storage formats: K/V are packed rows addressed by the byte strides
+ * (stride_b, stride_seq, stride_h) as returned by pkv_kv_storage. */
+int pkv_flash_attn(int quant, const float *q, const void *k_bytes, const void *v_bytes,
+                   const int64_t kv_strides[3], float scale, int batch, int num_heads,
+                   int num_kv_heads, int head_dim, int seq_q, int64_t seq_k,
+                   int64_t q_offset, int causal, float *out, pkv_stream stream);
+
+/* Batched decode over independent sequences (serving loop): caches[i] is a batch-1
+ * cache; appends one token to each (k, v: [n, n_kv_heads, head_dim]) then attends
+ * (q, out: [n, num_heads, head_dim]) in one launch. All caches share geometry. */
+int pkv_append_attend_batched(pkv_cache *const *caches, int n, const float *k,
+                              const float *v, const float *q, int num_heads, float scale,
+                              float *out, pkv_stream stream);
+
+/* ---- PrefixCache (qn:834-864, 2780-2884, 4066-4132, 5702-5750) ---- */
+int pkv_prefix_create(const uint32_t *prefix_tokens, size_t n_tokens, int n_layers,
+                      pkv_prefix **out);
+int pkv_prefix_free(pkv_prefix *p);
+int pkv_prefix_tokens(const pkv_prefix *p, const uint32_t **tokens, size_t *n_tokens);
+int pkv_prefix_num_layers(const pkv_prefix *p);
+int pkv_prefix_entry_kind(const pkv_prefix *p, int layer);
+/* save_kv_state (qn:2780-2815): snapshot rows [0, len) byte for byte (Empty if len 0). */
+int pkv_prefix_save_full(pkv_prefix *p, int layer, const pkv_cache *h);
+/* save_state_for_prefix (qn:4066-4104): deep copy of the Gated-DeltaNet state.
+ * ssm [b, heads, dk, dv], conv [b, conv_dim, k-1], gate_offset [b, heads] f32;
+ * gate_offset == NULL stores zeros (qn:4077-4093). */
+int pkv_prefix_save_linear(pkv_prefix *p, int layer, const float *ssm, size_t n_ssm,
+                           const float *conv, size_t n_conv, const float *gate_offset,
+                           size_t n_gate, pkv_stream stream);
+/* Saved element counts of a LINEAR entry (to size restore targets). */
+int pkv_prefix_linear_sizes(const pkv_prefix *p, int layer, size_t *n_ssm, size_t *n_conv,
+                            size_t *n_gate);
+/* Saved length of a FULL entry. */
+int64_t pkv_prefix_full_len(const pkv_prefix *p, int layer);
+
+/* Restore targets for one layer: exactly one of `cache` (full attention) or the three
+ * state pointers (linear attention) is set. `*state_valid` is written 1 if the state
+ * was restored, 0 if it was cleared (Empty or wrong entry kind, qn:4121-4130). */
+typedef struct {
+  pkv_cache *cache;
+  float *ssm;
+  float *conv;
+  float *gate_offset;
+  int *state_valid;
+} pkv_layer_target;
+
+/* restore_prefix_cache (qn:5726-5740): layer count must match (PKV_ERR_LAYERS);
+ * every layer is validated before anything is written; all copies go out as ONE
+ * batched gather/copy launch on `stream`. FULL entries restore into the cache
+ * (len = saved len), Empty/wrong-kind clear it (qn:2874-2882). Writes the prefix
+ * token count to *n_tokens_out. mode: PKV_RESTORE_BYTES or PKV_RESTORE_REQUANTIZE. */
+int pkv_prefix_restore(const pkv_prefix *p, const pkv_layer_target *targets, int n_layers,
+                       int mode, size_t *n_tokens_out, pkv_stream stream);
+
+/* ---- utilities ---- */
+/* Seeded synthetic data: dst[i] = normal(seed, stream_id, i) * scale, bit-identical
+ * to the CPU oracle's generator (Philox4x32-10, Irwin-Hall of eight 22-bit draws). */
+int pkv_fill_normal(float *dst, size_t n, uint64_t seed, uint64_t stream_id, float scale,
+                    pkv_stream stream);
+/* Multiply channels ch[0..n_ch) of the last dimension (size dim) by factor. */
+int pkv_scale_channels(float *x, size_t rows, int dim, const int *channels_host, int n_ch,
+                       float factor, pkv_stream stream);
+/* Device-to-device gather/copy of n segments in one launch (used by prefix restore). */
+int pkv_copy_segments(void *const *dst, const void *const *src, const size_t *bytes, int n,
+                      pkv_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PKV_H */

@@ -1,0 +1,126 @@
+/*
+ * pkv_oracle — CPU restatement of paramecia-model's quantized KV-cache path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This code is the checker for the HIP library in
+ * paramecia_amd/; only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it. The product path never calls it.
+ *
+ * What it restates (paths relative to the reference root):
+ *   - KvCacheQuantization modes ............ paramecia-model/src/qwen3_next.rs:88-166
+ *   - PreallocatedQuantizedKvCache ......... qwen3_next.rs:343-643 (new/append/get_kv/
+ *                                            truncate/clear/resize_batch)
+ *   - FullAttention cache offset rule ...... qwen3_next.rs:2430-2440
+ *   - CPU SDPA (repeat_kv, scale, mask,
+ *     clamp +-100, softmax, PV) ............ qwen3_next.rs:2580-2605, utils.rs:71-83,
+ *                                            causal mask qwen3_next.rs:5022-5028
+ *   - Q8_0 / Q4K codecs: the reference calls them through candle's
+ *     QTensor::quantize / dequantize (qwen3_next.rs:486-487, 541-564). candle is an
+ *     un-vendored git dependency (nicksenger/candle, branch paramecia, rev
+ *     2278f29b93305e3d0d110149879175cea2898216, Cargo.lock:388-390) that is not
+ *     present in this tree. The codecs below restate upstream candle's published
+ *     k_quants.rs algorithm (BlockQ8_0::from_float/to_float, BlockQ4K::from_float
+ *     with make_qkx1_quants(15, 5), BlockQ4K::to_float, get_scale_min_k4) and the
+ *     `half` crate's f16/bf16 round-to-nearest-even conversion.
+ *
+ * Parity status (how each function is pinned; see tests/test_oracle_*.py):
+ *   f16/bf16 conversion ....... pinned: exhaustive comparison against numpy's IEEE
+ *                               float16 and a bit-level RNE bfloat16 definition.
+ *   Q8_0 quantize/dequantize .. pinned: closed form per block, known-answer blocks
+ *                               (zero block, +-amax -> +-127, exact .5 ties rounded
+ *                               away from zero), idempotence of Q(DQ(.)).
+ *   Q4K dequantize ............ pinned: GGML block layout closed form (hand-built
+ *                               blocks with known scales/mins/nibbles).
+ *   Q4K quantize .............. partially pinned: hand-derived known-answer blocks,
+ *                               format invariants (6-bit codes, nibbles <= 15),
+ *                               per-sub-block reconstruction error bound, constant
+ *                               sub-block -> zero. Byte parity against the candle
+ *                               fork itself is UNPINNED (the fork is absent).
+ *   cache layout/offsets ...... pinned: closed-form row addressing and the
+ *                               overflow / offset-mismatch rules.
+ *   attention ................. pinned: float64 restatement compared with an
+ *                               independent numpy softmax(QK^T)V on small shapes.
+ *   RNG ....................... pinned: Philox4x32-10 known-answer vectors from
+ *                               Salmon et al. (SC'11) / Random123.
+ */
+#ifndef PKV_ORACLE_H
+#define PKV_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same numbering as include/pkv.h */
+enum { ORC_F16 = 1, ORC_BF16 = 2, ORC_Q8_0 = 3, ORC_Q4K = 4 };
+enum { ORC_OK = 0, ORC_ERR_OVERFLOW = 1, ORC_ERR_OFFSET = 2, ORC_ERR_ARG = 3 };
+
+/* ---- scalar conversions (half crate semantics) ---- */
+uint16_t orc_f32_to_f16(float x);
+float orc_f16_to_f32(uint16_t h);
+uint16_t orc_f32_to_bf16(float x);
+float orc_bf16_to_f32(uint16_t h);
+void orc_f32_to_f16_n(const float *x, uint16_t *out, size_t n);
+void orc_f32_to_bf16_n(const float *x, uint16_t *out, size_t n);
+void orc_f16_to_f32_n(const uint16_t *h, float *out, size_t n);
+
+/* ---- codecs: n = elements, multiple of the block size ---- */
+void orc_q8_0_quantize(const float *x, uint8_t *out, size_t n);
+void orc_q8_0_dequantize(const uint8_t *in, float *y, size_t n);
+void orc_make_qkx1_quants(const float *x, int n, int nmax, int ntry, float *scale,
+                          float *neg_min);
+void orc_get_scale_min_k4(int j, const uint8_t *scales, uint8_t *sc, uint8_t *m);
+void orc_q4k_quantize(const float *x, uint8_t *out, size_t n);
+void orc_q4k_dequantize(const uint8_t *in, float *y, size_t n);
+
+/* ---- seeded synthetic data (identical on the GPU side) ---- */
+void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+float orc_normal(uint64_t seed, uint64_t stream, uint64_t index);
+void orc_fill_normal(float *out, size_t n, uint64_t seed, uint64_t stream, float scale);
+
+/* ---- preallocated quantized cache ---- */
+typedef struct {
+  int quant, batch, n_kv_heads, head_dim, padded_head_dim, block;
+  int64_t max_seq_len, seq_len;
+  size_t bytes_per_row;
+  uint8_t *k, *v;
+} orc_cache;
+
+size_t orc_bytes_per_row(int quant, int head_dim);
+int orc_cache_init(orc_cache *c, int quant, int batch, int n_kv_heads, int head_dim,
+                   int64_t max_seq_len);
+void orc_cache_free(orc_cache *c);
+/* k, v: f32 [batch, n_kv_heads, n, head_dim] (the reference's append input). */
+int orc_cache_append(orc_cache *c, const float *k, const float *v, int64_t n);
+/* FullAttention rule: offset < len truncates, offset > len is an error. */
+int orc_cache_append_at(orc_cache *c, const float *k, const float *v, int64_t n,
+                        int64_t offset);
+void orc_cache_truncate(orc_cache *c, int64_t new_len);
+void orc_cache_clear(orc_cache *c);
+int orc_cache_resize_batch(orc_cache *c, int batch);
+/* get_kv: k_out, v_out f32 [batch, n_kv_heads, seq_len, head_dim]. */
+void orc_cache_get_kv(const orc_cache *c, float *k_out, float *v_out);
+
+/* ---- attention ----
+ * q: f32 [batch, l, num_heads, head_dim]; out: f32 [batch, l, num_heads, head_dim].
+ * Keys are the cache's first seq_len tokens. If causal, key j is visible to query i
+ * iff j <= i + q_offset (the reference's causal_mask, qwen3_next.rs:5022-5028, which
+ * its forward applies whenever l > 1; for l == 1 the mask hides nothing). Scores are
+ * scaled, masked (-> -inf), clamped to [-100, 100] (so masked scores become -100
+ * exactly as in the reference) and soft-maxed.
+ * threads: 0 = all cores.
+ */
+int orc_attend_f32(const orc_cache *c, const float *q, int l, int num_heads, float scale,
+                   int64_t q_offset, int causal, float *out, int threads);
+int orc_attend_f64(const orc_cache *c, const float *q, int l, int num_heads, double scale,
+                   int64_t q_offset, int causal, double *out);
+/* Faithful cost structure of qwen3_next.rs:2470-2473 + 2580-2605 (dequantize the whole
+ * cache, permute copy, repeat_kv copy, transposed-K copy, matmul, softmax, matmul). */
+int orc_attend_faithful(const orc_cache *c, const float *q, int l, int num_heads,
+                        float scale, int64_t q_offset, int causal, float *out, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,607 @@
+// C ABI of libpkv (include/pkv.h): cache handles, prefix snapshots and argument
+// checking around the kernels. The reference behaviour each function mirrors is cited
+// in include/pkv.h; error codes stand in for the reference's bail! strings.
+#include <ctype.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "pkv_internal.hpp"
+
+namespace pkv {
+
+static thread_local std::string g_error;
+
+int set_error(int code, const std::string &msg) {
+  g_error = msg;
+  return code;
+}
+
+int hip_error(hipError_t e, const char *what) {
+  g_error = std::string(what) + ": " + hipGetErrorString(e);
+  return PKV_ERR_HIP;
+}
+
+int Workspace::reserve(size_t need) {
+  if (need <= bytes) return PKV_OK;
+  size_t grow = need + need / 4 + 4096;
+  if (ptr) {
+    // A kernel may still read the old buffer; growth is rare, so wait for the device.
+    PKV_HIP(hipDeviceSynchronize());
+    PKV_HIP(hipFree(ptr));
+    ptr = nullptr;
+    bytes = 0;
+  }
+  PKV_HIP(hipMalloc(&ptr, grow));
+  bytes = grow;
+  return PKV_OK;
+}
+
+int Workspace::reserve_host(size_t need) {
+  if (host_pending) {
+    PKV_HIP(hipEventSynchronize(host_ev));
+    host_pending = false;
+  }
+  if (!host_ev) PKV_HIP(hipEventCreateWithFlags(&host_ev, hipEventDisableTiming));
+  if (need <= host_bytes) return PKV_OK;
+  if (host) PKV_HIP(hipHostFree(host));
+  host = nullptr;
+  host_bytes = 0;
+  PKV_HIP(hipHostMalloc(&host, need, hipHostMallocDefault));
+  host_bytes = need;
+  return PKV_OK;
+}
+
+int Workspace::mark_host_used(hipStream_t s) {
+  PKV_HIP(hipEventRecord(host_ev, s));
+  host_pending = true;
+  return PKV_OK;
+}
+
+Workspace::~Workspace() {
+  if (host_pending) (void)hipEventSynchronize(host_ev);
+  if (ptr) {
+    (void)hipDeviceSynchronize();
+    (void)hipFree(ptr);
+  }
+  if (host) (void)hipHostFree(host);
+  if (host_ev) (void)hipEventDestroy(host_ev);
+}
+
+static Workspace &util_workspace() {
+  static thread_local Workspace ws;
+  return ws;
+}
+
+static int norm_quant(int q) { return q == PKV_QUANT_NONE ? PKV_QUANT_F16 : q; }
+
+}  // namespace pkv
+
+using namespace pkv;
+
+// ---------------------------------------------------------------- prefix object
+namespace {
+struct Entry {
+  int kind = PKV_ENTRY_EMPTY;
+  // FULL: packed rows [0, len) of K and V, exactly as stored in the cache.
+  int quant = 0, batch = 0, heads = 0, head_dim = 0;
+  size_t bpr = 0;
+  int64_t len = 0;
+  uint8_t *k = nullptr, *v = nullptr;
+  // LINEAR: Gated-DeltaNet state copies.
+  float *ssm = nullptr, *conv = nullptr, *gate = nullptr;
+  size_t n_ssm = 0, n_conv = 0, n_gate = 0;
+  void release() {
+    if (k) (void)hipFree(k);
+    if (v) (void)hipFree(v);
+    if (ssm) (void)hipFree(ssm);
+    if (conv) (void)hipFree(conv);
+    if (gate) (void)hipFree(gate);
+    *this = Entry();
+  }
+};
+}  // namespace
+
+struct pkv_prefix {
+  std::vector<uint32_t> tokens;
+  std::vector<Entry> entries;
+};
+
+extern "C" {
+
+const char *pkv_last_error(void) { return g_error.c_str(); }
+const char *pkv_version(void) { return "paramecia_amd pkv 0.1 (gfx950)"; }
+
+int pkv_quant_parse(const char *s, int *quant_out) {
+  if (!s || !quant_out) return set_error(PKV_ERR_ARG, "null argument");
+  std::string t(s);
+  for (auto &c : t) c = (char)tolower((unsigned char)c);
+  int q;
+  if (t == "f16" || t == "fp16") q = PKV_QUANT_F16;
+  else if (t == "bf16" || t == "bfloat16") q = PKV_QUANT_BF16;
+  else if (t == "q8" || t == "q8_0") q = PKV_QUANT_Q8_0;
+  else if (t == "q4" || t == "q4k" || t == "q4_k") q = PKV_QUANT_Q4K;
+  else if (t == "none") q = PKV_QUANT_NONE;
+  else return set_error(PKV_ERR_ARG, "unknown KV cache quantization '" + std::string(s) + "'");
+  *quant_out = q;
+  return PKV_OK;
+}
+
+int pkv_quant_default(void) { return PKV_QUANT_Q4K; }
+int pkv_quant_block_size(int quant) { return block_size(norm_quant(quant)); }
+int pkv_quant_is_ggml(int quant) { return quant == PKV_QUANT_Q8_0 || quant == PKV_QUANT_Q4K; }
+size_t pkv_bytes_per_row(int quant, int head_dim) {
+  return head_dim > 0 ? row_bytes(norm_quant(quant), head_dim) : 0;
+}
+
+int pkv_create(int quant, int batch, int n_kv_heads, int head_dim, int64_t max_seq_len,
+               pkv_stream stream, pkv_cache **out) {
+  if (!out) return set_error(PKV_ERR_ARG, "null output handle");
+  *out = nullptr;
+  quant = norm_quant(quant);
+  if (quant < PKV_QUANT_F16 || quant > PKV_QUANT_Q4K)
+    return set_error(PKV_ERR_ARG, "unknown quantization");
+  if (batch <= 0 || n_kv_heads <= 0 || head_dim <= 0 || max_seq_len < 0)
+    return set_error(PKV_ERR_ARG, "batch, n_kv_heads, head_dim must be > 0, max_seq_len >= 0");
+  pkv_cache *h = new pkv_cache();
+  h->quant = quant;
+  h->batch = batch;
+  h->n_kv_heads = n_kv_heads;
+  h->head_dim = head_dim;
+  h->padded = padded_dim(quant, head_dim);
+  h->max_seq_len = max_seq_len;
+  h->seq_len = 0;
+  h->bpr = row_bytes(quant, head_dim);
+  h->stream = static_cast<hipStream_t>(stream);
+  h->k = h->v = nullptr;
+  const size_t total = (size_t)batch * n_kv_heads * (size_t)max_seq_len * h->bpr;
+  const size_t alloc = total ? total : 256;
+  hipError_t e = hipMalloc(&h->k, alloc);
+  if (e == hipSuccess) e = hipMalloc(&h->v, alloc);
+  if (e == hipSuccess) e = hipMemsetAsync(h->k, 0, alloc, h->stream);  // vec![0u8; total]
+  if (e == hipSuccess) e = hipMemsetAsync(h->v, 0, alloc, h->stream);
+  if (e != hipSuccess) {
+    if (h->k) (void)hipFree(h->k);
+    if (h->v) (void)hipFree(h->v);
+    delete h;
+    return hip_error(e, "pkv_create");
+  }
+  *out = h;
+  return PKV_OK;
+}
+
+int pkv_destroy(pkv_cache *h) {
+  if (!h) return PKV_OK;
+  (void)hipStreamSynchronize(h->stream);
+  (void)hipFree(h->k);
+  (void)hipFree(h->v);
+  delete h;
+  return PKV_OK;
+}
+
+int pkv_set_stream(pkv_cache *h, pkv_stream stream) {
+  if (!h) return set_error(PKV_ERR_ARG, "null handle");
+  h->stream = static_cast<hipStream_t>(stream);
+  return PKV_OK;
+}
+
+int64_t pkv_len(const pkv_cache *h) { return h ? h->seq_len : -1; }
+int64_t pkv_capacity(const pkv_cache *h) { return h ? h->max_seq_len : -1; }
+
+int pkv_geometry(const pkv_cache *h, int *quant, int *batch, int *n_kv_heads, int *head_dim,
+                 size_t *bpr) {
+  if (!h) return set_error(PKV_ERR_ARG, "null handle");
+  if (quant) *quant = h->quant;
+  if (batch) *batch = h->batch;
+  if (n_kv_heads) *n_kv_heads = h->n_kv_heads;
+  if (head_dim) *head_dim = h->head_dim;
+  if (bpr) *bpr = h->bpr;
+  return PKV_OK;
+}
+
+int pkv_truncate(pkv_cache *h, int64_t new_len) {
+  if (!h) return set_error(PKV_ERR_ARG, "null handle");
+  if (new_len < 0) new_len = 0;
+  if (new_len < h->seq_len) h->seq_len = new_len;
+  return PKV_OK;
+}
+
+int pkv_clear(pkv_cache *h) {
+  if (!h) return set_error(PKV_ERR_ARG, "null handle");
+  h->seq_len = 0;
+  return PKV_OK;
+}
+
+int pkv_resize_batch(pkv_cache *h, int batch) {
+  if (!h) return set_error(PKV_ERR_ARG, "null handle");
+  if (batch <= 0) return set_error(PKV_ERR_ARG, "batch must be > 0");
+  if (batch == h->batch) return PKV_OK;
+  const size_t total = (size_t)batch * h->n_kv_heads * (size_t)h->max_seq_len * h->bpr;
+  const size_t alloc = total ? total : 256;
+  uint8_t *k = nullptr, *v = nullptr;
+  hipError_t e = hipMalloc(&k, alloc);
+  if (e == hipSuccess) e = hipMalloc(&v, alloc);
+  if (e == hipSuccess) e = hipMemsetAsync(k, 0, alloc, h->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(v, 0, alloc, h->stream);
+  if (e != hipSuccess) {
+    if (k) (void)hipFree(k);
+    if (v) (void)hipFree(v);
+    return hip_error(e, "pkv_resize_batch");
+  }
+  PKV_HIP(hipStreamSynchronize(h->stream));
+  (void)hipFree(h->k);
+  (void)hipFree(h->v);
+  h->k = k;
+  h->v = v;
+  h->batch = batch;
+  h->seq_len = 0;
+  return PKV_OK;
+}
+
+// FullAttention offset rule (qwen3_next.rs:2430-2440) then the overflow rule (:435-441).
+static int position_for_append(pkv_cache *h, int64_t n, int64_t offset) {
+  if (n < 0) return set_error(PKV_ERR_ARG, "n must be >= 0");
+  if (offset >= 0 && offset != h->seq_len) {
+    if (offset <= h->seq_len)
+      h->seq_len = offset;
+    else
+      return set_error(PKV_ERR_OFFSET, "KV cache offset mismatch: offset=" +
+                                           std::to_string(offset) + " but cache has " +
+                                           std::to_string(h->seq_len) + " tokens");
+  }
+  if (h->seq_len + n > h->max_seq_len)
+    return set_error(PKV_ERR_OVERFLOW, "Quantized KV cache overflow: trying to store " +
+                                           std::to_string(h->seq_len + n) +
+                                           " tokens but max is " +
+                                           std::to_string(h->max_seq_len));
+  return PKV_OK;
+}
+
+int pkv_append(pkv_cache *h, const float *k, const float *v, int64_t n, int64_t offset) {
+  if (!h || (n > 0 && (!k || !v))) return set_error(PKV_ERR_ARG, "null argument");
+  int rc = position_for_append(h, n, offset);
+  if (rc) return rc;
+  rc = launch_append(h->quant, k, v, h->k, h->v, h->batch, h->n_kv_heads, h->head_dim, n,
+                     h->seq_len, h->stream);
+  if (rc) return rc;
+  h->seq_len += n;
+  return PKV_OK;
+}
+
+static AttnArgs cache_args(const pkv_cache *h, const float *q, int l, int num_heads, float scale,
+                           int64_t seq_k, int64_t q_offset, int causal, float *out) {
+  AttnArgs a;
+  a.quant = h->quant;
+  a.q = q;
+  a.k = h->k;
+  a.v = h->v;
+  a.rs = h->strides();
+  a.scale = scale;
+  a.batch = h->batch;
+  a.num_heads = num_heads;
+  a.num_kv_heads = h->n_kv_heads;
+  a.head_dim = h->head_dim;
+  a.l = l;
+  a.seq_k = seq_k;
+  a.q_offset = q_offset;
+  a.causal = causal;
+  a.out = out;
+  return a;
+}
+
+int pkv_attend(pkv_cache *h, const float *q, int l, int num_heads, float scale,
+               int64_t q_offset, int causal, float *out) {
+  if (!h || !q || !out) return set_error(PKV_ERR_ARG, "null argument");
+  if (h->seq_len == 0) return set_error(PKV_ERR_EMPTY, "Cannot attend over an empty cache");
+  return launch_attend(cache_args(h, q, l, num_heads, scale, h->seq_len, q_offset, causal, out),
+                       h->ws, h->stream);
+}
+
+int pkv_append_attend(pkv_cache *h, const float *k, const float *v, const float *q,
+                      int num_heads, float scale, int64_t offset, float *out) {
+  if (!h || !k || !v || !q || !out) return set_error(PKV_ERR_ARG, "null argument");
+  if (num_heads <= 0 || num_heads % h->n_kv_heads)
+    return set_error(PKV_ERR_ARG, "num_heads must be a multiple of num_kv_heads");
+  const int64_t saved = h->seq_len;
+  int rc = position_for_append(h, 1, offset);
+  if (rc) return rc;
+  const int64_t t_new = h->seq_len;
+  rc = launch_append_attend(cache_args(h, q, 1, num_heads, scale, t_new + 1, t_new, 1, out), k,
+                            v, h->k, h->v, t_new, h->ws, h->stream);
+  if (rc) {
+    if (rc != PKV_ERR_HIP) h->seq_len = saved;
+    return rc;
+  }
+  h->seq_len = t_new + 1;
+  return PKV_OK;
+}
+
+int pkv_get_kv(pkv_cache *h, float *k_out, float *v_out) {
+  if (!h) return set_error(PKV_ERR_ARG, "null handle");
+  if (h->seq_len == 0) return PKV_OK;
+  if (!k_out || !v_out) return set_error(PKV_ERR_ARG, "null argument");
+  return launch_dequant(h->quant, h->k, h->v, k_out, v_out, h->batch, h->n_kv_heads,
+                        h->head_dim, h->seq_len, h->stream);
+}
+
+int pkv_kv_storage(const pkv_cache *h, const void **k_bytes, const void **v_bytes,
+                   size_t *valid_bytes, int64_t strides[4]) {
+  if (!h) return set_error(PKV_ERR_ARG, "null handle");
+  if (h->seq_len == 0) return set_error(PKV_ERR_EMPTY, "Cannot get storage from empty cache");
+  if (k_bytes) *k_bytes = h->k;
+  if (v_bytes) *v_bytes = h->v;
+  if (valid_bytes) *valid_bytes = (size_t)h->seq_len * h->batch * h->n_kv_heads * h->bpr;
+  if (strides) {
+    const RowStrides r = h->strides();
+    strides[0] = r.b;
+    strides[1] = r.t;
+    strides[2] = r.h;
+    strides[3] = 1;
+  }
+  return PKV_OK;
+}
+
+int pkv_flash_attn(int quant, const float *q, const void *k_bytes, const void *v_bytes,
+                   const int64_t kv_strides[3], float scale, int batch, int num_heads,
+                   int num_kv_heads, int head_dim, int seq_q, int64_t seq_k, int64_t q_offset,
+                   int causal, float *out, pkv_stream stream) {
+  quant = norm_quant(quant);
+  if (!q || !k_bytes || !v_bytes || !kv_strides || !out)
+    return set_error(PKV_ERR_ARG, "null argument");
+  if (quant < PKV_QUANT_F16 || quant > PKV_QUANT_Q4K)
+    return set_error(PKV_ERR_ARG, "unknown quantization");
+  AttnArgs a;
+  a.quant = quant;
+  a.q = q;
+  a.k = static_cast<const uint8_t *>(k_bytes);
+  a.v = static_cast<const uint8_t *>(v_bytes);
+  a.rs = {kv_strides[0], kv_strides[1], kv_strides[2]};
+  a.scale = scale;
+  a.batch = batch;
+  a.num_heads = num_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.head_dim = head_dim;
+  a.l = seq_q;
+  a.seq_k = seq_k;
+  a.q_offset = q_offset;
+  a.causal = causal;
+  a.out = out;
+  return launch_attend(a, util_workspace(), static_cast<hipStream_t>(stream));
+}
+
+int pkv_append_attend_batched(pkv_cache *const *caches, int n, const float *k, const float *v,
+                              const float *q, int num_heads, float scale, float *out,
+                              pkv_stream stream) {
+  if (!caches || n <= 0 || !k || !v || !q || !out) return set_error(PKV_ERR_ARG, "bad argument");
+  const pkv_cache *c0 = caches[0];
+  if (!c0) return set_error(PKV_ERR_ARG, "null cache");
+  if (num_heads <= 0 || num_heads % c0->n_kv_heads)
+    return set_error(PKV_ERR_ARG, "num_heads must be a multiple of num_kv_heads");
+  std::vector<SeqDesc> seqs((size_t)n);
+  for (int i = 0; i < n; ++i) {
+    const pkv_cache *c = caches[i];
+    if (!c || c->batch != 1 || c->quant != c0->quant || c->n_kv_heads != c0->n_kv_heads ||
+        c->head_dim != c0->head_dim)
+      return set_error(PKV_ERR_ARG, "batched caches must be batch-1 with equal geometry");
+    if (c->seq_len + 1 > c->max_seq_len)
+      return set_error(PKV_ERR_OVERFLOW, "Quantized KV cache overflow in sequence " +
+                                             std::to_string(i));
+    seqs[(size_t)i] = {c->k, c->v, c->seq_len + 1};
+  }
+  int rc = launch_append_attend_batched(c0->quant, seqs.data(), n, k, v, q, num_heads,
+                                        c0->n_kv_heads, c0->head_dim, scale, out,
+                                        util_workspace(), static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  for (int i = 0; i < n; ++i) caches[i]->seq_len += 1;
+  return PKV_OK;
+}
+
+// ---------------------------------------------------------------- PrefixCache
+int pkv_prefix_create(const uint32_t *tokens, size_t n_tokens, int n_layers, pkv_prefix **out) {
+  if (!out || n_layers < 0 || (n_tokens && !tokens)) return set_error(PKV_ERR_ARG, "bad argument");
+  pkv_prefix *p = new pkv_prefix();
+  p->tokens.assign(tokens, tokens + n_tokens);
+  p->entries.resize((size_t)n_layers);
+  *out = p;
+  return PKV_OK;
+}
+
+int pkv_prefix_free(pkv_prefix *p) {
+  if (!p) return PKV_OK;
+  (void)hipDeviceSynchronize();
+  for (auto &e : p->entries) e.release();
+  delete p;
+  return PKV_OK;
+}
+
+int pkv_prefix_tokens(const pkv_prefix *p, const uint32_t **tokens, size_t *n) {
+  if (!p) return set_error(PKV_ERR_ARG, "null prefix");
+  if (tokens) *tokens = p->tokens.data();
+  if (n) *n = p->tokens.size();
+  return PKV_OK;
+}
+
+int pkv_prefix_num_layers(const pkv_prefix *p) { return p ? (int)p->entries.size() : -1; }
+
+int pkv_prefix_entry_kind(const pkv_prefix *p, int layer) {
+  if (!p || layer < 0 || layer >= (int)p->entries.size()) return -1;
+  return p->entries[(size_t)layer].kind;
+}
+
+int64_t pkv_prefix_full_len(const pkv_prefix *p, int layer) {
+  if (!p || layer < 0 || layer >= (int)p->entries.size()) return -1;
+  const Entry &e = p->entries[(size_t)layer];
+  return e.kind == PKV_ENTRY_FULL ? e.len : 0;
+}
+
+int pkv_prefix_linear_sizes(const pkv_prefix *p, int layer, size_t *n_ssm, size_t *n_conv,
+                            size_t *n_gate) {
+  if (!p || layer < 0 || layer >= (int)p->entries.size())
+    return set_error(PKV_ERR_ARG, "bad layer");
+  const Entry &e = p->entries[(size_t)layer];
+  if (n_ssm) *n_ssm = e.n_ssm;
+  if (n_conv) *n_conv = e.n_conv;
+  if (n_gate) *n_gate = e.n_gate;
+  return PKV_OK;
+}
+
+int pkv_prefix_save_full(pkv_prefix *p, int layer, const pkv_cache *h) {
+  if (!p || !h || layer < 0 || layer >= (int)p->entries.size())
+    return set_error(PKV_ERR_ARG, "bad argument");
+  Entry &e = p->entries[(size_t)layer];
+  e.release();
+  if (h->seq_len == 0) return PKV_OK;  // PrefixCacheEntry::Empty
+  const size_t bytes = (size_t)h->seq_len * h->batch * h->n_kv_heads * h->bpr;
+  PKV_HIP(hipMalloc(&e.k, bytes));
+  hipError_t er = hipMalloc(&e.v, bytes);
+  if (er != hipSuccess) {
+    e.release();
+    return hip_error(er, "pkv_prefix_save_full");
+  }
+  PKV_HIP(hipMemcpyAsync(e.k, h->k, bytes, hipMemcpyDeviceToDevice, h->stream));
+  PKV_HIP(hipMemcpyAsync(e.v, h->v, bytes, hipMemcpyDeviceToDevice, h->stream));
+  e.kind = PKV_ENTRY_FULL;
+  e.quant = h->quant;
+  e.batch = h->batch;
+  e.heads = h->n_kv_heads;
+  e.head_dim = h->head_dim;
+  e.bpr = h->bpr;
+  e.len = h->seq_len;
+  return PKV_OK;
+}
+
+int pkv_prefix_save_linear(pkv_prefix *p, int layer, const float *ssm, size_t n_ssm,
+                           const float *conv, size_t n_conv, const float *gate, size_t n_gate,
+                           pkv_stream stream) {
+  if (!p || layer < 0 || layer >= (int)p->entries.size() || !ssm || !conv)
+    return set_error(PKV_ERR_ARG, "bad argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Entry &e = p->entries[(size_t)layer];
+  e.release();
+  hipError_t er = hipMalloc(&e.ssm, (n_ssm ? n_ssm : 1) * 4);
+  if (er == hipSuccess) er = hipMalloc(&e.conv, (n_conv ? n_conv : 1) * 4);
+  if (er == hipSuccess) er = hipMalloc(&e.gate, (n_gate ? n_gate : 1) * 4);
+  if (er == hipSuccess) er = hipMemcpyAsync(e.ssm, ssm, n_ssm * 4, hipMemcpyDeviceToDevice, s);
+  if (er == hipSuccess) er = hipMemcpyAsync(e.conv, conv, n_conv * 4, hipMemcpyDeviceToDevice, s);
+  if (er == hipSuccess) {
+    if (gate)
+      er = hipMemcpyAsync(e.gate, gate, n_gate * 4, hipMemcpyDeviceToDevice, s);
+    else
+      er = hipMemsetAsync(e.gate, 0, n_gate * 4, s);  // zero offset (qwen3_next.rs:4077-4093)
+  }
+  if (er != hipSuccess) {
+    e.release();
+    return hip_error(er, "pkv_prefix_save_linear");
+  }
+  e.kind = PKV_ENTRY_LINEAR;
+  e.n_ssm = n_ssm;
+  e.n_conv = n_conv;
+  e.n_gate = n_gate;
+  return PKV_OK;
+}
+
+int pkv_prefix_restore(const pkv_prefix *p, const pkv_layer_target *targets, int n_layers,
+                       int mode, size_t *n_tokens_out, pkv_stream stream) {
+  if (!p || (n_layers && !targets)) return set_error(PKV_ERR_ARG, "bad argument");
+  if ((size_t)n_layers != p->entries.size())
+    return set_error(PKV_ERR_LAYERS, "Prefix cache layer count mismatch: " +
+                                         std::to_string(p->entries.size()) + " vs " +
+                                         std::to_string(n_layers));
+  if (mode != PKV_RESTORE_BYTES && mode != PKV_RESTORE_REQUANTIZE)
+    return set_error(PKV_ERR_ARG, "unknown restore mode");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Validate every layer before writing anything.
+  for (int i = 0; i < n_layers; ++i) {
+    const Entry &e = p->entries[(size_t)i];
+    const pkv_layer_target &t = targets[i];
+    if (t.cache && (t.ssm || t.conv || t.gate_offset))
+      return set_error(PKV_ERR_ARG, "layer " + std::to_string(i) + ": both cache and state set");
+    if (t.cache && e.kind == PKV_ENTRY_FULL) {
+      const pkv_cache *c = t.cache;
+      if (c->quant != e.quant || c->n_kv_heads != e.heads || c->head_dim != e.head_dim ||
+          c->batch != e.batch)
+        return set_error(PKV_ERR_LAYOUT, "layer " + std::to_string(i) +
+                                             ": snapshot geometry differs from the cache");
+      if (e.len > c->max_seq_len)
+        return set_error(PKV_ERR_OVERFLOW, "Quantized KV cache overflow: trying to store " +
+                                               std::to_string(e.len) + " tokens but max is " +
+                                               std::to_string(c->max_seq_len));
+    }
+    if (!t.cache && e.kind == PKV_ENTRY_LINEAR && (!t.ssm || !t.conv || !t.gate_offset))
+      return set_error(PKV_ERR_ARG, "layer " + std::to_string(i) + ": missing state targets");
+  }
+  std::vector<void *> dst;
+  std::vector<const void *> src;
+  std::vector<size_t> bytes;
+  for (int i = 0; i < n_layers; ++i) {
+    const Entry &e = p->entries[(size_t)i];
+    const pkv_layer_target &t = targets[i];
+    if (t.cache) {
+      if (e.kind == PKV_ENTRY_FULL) {
+        if (mode == PKV_RESTORE_BYTES) {
+          const size_t nb = (size_t)e.len * e.batch * e.heads * e.bpr;
+          dst.push_back(t.cache->k); src.push_back(e.k); bytes.push_back(nb);
+          dst.push_back(t.cache->v); src.push_back(e.v); bytes.push_back(nb);
+        }
+      }
+    } else if (e.kind == PKV_ENTRY_LINEAR) {
+      dst.push_back(t.ssm); src.push_back(e.ssm); bytes.push_back(e.n_ssm * 4);
+      dst.push_back(t.conv); src.push_back(e.conv); bytes.push_back(e.n_conv * 4);
+      dst.push_back(t.gate_offset); src.push_back(e.gate); bytes.push_back(e.n_gate * 4);
+    }
+  }
+  int rc = launch_copy_segments(dst.data(), src.data(), bytes.data(), (int)dst.size(),
+                                util_workspace(), s);
+  if (rc) return rc;
+  for (int i = 0; i < n_layers; ++i) {
+    const Entry &e = p->entries[(size_t)i];
+    const pkv_layer_target &t = targets[i];
+    if (t.cache) {
+      pkv_cache *c = t.cache;
+      if (e.kind != PKV_ENTRY_FULL) {
+        c->seq_len = 0;  // Empty / wrong kind -> clear_kv_cache (qwen3_next.rs:2874-2882)
+        continue;
+      }
+      if (mode == PKV_RESTORE_REQUANTIZE) {
+        // clear(); append(dequantized saved K/V) — the reference's restore path.
+        const size_t n = (size_t)e.batch * e.heads * (size_t)e.len * e.head_dim;
+        rc = c->ws.reserve(2 * n * sizeof(float));
+        if (rc) return rc;
+        float *kf = static_cast<float *>(c->ws.ptr), *vf = kf + n;
+        rc = launch_dequant(e.quant, e.k, e.v, kf, vf, e.batch, e.heads, e.head_dim, e.len, s);
+        if (!rc)
+          rc = launch_append(c->quant, kf, vf, c->k, c->v, c->batch, c->n_kv_heads,
+                             c->head_dim, e.len, 0, s);
+        if (rc) return rc;
+      }
+      c->seq_len = e.len;
+    } else if (t.state_valid) {
+      *t.state_valid = e.kind == PKV_ENTRY_LINEAR ? 1 : 0;
+    }
+  }
+  if (n_tokens_out) *n_tokens_out = p->tokens.size();
+  return PKV_OK;
+}
+
+int pkv_fill_normal(float *dst, size_t n, uint64_t seed, uint64_t stream_id, float scale,
+                    pkv_stream stream) {
+  if (!dst && n) return set_error(PKV_ERR_ARG, "null destination");
+  return launch_fill_normal(dst, n, seed, stream_id, scale, static_cast<hipStream_t>(stream));
+}
+
+int pkv_scale_channels(float *x, size_t rows, int dim, const int *channels, int n_ch,
+                       float factor, pkv_stream stream) {
+  if (!x || (n_ch && !channels) || dim <= 0) return set_error(PKV_ERR_ARG, "bad argument");
+  return launch_scale_channels(x, rows, dim, channels, n_ch, factor,
+                               static_cast<hipStream_t>(stream));
+}
+
+int pkv_copy_segments(void *const *dst, const void *const *src, const size_t *bytes, int n,
+                      pkv_stream stream) {
+  if (n < 0 || (n && (!dst || !src || !bytes))) return set_error(PKV_ERR_ARG, "bad argument");
+  return launch_copy_segments(dst, src, bytes, n, util_workspace(),
+                              static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,125 @@
+// Internal declarations shared by the libpkv translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/pkv.h"
+
+namespace pkv {
+
+// Thread-local error slot behind pkv_last_error().
+int set_error(int code, const std::string &msg);
+int hip_error(hipError_t e, const char *what);
+
+#define PKV_HIP(call)                                     \
+  do {                                                    \
+    hipError_t e_ = (call);                               \
+    if (e_ != hipSuccess) return ::pkv::hip_error(e_, #call); \
+  } while (0)
+
+inline int block_size(int quant) {
+  return quant == PKV_QUANT_Q8_0 ? 32 : quant == PKV_QUANT_Q4K ? 256 : 1;
+}
+inline int padded_dim(int quant, int head_dim) {
+  int bs = block_size(quant);
+  return (head_dim + bs - 1) / bs * bs;
+}
+inline size_t row_bytes(int quant, int head_dim) {
+  int p = padded_dim(quant, head_dim);
+  switch (quant) {
+    case PKV_QUANT_Q8_0: return (size_t)(p / 32) * 34;
+    case PKV_QUANT_Q4K: return (size_t)(p / 256) * 144;
+    case PKV_QUANT_F16:
+    case PKV_QUANT_BF16: return (size_t)p * 2;
+    default: return 0;
+  }
+}
+
+// Byte addressing of packed rows: row(b, t, h) = base + b*sb + t*st + h*sh.
+struct RowStrides {
+  int64_t b, t, h;
+};
+
+// Split-K scratch owned by a cache handle or by a stateless call.
+// Device scratch grows (hipMalloc) on demand, never inside a kernel. The pinned host
+// buffer stages small descriptor tables; an event guards its reuse.
+struct Workspace {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+  void *host = nullptr;
+  size_t host_bytes = 0;
+  hipEvent_t host_ev = nullptr;
+  bool host_pending = false;
+  int reserve(size_t need);
+  int reserve_host(size_t need);   // waits for the previous staged copy first
+  int mark_host_used(hipStream_t s);
+  ~Workspace();
+};
+
+}  // namespace pkv
+
+struct pkv_cache {
+  int quant, batch, n_kv_heads, head_dim, padded;
+  int64_t max_seq_len, seq_len;
+  size_t bpr;
+  uint8_t *k, *v;
+  hipStream_t stream;
+  pkv::Workspace ws;
+  pkv::RowStrides strides() const {
+    return {(int64_t)n_kv_heads * (int64_t)bpr, (int64_t)batch * n_kv_heads * (int64_t)bpr,
+            (int64_t)bpr};
+  }
+};
+
+namespace pkv {
+
+// ---- launchers (pkv_quant.hip) ----
+// Quantize n new tokens of k and v ([batch, heads, n, head_dim] f32) into rows
+// starting at token `t0` of the K and V buffers.
+int launch_append(int quant, const float *k, const float *v, uint8_t *kc, uint8_t *vc,
+                  int batch, int heads, int head_dim, int64_t n, int64_t t0, hipStream_t s);
+// Dequantize rows [0, S) to f32 [batch, heads, S, head_dim].
+int launch_dequant(int quant, const uint8_t *kc, const uint8_t *vc, float *ko, float *vo,
+                   int batch, int heads, int head_dim, int64_t S, hipStream_t s);
+
+// ---- launchers (pkv_attn.hip) ----
+struct AttnArgs {
+  int quant;
+  const float *q;  // [batch, l, num_heads, head_dim]
+  const uint8_t *k, *v;
+  RowStrides rs;
+  float scale;
+  int batch, num_heads, num_kv_heads, head_dim, l;
+  int64_t seq_k, q_offset;
+  int causal;
+  float *out;  // [batch, l, num_heads, head_dim]
+};
+int launch_attend(const AttnArgs &a, Workspace &ws, hipStream_t s);
+
+// Fused decode step: quantize one token (k, v [batch, heads, 1, head_dim]) into row
+// t_new and attend over keys [0, t_new].
+int launch_append_attend(const AttnArgs &a, const float *k_new, const float *v_new,
+                         uint8_t *kc, uint8_t *vc, int64_t t_new, Workspace &ws,
+                         hipStream_t s);
+
+struct SeqDesc {
+  uint8_t *k, *v;
+  int64_t len;  // keys after the append
+};
+int launch_append_attend_batched(int quant, const SeqDesc *seqs_host, int n, const float *k,
+                                 const float *v, const float *q, int num_heads,
+                                 int num_kv_heads, int head_dim, float scale, float *out,
+                                 Workspace &ws, hipStream_t s);
+
+// ---- launchers (pkv_util.hip) ----
+int launch_fill_normal(float *dst, size_t n, uint64_t seed, uint64_t stream_id, float scale,
+                       hipStream_t s);
+int launch_scale_channels(float *x, size_t rows, int dim, const int *ch, int n_ch,
+                          float factor, hipStream_t s);
+int launch_copy_segments(void *const *dst, const void *const *src, const size_t *bytes, int n,
+                         Workspace &ws, hipStream_t s);
+
+}  // namespace pkv

@@ -1,0 +1,332 @@
+// Quantize-on-append and dequantize kernels for the packed KV rows.
+//
+// Reference: PreallocatedQuantizedKvCache::append_quantized
+// (paramecia-model/src/qwen3_next.rs:431-509) quantizes the new [b, h, n, d] K/V on
+// the CPU with candle's QTensor::quantize and memcpy's the rows at
+// seq_len*b*h*bytes_per_row; get_kv (qwen3_next.rs:520-575) dequantizes them.
+// Here both run on the GPU, writing/reading the same seq-major rows in HBM.
+//
+// Bit-exactness: every a*b+c below must round twice like the Rust code, so
+// contraction is off for this whole file, divisions are IEEE (hipcc's default), and
+// each Q4K sub-block's sums run sequentially in one lane.
+#pragma clang fp contract(off)
+
+#include "pkv_internal.hpp"
+#include "pkv_scalar.hpp"
+
+namespace pkv {
+namespace {
+
+struct AppendArgs {
+  const float *src[2];  // k, v: [batch, heads, n, head_dim]
+  uint8_t *dst[2];      // K, V row buffers
+  int batch, heads, head_dim, padded;
+  int64_t n, t0;
+  int64_t bpr;
+};
+
+// Source element e (< padded) of new row (t, b, h); zero padding past head_dim.
+__device__ __forceinline__ float load_elem(const float *src, const AppendArgs &a, int64_t t,
+                                           int b, int h, int e) {
+  if (e >= a.head_dim) return 0.0f;
+  return src[(((int64_t)b * a.heads + h) * a.n + t) * a.head_dim + e];
+}
+
+__device__ __forceinline__ int64_t dst_row(const AppendArgs &a, int64_t t, int b, int h) {
+  return ((a.t0 + t) * a.batch + b) * a.heads + h;
+}
+
+// candle make_qkx1_quants(nmax = 15, ntry = 5) over the 32 values of one sub-block.
+__device__ void make_qkx1_quants_32(const float x[32], float &scale_out, float &neg_min_out) {
+  float mn = x[0], mx = x[0];
+#pragma unroll
+  for (int i = 1; i < 32; ++i) {
+    if (total_key(x[i]) < total_key(mn)) mn = x[i];
+    if (total_key(x[i]) >= total_key(mx)) mx = x[i];
+  }
+  if (mx == mn) {
+    scale_out = 0.0f;
+    neg_min_out = 0.0f;
+    return;
+  }
+  uint8_t L[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) L[i] = 0;
+  float min = fmin_rs(mn, 0.0f);
+  float iscale = 15.0f / (mx - min);
+  float scale = 1.0f / iscale;
+  for (int t = 0; t < 5; ++t) {
+    float sumlx = 0.0f;
+    int32_t suml2 = 0;
+    bool did_change = false;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      int32_t li = nearest_int(iscale * (x[i] - min));
+      li = li < 0 ? 0 : (li > 15 ? 15 : li);
+      if ((uint8_t)li != L[i]) {
+        L[i] = (uint8_t)li;
+        did_change = true;
+      }
+      sumlx += (x[i] - min) * (float)li;
+      suml2 += li * li;
+    }
+    scale = sumlx / (float)suml2;
+    float sum = -0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) sum += x[i] - scale * (float)L[i];
+    min = sum / 32.0f;
+    if (min > 0.0f) min = 0.0f;
+    iscale = 1.0f / scale;
+    if (!did_change) break;
+  }
+  scale_out = scale;
+  neg_min_out = -min;
+}
+
+// Q4K (BlockQ4K::from_float): 8 lanes per 256-element superblock, lane j owns
+// sub-block j. Cross-lane work is limited to exact max reductions and byte shuffles.
+__global__ __launch_bounds__(256) void q4k_append_kernel(AppendArgs a, int64_t units_per_tensor,
+                                                         int nsb) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t unit = gid >> 3;
+  const int j = (int)(gid & 7);
+  const int64_t total = 2 * units_per_tensor;
+  const bool active = unit < total;
+  if (!active) unit = total - 1;  // compute redundantly, store nothing
+  const int p = (int)(unit / units_per_tensor);
+  int64_t u = unit % units_per_tensor;
+  const int sb = (int)(u % nsb);
+  u /= nsb;
+  const int h = (int)(u % a.heads);
+  u /= a.heads;
+  const int b = (int)(u % a.batch);
+  const int64_t t = u / a.batch;
+
+  float x[32];
+  const int e0 = sb * 256 + 32 * j;
+  const float *src = a.src[p];
+  if ((a.head_dim & 3) == 0 && e0 + 32 <= a.head_dim) {
+    const float4 *s4 = reinterpret_cast<const float4 *>(
+        src + (((int64_t)b * a.heads + h) * a.n + t) * a.head_dim + e0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float4 f = s4[i];
+      x[4 * i] = f.x;
+      x[4 * i + 1] = f.y;
+      x[4 * i + 2] = f.z;
+      x[4 * i + 3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) x[i] = load_elem(src, a, t, b, h, e0 + i);
+  }
+
+  float scale, mins;
+  make_qkx1_quants_32(x, scale, mins);
+
+  float max_scale = scale, max_min = mins;
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) {
+    max_scale = fmax_rs(max_scale, __shfl_xor(max_scale, o, 8));
+    max_min = fmax_rs(max_min, __shfl_xor(max_min, o, 8));
+  }
+  max_scale = fmax_rs(max_scale, 0.0f);
+  max_min = fmax_rs(max_min, 0.0f);
+  const float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+  const float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+  int32_t ls32 = nearest_int(inv_scale * scale);
+  int32_t lm32 = nearest_int(inv_min * mins);
+  const uint32_t ls = (uint8_t)(ls32 < 63 ? ls32 : 63);
+  const uint32_t lm = (uint8_t)(lm32 < 63 ? lm32 : 63);
+
+  const uint16_t dh = f32_to_f16(max_scale / 63.0f);
+  const uint16_t mh = f32_to_f16(max_min / 63.0f);
+
+  // get_scale_min_k4(j) of the packed codes returns (ls, lm) for this sub-block.
+  uint32_t Lw[4] = {0u, 0u, 0u, 0u};
+  const float dd = f16_to_f32(dh) * (float)ls;
+  if (dd != 0.0f) {
+    const float dm = f16_to_f32(mh) * (float)lm;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      int32_t l = nearest_int((x[i] + dm) / dd);
+      l = l < 0 ? 0 : (l > 15 ? 15 : l);
+      Lw[i >> 3] |= (uint32_t)l << (4 * (i & 7));
+    }
+  }
+
+  // Header: d, dmin, and the 12 packed scale bytes, gathered from the 8 lanes.
+  uint32_t code = ls | (lm << 8);
+  uint32_t codes[8];
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) codes[jj] = __shfl(code, jj, 8);
+  uint8_t sc[12];
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const uint32_t ls_lo = codes[jj] & 0xFF, lm_lo = codes[jj] >> 8;
+    const uint32_t ls_hi = codes[jj + 4] & 0xFF, lm_hi = codes[jj + 4] >> 8;
+    sc[jj] = (uint8_t)(ls_lo | ((ls_hi >> 4) << 6));
+    sc[jj + 4] = (uint8_t)(lm_lo | ((lm_hi >> 4) << 6));
+    sc[jj + 8] = (uint8_t)((ls_hi & 0xF) | ((lm_hi & 0xF) << 4));
+  }
+
+  // Nibbles: qs[32c + l] = L_{2c}[l] | L_{2c+1}[l] << 4. Lane j writes qs[16j, 16j+16).
+  const bool odd = (j & 1) != 0;
+  uint32_t s0 = odd ? Lw[0] : Lw[2], s1 = odd ? Lw[1] : Lw[3];
+  uint32_t r0 = __shfl_xor(s0, 1, 8), r1 = __shfl_xor(s1, 1, 8);
+  uint32_t lo0 = odd ? r0 : Lw[0], lo1 = odd ? r1 : Lw[1];
+  uint32_t hi0 = odd ? Lw[2] : r0, hi1 = odd ? Lw[3] : r1;
+  uint32_t outw[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t lo = (w < 2) ? lo0 : lo1, hi = (w < 2) ? hi0 : hi1;
+    const int sh = (w & 1) * 16;
+    uint32_t v = 0;
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+      uint32_t ln = (lo >> (sh + 4 * bb)) & 0xF, hn = (hi >> (sh + 4 * bb)) & 0xF;
+      v |= (ln | (hn << 4)) << (8 * bb);
+    }
+    outw[w] = v;
+  }
+  if (!active) return;
+  uint8_t *blk = a.dst[p] + dst_row(a, t, b, h) * a.bpr + (int64_t)sb * 144;
+  uint4 q4 = {outw[0], outw[1], outw[2], outw[3]};
+  *reinterpret_cast<uint4 *>(blk + 16 + 16 * j) = q4;
+  if (j == 0) {
+    uint4 hd;
+    hd.x = (uint32_t)dh | ((uint32_t)mh << 16);
+    hd.y = (uint32_t)sc[0] | ((uint32_t)sc[1] << 8) | ((uint32_t)sc[2] << 16) | ((uint32_t)sc[3] << 24);
+    hd.z = (uint32_t)sc[4] | ((uint32_t)sc[5] << 8) | ((uint32_t)sc[6] << 16) | ((uint32_t)sc[7] << 24);
+    hd.w = (uint32_t)sc[8] | ((uint32_t)sc[9] << 8) | ((uint32_t)sc[10] << 16) | ((uint32_t)sc[11] << 24);
+    *reinterpret_cast<uint4 *>(blk) = hd;
+  }
+}
+
+// Q8_0 (BlockQ8_0::from_float): one lane per 32-element block.
+__global__ __launch_bounds__(256) void q8_0_append_kernel(AppendArgs a, int64_t units_per_tensor,
+                                                          int nblk) {
+  const int64_t unit = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (unit >= 2 * units_per_tensor) return;
+  const int p = (int)(unit / units_per_tensor);
+  int64_t u = unit % units_per_tensor;
+  const int blk = (int)(u % nblk);
+  u /= nblk;
+  const int h = (int)(u % a.heads);
+  u /= a.heads;
+  const int b = (int)(u % a.batch);
+  const int64_t t = u / a.batch;
+  float x[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) x[i] = load_elem(a.src[p], a, t, b, h, blk * 32 + i);
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmax_rs(amax, __builtin_fabsf(x[i]));
+  const float d = amax / 127.0f;
+  const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+  uint16_t w[17];
+  w[0] = f32_to_f16(d);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    uint32_t q0 = (uint8_t)rs_as_i8(__builtin_roundf(x[2 * i] * id));
+    uint32_t q1 = (uint8_t)rs_as_i8(__builtin_roundf(x[2 * i + 1] * id));
+    w[1 + i] = (uint16_t)(q0 | (q1 << 8));
+  }
+  uint16_t *dst =
+      reinterpret_cast<uint16_t *>(a.dst[p] + dst_row(a, t, b, h) * a.bpr + (int64_t)blk * 34);
+#pragma unroll
+  for (int i = 0; i < 17; ++i) dst[i] = w[i];
+}
+
+// F16 / BF16 rows: element-wise round-to-nearest-even conversion.
+template <bool BF>
+__global__ __launch_bounds__(256) void half_append_kernel(AppendArgs a, int64_t elems_per_tensor) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= 2 * elems_per_tensor) return;
+  const int p = (int)(i / elems_per_tensor);
+  int64_t u = i % elems_per_tensor;
+  const int e = (int)(u % a.padded);
+  u /= a.padded;
+  const int h = (int)(u % a.heads);
+  u /= a.heads;
+  const int b = (int)(u % a.batch);
+  const int64_t t = u / a.batch;
+  const float x = load_elem(a.src[p], a, t, b, h, e);
+  uint16_t *dst = reinterpret_cast<uint16_t *>(a.dst[p] + dst_row(a, t, b, h) * a.bpr);
+  dst[e] = BF ? f32_to_bf16(x) : f32_to_f16(x);
+}
+
+__global__ __launch_bounds__(256) void dequant_kernel(int quant, const uint8_t *kc,
+                                                      const uint8_t *vc, float *ko, float *vo,
+                                                      int batch, int heads, int head_dim,
+                                                      int64_t S, int64_t bpr) {
+  const int64_t per = (int64_t)batch * heads * S * head_dim;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= 2 * per) return;
+  const int p = (int)(i / per);
+  int64_t u = i % per;  // index into [b, h, S, d]
+  const int e = (int)(u % head_dim);
+  u /= head_dim;
+  const int64_t t = u % S;
+  u /= S;
+  const int h = (int)(u % heads);
+  const int b = (int)(u / heads);
+  const int64_t r = (t * batch + b) * heads + h;
+  const uint8_t *row = (p ? vc : kc) + r * bpr;
+  (p ? vo : ko)[i % per] = decode_elem(quant, row, e);
+}
+
+}  // namespace
+
+int launch_append(int quant, const float *k, const float *v, uint8_t *kc, uint8_t *vc,
+                  int batch, int heads, int head_dim, int64_t n, int64_t t0, hipStream_t s) {
+  if (n == 0) return PKV_OK;
+  AppendArgs a;
+  a.src[0] = k;
+  a.src[1] = v;
+  a.dst[0] = kc;
+  a.dst[1] = vc;
+  a.batch = batch;
+  a.heads = heads;
+  a.head_dim = head_dim;
+  a.padded = padded_dim(quant, head_dim);
+  a.n = n;
+  a.t0 = t0;
+  a.bpr = (int64_t)row_bytes(quant, head_dim);
+  const int64_t rows = n * batch * heads;
+  if (quant == PKV_QUANT_Q4K) {
+    const int nsb = a.padded / 256;
+    const int64_t units = rows * nsb;
+    const int64_t threads = 2 * units * 8;
+    hipLaunchKernelGGL(q4k_append_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       s, a, units, nsb);
+  } else if (quant == PKV_QUANT_Q8_0) {
+    const int nblk = a.padded / 32;
+    const int64_t units = rows * nblk;
+    hipLaunchKernelGGL(q8_0_append_kernel, dim3((unsigned)((2 * units + 255) / 256)), dim3(256),
+                       0, s, a, units, nblk);
+  } else {
+    const int64_t elems = rows * a.padded;
+    if (quant == PKV_QUANT_BF16)
+      hipLaunchKernelGGL(half_append_kernel<true>, dim3((unsigned)((2 * elems + 255) / 256)),
+                         dim3(256), 0, s, a, elems);
+    else
+      hipLaunchKernelGGL(half_append_kernel<false>, dim3((unsigned)((2 * elems + 255) / 256)),
+                         dim3(256), 0, s, a, elems);
+  }
+  PKV_HIP(hipGetLastError());
+  return PKV_OK;
+}
+
+int launch_dequant(int quant, const uint8_t *kc, const uint8_t *vc, float *ko, float *vo,
+                   int batch, int heads, int head_dim, int64_t S, hipStream_t s) {
+  const int64_t total = 2 * (int64_t)batch * heads * S * head_dim;
+  if (total == 0) return PKV_OK;
+  hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     quant, kc, vc, ko, vo, batch, heads, head_dim, S,
+                     (int64_t)row_bytes(quant, head_dim));
+  PKV_HIP(hipGetLastError());
+  return PKV_OK;
+}
+
+}  // namespace pkv

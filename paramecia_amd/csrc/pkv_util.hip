@@ -1,0 +1,140 @@
+// Utility kernels: seeded synthetic data, channel scaling, and the batched
+// gather/copy used by PrefixCache restore (qwen3_next.rs:2819-2884 restores every
+// layer separately on the CPU; here all segments of a prefix go out in one launch).
+#include <string.h>
+
+#include <vector>
+
+#include "pkv_internal.hpp"
+#include "pkv_scalar.hpp"
+
+namespace pkv {
+namespace {
+
+__global__ __launch_bounds__(256) void fill_normal_kernel(float *dst, size_t n, uint64_t seed,
+                                                          uint64_t stream_id, float scale) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = seeded_normal(seed, stream_id, i) * scale;
+}
+
+constexpr int kMaxChannels = 64;
+struct Channels {
+  int ch[kMaxChannels];
+};
+
+__global__ __launch_bounds__(256) void scale_channels_kernel(float *x, size_t rows, int dim,
+                                                             Channels c, int n_ch,
+                                                             float factor) {
+  const size_t total = rows * (size_t)n_ch;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t r = i / n_ch;
+    x[r * dim + c.ch[i % n_ch]] *= factor;
+  }
+}
+
+// Segment table for the batched copy. Chunk c of the launch belongs to the segment s
+// with first_chunk[s] <= c < first_chunk[s+1].
+struct Segment {
+  uint8_t *dst;
+  const uint8_t *src;
+  uint64_t bytes;
+  uint64_t first_chunk;
+};
+constexpr uint64_t kChunk = 64 * 1024;  // bytes per workgroup
+
+__global__ __launch_bounds__(256) void copy_segments_kernel(const Segment *segs, int n) {
+  const uint64_t c = blockIdx.x;
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {  // last segment with first_chunk <= c
+    const int mid = (lo + hi + 1) >> 1;
+    if (segs[mid].first_chunk <= c) lo = mid; else hi = mid - 1;
+  }
+  const Segment sg = segs[lo];
+  const uint64_t off = (c - sg.first_chunk) * kChunk;
+  const uint64_t len = sg.bytes - off < kChunk ? sg.bytes - off : kChunk;
+  uint8_t *d = sg.dst + off;
+  const uint8_t *s = sg.src + off;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(d) | reinterpret_cast<uintptr_t>(s)) & 15) == 0;
+  uint64_t done = 0;
+  if (aligned) {
+    const uint64_t n16 = len / 16;
+    const uint4 *s4 = reinterpret_cast<const uint4 *>(s);
+    uint4 *d4 = reinterpret_cast<uint4 *>(d);
+    uint64_t i = threadIdx.x;
+    for (; i + 3 * 256 < n16; i += 4 * 256) {  // four loads in flight per lane
+      const uint4 a0 = s4[i], a1 = s4[i + 256], a2 = s4[i + 512], a3 = s4[i + 768];
+      d4[i] = a0;
+      d4[i + 256] = a1;
+      d4[i + 512] = a2;
+      d4[i + 768] = a3;
+    }
+    for (; i < n16; i += 256) d4[i] = s4[i];
+    done = n16 * 16;
+  }
+  for (uint64_t i = done + threadIdx.x; i < len; i += 256) d[i] = s[i];
+}
+
+}  // namespace
+
+int launch_fill_normal(float *dst, size_t n, uint64_t seed, uint64_t stream_id, float scale,
+                       hipStream_t s) {
+  if (n == 0) return PKV_OK;
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(fill_normal_kernel, dim3((unsigned)blocks), dim3(256), 0, s, dst, n, seed,
+                     stream_id, scale);
+  PKV_HIP(hipGetLastError());
+  return PKV_OK;
+}
+
+int launch_scale_channels(float *x, size_t rows, int dim, const int *ch, int n_ch, float factor,
+                          hipStream_t s) {
+  if (n_ch < 0 || n_ch > kMaxChannels) return set_error(PKV_ERR_ARG, "at most 64 channels");
+  Channels c{};
+  for (int i = 0; i < n_ch; ++i) {
+    if (ch[i] < 0 || ch[i] >= dim) return set_error(PKV_ERR_ARG, "channel index out of range");
+    c.ch[i] = ch[i];
+  }
+  const size_t total = rows * (size_t)n_ch;
+  if (total == 0) return PKV_OK;
+  size_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(scale_channels_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, rows,
+                     dim, c, n_ch, factor);
+  PKV_HIP(hipGetLastError());
+  return PKV_OK;
+}
+
+int launch_copy_segments(void *const *dst, const void *const *src, const size_t *bytes, int n,
+                         Workspace &ws, hipStream_t s) {
+  std::vector<Segment> segs;
+  uint64_t chunks = 0;
+  for (int i = 0; i < n; ++i) {
+    if (bytes[i] == 0) continue;
+    Segment g;
+    g.dst = static_cast<uint8_t *>(dst[i]);
+    g.src = static_cast<const uint8_t *>(src[i]);
+    g.bytes = bytes[i];
+    g.first_chunk = chunks;
+    chunks += (bytes[i] + kChunk - 1) / kChunk;
+    segs.push_back(g);
+  }
+  if (segs.empty()) return PKV_OK;
+  if (chunks > 0x7FFFFFFFull) return set_error(PKV_ERR_ARG, "copy too large for one launch");
+  const size_t table = segs.size() * sizeof(Segment);
+  int rc = ws.reserve(table);
+  if (!rc) rc = ws.reserve_host(table);
+  if (rc) return rc;
+  memcpy(ws.host, segs.data(), table);
+  PKV_HIP(hipMemcpyAsync(ws.ptr, ws.host, table, hipMemcpyHostToDevice, s));
+  rc = ws.mark_host_used(s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(copy_segments_kernel, dim3((unsigned)chunks), dim3(256), 0, s,
+                     static_cast<const Segment *>(ws.ptr), (int)segs.size());
+  PKV_HIP(hipGetLastError());
+  return PKV_OK;
+}
+
+}  // namespace pkv

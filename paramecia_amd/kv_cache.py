@@ -1,0 +1,448 @@
+"""Host-side mirror of paramecia-model's KV-cache API on top of libpkv.
+
+Names, argument meaning and error behaviour follow the reference
+(paramecia-model/src/qwen3_next.rs): KvCacheQuantization (:88-166),
+PreallocatedQuantizedKvCache (:343-643), the cache block of FullAttention::forward
+(:2401-2561), RecurrentState / PrefixCacheEntry / PrefixCache (:683-864) and the
+ModelWeights cache methods (:5466-5501, :5685-5750). Tensors are torch device tensors;
+torch provides memory and streams only, every kernel is libpkv's.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+from dataclasses import dataclass, field
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import PkvError, check, lib
+
+
+# ------------------------------------------------------------------ errors
+class KvCacheError(RuntimeError):
+    """candle::bail! on the KV-cache path."""
+
+
+class KvCacheOverflow(KvCacheError):
+    pass
+
+
+class KvCacheOffsetMismatch(KvCacheError):
+    pass
+
+
+class EmptyCacheError(KvCacheError):
+    pass
+
+
+class PrefixLayerMismatch(KvCacheError):
+    pass
+
+
+_ERRORS = {
+    _lib.ERR_OVERFLOW: KvCacheOverflow,
+    _lib.ERR_OFFSET: KvCacheOffsetMismatch,
+    _lib.ERR_EMPTY: EmptyCacheError,
+    _lib.ERR_LAYERS: PrefixLayerMismatch,
+}
+
+
+def _call(rc: int) -> None:
+    if rc != _lib.OK:
+        msg = lib().pkv_last_error().decode()
+        raise _ERRORS.get(rc, KvCacheError)(f"[pkv {rc}] {msg}")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _f32(t: torch.Tensor, name: str) -> torch.Tensor:
+    if not t.is_cuda or t.dtype != torch.float32:
+        raise KvCacheError(f"{name} must be a float32 device tensor")
+    return t.contiguous()
+
+
+class _DeviceBytes:
+    """__cuda_array_interface__ view of library-owned device bytes."""
+
+    def __init__(self, ptr: int, n: int):
+        self.__cuda_array_interface__ = {
+            "shape": (n,), "typestr": "|u1", "data": (ptr, False), "version": 3,
+            "strides": None,
+        }
+
+
+# ------------------------------------------------------------------ KvCacheQuantization
+class KvCacheQuantization(enum.IntEnum):
+    NONE = _lib.QUANT_NONE  # deprecated alias of F16
+    F16 = _lib.QUANT_F16
+    BF16 = _lib.QUANT_BF16
+    Q8_0 = _lib.QUANT_Q8_0
+    Q4K = _lib.QUANT_Q4K
+
+    @classmethod
+    def default(cls) -> "KvCacheQuantization":
+        return cls(lib().pkv_quant_default())
+
+    @classmethod
+    def from_str(cls, s: str) -> Optional["KvCacheQuantization"]:
+        out = ctypes.c_int()
+        rc = lib().pkv_quant_parse(s.encode(), ctypes.byref(out))
+        return cls(out.value) if rc == _lib.OK else None
+
+    def block_size(self) -> int:
+        return lib().pkv_quant_block_size(int(self))
+
+    def to_ggml_dtype(self) -> Optional[str]:
+        return {KvCacheQuantization.Q8_0: "Q8_0", KvCacheQuantization.Q4K: "Q4K"}.get(self)
+
+    def cache_dtype(self) -> Optional[torch.dtype]:
+        if self in (KvCacheQuantization.NONE, KvCacheQuantization.F16):
+            return torch.float16
+        if self == KvCacheQuantization.BF16:
+            return torch.bfloat16
+        return None
+
+
+# ------------------------------------------------------------------ the cache
+class PreallocatedQuantizedKvCache:
+    """Device-resident preallocated cache with O(1) append and quantize-on-write."""
+
+    def __init__(self, batch_size: int, num_kv_heads: int, max_seq_len: int, head_dim: int,
+                 quant: KvCacheQuantization = KvCacheQuantization.Q4K, stream: Optional[int] = None):
+        h = ctypes.c_void_p()
+        _call(lib().pkv_create(int(quant), batch_size, num_kv_heads, head_dim, max_seq_len,
+                               ctypes.c_void_p(stream if stream is not None else _stream()),
+                               ctypes.byref(h)))
+        self._h = h
+        self.quant = KvCacheQuantization(int(quant) or _lib.QUANT_F16)
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.max_seq_len = max_seq_len
+        self.bytes_per_row = lib().pkv_bytes_per_row(int(quant), head_dim)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            lib().pkv_destroy(h)
+            self._h = None
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    @property
+    def seq_len(self) -> int:
+        return lib().pkv_len(self._h)
+
+    @property
+    def batch_size(self) -> int:
+        b = ctypes.c_int()
+        check(lib().pkv_geometry(self._h, None, ctypes.byref(b), None, None, None))
+        return b.value
+
+    def set_stream(self, stream: int) -> None:
+        check(lib().pkv_set_stream(self._h, ctypes.c_void_p(stream)))
+
+    def append_quantized(self, new_k: torch.Tensor, new_v: torch.Tensor,
+                         offset: int = -1) -> None:
+        """new_k, new_v: [batch, num_kv_heads, n, head_dim] f32 (qwen3_next.rs:431)."""
+        k, v = _f32(new_k, "new_k"), _f32(new_v, "new_v")
+        if k.shape != v.shape or k.dim() != 4:
+            raise KvCacheError("new_k/new_v must both be [batch, heads, n, head_dim]")
+        _call(lib().pkv_append(self._h, _ptr(k), _ptr(v), k.shape[2], offset))
+
+    def append(self, new_k: torch.Tensor, new_v: torch.Tensor):
+        self.append_quantized(new_k, new_v)
+        return self.get_kv()
+
+    def get_kv(self):
+        """Dequantized [batch, heads, seq_len, head_dim] f32 tensors (qwen3_next.rs:520)."""
+        shape = (self.batch_size, self.num_kv_heads, self.seq_len, self.head_dim)
+        k = torch.empty(shape, dtype=torch.float32, device="cuda")
+        v = torch.empty(shape, dtype=torch.float32, device="cuda")
+        _call(lib().pkv_get_kv(self._h, _ptr(k), _ptr(v)))
+        return k, v
+
+    def get_kv_storage(self):
+        """(k_ptr, v_ptr, valid_bytes, (stride_b, stride_seq, stride_h, stride_d))."""
+        kp, vp, n = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_size_t()
+        st = (ctypes.c_int64 * 4)()
+        _call(lib().pkv_kv_storage(self._h, ctypes.byref(kp), ctypes.byref(vp), ctypes.byref(n), st))
+        return kp.value, vp.value, n.value, tuple(st)
+
+    def raw_bytes(self):
+        """Copies of the valid packed K and V bytes as uint8 device tensors."""
+        if self.seq_len == 0:
+            e = torch.empty(0, dtype=torch.uint8, device="cuda")
+            return e, e.clone()
+        kp, vp, n, _ = self.get_kv_storage()
+        k = torch.as_tensor(_DeviceBytes(kp, n), device="cuda").clone()
+        v = torch.as_tensor(_DeviceBytes(vp, n), device="cuda").clone()
+        return k, v
+
+    def attend(self, q: torch.Tensor, scale: float, q_offset: int, causal: bool = True) -> torch.Tensor:
+        """q: [batch, l, num_heads, head_dim] f32 -> out of the same shape."""
+        q = _f32(q, "q")
+        out = torch.empty_like(q)
+        _call(lib().pkv_attend(self._h, _ptr(q), q.shape[1], q.shape[2], scale, q_offset,
+                               int(causal), _ptr(out)))
+        return out
+
+    def append_attend(self, new_k, new_v, q, scale: float, offset: int = -1) -> torch.Tensor:
+        """Fused decode step: append one token and attend over every key."""
+        k, v, q = _f32(new_k, "new_k"), _f32(new_v, "new_v"), _f32(q, "q")
+        out = torch.empty_like(q)
+        _call(lib().pkv_append_attend(self._h, _ptr(k), _ptr(v), _ptr(q), q.shape[2], scale,
+                                      offset, _ptr(out)))
+        return out
+
+    def clear(self) -> None:
+        check(lib().pkv_clear(self._h))
+
+    def truncate(self, new_len: int) -> None:
+        check(lib().pkv_truncate(self._h, new_len))
+
+    def resize_batch(self, batch_size: int) -> None:
+        _call(lib().pkv_resize_batch(self._h, batch_size))
+
+
+def flash_attn(quant: KvCacheQuantization, q: torch.Tensor, k_ptr: int, v_ptr: int,
+               strides: Sequence[int], scale: float, num_kv_heads: int, seq_k: int,
+               q_offset: int, causal: bool) -> torch.Tensor:
+    """ops::flash_attn_q8 (paramecia-model/src/ops.rs:756) over caller-owned packed rows."""
+    q = _f32(q, "q")
+    b, l, H, d = q.shape
+    out = torch.empty_like(q)
+    st = (ctypes.c_int64 * 3)(*strides[:3])
+    _call(lib().pkv_flash_attn(int(quant), _ptr(q), ctypes.c_void_p(k_ptr), ctypes.c_void_p(v_ptr),
+                               st, scale, b, H, num_kv_heads, d, l, seq_k, q_offset, int(causal),
+                               _ptr(out), ctypes.c_void_p(_stream())))
+    return out
+
+
+def append_attend_batched(caches: Sequence[PreallocatedQuantizedKvCache], k: torch.Tensor,
+                          v: torch.Tensor, q: torch.Tensor, scale: float) -> torch.Tensor:
+    """One decode step over independent batch-1 sequences in one launch.
+    k, v: [n, num_kv_heads, head_dim]; q: [n, num_heads, head_dim]."""
+    k, v, q = _f32(k, "k"), _f32(v, "v"), _f32(q, "q")
+    out = torch.empty_like(q)
+    arr = (ctypes.c_void_p * len(caches))(*[c.handle.value for c in caches])
+    _call(lib().pkv_append_attend_batched(arr, len(caches), _ptr(k), _ptr(v), _ptr(q), q.shape[1],
+                                          scale, _ptr(out), ctypes.c_void_p(_stream())))
+    return out
+
+
+def fill_normal(t: torch.Tensor, seed: int, stream_id: int, scale: float = 1.0) -> torch.Tensor:
+    """Seeded synthetic data identical to the CPU oracle's generator."""
+    t = _f32(t, "t")
+    _call(lib().pkv_fill_normal(_ptr(t), t.numel(), seed, stream_id, scale,
+                                ctypes.c_void_p(_stream())))
+    return t
+
+
+def scale_channels(t: torch.Tensor, channels: Sequence[int], factor: float) -> torch.Tensor:
+    t = _f32(t, "t")
+    arr = (ctypes.c_int * len(channels))(*channels)
+    _call(lib().pkv_scale_channels(_ptr(t), t.numel() // t.shape[-1], t.shape[-1], arr,
+                                   len(channels), factor, ctypes.c_void_p(_stream())))
+    return t
+
+
+# ------------------------------------------------------------------ FullAttention's cache block
+class FullAttentionKv:
+    """The KV-cache half of FullAttention::forward (qwen3_next.rs:2401-2561): lazy cache
+    creation, the offset rule (smaller offset truncates, larger errors), append, then
+    causal GQA attention with q_offset = seq_len - l and scale 1/sqrt(head_dim)."""
+
+    def __init__(self, num_heads: int, num_kv_heads: int, head_dim: int, max_seq_len: int,
+                 quant: KvCacheQuantization = KvCacheQuantization.Q4K):
+        self.num_heads, self.num_kv_heads, self.head_dim = num_heads, num_kv_heads, head_dim
+        self.max_seq_len = max_seq_len
+        self.kv_cache_quantization = quant
+        self.quantized_cache: Optional[PreallocatedQuantizedKvCache] = None
+        self.scale = float(1.0 / (head_dim ** 0.5))
+
+    def _ensure(self, b: int) -> PreallocatedQuantizedKvCache:
+        if self.quantized_cache is None:
+            self.quantized_cache = PreallocatedQuantizedKvCache(
+                b, self.num_kv_heads, self.max_seq_len, self.head_dim, self.kv_cache_quantization)
+        return self.quantized_cache
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, offset: int) -> torch.Tensor:
+        """q: [b, l, num_heads, d]; k, v: [b, num_kv_heads, l, d]. Returns [b, l, num_heads*d]."""
+        b, l = q.shape[0], q.shape[1]
+        cache = self._ensure(b)
+        if l == 1:
+            out = cache.append_attend(k, v, q, self.scale, offset)
+        else:
+            cache.append_quantized(k, v, offset)
+            seq_k = cache.seq_len
+            out = cache.attend(q, self.scale, seq_k - l, causal=True)
+        return out.reshape(b, l, self.num_heads * self.head_dim)
+
+    def cache_seq_len(self) -> int:
+        return 0 if self.quantized_cache is None else self.quantized_cache.seq_len
+
+    def clear_kv_cache(self) -> None:
+        if self.quantized_cache is not None:
+            self.quantized_cache.clear()
+
+    def truncate_kv_cache(self, new_len: int) -> None:
+        if self.quantized_cache is not None:
+            self.quantized_cache.truncate(new_len)
+
+
+@dataclass
+class RecurrentState:
+    """Gated-DeltaNet state of one linear-attention layer (qwen3_next.rs:683-700)."""
+    ssm_state: torch.Tensor             # [b, heads, dk, dv] f32
+    conv_state: torch.Tensor            # [b, conv_dim, kernel-1] f32
+    gate_cumsum_offset: Optional[torch.Tensor] = None  # [b, heads] f32
+
+
+class LinearAttentionState:
+    def __init__(self):
+        self.recurrent_state: Optional[RecurrentState] = None
+
+    def clear_state(self) -> None:
+        self.recurrent_state = None
+
+
+# ------------------------------------------------------------------ PrefixCache
+@dataclass
+class PrefixCacheEntry:
+    """FullAttention / LinearAttention / Empty (qwen3_next.rs:834-854). The payload lives in
+    the native prefix object; seq_len (FullAttention) and the state shapes
+    (LinearAttention) are kept here."""
+    kind: str
+    seq_len: int = 0
+    shapes: Optional[tuple] = None
+
+
+@dataclass
+class PrefixCache:
+    prefix_tokens: List[int]
+    layer_caches: List[PrefixCacheEntry] = field(default_factory=list)
+    _native: Optional[ctypes.c_void_p] = None
+
+    def __del__(self):
+        if self._native is not None and self._native.value:
+            lib().pkv_prefix_free(self._native)
+            self._native = None
+
+
+class ModelKvState:
+    """Cache management of ModelWeights restricted to the attention state: a list of
+    layers, full attention where (i+1) % interval == 0 (qwen3_next.rs:4574-4583)."""
+
+    def __init__(self, n_layers: int, full_attention_interval: int, num_heads: int,
+                 num_kv_heads: int, head_dim: int, max_seq_len: int,
+                 quant: KvCacheQuantization = KvCacheQuantization.Q4K):
+        self.layers = []
+        for i in range(n_layers):
+            if (i + 1) % full_attention_interval == 0:
+                self.layers.append(FullAttentionKv(num_heads, num_kv_heads, head_dim, max_seq_len, quant))
+            else:
+                self.layers.append(LinearAttentionState())
+
+    def full_layers(self) -> List[FullAttentionKv]:
+        return [l for l in self.layers if isinstance(l, FullAttentionKv)]
+
+    def clear_kv_cache(self) -> None:
+        for l in self.layers:
+            if isinstance(l, FullAttentionKv):
+                l.clear_kv_cache()
+            else:
+                l.clear_state()
+
+    clear_cache = clear_kv_cache
+
+    def truncate_cache(self, new_len: int) -> None:
+        """Full layers truncate, linear layers clear (qwen3_next.rs:4301-4306)."""
+        for l in self.layers:
+            if isinstance(l, FullAttentionKv):
+                l.truncate_kv_cache(new_len)
+            else:
+                l.clear_state()
+
+    def cache_seq_len(self) -> int:
+        for l in self.layers:
+            if isinstance(l, FullAttentionKv):
+                return l.cache_seq_len()
+        return 0
+
+    def save_prefix_cache(self, prefix_tokens: Sequence[int]) -> PrefixCache:
+        toks = (ctypes.c_uint32 * max(len(prefix_tokens), 1))(*prefix_tokens)
+        p = ctypes.c_void_p()
+        _call(lib().pkv_prefix_create(toks, len(prefix_tokens), len(self.layers), ctypes.byref(p)))
+        pc = PrefixCache(list(prefix_tokens), [], p)
+        s = ctypes.c_void_p(_stream())
+        for i, l in enumerate(self.layers):
+            if isinstance(l, FullAttentionKv):
+                c = l.quantized_cache
+                if c is not None and c.seq_len > 0:
+                    _call(lib().pkv_prefix_save_full(p, i, c.handle))
+                    pc.layer_caches.append(PrefixCacheEntry("FullAttention", c.seq_len))
+                else:
+                    pc.layer_caches.append(PrefixCacheEntry("Empty"))
+            else:
+                rs = l.recurrent_state
+                if rs is None:
+                    pc.layer_caches.append(PrefixCacheEntry("Empty"))
+                    continue
+                ssm, conv = rs.ssm_state.contiguous(), rs.conv_state.contiguous()
+                gate = rs.gate_cumsum_offset
+                gshape = (ssm.shape[0], ssm.shape[1])
+                _call(lib().pkv_prefix_save_linear(
+                    p, i, _ptr(ssm), ssm.numel(), _ptr(conv), conv.numel(),
+                    _ptr(gate.contiguous()) if gate is not None else None,
+                    gshape[0] * gshape[1], s))
+                pc.layer_caches.append(PrefixCacheEntry(
+                    "LinearAttention", shapes=(tuple(ssm.shape), tuple(conv.shape), gshape)))
+        return pc
+
+    def restore_prefix_cache(self, cache: PrefixCache, requantize: bool = False) -> int:
+        """All layers restore in one batched copy launch; requantize=True reproduces the
+        reference's clear()+append(dequantized) bytes instead of the exact snapshot."""
+        n = len(self.layers)
+        p = cache._native
+        if len(cache.layer_caches) != n or lib().pkv_prefix_num_layers(p) != n:
+            raise PrefixLayerMismatch(
+                f"Prefix cache layer count mismatch: {len(cache.layer_caches)} vs {n}")
+        targets = (_lib.LayerTarget * n)()
+        valid = (ctypes.c_int * n)()
+        restored = {}
+        for i, l in enumerate(self.layers):
+            kind = lib().pkv_prefix_entry_kind(p, i)
+            if isinstance(l, FullAttentionKv):
+                if kind == _lib.ENTRY_FULL and l.quantized_cache is None:
+                    l._ensure(1)  # lazily created with max_seq_len (qwen3_next.rs:2830-2840)
+                if l.quantized_cache is not None:
+                    targets[i].cache = l.quantized_cache.handle.value
+                continue
+            if kind == _lib.ENTRY_LINEAR:
+                ss, cs, gs = cache.layer_caches[i].shapes
+                t = tuple(torch.empty(sh, dtype=torch.float32, device="cuda") for sh in (ss, cs, gs))
+                restored[i] = t
+                targets[i].ssm, targets[i].conv, targets[i].gate_offset = (x.data_ptr() for x in t)
+            targets[i].state_valid = ctypes.cast(ctypes.addressof(valid) + 4 * i,
+                                                 ctypes.POINTER(ctypes.c_int))
+        ntok = ctypes.c_size_t()
+        mode = _lib.RESTORE_REQUANTIZE if requantize else _lib.RESTORE_BYTES
+        _call(lib().pkv_prefix_restore(p, targets, n, mode, ctypes.byref(ntok),
+                                       ctypes.c_void_p(_stream())))
+        for i, l in enumerate(self.layers):
+            if isinstance(l, LinearAttentionState):
+                if valid[i] and i in restored:
+                    l.recurrent_state = RecurrentState(*restored[i])
+                else:
+                    l.clear_state()  # Empty or wrong kind (qwen3_next.rs:4121-4130)
+        return ntok.value

@@ -1,0 +1,255 @@
+"""GPU parity tests: libpkv (through its C ABI) against the CPU oracle on the same
+seeded inputs. Packed bytes, offsets and restores must be bit-exact; attention must be
+within 2e-3 absolute + 1e-3 relative of the oracle's f32 dequant-then-attend."""
+import sys
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+F16, BF16, Q8_0, Q4K = 1, 2, 3, 4
+ATOL, RTOL = 2e-3, 1e-3
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def pk():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import paramecia_amd
+    paramecia_amd.lib()
+    return paramecia_amd
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def special_rows(rng, n_rows, d):
+    """Random rows plus the edge cases the codecs must agree on."""
+    x = rng.standard_normal((n_rows, d)).astype(np.float32)
+    if n_rows >= 12:
+        x[0] = 0.0
+        x[1, : d // 2] = 3.25                                 # constant sub-blocks
+        x[2] = np.round(x[2] * 4) / 4                         # quarter-grid ties
+        x[3] *= 1e-30                                         # tiny
+        x[4] *= 1e4                                           # huge
+        x[5] = np.abs(x[5])                                   # all non-negative
+        x[6] = -np.abs(x[6])                                  # all non-positive
+        x[7, ::7] *= 20                                       # outlier channels
+        x[8] = (np.arange(d) % 16 - 8).astype(np.float32)     # exact grid
+        x[9] = np.where(np.arange(d) % 2, 1.0, -1.0)
+        x[10, :] = 0.0
+        x[10, 5] = 1e-3
+        x[11] *= 65504.0 / np.abs(x[11]).max()                # f16 max range
+    return x
+
+
+@pytest.mark.parametrize("quant,B,H,D", [(Q4K, 2, 2, 256), (Q8_0, 2, 2, 256), (F16, 1, 2, 128),
+                                         (BF16, 1, 2, 64), (Q8_0, 1, 3, 100), (Q4K, 1, 2, 320)])
+def test_append_bytes_and_get_kv_bitexact(pk, orc, quant, B, H, D):
+    say(f"append parity quant={quant} B={B} H={H} D={D}")
+    rng = np.random.default_rng(100 + quant + D)
+    cap = 64
+    g = pk.PreallocatedQuantizedKvCache(B, H, cap, D, pk.KvCacheQuantization(quant))
+    c = orc.Cache(quant, B, H, D, cap)
+    for n in (1, 7, 24):
+        k = special_rows(rng, B * H * n, D).reshape(B, H, n, D)
+        v = special_rows(rng, B * H * n, D).reshape(B, H, n, D)[:, :, ::-1].copy()
+        g.append_quantized(dev(k), dev(v))
+        assert c.append(k, v) == 0
+    assert g.seq_len == c.seq_len == 32
+    gk, gv = g.raw_bytes()
+    ok, ov = c.valid_bytes()
+    assert np.array_equal(host(gk), ok)
+    assert np.array_equal(host(gv), ov)
+    k, v = g.get_kv()
+    rk, rv = c.get_kv()
+    assert np.array_equal(host(k).view(np.uint32), rk.view(np.uint32))
+    assert np.array_equal(host(v).view(np.uint32), rv.view(np.uint32))
+
+
+def test_fill_normal_bitexact(pk, orc):
+    say("fill_normal parity")
+    t = torch.empty(1 << 20, dtype=torch.float32, device="cuda")
+    pk.fill_normal(t, 1234, 99, 0.5)
+    ref = orc.normal(1 << 20, 1234, 99, 0.5)
+    assert np.array_equal(host(t).view(np.uint32), ref.view(np.uint32))
+
+
+def test_offset_overflow_rules(pk):
+    say("offset/overflow rules")
+    g = pk.PreallocatedQuantizedKvCache(1, 2, 8, 256, pk.KvCacheQuantization.Q4K)
+    kv = lambda n: torch.randn(1, 2, n, 256, device="cuda")
+    g.append_quantized(kv(6), kv(6))
+    before = [host(x) for x in g.raw_bytes()]
+    with pytest.raises(pk.KvCacheOverflow):
+        g.append_quantized(kv(3), kv(3))
+    assert g.seq_len == 6
+    assert all(np.array_equal(a, host(b)) for a, b in zip(before, g.raw_bytes()))
+    with pytest.raises(pk.KvCacheOffsetMismatch):
+        g.append_quantized(kv(1), kv(1), offset=7)
+    g.append_quantized(kv(2), kv(2), offset=4)
+    assert g.seq_len == 6
+    g.truncate(100)
+    assert g.seq_len == 6
+    g.clear()
+    with pytest.raises(pk.EmptyCacheError):
+        g.attend(torch.randn(1, 1, 16, 256, device="cuda"), 1 / 16, 0)
+    g.resize_batch(2)
+    assert g.batch_size == 2 and g.seq_len == 0
+
+
+def _attend_case(pk, orc, quant, B, H, Hkv, D, S, L, causal, seed, amp=1.0, fused=False):
+    rng = np.random.default_rng(seed)
+    g = pk.PreallocatedQuantizedKvCache(B, Hkv, S + L, D, pk.KvCacheQuantization(quant))
+    c = orc.Cache(quant, B, Hkv, D, S + L)
+    k = (rng.standard_normal((B, Hkv, S, D)) * amp).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    g.append_quantized(dev(k), dev(v))
+    assert c.append(k, v) == 0
+    q = rng.standard_normal((B, L, H, D)).astype(np.float32)
+    scale = float(1 / np.sqrt(D))
+    if fused:
+        kn = rng.standard_normal((B, Hkv, 1, D)).astype(np.float32)
+        vn = rng.standard_normal((B, Hkv, 1, D)).astype(np.float32)
+        out = g.append_attend(dev(kn), dev(vn), dev(q), scale)
+        assert c.append(kn, vn) == 0
+        ref = c.attend(q, scale, S, True, mode="f32")
+        gk, _ = g.raw_bytes()
+        assert np.array_equal(host(gk), c.valid_bytes()[0])
+    else:
+        out = g.attend(dev(q), scale, S - L, causal)
+        ref = c.attend(q, scale, S - L, causal, mode="f32")
+    got = host(out)
+    np.testing.assert_allclose(got, ref, atol=ATOL, rtol=RTOL)
+    return got, ref
+
+
+@pytest.mark.parametrize("quant,B,H,Hkv,D,S,L,causal", [
+    (Q8_0, 1, 16, 2, 256, 4097, 1, True),    # config 1 shape
+    (Q4K, 1, 16, 2, 256, 3000, 1, True),
+    (Q4K, 2, 16, 2, 256, 700, 5, True),
+    (Q4K, 1, 16, 2, 256, 600, 40, True),     # prefill chunk with q_offset
+    (Q8_0, 1, 8, 8, 128, 300, 3, False),
+    (F16, 1, 4, 2, 64, 257, 2, True),
+    (BF16, 1, 16, 1, 256, 129, 1, True),
+    (Q8_0, 1, 2, 1, 512, 90, 1, True),
+])
+def test_attend_parity(pk, orc, quant, B, H, Hkv, D, S, L, causal):
+    say(f"attend parity quant={quant} B={B} H={H}/{Hkv} D={D} S={S} L={L} causal={causal}")
+    _attend_case(pk, orc, quant, B, H, Hkv, D, S, L, causal, seed=S + L)
+
+
+@pytest.mark.parametrize("quant", [Q4K, Q8_0])
+def test_append_attend_fused(pk, orc, quant):
+    say(f"fused append+attend quant={quant}")
+    _attend_case(pk, orc, quant, 1, 16, 2, 256, 5000, 1, True, seed=7, fused=True)
+
+
+def test_attend_clamp_and_outliers(pk, orc):
+    say("attend clamp/outliers")
+    _attend_case(pk, orc, Q4K, 1, 16, 2, 256, 1500, 1, True, seed=8, amp=20.0)
+
+
+def test_flash_attn_stateless_matches_cache(pk):
+    say("stateless flash_attn")
+    g = pk.PreallocatedQuantizedKvCache(1, 2, 2048, 256, pk.KvCacheQuantization.Q8_0)
+    g.append_quantized(torch.randn(1, 2, 2000, 256, device="cuda"),
+                       torch.randn(1, 2, 2000, 256, device="cuda"))
+    q = torch.randn(1, 3, 16, 256, device="cuda")
+    a = g.attend(q, 1 / 16, 1997, True)
+    kp, vp, n, st = g.get_kv_storage()
+    assert n == 2000 * 2 * 272 and st == (2 * 272, 2 * 272, 272, 1)
+    b = pk.flash_attn(pk.KvCacheQuantization.Q8_0, q, kp, vp, st, 1 / 16, 2, 2000, 1997, True)
+    assert torch.equal(a, b)
+
+
+def test_prefix_restore_bytes_and_requantize(pk, orc):
+    say("prefix restore")
+    from paramecia_amd import workloads as W
+    m = pk.ModelKvState(8, 4, 16, 2, 256, 512, pk.KvCacheQuantization.Q4K)
+    rng = np.random.default_rng(9)
+    full = m.full_layers()
+    for l in full:
+        x = rng.standard_normal((2, 1, 2, 300, 256)).astype(np.float32)
+        l._ensure(1).append_quantized(dev(x[0]), dev(x[1]))
+    states = []
+    for l in m.layers:
+        if isinstance(l, pk.LinearAttentionState):
+            s = pk.RecurrentState(torch.randn(1, 4, 8, 8, device="cuda") * 0.02,
+                                  torch.randn(1, 16, 3, device="cuda"), None)
+            l.recurrent_state = s
+            states.append(s)
+    snap = [tuple(host(x) for x in l.quantized_cache.raw_bytes()) for l in full]
+    sstate = [(host(s.ssm_state), host(s.conv_state)) for s in states]
+    pc = m.save_prefix_cache(list(range(300)))
+    assert [e.kind for e in pc.layer_caches].count("FullAttention") == 2
+    # diverge, then restore
+    for l in full:
+        l.quantized_cache.append_quantized(torch.randn(1, 2, 50, 256, device="cuda"),
+                                           torch.randn(1, 2, 50, 256, device="cuda"), offset=100)
+    m.clear_kv_cache()
+    assert m.restore_prefix_cache(pc) == 300
+    assert m.cache_seq_len() == 300
+    for l, (kb, vb) in zip(full, snap):
+        gk, gv = l.quantized_cache.raw_bytes()
+        assert np.array_equal(host(gk), kb) and np.array_equal(host(gv), vb)
+    lin = [l for l in m.layers if isinstance(l, pk.LinearAttentionState)]
+    for l, (ss, cs) in zip(lin, sstate):
+        assert np.array_equal(host(l.recurrent_state.ssm_state), ss)
+        assert np.array_equal(host(l.recurrent_state.conv_state), cs)
+        assert not host(l.recurrent_state.gate_cumsum_offset).any()  # zeros when absent
+    # reference semantics: restore = quantize(dequantize(saved))
+    assert m.restore_prefix_cache(pc, requantize=True) == 300
+    for l, (kb, vb) in zip(full, snap):
+        c = orc.Cache(Q4K, 1, 2, 256, 512)
+        c.load_bytes(kb, vb, 300)
+        k, v = c.get_kv()
+        c2 = orc.Cache(Q4K, 1, 2, 256, 512)
+        c2.append(k, v)
+        gk, gv = l.quantized_cache.raw_bytes()
+        assert np.array_equal(host(gk), c2.valid_bytes()[0])
+        assert np.array_equal(host(gv), c2.valid_bytes()[1])
+    # layer-count mismatch bails before touching anything
+    m2 = pk.ModelKvState(4, 4, 16, 2, 256, 512, pk.KvCacheQuantization.Q4K)
+    with pytest.raises(pk.PrefixLayerMismatch):
+        m2.restore_prefix_cache(pc)
+
+
+def test_batched_decode_matches_per_sequence(pk, orc):
+    say("batched decode")
+    rng = np.random.default_rng(10)
+    lens = [100, 1500, 37, 800]
+    caches, oracles = [], []
+    for n in lens:
+        g = pk.PreallocatedQuantizedKvCache(1, 2, 2048, 256, pk.KvCacheQuantization.Q4K)
+        c = orc.Cache(Q4K, 1, 2, 256, 2048)
+        k = rng.standard_normal((1, 2, n, 256)).astype(np.float32)
+        v = rng.standard_normal((1, 2, n, 256)).astype(np.float32)
+        g.append_quantized(dev(k), dev(v))
+        c.append(k, v)
+        caches.append(g)
+        oracles.append(c)
+    kn = rng.standard_normal((4, 2, 256)).astype(np.float32)
+    vn = rng.standard_normal((4, 2, 256)).astype(np.float32)
+    q = rng.standard_normal((4, 16, 256)).astype(np.float32)
+    out = host(pk.append_attend_batched(caches, dev(kn), dev(vn), dev(q), 1 / 16))
+    for i, (g, c) in enumerate(zip(caches, oracles)):
+        c.append(kn[i][None, :, None], vn[i][None, :, None])
+        ref = c.attend(q[i][None, None], 1 / 16, lens[i], True, mode="f32")[0, 0]
+        np.testing.assert_allclose(out[i], ref, atol=ATOL, rtol=RTOL)
+        assert g.seq_len == lens[i] + 1
+        assert np.array_equal(host(g.raw_bytes()[0]), c.valid_bytes()[0])
