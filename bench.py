@@ -133,8 +133,10 @@ def main() -> int:
     # while the host enqueues, so each event pair brackets device time only
     ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(L)] for _ in range(args.steps)]
+    sleep = getattr(torch.cuda, "_sleep", None)
     for s_ in range(args.steps):
-        torch.cuda._sleep(20_000_000)
+        if sleep is not None:
+            sleep(20_000_000)
         step(ev[s_])
     torch.cuda.synchronize()
     per_launch_ms = sum(a.elapsed_time(b) for row in ev for a, b in row) / (args.steps * L)

@@ -167,6 +167,7 @@ int launch_attend_generic(const AttnArgs &a, Workspace &ws, hipStream_t s) {
   const int groups = a.batch * a.l * a.num_kv_heads;
   // Enough waves to fill the GPU, at least 16 keys per wave.
   int64_t want = (16384 + groups - 1) / groups;
+  if (want > 4096) want = 4096;  // combine keeps one weight per split in LDS
   int64_t max_waves = (a.seq_k + 15) / 16;
   int64_t wpg = want < max_waves ? want : max_waves;
   wpg = (wpg + kWaves - 1) / kWaves * kWaves;
