@@ -1,0 +1,138 @@
+// Latency-oriented, bit-exact Q4K quantizer (candle BlockQ4K::from_float with
+// make_qkx1_quants(15, 5), restated; reference call site
+// paramecia-model/src/qwen3_next.rs:486-487): 256 threads per 256-element superblock,
+// one element per lane, 32 lanes per sub-block. The two f32 sums of make_qkx1_quants
+// accumulate in element order in the reference, so every lane of a sub-block stages
+// its term in LDS and replays the 32-term chain in order; the element-wise work
+// (rounding, clamping, products, the final division) runs in parallel. The bytes
+// equal those of the 8-lane throughput kernel and of the CPU oracle.
+// Include-only; every function keeps a*b+c as two roundings (contraction off).
+#pragma once
+#include "pkv_scalar.hpp"
+
+namespace pkv {
+
+struct Q4kScratch {
+  float scr[256];
+  float red[2][8];
+  uint32_t codes[8];
+  uint8_t nib[256];
+};
+
+__device__ __forceinline__ float q4k_chain_sum_32(float *scr, int i, float term, float init) {
+#pragma clang fp contract(off)
+  scr[i] = term;
+  __builtin_amdgcn_wave_barrier();
+  const float4 *s4 = reinterpret_cast<const float4 *>(scr);
+  float acc = init;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const float4 t = s4[q];
+    acc += t.x;
+    acc += t.y;
+    acc += t.z;
+    acc += t.w;
+  }
+  __builtin_amdgcn_wave_barrier();
+  return acc;
+}
+
+// x: this thread's element (tid = 32 * sub-block + element); blk: 144 output bytes.
+// Called by 256 threads of one workgroup together (contains __syncthreads()).
+static __device__ __noinline__ void q4k_quantize_superblock_lanes(float x, uint8_t *blk, Q4kScratch *S,
+                                                           int tid) {
+#pragma clang fp contract(off)
+  const int j = tid >> 5, i = tid & 31;
+  float *mine = S->scr + 32 * j;
+  int32_t kmin = total_key(x), kmax = kmin;
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) {
+    kmin = min(kmin, __shfl_xor(kmin, o, 32));
+    kmax = max(kmax, __shfl_xor(kmax, o, 32));
+  }
+  auto from_key = [](int32_t k) {
+    return u2f((uint32_t)(k ^ (int32_t)(((uint32_t)(k >> 31)) >> 1)));
+  };
+  const float mn = from_key(kmin), mx = from_key(kmax);
+  float scale = 0.0f, neg_min = 0.0f;
+  uint32_t L = 0;
+  if (!(mx == mn)) {
+    float fmin = fmin_rs(mn, 0.0f);
+    float iscale = 15.0f / (mx - fmin);
+    scale = 1.0f / iscale;
+    for (int t = 0; t < 5; ++t) {
+      int32_t li = nearest_int(iscale * (x - fmin));
+      li = li < 0 ? 0 : (li > 15 ? 15 : li);
+      const bool changed = (uint32_t)li != L;
+      L = (uint32_t)li;
+      const float sumlx = q4k_chain_sum_32(mine, i, (x - fmin) * (float)li, 0.0f);
+      int32_t l2 = li * li;
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) l2 += __shfl_xor(l2, o, 32);
+      scale = sumlx / (float)l2;
+      const float sum = q4k_chain_sum_32(mine, i, x - scale * (float)L, -0.0f);
+      fmin = sum / 32.0f;
+      if (fmin > 0.0f) fmin = 0.0f;
+      iscale = 1.0f / scale;
+      // did_change of this sub-block: its half of the wave's ballot
+      const uint64_t bal = __ballot(changed);
+      const uint32_t mask = (uint32_t)(bal >> (32 * ((tid >> 5) & 1)));
+      if (mask == 0u) break;
+    }
+    neg_min = -fmin;
+  }
+  if (i == 0) {
+    S->red[0][j] = scale;
+    S->red[1][j] = neg_min;
+  }
+  __syncthreads();
+  float max_scale = 0.0f, max_min = 0.0f;  // fold from +0, NaN-dropping maxNum
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) {
+    max_scale = fmax_rs(S->red[0][jj], max_scale);
+    max_min = fmax_rs(S->red[1][jj], max_min);
+  }
+  const float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+  const float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+  const int32_t ls32 = nearest_int(inv_scale * scale), lm32 = nearest_int(inv_min * neg_min);
+  const uint32_t ls = (uint8_t)(ls32 < 63 ? ls32 : 63), lm = (uint8_t)(lm32 < 63 ? lm32 : 63);
+  const uint16_t dh = f32_to_f16(max_scale / 63.0f), mh = f32_to_f16(max_min / 63.0f);
+  uint32_t q = 0;
+  const float dd = f16_to_f32(dh) * (float)ls;
+  if (dd != 0.0f) {
+    const float dm = f16_to_f32(mh) * (float)lm;
+    const int32_t l = nearest_int((x + dm) / dd);
+    q = (uint32_t)(l < 0 ? 0 : (l > 15 ? 15 : l));
+  }
+  if (i == 0) S->codes[j] = ls | (lm << 8);
+  S->nib[tid] = (uint8_t)q;
+  __syncthreads();
+  if (tid < 32) {  // qs[32c + l] = L_{2c}[l] | L_{2c+1}[l] << 4, 4 bytes per thread
+    uint32_t w = 0;
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+      const int byte = 4 * tid + bb, c = byte >> 5, l = byte & 31;
+      w |= ((uint32_t)S->nib[64 * c + l] | ((uint32_t)S->nib[64 * c + 32 + l] << 4)) << (8 * bb);
+    }
+    reinterpret_cast<uint32_t *>(blk + 16)[tid] = w;
+  } else if (tid == 32) {
+    uint8_t sc[12];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const uint32_t ls_lo = S->codes[jj] & 0xFF, lm_lo = S->codes[jj] >> 8;
+      const uint32_t ls_hi = S->codes[jj + 4] & 0xFF, lm_hi = S->codes[jj + 4] >> 8;
+      sc[jj] = (uint8_t)(ls_lo | ((ls_hi >> 4) << 6));
+      sc[jj + 4] = (uint8_t)(lm_lo | ((lm_hi >> 4) << 6));
+      sc[jj + 8] = (uint8_t)((ls_hi & 0xF) | ((lm_hi & 0xF) << 4));
+    }
+    uint4 hd;
+    hd.x = (uint32_t)dh | ((uint32_t)mh << 16);
+    hd.y = (uint32_t)sc[0] | ((uint32_t)sc[1] << 8) | ((uint32_t)sc[2] << 16) | ((uint32_t)sc[3] << 24);
+    hd.z = (uint32_t)sc[4] | ((uint32_t)sc[5] << 8) | ((uint32_t)sc[6] << 16) | ((uint32_t)sc[7] << 24);
+    hd.w = (uint32_t)sc[8] | ((uint32_t)sc[9] << 8) | ((uint32_t)sc[10] << 16) | ((uint32_t)sc[11] << 24);
+    *reinterpret_cast<uint4 *>(blk) = hd;
+  }
+  __syncthreads();  // scratch is reused by the next call
+}
+
+}  // namespace pkv

@@ -13,6 +13,7 @@
 
 #include "pkv_internal.hpp"
 #include "pkv_scalar.hpp"
+#include "pkv_q4k_lanes.hpp"
 
 namespace pkv {
 namespace {
@@ -203,6 +204,23 @@ __global__ __launch_bounds__(256) void q4k_append_kernel(AppendArgs a, int64_t u
   }
 }
 
+// One workgroup per (tensor, token, batch, head, superblock); for appends of a few rows.
+__global__ __launch_bounds__(256) void q4k_append_small_kernel(AppendArgs a, int nsb) {
+  __shared__ Q4kScratch scr;
+  int64_t u = blockIdx.x;
+  const int sb = (int)(u % nsb);
+  u /= nsb;
+  const int h = (int)(u % a.heads);
+  u /= a.heads;
+  const int b = (int)(u % a.batch);
+  u /= a.batch;
+  const int64_t t = u % a.n;
+  const int p = (int)(u / a.n);
+  const float x = load_elem(a.src[p], a, t, b, h, sb * 256 + (int)threadIdx.x);
+  uint8_t *blk = a.dst[p] + dst_row(a, t, b, h) * a.bpr + (int64_t)sb * 144;
+  q4k_quantize_superblock_lanes(x, blk, &scr, (int)threadIdx.x);
+}
+
 // Q8_0 (BlockQ8_0::from_float): one lane per 32-element block.
 __global__ __launch_bounds__(256) void q8_0_append_kernel(AppendArgs a, int64_t units_per_tensor,
                                                           int nblk) {
@@ -294,7 +312,12 @@ int launch_append(int quant, const float *k, const float *v, uint8_t *kc, uint8_
   a.t0 = t0;
   a.bpr = (int64_t)row_bytes(quant, head_dim);
   const int64_t rows = n * batch * heads;
-  if (quant == PKV_QUANT_Q4K) {
+  if (quant == PKV_QUANT_Q4K && rows * (a.padded / 256) * 2 <= 1024) {
+    // few superblocks: latency-bound, one workgroup each
+    const int nsb = a.padded / 256;
+    hipLaunchKernelGGL(q4k_append_small_kernel, dim3((unsigned)(2 * rows * nsb)), dim3(256), 0,
+                       s, a, nsb);
+  } else if (quant == PKV_QUANT_Q4K) {
     const int nsb = a.padded / 256;
     const int64_t units = rows * nsb;
     const int64_t threads = 2 * units * 8;

@@ -122,6 +122,7 @@ class PreallocatedQuantizedKvCache:
                                ctypes.c_void_p(stream if stream is not None else _stream()),
                                ctypes.byref(h)))
         self._h = h
+        self._stream = stream if stream is not None else _stream()
         self.quant = KvCacheQuantization(int(quant) or _lib.QUANT_F16)
         self.num_kv_heads = num_kv_heads
         self.head_dim = head_dim
@@ -150,10 +151,18 @@ class PreallocatedQuantizedKvCache:
 
     def set_stream(self, stream: int) -> None:
         check(lib().pkv_set_stream(self._h, ctypes.c_void_p(stream)))
+        self._stream = stream
+
+    def _follow_stream(self) -> None:
+        """Work is enqueued on torch's current stream (so graph capture sees it)."""
+        s = _stream()
+        if s != self._stream:
+            self.set_stream(s)
 
     def append_quantized(self, new_k: torch.Tensor, new_v: torch.Tensor,
                          offset: int = -1) -> None:
         """new_k, new_v: [batch, num_kv_heads, n, head_dim] f32 (qwen3_next.rs:431)."""
+        self._follow_stream()
         k, v = _f32(new_k, "new_k"), _f32(new_v, "new_v")
         if k.shape != v.shape or k.dim() != 4:
             raise KvCacheError("new_k/new_v must both be [batch, heads, n, head_dim]")
@@ -165,6 +174,7 @@ class PreallocatedQuantizedKvCache:
 
     def get_kv(self):
         """Dequantized [batch, heads, seq_len, head_dim] f32 tensors (qwen3_next.rs:520)."""
+        self._follow_stream()
         shape = (self.batch_size, self.num_kv_heads, self.seq_len, self.head_dim)
         k = torch.empty(shape, dtype=torch.float32, device="cuda")
         v = torch.empty(shape, dtype=torch.float32, device="cuda")
@@ -190,6 +200,7 @@ class PreallocatedQuantizedKvCache:
 
     def attend(self, q: torch.Tensor, scale: float, q_offset: int, causal: bool = True) -> torch.Tensor:
         """q: [batch, l, num_heads, head_dim] f32 -> out of the same shape."""
+        self._follow_stream()
         q = _f32(q, "q")
         out = torch.empty_like(q)
         _call(lib().pkv_attend(self._h, _ptr(q), q.shape[1], q.shape[2], scale, q_offset,
@@ -198,6 +209,7 @@ class PreallocatedQuantizedKvCache:
 
     def append_attend(self, new_k, new_v, q, scale: float, offset: int = -1) -> torch.Tensor:
         """Fused decode step: append one token and attend over every key."""
+        self._follow_stream()
         k, v, q = _f32(new_k, "new_k"), _f32(new_v, "new_v"), _f32(q, "q")
         out = torch.empty_like(q)
         _call(lib().pkv_append_attend(self._h, _ptr(k), _ptr(v), _ptr(q), q.shape[2], scale,
@@ -211,6 +223,7 @@ class PreallocatedQuantizedKvCache:
         check(lib().pkv_truncate(self._h, new_len))
 
     def resize_batch(self, batch_size: int) -> None:
+        self._follow_stream()
         _call(lib().pkv_resize_batch(self._h, batch_size))
 
 

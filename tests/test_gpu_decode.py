@@ -1,0 +1,131 @@
+"""GPU tests of the MFMA decode path (Q4K, 16 q heads / 2 KV heads / head_dim 256):
+block-boundary sizes, batch > 1, outlier channels, and one full-size layer of the
+headline configuration (131072 cached tokens) against the CPU oracle."""
+import sys
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+Q4K = 4
+ATOL, RTOL = 2e-3, 1e-3
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def pk():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import paramecia_amd
+    paramecia_amd.lib()
+    return paramecia_amd
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def run_decode(pk, orc, S, B=1, fused=True, seed=0, k_scale=None, chans=None):
+    rng = np.random.default_rng(seed)
+    g = pk.PreallocatedQuantizedKvCache(B, 2, S + 1, 256, pk.KvCacheQuantization.Q4K)
+    c = orc.Cache(Q4K, B, 2, 256, S + 1)
+    k = rng.standard_normal((B, 2, S, 256)).astype(np.float32)
+    v = rng.standard_normal((B, 2, S, 256)).astype(np.float32)
+    q = rng.standard_normal((B, 1, 16, 256)).astype(np.float32)
+    kn = rng.standard_normal((B, 2, 1, 256)).astype(np.float32)
+    vn = rng.standard_normal((B, 2, 1, 256)).astype(np.float32)
+    if chans is not None:
+        for x in (k, v, kn, vn):
+            x[..., chans] *= 20.0
+    if S > 0:
+        g.append_quantized(dev(k), dev(v))
+        assert c.append(k, v) == 0
+    if fused:
+        out = g.append_attend(dev(kn), dev(vn), dev(q), 1 / 16)
+        assert c.append(kn, vn) == 0
+        seq = S + 1
+    else:
+        out = g.attend(dev(q), 1 / 16, S - 1, True)
+        seq = S
+    ref = c.attend(q, 1 / 16, seq - 1, True, mode="f32")
+    got = host(out)
+    np.testing.assert_allclose(got, ref, atol=ATOL, rtol=RTOL)
+    gk, gv = g.raw_bytes()
+    ok, ov = c.valid_bytes()
+    assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
+    return np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("S", [0, 1, 2, 31, 32, 33, 95, 96, 97, 128, 129, 255, 1000, 4096, 4127])
+def test_decode_fused_boundaries(pk, orc, S):
+    say(f"fused decode S={S}")
+    run_decode(pk, orc, S, fused=True, seed=S)
+
+
+@pytest.mark.parametrize("S", [1, 32, 33, 130, 2049])
+def test_decode_attend_only(pk, orc, S):
+    say(f"attend-only decode S={S}")
+    run_decode(pk, orc, S, fused=False, seed=1000 + S)
+
+
+def test_decode_batch2(pk, orc):
+    say("decode batch 2")
+    run_decode(pk, orc, 777, B=2, seed=5)
+
+
+def test_decode_outlier_channels(pk, orc):
+    say("decode outlier channels")
+    from paramecia_amd import workloads as W
+    run_decode(pk, orc, 20000, seed=6, chans=W.c5_channels())
+
+
+def test_decode_full_size_layer(pk, orc):
+    """One layer of the headline workload: seeded data generated on the GPU and on the
+    CPU must give the same Q4K bytes (131072 tokens x 4 rows), and the fused decode
+    step must match the oracle's f32 attention over 131073 keys."""
+    from paramecia_amd import workloads as W
+    S = 131072
+    say("full-size layer: generate + quantize on GPU")
+    kbuf = torch.empty((1, 2, S, 256), dtype=torch.float32, device="cuda")
+    vbuf = torch.empty_like(kbuf)
+    pk.fill_normal(kbuf, W.SEED, W.stream_id(3, W.T_PREFILL_K, 0))
+    pk.fill_normal(vbuf, W.SEED, W.stream_id(3, W.T_PREFILL_V, 0))
+    g = pk.PreallocatedQuantizedKvCache(1, 2, S + 1, 256, pk.KvCacheQuantization.Q4K)
+    g.append_quantized(kbuf, vbuf)
+    q = torch.empty((1, 1, 16, 256), dtype=torch.float32, device="cuda")
+    kn = torch.empty((1, 2, 1, 256), dtype=torch.float32, device="cuda")
+    vn = torch.empty_like(kn)
+    pk.fill_normal(q, W.SEED, W.stream_id(3, W.T_Q, 0))
+    pk.fill_normal(kn, W.SEED, W.stream_id(3, W.T_NEW_K, 0))
+    pk.fill_normal(vn, W.SEED, W.stream_id(3, W.T_NEW_V, 0))
+    out = host(g.append_attend(kn, vn, q, W.SCALE, offset=S))
+    gk, gv = (host(x) for x in g.raw_bytes())
+    del kbuf, vbuf
+    say("full-size layer: CPU oracle quantize + attend")
+    c = orc.Cache(Q4K, 1, 2, 256, S + 1)
+    k = orc.normal(2 * S * 256, W.SEED, W.stream_id(3, W.T_PREFILL_K, 0)).reshape(1, 2, S, 256)
+    v = orc.normal(2 * S * 256, W.SEED, W.stream_id(3, W.T_PREFILL_V, 0)).reshape(1, 2, S, 256)
+    assert c.append(k, v) == 0
+    del k, v
+    knp = orc.normal(512, W.SEED, W.stream_id(3, W.T_NEW_K, 0)).reshape(1, 2, 1, 256)
+    vnp = orc.normal(512, W.SEED, W.stream_id(3, W.T_NEW_V, 0)).reshape(1, 2, 1, 256)
+    qnp = orc.normal(4096, W.SEED, W.stream_id(3, W.T_Q, 0)).reshape(1, 1, 16, 256)
+    assert c.append(knp, vnp) == 0
+    ok, ov = c.valid_bytes()
+    assert np.array_equal(gk, ok), "K bytes differ"
+    assert np.array_equal(gv, ov), "V bytes differ"
+    ref = c.attend(qnp, W.SCALE, S, True, mode="f32")
+    err = np.abs(out - ref)
+    say(f"full-size layer: max|diff| = {err.max():.3e}")
+    np.testing.assert_allclose(out, ref, atol=ATOL, rtol=RTOL)

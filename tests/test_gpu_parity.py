@@ -81,6 +81,23 @@ def test_append_bytes_and_get_kv_bitexact(pk, orc, quant, B, H, D):
     assert np.array_equal(host(v).view(np.uint32), rv.view(np.uint32))
 
 
+@pytest.mark.parametrize("quant", [Q4K, Q8_0])
+def test_bulk_append_bitexact(pk, orc, quant):
+    """Large appends take the throughput kernels, small ones the latency kernels."""
+    say(f"bulk append quant={quant}")
+    rng = np.random.default_rng(200 + quant)
+    g = pk.PreallocatedQuantizedKvCache(1, 2, 2048, 256, pk.KvCacheQuantization(quant))
+    c = orc.Cache(quant, 1, 2, 256, 2048)
+    for n in (1500, 1, 3):
+        k = special_rows(rng, 2 * n, 256).reshape(1, 2, n, 256) * 3
+        v = rng.standard_normal((1, 2, n, 256)).astype(np.float32)
+        g.append_quantized(dev(k), dev(v))
+        assert c.append(k, v) == 0
+    gk, gv = g.raw_bytes()
+    ok, ov = c.valid_bytes()
+    assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
+
+
 def test_fill_normal_bitexact(pk, orc):
     say("fill_normal parity")
     t = torch.empty(1 << 20, dtype=torch.float32, device="cuda")
