@@ -36,7 +36,7 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 512;
+constexpr int kThreads = 256;  // 4 waves: 2 per KV head, one wave per SIMD
 constexpr int kBlk = 32;
 constexpr int kMainWGs = 256;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -47,12 +47,13 @@ struct DecodeArgs {
   const uint8_t *k, *v;
   uint8_t *kw, *vw;
   int64_t rs_b, rs_t, rs_h;
-  int64_t seq_k;
+  int64_t seq_k;  // keys held in the cache before this step's append (all attended)
   int nblk, nwg_main, bpw;
   float sl2;  // scale * log2(e)
-  const float *k_new, *v_new;  // [B][2][256] or null
+  const float *k_new, *v_new;  // [B][2][256] or null (fused decode step)
   int64_t t_new;
-  float *part;  // [B][nwg_main + 1][16][258]
+  float *part;  // [B][nwg_main][16][258]
+  float *dq;    // [B][4][256] dequantized new rows (K kv0, K kv1, V kv0, V kv1)
 };
 
 // Per-wave tables rebuilt for every 32-key block.
@@ -62,25 +63,41 @@ struct WaveTab {
   _Float16 vsc[8][kBlk], vc[8][kBlk], vm[8][kBlk];  // V: fp16 constants [j][key]
 };
 
+struct Stage;
 struct Smem {
   union {
     struct {
       h8 qb[2][8][64];  // QK B operands [kv][step][lane]
       h4 q2[2][64];     // S2 B operands [kv][lane]
-      WaveTab tab[8];
+      float qf[16][256];  // q staged before the operands are built
+      float qs[16][8];    // per head, per 32-element sub-block sums of q
+    } qsetup;
+    struct {
+      WaveTab tab[4];
+      char stages[4 * 3 * 2 * 320 * 16];  // Stage[wave][kStages]
     } run;
     struct {
-      float o[4][8][256];  // merge staging for up to 4 waves
-      float m[4][8], l[4][8];
-      float cmin[8][8][8];  // per wave [head][j]
+      float o[2][8][256];  // the second wave of each KV head
+      float m[2][8], l[2][8];
+      float cmin[4][8][8];  // per wave [head][j]
     } merge;
-    Q4kScratch quant[2];
+    Q4kScratch quant;
   };
 };
 
 __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
   return (x & m) | o;
 }
+// Constants kept in VGPRs so that (x & mask) | magic is a single v_and_or_b32 (gfx9
+// VOP3 encodings take no literal operands).
+__device__ __forceinline__ uint32_t vconst(uint32_t c) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
+  return r;
+}
+struct Masks {
+  uint32_t lo, hi, magic;
+};
 __device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
 __device__ __forceinline__ uint32_t as_u(h2 x) { return __builtin_bit_cast(uint32_t, x); }
 __device__ __forceinline__ h2 pk_fma(h2 a, h2 b, h2 c) { return __builtin_elementwise_fma(a, b, c); }
@@ -99,68 +116,110 @@ __device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
 // 0-3, s1 = 4-7, s2 = 8-11), get_scale_min_k4.
 __device__ __forceinline__ void scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j,
                                           uint32_t &sc, uint32_t &m) {
-  const int jj = j & 3;
-  const uint32_t b_lo = (s0 >> (8 * jj)) & 0xFF;  // byte j (j < 4) or j-4
-  const uint32_t b_mid = (s1 >> (8 * jj)) & 0xFF; // byte j+4 (j < 4) or j
-  const uint32_t b_hi = (s2 >> (8 * jj)) & 0xFF;  // byte j+4 (j >= 4)
-  if (j < 4) {
-    sc = b_lo & 63;
-    m = b_mid & 63;
-  } else {
-    sc = (b_hi & 0xF) | ((b_lo >> 6) << 4);
-    m = (b_hi >> 4) | ((b_mid >> 6) << 4);
-  }
+  const int sh = 8 * (j & 3);
+  const uint32_t b_lo = (s0 >> sh) & 0xFF;   // byte j (j < 4) or j-4
+  const uint32_t b_mid = (s1 >> sh) & 0xFF;  // byte j+4 (j < 4) or j
+  const uint32_t b_hi = (s2 >> sh) & 0xFF;   // byte j+4 (j >= 4)
+  const uint32_t sc_lo = b_lo & 63, m_lo = b_mid & 63;
+  const uint32_t sc_hi = (b_hi & 0xF) | ((b_lo >> 6) << 4);
+  const uint32_t m_hi = (b_hi >> 4) | ((b_mid >> 6) << 4);
+  sc = j < 4 ? sc_lo : sc_hi;
+  m = j < 4 ? m_lo : m_hi;
+}
+
+// exact f16 -> f32 (hardware conversion)
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
 
 // exponent e in [-20, 0] and mantissa d * 2^-e of a non-negative f16 scale
 __device__ __forceinline__ void split_scale(float d, int &e, float &mant) {
-  if (d == 0.0f) {
-    e = -20;
-    mant = 0.0f;
-    return;
-  }
-  int ex = (int)((f2u(d) >> 23) & 0xFF) - 127;
+  const int ex = (int)((f2u(d) >> 23) & 0xFF) - 127;  // d == 0 gives -127 -> -20, mant 0
   e = ex < -20 ? -20 : (ex > 0 ? 0 : ex);
   mant = __builtin_ldexpf(d, -e);
 }
 
-struct BlockLoads {
-  u4 khdr[2], kq0[2], kq1[2];  // per QK tile
-  uint32_t vq[2][8];           // [dword set][key]
-  u4 vhdr;
+typedef uint32_t u4s __attribute__((ext_vector_type(4)));
+#define PKV_LDS __attribute__((address_space(3)))
+
+// ---- LDS staging of 32-key blocks. Rows (144 B = 9 slots of 16 B) of one KV head are
+// placed at slot 9R + 4*(R/8): the 64 B gap after every 8 rows puts the four 8-row
+// groups that a transposed V read touches at once on disjoint LDS banks.
+constexpr int kSlots = 320;   // 5 loads of 64 lanes x 16 B; 304 slots used
+constexpr int kStages = 3;
+struct Stage {
+  u4 k[kSlots];
+  u4 v[kSlots];
+};
+__device__ __forceinline__ int row_slot(int R) { return 9 * R + 4 * (R >> 3); }
+
+// Buffer resource of a byte range (raw, stride 0; out-of-range loads return zero).
+__device__ __forceinline__ u4s make_rsrc(const void *base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  u4s r;
+  r.x = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32) & 0xFFFFu);
+  r.z = __builtin_amdgcn_readfirstlane(bytes);
+  r.w = 0x00020000u;
+  return r;
+}
+
+// One lane's part of staging a block: up to 5 16-byte pieces per tensor. Issued from
+// inline asm so that the compiler's wait-count pass does not serialise the LDS reads
+// behind these transfers; the kernel places its own s_waitcnt vmcnt before a stage is
+// read.
+struct LoadPlan {
+  uint32_t voff[5];
+  uint32_t valid;
 };
 
-__device__ __forceinline__ const uint8_t *row_ptr(const uint8_t *base, const DecodeArgs &a,
-                                                  int b, int64_t key, int kv) {
-  return base + b * a.rs_b + key * a.rs_t + kv * a.rs_h;
+__device__ __forceinline__ LoadPlan make_plan(int lane, uint32_t rs_t) {
+  LoadPlan P;
+  P.valid = 0;
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    const int slot = 64 * i + lane;
+    const int G = slot / 76, w = slot % 76;
+    const bool ok = G < 4 && w < 72;
+    const int R = 8 * G + w / 9, piece = w % 9;
+    P.voff[i] = ok ? (uint32_t)R * rs_t + 16u * (uint32_t)piece : 0u;
+    P.valid |= (ok ? 1u : 0u) << i;
+  }
+  return P;
 }
 
-__device__ __forceinline__ void load_block(BlockLoads &L, const DecodeArgs &a, int b, int kv,
-                                           int bi, int lane) {
-  const int r = lane & 15, g = lane >> 4;
-  const int64_t kb = (int64_t)bi * kBlk, last = a.seq_k - 1;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    int64_t key = kb + 8 * (r >> 2) + 4 * t + (r & 3);
-    key = key > last ? last : key;
-    const uint8_t *row = row_ptr(a.k, a, b, key, kv);
-    L.khdr[t] = *reinterpret_cast<const u4 *>(row);
-    L.kq0[t] = *reinterpret_cast<const u4 *>(row + 16 + 32 * g);
-    L.kq1[t] = *reinterpret_cast<const u4 *>(row + 32 + 32 * g);
-  }
-  const int n = lane & 15;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    int64_t key = kb + 8 * g + k;
-    key = key > last ? last : key;
-    const uint8_t *row = row_ptr(a.v, a, b, key, kv);
-    L.vq[0][k] = *reinterpret_cast<const uint32_t *>(row + 16 + 4 * n);
-    L.vq[1][k] = *reinterpret_cast<const uint32_t *>(row + 80 + 4 * n);
-  }
-  int64_t key = kb + (lane & 31);
-  key = key > last ? last : key;
-  L.vhdr = *reinterpret_cast<const u4 *>(row_ptr(a.v, a, b, key, kv));
+__device__ __forceinline__ void lds_dma16(uint32_t lds, uint32_t voff, u4s rsrc, uint32_t soff) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+      : "memory");
 }
+
+__device__ __forceinline__ void issue_stage(Stage *st, const LoadPlan &P, u4s rk, u4s rv,
+                                            uint32_t soff) {
+  soff = __builtin_amdgcn_readfirstlane(soff);
+  const uint32_t lk = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&st->k[0]));
+  const uint32_t lv = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&st->v[0]));
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    if (P.valid & (1u << i)) {
+      lds_dma16(lk + 1024u * i, P.voff[i], rk, soff);
+      lds_dma16(lv + 1024u * i, P.voff[i], rv, soff);
+    }
+  }
+}
+
+// every lane issues exactly 10 loads per stage, so the count below is static
+__device__ __forceinline__ void wait_stage_ready() {
+  asm volatile("s_waitcnt vmcnt(20)" ::: "memory");  // the two younger stages may fly
+}
+
+
 
 struct WaveState {
   f4 acc[16];  // PV accumulators, tile T = 8h + 2*byte + hl
@@ -168,74 +227,42 @@ struct WaveState {
   float m_run, lsum;
 };
 
-__device__ __forceinline__ void process_block(const BlockLoads &L, WaveState &S, WaveTab &T,
-                                              const h8 *qb, h4 q2, const DecodeArgs &a, int bi,
-                                              int lane) {
-  const int n = lane & 15, g = lane >> 4;
-  // ---- V header -> constant tables (lanes 0-31: scale tables, 32-63: min tables)
-  {
-    const int kk = lane & 31;
-    const uint32_t s0 = L.vhdr.y, s1 = L.vhdr.z, s2 = L.vhdr.w;
-    const float d = f16_to_f32((uint16_t)(L.vhdr.x & 0xFFFF));
-    const float dmin = f16_to_f32((uint16_t)(L.vhdr.x >> 16));
-    if (lane < 32) {
-      int e;
-      float mant;
-      split_scale(d, e, mant);
-      T.vmd[kk] = mant;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        uint32_t sc, m;
-        scale_min(s0, s1, s2, j, sc, m);
-        const float scp = __builtin_ldexpf((float)sc, e);
-        T.vsc[j][kk] = (_Float16)((j & 1) ? scp * 0.0625f : scp);
-        T.vc[j][kk] = (_Float16)((j & 1) ? -64.0f * scp : -1024.0f * scp);
-      }
-    } else {
-      int e;
-      float mant;
-      split_scale(dmin, e, mant);
-      T.vmdm[kk] = mant;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        uint32_t sc, m;
-        scale_min(s0, s1, s2, j, sc, m);
-        T.vm[j][kk] = (_Float16)__builtin_ldexpf((float)m, e);
-      }
-    }
-  }
-  // ---- QK for the two 16-key tiles
-  float sc8[8];
+// ---- per-block phases. The loop runs P(i) and Q(i+1) in one branch-free region so
+// the scheduler can overlap the MFMA chains, LDS reads and VALU work of two blocks.
+struct QKOut {
+  f4 s1[2], s2[2];  // per 16-key tile: sum_e (n*sc)_e q_e and sum_j m_j qsum_j
+};
+
+// Phase Q: K rows of a staged block -> raw QK sums; per-key d, dmin into the tables.
+__device__ __forceinline__ void phase_q(const Stage &st, WaveTab &T, const h8 *qb, h4 q2,
+                                        float sl2, const Masks &MK, int lane, QKOut &o) {
+  const int r = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const u4 hd = L.khdr[t];
-    const float d = f16_to_f32((uint16_t)(hd.x & 0xFFFF));
-    const float dmin = f16_to_f32((uint16_t)(hd.x >> 16));
-    const int r = lane & 15;
     const int kk = 8 * (r >> 2) + 4 * t + (r & 3);
-    if (g == 0) {
-      T.kd[kk] = d * a.sl2;
-      T.kdm[kk] = dmin * a.sl2;
-    }
+    const int sl = row_slot(kk);
+    const u4 hd = st.k[sl];
+    const u4 q0 = st.k[sl + 1 + 2 * g], q1 = st.k[sl + 2 + 2 * g];
+    // lanes of one key (g = 0..3) store the same values
+    T.kd[kk] = h2f(hd.x & 0xFFFF) * sl2;
+    T.kdm[kk] = h2f(hd.x >> 16) * sl2;
     uint32_t sc0, sc1, mm;
     scale_min(hd.y, hd.z, hd.w, 2 * g, sc0, mm);
     scale_min(hd.y, hd.z, hd.w, 2 * g + 1, sc1, mm);
     const _Float16 f0 = (_Float16)(float)sc0, f1 = (_Float16)((float)sc1 * 0.0625f);
-    const h2 SC0 = {f0, f0}, SC1 = {f1, f1};
     const _Float16 c0 = (_Float16)(-1024.0f * (float)sc0), c1 = (_Float16)(-64.0f * (float)sc1);
-    const h2 C0 = {c0, c0}, C1 = {c1, c1};
+    const h2 SC0 = {f0, f0}, SC1 = {f1, f1}, C0 = {c0, c0}, C1 = {c1, c1};
+    const uint32_t qd[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
     f4 s1 = {0.f, 0.f, 0.f, 0.f};
-    const uint32_t qd[8] = {L.kq0[t].x, L.kq0[t].y, L.kq0[t].z, L.kq0[t].w,
-                            L.kq1[t].x, L.kq1[t].y, L.kq1[t].z, L.kq1[t].w};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const uint32_t d0 = qd[2 * s], d1 = qd[2 * s + 1];
       const uint32_t d0s = d0 >> 8, d1s = d1 >> 8;
+      const uint32_t lw[4] = {and_or(d0, MK.lo, MK.magic), and_or(d0s, MK.lo, MK.magic),
+                              and_or(d1, MK.lo, MK.magic), and_or(d1s, MK.lo, MK.magic)};
+      const uint32_t hw[4] = {and_or(d0, MK.hi, MK.magic), and_or(d0s, MK.hi, MK.magic),
+                              and_or(d1, MK.hi, MK.magic), and_or(d1s, MK.hi, MK.magic)};
       h8 lo, hi;
-      const uint32_t lw[4] = {and_or(d0, 0x000F000Fu, 0x64006400u), and_or(d0s, 0x000F000Fu, 0x64006400u),
-                              and_or(d1, 0x000F000Fu, 0x64006400u), and_or(d1s, 0x000F000Fu, 0x64006400u)};
-      const uint32_t hw[4] = {and_or(d0, 0x00F000F0u, 0x64006400u), and_or(d0s, 0x00F000F0u, 0x64006400u),
-                              and_or(d1, 0x00F000F0u, 0x64006400u), and_or(d1s, 0x00F000F0u, 0x64006400u)};
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const h2 l2 = pk_fma(as_h2(lw[w]), SC0, C0);
@@ -248,38 +275,58 @@ __device__ __forceinline__ void process_block(const BlockLoads &L, WaveState &S,
       s1 = mfma32(lo, qb[s], s1);
       s1 = mfma32(hi, qb[4 + s], s1);
     }
-    // S2 = sum_j m_j * qsum_j
-    h4 a2 = {0, 0, 0, 0};
-    if (g < 2) {
+    h4 a2;
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        uint32_t scx, m;
-        scale_min(hd.y, hd.z, hd.w, 4 * g + jj, scx, m);
-        a2[jj] = (_Float16)(float)m;
-      }
+    for (int jj = 0; jj < 4; ++jj) {
+      uint32_t scx, m;
+      scale_min(hd.y, hd.z, hd.w, (4 * g + jj) & 7, scx, m);
+      a2[jj] = g < 2 ? (_Float16)(float)m : (_Float16)0.0f;
     }
-    f4 s2 = {0.f, 0.f, 0.f, 0.f};
-    s2 = mfma16(a2, q2, s2);
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    o.s1[t] = s1;
+    o.s2[t] = mfma16(a2, q2, f4{0.f, 0.f, 0.f, 0.f});
+  }
+}
+
+// Cross-lane max through v_permlane{16,32}_swap: with both operands x, the two results
+// hold x of lanes l and l ^ 16 (l ^ 32). The elements are copied to scalars before the
+// bit cast: __builtin_bit_cast of a vector element r[1] reads element 0 (clang lowers
+// it through the vector's address).
+__device__ __forceinline__ float max_pair(uint32_t a, uint32_t b) {
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+__device__ __forceinline__ float xmax16(float x) {  // max over lanes l and l ^ 16
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return max_pair(r0, r1);
+}
+__device__ __forceinline__ float xmax32(float x) {  // max over lanes l and l ^ 32
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return max_pair(r0, r1);
+}
+
+// Phase S: scores (log2 units) and the online softmax; p[k] for key 8g + k, head n % 8.
+__device__ __forceinline__ void phase_s(const QKOut &o, WaveState &S, const WaveTab &T,
+                                        int64_t key0, int64_t seq_k, int lane, float p[8]) {
+  const int g = lane >> 4;
+  float sc8[8];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int key_local = 8 * g + 4 * t + i;
-      const float v1 = s1[i] + ror8(s1[i]);
-      const float v2 = s2[i] + ror8(s2[i]);
-      float sc = T.kd[key_local] * v1 - T.kdm[key_local] * v2;
+      const int kk = 8 * g + 4 * t + i;
+      const float v1 = o.s1[t][i] + ror8(o.s1[t][i]);
+      const float v2 = o.s2[t][i] + ror8(o.s2[t][i]);
+      float sc = T.kd[kk] * v1 - T.kdm[kk] * v2;
       sc = fminf(fmaxf(sc, -kClampL2), kClampL2);
-      if ((int64_t)bi * kBlk + key_local >= a.seq_k) sc = -INFINITY;
-      sc8[4 * t + i] = sc;
+      sc8[4 * t + i] = key0 + kk < seq_k ? sc : -INFINITY;
     }
-  }
-  // ---- online softmax (head n % 8; lanes n and n+8 hold the same values)
   float bm = sc8[0];
 #pragma unroll
   for (int k = 1; k < 8; ++k) bm = fmaxf(bm, sc8[k]);
-  bm = fmaxf(bm, __shfl_xor(bm, 16));
-  bm = fmaxf(bm, __shfl_xor(bm, 32));
+  bm = xmax32(xmax16(bm));
   if (__any(bm > S.m_run)) {
     const float m_new = fmaxf(S.m_run, bm);
     const float alpha = (S.m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(S.m_run - m_new);
@@ -295,18 +342,51 @@ __device__ __forceinline__ void process_block(const BlockLoads &L, WaveState &S,
 #pragma unroll
     for (int i = 0; i < 4; ++i) S.accm[i] *= ai[i];
   }
-  float p[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     p[k] = __builtin_amdgcn_exp2f(sc8[k] - S.m_run);
     S.lsum += p[k];
   }
-  // ---- PV A operand: rows 0-7 p * mant(d), rows 8-15 p * mant(dmin)
+}
+
+// Phase P: V header tables, PV A/B operands and MFMAs, min term.
+__device__ __forceinline__ void phase_p(const Stage &st, WaveState &S, WaveTab &T,
+                                        const float p[8], const Masks &MK, int lane) {
+  const int n = lane & 15, g = lane >> 4;
+  // V header -> constant tables. Lane l handles key l % 32 and sub-blocks 4*(l/32)..+3.
+  {
+    const int kk = lane & 31, half = lane >> 5;
+    const u4 vh = st.v[row_slot(kk)];
+    int ed, em;
+    float md, mm;
+    split_scale(h2f(vh.x & 0xFFFF), ed, md);
+    split_scale(h2f(vh.x >> 16), em, mm);
+    (half ? T.vmdm : T.vmd)[kk] = half ? mm : md;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int j = 4 * half + jj;
+      uint32_t sc, m;
+      scale_min(vh.y, vh.z, vh.w, j, sc, m);
+      const float scp = __builtin_ldexpf((float)sc, ed);
+      T.vsc[j][kk] = (_Float16)((jj & 1) ? scp * 0.0625f : scp);
+      T.vc[j][kk] = (_Float16)((jj & 1) ? -64.0f * scp : -1024.0f * scp);
+      T.vm[j][kk] = (_Float16)__builtin_ldexpf((float)m, em);
+    }
+  }
+  // V rows, transposed: dword at qs byte 64h + 4n of keys 8g..8g+7
+  uint32_t vq[2][8];
+  const uint32_t *v32 = reinterpret_cast<const uint32_t *>(st.v);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int base = 4 * row_slot(8 * g + k) + 4 + n;
+    vq[0][k] = v32[base];
+    vq[1][k] = v32[base + 16];
+  }
+  // A: rows 0-7 p * mant(d), rows 8-15 p * mant(dmin)
   const float *mult = (n < 8) ? T.vmd : T.vmdm;
   h8 A;
 #pragma unroll
   for (int k = 0; k < 8; ++k) A[k] = (_Float16)(p[k] * mult[8 * g + k]);
-  // ---- PV B operands and MFMAs
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int c = 2 * h + (n >> 3);
@@ -320,10 +400,10 @@ __device__ __forceinline__ void process_block(const BlockLoads &L, WaveState &S,
       h8 blo, bhi;
 #pragma unroll
       for (int pp = 0; pp < 4; ++pp) {
-        const uint32_t x = __builtin_amdgcn_perm(L.vq[h][2 * pp + 1], L.vq[h][2 * pp], sel);
-        const h2 lo = pk_fma(as_h2(and_or(x, 0x000F000Fu, 0x64006400u)),
+        const uint32_t x = __builtin_amdgcn_perm(vq[h][2 * pp + 1], vq[h][2 * pp], sel);
+        const h2 lo = pk_fma(as_h2(and_or(x, MK.lo, MK.magic)),
                              h2{SL[2 * pp], SL[2 * pp + 1]}, h2{CL[2 * pp], CL[2 * pp + 1]});
-        const h2 hi = pk_fma(as_h2(and_or(x, 0x00F000F0u, 0x64006400u)),
+        const h2 hi = pk_fma(as_h2(and_or(x, MK.hi, MK.magic)),
                              h2{SH[2 * pp], SH[2 * pp + 1]}, h2{CH[2 * pp], CH[2 * pp + 1]});
         blo[2 * pp] = lo[0];
         blo[2 * pp + 1] = lo[1];
@@ -334,11 +414,10 @@ __device__ __forceinline__ void process_block(const BlockLoads &L, WaveState &S,
       S.acc[8 * h + 2 * byte + 1] = mfma32(A, bhi, S.acc[8 * h + 2 * byte + 1]);
     }
   }
-  // ---- min term: C'[8 + head][j] += sum_k p * mant(dmin) * m_kj * 2^e_dmin
-  h8 Bm = {0, 0, 0, 0, 0, 0, 0, 0};
-  if (n < 8) Bm = *reinterpret_cast<const h8 *>(&T.vm[n][8 * g]);
-  S.accm = mfma32(A, Bm, S.accm);
-  __builtin_amdgcn_wave_barrier();
+  // min term: C'[8 + head][j] += sum_k p * mant(dmin) * m_kj * 2^e_dmin
+  const h8 Bm0 = *reinterpret_cast<const h8 *>(&T.vm[n & 7][8 * g]);
+  const h8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  S.accm = mfma32(A, n < 8 ? Bm0 : zero8, S.accm);
 }
 
 // e (0..255) of PV tile T at lane column n
@@ -351,68 +430,78 @@ __device__ __forceinline__ int tile_e(int T, int n) {
 __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   __shared__ Smem sm;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int kv = wave >> 2, wsub = wave & 3;
+  const int kv = wave >> 1, wsub = wave & 1;
   const int b = blockIdx.y, wg = blockIdx.x;
-  const bool tail = wg == a.nwg_main;
   const int n = lane & 15, g = lane >> 4;
 
-  // ---- fused append: the tail workgroup quantizes the new token's 4 rows first
-  if (tail && a.k_new != nullptr) {
-    const int half = tid >> 8, t2 = tid & 255;
-#pragma unroll 1
-    for (int round = 0; round < 2; ++round) {
-      const int rowid = 2 * round + half;  // 0: K kv0, 1: K kv1, 2: V kv0, 3: V kv1
-      const int p = rowid >> 1, kvr = rowid & 1;
-      const float *src = (p ? a.v_new : a.k_new) + ((int64_t)b * 2 + kvr) * 256;
-      uint8_t *dst = (p ? a.vw : a.kw) + b * a.rs_b + a.t_new * a.rs_t + kvr * a.rs_h;
-      q4k_quantize_superblock_lanes(src[t2], dst, &sm.quant[half], t2);
-    }
-    __threadfence_block();
-    __syncthreads();
+  // ---- fused append: workgroups past the main ones each quantize one new row and
+  // publish it dequantized for the combine step (which attends to the new key)
+  if (wg >= a.nwg_main) {
+    const int rowid = wg - a.nwg_main;  // 0: K kv0, 1: K kv1, 2: V kv0, 3: V kv1
+    const int p = rowid >> 1, kvr = rowid & 1;
+    const float *src = (p ? a.v_new : a.k_new) + ((int64_t)b * 2 + kvr) * 256;
+    uint8_t *dst = (p ? a.vw : a.kw) + b * a.rs_b + a.t_new * a.rs_t + kvr * a.rs_h;
+    float deq;
+    q4k_quantize_superblock_lanes(src[tid], dst, &sm.quant, tid, &deq);
+    a.dq[((int64_t)b * 4 + rowid) * 256 + tid] = deq;
+    return;
   }
 
-  // ---- q operands (fp16 hi/lo, columns 0-7 hi, 8-15 lo) into LDS
-  const float *qb_src = a.q + (int64_t)b * 16 * 256;
-  for (int x = tid; x < 2 * 8 * 64 * 8; x += kThreads) {
-    const int slot = x & 7, ln = (x >> 3) & 63, s = (x >> 9) & 7, kvx = x >> 12;
-    const int nn = ln & 15, gg = ln >> 4;
-    const int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-    const int e = 64 * gg + 32 * (s >> 2) + 8 * (s & 3) + perm[slot];
-    const float qv = qb_src[(8 * kvx + (nn & 7)) * 256 + e];
-    const _Float16 hi = (_Float16)qv;
-    const _Float16 lo = (_Float16)(qv - (float)hi);
-    sm.run.qb[kvx][s][ln][slot] = (nn < 8) ? hi : lo;
-  }
-  for (int x = tid; x < 2 * 64 * 4; x += kThreads) {
-    const int slot = x & 3, ln = (x >> 2) & 63, kvx = x >> 8;
-    const int nn = ln & 15, gg = ln >> 4;
-    _Float16 val = 0;
-    if (gg < 2) {
-      const int j = 4 * gg + slot;
-      const float *qq = qb_src + (8 * kvx + (nn & 7)) * 256 + 32 * j;
-      float s = 0.0f;
-      for (int e = 0; e < 32; ++e) s += qq[e];
-      const _Float16 hi = (_Float16)s;
-      val = (nn < 8) ? hi : (_Float16)(s - (float)hi);
+  // ---- q operands (fp16 hi/lo, columns 0-7 hi, 8-15 lo) into LDS. q is staged in the
+  // (not yet used) table area with coalesced loads first.
+  {
+    float *qf = &sm.qsetup.qf[0][0];
+    float *qs = &sm.qsetup.qs[0][0];
+    const float4 *src4 = reinterpret_cast<const float4 *>(a.q + (int64_t)b * 16 * 256);
+    for (int x = tid; x < 16 * 256 / 4; x += kThreads) reinterpret_cast<float4 *>(qf)[x] = src4[x];
+    __syncthreads();
+    if (tid < 128) {
+      const float *qq = qf + (tid >> 3) * 256 + 32 * (tid & 7);
+      float sacc = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) sacc += qq[e];
+      qs[tid] = sacc;
     }
-    sm.run.q2[kvx][ln][slot] = val;
+    __syncthreads();
+    constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    for (int x = tid; x < 2 * 8 * 64; x += kThreads) {
+      const int ln = x & 63, st = (x >> 6) & 7, kvx = x >> 9;
+      const int nn = ln & 15, gg = ln >> 4;
+      const float *qrow = qf + (8 * kvx + (nn & 7)) * 256 + 64 * gg + 32 * (st >> 2) + 8 * (st & 3);
+      h8 val;
+#pragma unroll
+      for (int slot = 0; slot < 8; ++slot) {
+        const float qv = qrow[perm[slot]];
+        const _Float16 hi = (_Float16)qv;
+        val[slot] = (nn < 8) ? hi : (_Float16)(qv - (float)hi);
+      }
+      sm.qsetup.qb[kvx][st][ln] = val;
+    }
+    if (tid < 128) {
+      const int ln = tid & 63, kvx = tid >> 6;
+      const int nn = ln & 15, gg = ln >> 4;
+      h4 val = {0, 0, 0, 0};
+      if (gg < 2) {
+#pragma unroll
+        for (int slot = 0; slot < 4; ++slot) {
+          const float sv = qs[(8 * kvx + (nn & 7)) * 8 + 4 * gg + slot];
+          const _Float16 hi = (_Float16)sv;
+          val[slot] = (nn < 8) ? hi : (_Float16)(sv - (float)hi);
+        }
+      }
+      sm.qsetup.q2[kvx][ln] = val;
+    }
   }
   __syncthreads();
   h8 qb[8];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) qb[s] = sm.run.qb[kv][s][lane];
-  const h4 q2 = sm.run.q2[kv][lane];
+  for (int s = 0; s < 8; ++s) qb[s] = sm.qsetup.qb[kv][s][lane];
+  const h4 q2 = sm.qsetup.q2[kv][lane];
+  __syncthreads();  // the staging area becomes the wave tables
 
-  // ---- block range
-  int b0, b1;
-  if (tail) {
-    b0 = a.nblk - 1;
-    b1 = a.nblk;
-  } else {
-    b0 = wg * a.bpw;
-    b1 = b0 + a.bpw;
-    if (b1 > a.nblk - 1) b1 = a.nblk - 1;
-  }
+  // ---- block range of this workgroup
+  const int b0 = wg * a.bpw;
+  const int b1 = b0 + a.bpw < a.nblk ? b0 + a.bpw : a.nblk;
   WaveState S;
 #pragma unroll
   for (int T2 = 0; T2 < 16; ++T2) S.acc[T2] = f4{0.f, 0.f, 0.f, 0.f};
@@ -420,17 +509,45 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   S.m_run = -INFINITY;
   S.lsum = 0.0f;
   WaveTab &T = sm.run.tab[wave];
-  int bi = b0 + wsub;
-  if (bi < b1) {
-    BlockLoads cur;
-    load_block(cur, a, b, kv, bi, lane);
-    for (; bi < b1; bi += 4) {
-      BlockLoads nxt;
-      const bool more = bi + 4 < b1;
-      if (more) load_block(nxt, a, b, kv, bi + 4, lane);
-      process_block(cur, S, T, qb, q2, a, bi, lane);
-      if (more) cur = nxt;
+  const int kvu = __builtin_amdgcn_readfirstlane(kv);
+  const uint8_t *kbase = a.k + b * a.rs_b + kvu * a.rs_h;
+  const uint8_t *vbase = a.v + b * a.rs_b + kvu * a.rs_h;
+  const uint32_t rs_t = (uint32_t)a.rs_t;
+  // rows of keys [0, seq_k) of this head; loads past them return zeros (and are masked)
+  const uint32_t span = (uint32_t)(a.seq_k - 1) * rs_t + 144u;
+  const u4s rk = make_rsrc(kbase, span), rv = make_rsrc(vbase, span);
+  const LoadPlan P = make_plan(lane, rs_t);
+  const Masks MK = {vconst(0x000F000Fu), vconst(0x00F000F0u), vconst(0x64006400u)};
+  Stage *stages = reinterpret_cast<Stage *>(sm.run.stages) + wave * kStages;
+  // Three-stage pipeline: blocks first, first+2, first+4, ... of this wave are staged
+  // into LDS two ahead of the one being processed. Every iteration issues one stage
+  // (a block past the end reads out of range, which moves no data) so the wait count
+  // stays constant.
+  const int first = b0 + wsub;
+  const int nmine = first < b1 ? (b1 - first + 1) / 2 : 0;
+  auto soff_of = [&](int i) -> uint32_t {
+    return i < nmine ? (uint32_t)(first + 2 * i) * kBlk * rs_t : 0xFFFFFF00u;
+  };
+  if (nmine > 0) {
+    issue_stage(&stages[0], P, rk, rv, soff_of(0));
+    issue_stage(&stages[1], P, rk, rv, soff_of(1));
+    issue_stage(&stages[2], P, rk, rv, soff_of(2));
+    asm volatile("s_waitcnt vmcnt(20)" ::: "memory");  // stage 0 landed
+    QKOut qo;
+    float pv[8];
+    phase_q(stages[0], T, qb, q2, a.sl2, MK, lane, qo);
+    phase_s(qo, S, T, (int64_t)first * kBlk, a.seq_k, lane, pv);
+    for (int i = 0; i < nmine; ++i) {
+      asm volatile("s_waitcnt vmcnt(10)" ::: "memory");  // stage i+1 landed
+      // P(i) and Q(i+1) form one straight-line region
+      phase_p(stages[i % kStages], S, T, pv, MK, lane);
+      phase_q(stages[(i + 1) % kStages], T, qb, q2, a.sl2, MK, lane, qo);
+      // stage i is refilled with block i+3 once its LDS reads have completed
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue_stage(&stages[i % kStages], P, rk, rv, soff_of(i + 3));
+      if (i + 1 < nmine) phase_s(qo, S, T, (int64_t)(first + 2 * (i + 1)) * kBlk, a.seq_k, lane, pv);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   // ---- per-wave reductions
   S.lsum += __shfl_xor(S.lsum, 16);
@@ -450,59 +567,46 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[T2][i] = S.acc[T2][i] - sm.merge.cmin[wave][(4 * g + i) & 7][e >> 5];
   }
-  // ---- merge the 4 waves of each KV head (pairwise through LDS)
+  // ---- merge the two waves of each KV head through LDS
   float mw = S.m_run;  // for head n % 8
   float lw = S.lsum;
-#pragma unroll 1
-  for (int step = 2; step >= 1; step >>= 1) {
-    __syncthreads();
-    const bool writer = wsub >= step && wsub < 2 * step;
-    const int slot = kv * 2 + (wsub - step);  // staging slot (0..3)
-    if (writer) {
-      if (g < 2) {
-#pragma unroll
-        for (int T2 = 0; T2 < 16; ++T2)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sm.merge.o[slot][4 * g + i][tile_e(T2, n)] = o[T2][i];
-      }
-      if (g == 0 && n < 8) {
-        sm.merge.m[slot][n] = mw;
-        sm.merge.l[slot][n] = lw;
-      }
-    }
-    __syncthreads();
-    if (wsub < step) {
-      const int src = kv * 2 + wsub;
-      const float mo = sm.merge.m[src][n & 7], lo2 = sm.merge.l[src][n & 7];
-      const float M = fmaxf(mw, mo);
-      const float fa = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-      const float fb = (mo == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mo - M);
-      // o rows are head 4g+i: need factors of heads 4(g&1)+i
-      float fai[4], fbi[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        fai[i] = __shfl(fa, 4 * (g & 1) + i);
-        fbi[i] = __shfl(fb, 4 * (g & 1) + i);
-      }
-      if (g < 2) {
-#pragma unroll
-        for (int T2 = 0; T2 < 16; ++T2)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            o[T2][i] = o[T2][i] * fai[i] + sm.merge.o[src][4 * g + i][tile_e(T2, n)] * fbi[i];
-      }
-      lw = lw * fa + lo2 * fb;
-      mw = M;
-    }
-  }
-  // ---- write the workgroup partial: [16 heads][256 e | m | l]
-  if (wsub == 0) {
-    float *dst = a.part + ((int64_t)b * (a.nwg_main + 1) + wg) * 16 * 258;
+  __syncthreads();
+  if (wsub == 1) {
     if (g < 2) {
 #pragma unroll
       for (int T2 = 0; T2 < 16; ++T2)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dst[(8 * kv + 4 * g + i) * 258 + tile_e(T2, n)] = o[T2][i];
+        for (int i = 0; i < 4; ++i) sm.merge.o[kv][4 * g + i][tile_e(T2, n)] = o[T2][i];
+    }
+    if (g == 0 && n < 8) {
+      sm.merge.m[kv][n] = mw;
+      sm.merge.l[kv][n] = lw;
+    }
+  }
+  __syncthreads();
+  if (wsub == 0) {
+    const float mo = sm.merge.m[kv][n & 7], lo2 = sm.merge.l[kv][n & 7];
+    const float M = fmaxf(mw, mo);
+    const float fa = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+    const float fb = (mo == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mo - M);
+    float fai[4], fbi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // o rows are head 4g+i: factors of heads 4(g&1)+i
+      fai[i] = __shfl(fa, 4 * (g & 1) + i);
+      fbi[i] = __shfl(fb, 4 * (g & 1) + i);
+    }
+    lw = lw * fa + lo2 * fb;
+    mw = M;
+    float *dst = a.part + ((int64_t)b * a.nwg_main + wg) * 16 * 258;
+    if (g < 2) {
+#pragma unroll
+      for (int T2 = 0; T2 < 16; ++T2) {
+        const int e = tile_e(T2, n);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          dst[(8 * kv + 4 * g + i) * 258 + e] =
+              o[T2][i] * fai[i] + sm.merge.o[kv][4 * g + i][e] * fbi[i];
+      }
     }
     if (g == 0 && n < 8) {
       dst[(8 * kv + n) * 258 + 256] = mw;
@@ -511,21 +615,70 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   }
 }
 
-// out[b][h][e] = sum_w o_w e^(m_w - M) / sum_w l_w e^(m_w - M); one workgroup per (b, h).
+// out[b][h][e] = sum_w o_w 2^(m_w - M) / sum_w l_w 2^(m_w - M).
+// One workgroup per (head, 64-wide slice of e, batch); 4 thread groups split the partials.
+constexpr int kMaxPartials = 1024;
+// out[b][h][e] = (sum_w o_w 2^(m_w - M) + [new key]) / (sum_w l_w 2^(m_w - M) + [new key]).
+// One workgroup per (head, 64-wide slice of e, batch); 4 thread groups split the
+// partials. For a fused decode step the appended key enters here, from its exactly
+// dequantized K and V rows: score = clamp(q . k_new * scale), weight 2^(score - M).
 __global__ __launch_bounds__(256) void q4k_decode_combine_kernel(const float *part, int nwg,
-                                                                 float *out) {
-  const int h = blockIdx.x, b = blockIdx.y, e = threadIdx.x;
+                                                                 const float *q, const float *dq,
+                                                                 float sl2, float *out) {
+  __shared__ float wts[kMaxPartials];
+  __shared__ float red[256];
+  __shared__ float acc4[4][64];
+  const int h = blockIdx.x >> 2, e0 = 64 * (blockIdx.x & 3), b = blockIdx.y;
+  const int tid = threadIdx.x;
   const float *P = part + (int64_t)b * nwg * 16 * 258 + h * 258;
-  float M = -INFINITY;
-  for (int w = 0; w < nwg; ++w) M = fmaxf(M, P[(int64_t)w * 16 * 258 + 256]);
-  float acc = 0.0f, L = 0.0f;
-  for (int w = 0; w < nwg; ++w) {
+  // new key's score (log2 units), every thread gets it
+  float s_new = -INFINITY;
+  if (dq != nullptr) {
+    red[tid] = q[((int64_t)b * 16 + h) * 256 + tid] * dq[((int64_t)b * 4 + (h >> 3)) * 256 + tid];
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+      if (tid < o) red[tid] += red[tid + o];
+      __syncthreads();
+    }
+    s_new = fminf(fmaxf(red[0] * sl2, -kClampL2), kClampL2);
+    __syncthreads();
+  }
+  float M = s_new;
+  for (int w = tid; w < nwg; w += 256) M = fmaxf(M, P[(int64_t)w * 16 * 258 + 256]);
+  red[tid] = M;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (tid < o) red[tid] = fmaxf(red[tid], red[tid + o]);
+    __syncthreads();
+  }
+  M = red[0];
+  __syncthreads();
+  float L = 0.0f;
+  for (int w = tid; w < nwg; w += 256) {
     const float mw = P[(int64_t)w * 16 * 258 + 256];
     const float f = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-    acc += f * P[(int64_t)w * 16 * 258 + e];
+    wts[w] = f;
     L += f * P[(int64_t)w * 16 * 258 + 257];
   }
-  out[((int64_t)b * 16 + h) * 256 + e] = L > 0.0f ? acc / L : 0.0f;
+  red[tid] = L;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (tid < o) red[tid] += red[tid + o];
+    __syncthreads();
+  }
+  const float f_new = (s_new == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_new - M);
+  L = red[0] + f_new;
+  const int e = tid & 63, r = tid >> 6;
+  float acc = 0.0f;
+#pragma unroll 8
+  for (int w = r; w < nwg; w += 4) acc += wts[w] * P[(int64_t)w * 16 * 258 + e0 + e];
+  acc4[r][e] = acc;
+  __syncthreads();
+  if (tid < 64) {
+    float sum = acc4[0][tid] + acc4[1][tid] + acc4[2][tid] + acc4[3][tid];
+    if (dq != nullptr) sum += f_new * dq[((int64_t)b * 4 + 2 + (h >> 3)) * 256 + e0 + tid];
+    out[((int64_t)b * 16 + h) * 256 + e0 + tid] = L > 0.0f ? sum / L : 0.0f;
+  }
 }
 
 }  // namespace
@@ -537,6 +690,11 @@ int launch_attend_mfma(const AttnArgs &a, const float *k_new, const float *v_new
     return PKV_ERR_UNSUPPORTED;
   // decode only: the single query sees every key
   if (a.causal && a.q_offset + 1 < a.seq_k) return PKV_ERR_UNSUPPORTED;
+  const bool fused = k_new != nullptr;
+  // rows are addressed with 32-bit offsets (key * row stride) from a per-head base
+  if (a.rs.t >= (1 << 24) || a.seq_k >= (1 << 24) ||
+      (uint64_t)a.seq_k * (uint64_t)a.rs.t >= (1ull << 32))
+    return PKV_ERR_UNSUPPORTED;
   DecodeArgs d;
   d.q = a.q;
   d.k = a.k;
@@ -546,31 +704,32 @@ int launch_attend_mfma(const AttnArgs &a, const float *k_new, const float *v_new
   d.rs_b = a.rs.b;
   d.rs_t = a.rs.t;
   d.rs_h = a.rs.h;
-  d.seq_k = a.seq_k;
-  d.nblk = (int)((a.seq_k + kBlk - 1) / kBlk);
-  const int main_blocks = d.nblk - 1;
-  int nwg = (main_blocks + 3) / 4;
-  if (nwg > kMainWGs) nwg = kMainWGs;
+  d.seq_k = fused ? a.seq_k - 1 : a.seq_k;  // old keys; the new one joins in the combine
+  d.nblk = (int)((d.seq_k + kBlk - 1) / kBlk);
+  int nwg = (d.nblk + 1) / 2;
+  if (nwg > kMainWGs) nwg = kMainWGs;  // nwg <= kMaxPartials
   if (nwg < 1) nwg = 1;
-  d.bpw = (main_blocks + nwg - 1) / nwg;
-  d.bpw = (d.bpw + 3) / 4 * 4;
-  if (d.bpw < 4) d.bpw = 4;
-  nwg = (main_blocks + d.bpw - 1) / d.bpw;
+  d.bpw = (d.nblk + nwg - 1) / nwg;
+  d.bpw = (d.bpw + 1) / 2 * 2;
+  if (d.bpw < 2) d.bpw = 2;
+  nwg = (d.nblk + d.bpw - 1) / d.bpw;
   if (nwg < 1) nwg = 1;
   d.nwg_main = nwg;
   d.sl2 = a.scale * kLog2e;
   d.k_new = k_new;
   d.v_new = v_new;
   d.t_new = t_new;
-  const size_t need = (size_t)a.batch * (nwg + 1) * 16 * 258 * sizeof(float);
+  const size_t part_floats = (size_t)a.batch * nwg * 16 * 258;
+  const size_t need = (part_floats + (size_t)a.batch * 4 * 256) * sizeof(float);
   int rc = ws.reserve(need);
   if (rc) return rc;
   d.part = static_cast<float *>(ws.ptr);
-  hipLaunchKernelGGL(q4k_decode_kernel, dim3((unsigned)(nwg + 1), (unsigned)a.batch),
+  d.dq = d.part + part_floats;
+  hipLaunchKernelGGL(q4k_decode_kernel, dim3((unsigned)(nwg + (fused ? 4 : 0)), (unsigned)a.batch),
                      dim3(kThreads), 0, s, d);
   PKV_HIP(hipGetLastError());
-  hipLaunchKernelGGL(q4k_decode_combine_kernel, dim3(16, (unsigned)a.batch), dim3(256), 0, s,
-                     d.part, nwg + 1, a.out);
+  hipLaunchKernelGGL(q4k_decode_combine_kernel, dim3(64, (unsigned)a.batch), dim3(256), 0, s,
+                     d.part, nwg, a.q, fused ? d.dq : nullptr, d.sl2, a.out);
   PKV_HIP(hipGetLastError());
   return PKV_OK;
 }

@@ -39,8 +39,9 @@ __device__ __forceinline__ float q4k_chain_sum_32(float *scr, int i, float term,
 
 // x: this thread's element (tid = 32 * sub-block + element); blk: 144 output bytes.
 // Called by 256 threads of one workgroup together (contains __syncthreads()).
-static __device__ __noinline__ void q4k_quantize_superblock_lanes(float x, uint8_t *blk, Q4kScratch *S,
-                                                           int tid) {
+static __device__ __forceinline__ void q4k_quantize_superblock_lanes(float x, uint8_t *blk,
+                                                                   Q4kScratch *S, int tid,
+                                                                   float *deq = nullptr) {
 #pragma clang fp contract(off)
   const int j = tid >> 5, i = tid & 31;
   float *mine = S->scr + 32 * j;
@@ -103,6 +104,10 @@ static __device__ __noinline__ void q4k_quantize_superblock_lanes(float x, uint8
     const float dm = f16_to_f32(mh) * (float)lm;
     const int32_t l = nearest_int((x + dm) / dd);
     q = (uint32_t)(l < 0 ? 0 : (l > 15 ? 15 : l));
+  }
+  if (deq != nullptr) {  // to_float of this element: d * sc * q - dmin * m (two roundings)
+    const float d1 = f16_to_f32(dh) * (float)ls, m1 = f16_to_f32(mh) * (float)lm;
+    *deq = d1 * (float)q - m1;
   }
   if (i == 0) S->codes[j] = ls | (lm << 8);
   S->nib[tid] = (uint8_t)q;

@@ -122,6 +122,7 @@ class PreallocatedQuantizedKvCache:
                                ctypes.c_void_p(stream if stream is not None else _stream()),
                                ctypes.byref(h)))
         self._h = h
+        self._lib = lib()  # held for __del__, which may run during interpreter shutdown
         self._stream = stream if stream is not None else _stream()
         self.quant = KvCacheQuantization(int(quant) or _lib.QUANT_F16)
         self.num_kv_heads = num_kv_heads
@@ -132,7 +133,7 @@ class PreallocatedQuantizedKvCache:
     def __del__(self):
         h = getattr(self, "_h", None)
         if h is not None and h.value:
-            lib().pkv_destroy(h)
+            self._lib.pkv_destroy(h)
             self._h = None
 
     @property
@@ -348,7 +349,7 @@ class PrefixCache:
 
     def __del__(self):
         if self._native is not None and self._native.value:
-            lib().pkv_prefix_free(self._native)
+            self._free(self._native)
             self._native = None
 
 
@@ -397,6 +398,7 @@ class ModelKvState:
         p = ctypes.c_void_p()
         _call(lib().pkv_prefix_create(toks, len(prefix_tokens), len(self.layers), ctypes.byref(p)))
         pc = PrefixCache(list(prefix_tokens), [], p)
+        pc._free = lib().pkv_prefix_free  # held for __del__ at interpreter shutdown
         s = ctypes.c_void_p(_stream())
         for i, l in enumerate(self.layers):
             if isinstance(l, FullAttentionKv):
