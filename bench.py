@@ -44,6 +44,10 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=12)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="after the timed runs, launch a plain elementwise copy of this many MiB "
+                         "(read N, write N) 3 times: the reference kernel that scales rocprofv3's "
+                         "FETCH_SIZE / WRITE_SIZE counters to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures the single-GPU path only: every GPU box in this build has "
@@ -178,6 +182,14 @@ def main() -> int:
         "append_tokens_per_s": round(L * S / fill_s, 1),
     }
 
+    if args.calib_copy_mib > 0:
+        n = args.calib_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(caches[0], kn[0], vn[0], q[0], S, args.cpu_threads)
     print(json.dumps(result), flush=True)
