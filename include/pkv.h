@@ -101,7 +101,7 @@ int pkv_attend(pkv_cache *h, const float *q, int l, int num_heads, float scale,
                int64_t q_offset, int causal, float *out);
 
 /* One decode step of one full-attention layer: append one token (offset rule as
- * pkv_append) then attend over all len+1 keys, in a single launch.
+ * pkv_append) then attend over all len+1 keys, in one call.
  * k, v: [batch, n_kv_heads, 1, head_dim]; q, out: [batch, 1, num_heads, head_dim]. */
 int pkv_append_attend(pkv_cache *h, const float *k, const float *v, const float *q,
                       int num_heads, float scale, int64_t offset, float *out);
