@@ -5,11 +5,12 @@
 // (paramecia-model/src/ops.rs:756-792, called at qwen3_next.rs:2531-2561) and the CPU
 // SDPA it falls back to (qwen3_next.rs:2580-2605), for a decode step (one query).
 //
-// Work split: split-K over 32-key blocks. A workgroup (8 waves) owns a contiguous
-// block range; waves 0-3 handle KV head 0 and waves 4-7 KV head 1 of the same
-// blocks, so the two waves reading the interleaved K/V rows of a token (288 bytes)
-// run side by side on one CU. The last workgroup owns the final block and, for a
-// fused decode step, first quantizes the new token's rows (bit-exact Q4K).
+// Work split: split-K over 32-key blocks. A workgroup of 8 waves (two per SIMD, so each
+// SIMD always has a second wave to issue while one waits) owns a contiguous block
+// range; waves 2s and 2s+1 take KV heads 0 and 1 of the same blocks, so the two halves
+// of a token's 288-byte K (and V) rows are read together. Each wave streams its blocks
+// through two LDS stages with buffer_load ... lds. Extra workgroups past the main ones
+// quantize the new token's rows for a fused decode step (bit-exact Q4K).
 //
 // Arithmetic (per KV head, per 16 keys, MFMA f32_16x16x32_f16):
 //   QK: A[key][e] = nibble * sub-block scale code, an integer <= 945 built exactly in
@@ -22,6 +23,8 @@
 //       and feed the min-term MFMA against B'[key][j] = m_j * 2^e_dmin.
 //   All accumulation is f32. Softmax runs in base 2 with the 1/sqrt(d) scale folded
 //   in, scores clamped to [-100, 100] (in natural-log units) as the reference does.
+//   The running max is raised only when a block exceeds it by 2^8 (p <= 256 is exact
+//   enough in fp16 and the f32 sums), so the accumulators are rarely rescaled.
 #include "pkv_internal.hpp"
 #include "pkv_scalar.hpp"
 #include "pkv_q4k_lanes.hpp"
@@ -36,11 +39,13 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;  // 4 waves: 2 per KV head, one wave per SIMD
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;  // two waves per SIMD
 constexpr int kBlk = 32;
 constexpr int kMainWGs = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kClampL2 = 100.0f * 1.4426950408889634f;  // +-100 nats in log2 units
+constexpr float kLazy = 8.0f;  // log2 headroom of the running max before a rescale
 
 struct DecodeArgs {
   const float *q;  // [B][16][256]
@@ -54,35 +59,6 @@ struct DecodeArgs {
   int64_t t_new;
   float *part;  // [B][nwg_main][16][258]
   float *dq;    // [B][4][256] dequantized new rows (K kv0, K kv1, V kv0, V kv1)
-};
-
-// Per-wave tables rebuilt for every 32-key block.
-struct WaveTab {
-  float kd[kBlk], kdm[kBlk];                     // K: d*sl2, dmin*sl2
-  float vmd[kBlk], vmdm[kBlk];                   // V: mantissas of d and dmin
-  _Float16 vsc[8][kBlk], vc[8][kBlk], vm[8][kBlk];  // V: fp16 constants [j][key]
-};
-
-struct Stage;
-struct Smem {
-  union {
-    struct {
-      h8 qb[2][8][64];  // QK B operands [kv][step][lane]
-      h4 q2[2][64];     // S2 B operands [kv][lane]
-      float qf[16][256];  // q staged before the operands are built
-      float qs[16][8];    // per head, per 32-element sub-block sums of q
-    } qsetup;
-    struct {
-      WaveTab tab[4];
-      char stages[4 * 3 * 2 * 320 * 16];  // Stage[wave][kStages]
-    } run;
-    struct {
-      float o[2][8][256];  // the second wave of each KV head
-      float m[2][8], l[2][8];
-      float cmin[4][8][8];  // per wave [head][j]
-    } merge;
-    Q4kScratch quant;
-  };
 };
 
 __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
@@ -142,16 +118,56 @@ __device__ __forceinline__ void split_scale(float d, int &e, float &mant) {
 typedef uint32_t u4s __attribute__((ext_vector_type(4)));
 #define PKV_LDS __attribute__((address_space(3)))
 
-// ---- LDS staging of 32-key blocks. Rows (144 B = 9 slots of 16 B) of one KV head are
-// placed at slot 9R + 4*(R/8): the 64 B gap after every 8 rows puts the four 8-row
-// groups that a transposed V read touches at once on disjoint LDS banks.
-constexpr int kSlots = 320;   // 5 loads of 64 lanes x 16 B; 304 slots used
-constexpr int kStages = 3;
-struct Stage {
-  u4 k[kSlots];
-  u4 v[kSlots];
+// ---- LDS staging of 32-key blocks. One tensor (K or V) of one KV head: the 16-byte
+// header of row R at hdr[R], and the row's eight 16-byte nibble pieces at
+// nib[8R + (piece ^ swz(R))]. The XOR swizzle makes the row-wise K reads of phase Q
+// conflict-free and keeps the transposed V reads of phase P at two ways.
+struct TensorStage {
+  u4 hdr[kBlk];
+  u4 nib[8 * kBlk];
 };
-__device__ __forceinline__ int row_slot(int R) { return 9 * R + 4 * (R >> 3); }
+struct Stage {
+  TensorStage k, v;
+};
+constexpr int kStages = 2;
+constexpr int kLoadsPerStage = 12;  // 4 x dwordx4 (pieces) + 2 x dword (headers), K and V
+__device__ __forceinline__ int swz(int R) { return ((R >> 1) & 1) | (((R >> 3) & 3) << 1); }
+
+// Per-wave tables rebuilt for every 32-key block.
+struct WaveTab {
+  float kd[kBlk], kdm[kBlk];                        // K: d*sl2, dmin*sl2
+  float vmd[kBlk], vmdm[kBlk];                      // V: mantissas of d and dmin
+  _Float16 vsc[8][kBlk], vc[8][kBlk], vm[8][kBlk];  // V: fp16 constants [j][key]
+};
+
+// LDS of one workgroup. Each wave owns stage buffers st0/st1 and a table area; before
+// its first refill of st1 a wave stages its KV head's q rows there, and the quantizer
+// scratch of the quantizing waves 0-3 overlaps their tables. The merge area reuses the
+// st0 buffers once every wave has left the loop.
+constexpr int kMergeRow = 264;  // padded row of a wave's per-head output in tile order
+struct Smem {
+  union {
+    struct {
+      Stage st0[kWaves];
+      Stage st1[kWaves];
+      union {
+        WaveTab tab[kWaves];
+        struct {
+          Q4kScratch scr;
+          uint32_t arrivals;  // barrier counter of the quantizing waves 0-3
+        } quant;
+      } t;
+    } run;
+    struct {
+      float o[kWaves][8][kMergeRow];
+      float m[kWaves][8], l[kWaves][8];
+    } merge;
+  };
+};
+static_assert(sizeof(Q4kScratch) + 4 <= sizeof(WaveTab), "quantizer scratch within wave 0's tables");
+static_assert(sizeof(float[kWaves][8][kMergeRow]) + 2 * sizeof(float[kWaves][8]) <=
+                  sizeof(Stage[kWaves]), "merge area within the st0 buffers");
+static_assert(sizeof(Smem) <= 160 * 1024, "LDS budget of one workgroup");
 
 // Buffer resource of a byte range (raw, stride 0; out-of-range loads return zero).
 __device__ __forceinline__ u4s make_rsrc(const void *base, uint32_t bytes) {
@@ -164,62 +180,106 @@ __device__ __forceinline__ u4s make_rsrc(const void *base, uint32_t bytes) {
   return r;
 }
 
-// One lane's part of staging a block: up to 5 16-byte pieces per tensor. Issued from
-// inline asm so that the compiler's wait-count pass does not serialise the LDS reads
-// behind these transfers; the kernel places its own s_waitcnt vmcnt before a stage is
-// read.
+// One lane's part of staging a block, as byte offsets from the block's first row
+// (the same for K and V, whose rows share the stride). The block's own offset is
+// added in the voffset operand, so the buffer range check covers the whole address.
 struct LoadPlan {
-  uint32_t voff[5];
-  uint32_t valid;
+  uint32_t nib[4];  // dwordx4 load i: slot 64 i + lane
+  uint32_t hdr[2];  // dword load j: dword (lane & 3) of header 16 j + lane / 4
 };
 
 __device__ __forceinline__ LoadPlan make_plan(int lane, uint32_t rs_t) {
   LoadPlan P;
-  P.valid = 0;
 #pragma unroll
-  for (int i = 0; i < 5; ++i) {
-    const int slot = 64 * i + lane;
-    const int G = slot / 76, w = slot % 76;
-    const bool ok = G < 4 && w < 72;
-    const int R = 8 * G + w / 9, piece = w % 9;
-    P.voff[i] = ok ? (uint32_t)R * rs_t + 16u * (uint32_t)piece : 0u;
-    P.valid |= (ok ? 1u : 0u) << i;
+  for (int i = 0; i < 4; ++i) {
+    const int slot = 64 * i + lane, R = slot >> 3;
+    const int piece = (slot & 7) ^ swz(R);
+    P.nib[i] = (uint32_t)R * rs_t + 16u + 16u * (uint32_t)piece;
   }
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    P.hdr[j] = (uint32_t)(16 * j + (lane >> 2)) * rs_t + 4u * (uint32_t)(lane & 3);
   return P;
 }
 
-__device__ __forceinline__ void lds_dma16(uint32_t lds, uint32_t voff, u4s rsrc, uint32_t soff) {
+// Stage one block (K and V) into LDS: 12 buffer_load ... lds, written from inline asm
+// so that the compiler's wait-count pass does not serialise later LDS reads behind
+// them; the kernel places its own s_waitcnt vmcnt before a stage is read. M0 holds
+// the LDS destination of each load (lane l writes M0 + 16 l, or M0 + 4 l for dwords);
+// one wait state separates an M0 write from the load that reads it.
+__device__ __forceinline__ void issue_stage(Stage *st, const LoadPlan &P, u4s rk, u4s rv,
+                                            uint32_t boff) {
+  const uint32_t kn = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&st->k.nib[0]));
+  const uint32_t kh = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&st->k.hdr[0]));
+  const uint32_t vn = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&st->v.nib[0]));
+  const uint32_t vh = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&st->v.hdr[0]));
+  const uint32_t o0 = P.nib[0] + boff, o1 = P.nib[1] + boff, o2 = P.nib[2] + boff,
+                 o3 = P.nib[3] + boff, h0 = P.hdr[0] + boff, h1 = P.hdr[1] + boff;
   uint32_t saved;
   asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
-      : "memory");
+      "s_mov_b32 %[sv], m0\n\t"
+      "s_mov_b32 m0, %[kn]\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o0], %[rk], 0 offen lds\n\t"
+      "s_add_u32 m0, %[kn], 0x400\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o1], %[rk], 0 offen lds\n\t"
+      "s_add_u32 m0, %[kn], 0x800\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o2], %[rk], 0 offen lds\n\t"
+      "s_add_u32 m0, %[kn], 0xc00\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o3], %[rk], 0 offen lds\n\t"
+      "s_mov_b32 m0, %[kh]\n\ts_nop 0\n\t"
+      "buffer_load_dword %[h0], %[rk], 0 offen lds\n\t"
+      "s_add_u32 m0, %[kh], 0x100\n\ts_nop 0\n\t"
+      "buffer_load_dword %[h1], %[rk], 0 offen lds\n\t"
+      "s_mov_b32 m0, %[vn]\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o0], %[rv], 0 offen lds\n\t"
+      "s_add_u32 m0, %[vn], 0x400\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o1], %[rv], 0 offen lds\n\t"
+      "s_add_u32 m0, %[vn], 0x800\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o2], %[rv], 0 offen lds\n\t"
+      "s_add_u32 m0, %[vn], 0xc00\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o3], %[rv], 0 offen lds\n\t"
+      "s_mov_b32 m0, %[vh]\n\ts_nop 0\n\t"
+      "buffer_load_dword %[h0], %[rv], 0 offen lds\n\t"
+      "s_add_u32 m0, %[vh], 0x100\n\ts_nop 0\n\t"
+      "buffer_load_dword %[h1], %[rv], 0 offen lds\n\t"
+      "s_mov_b32 m0, %[sv]"
+      : [sv] "=&s"(saved)
+      : [kn] "s"(kn), [kh] "s"(kh), [vn] "s"(vn), [vh] "s"(vh), [o0] "v"(o0), [o1] "v"(o1),
+        [o2] "v"(o2), [o3] "v"(o3), [h0] "v"(h0), [h1] "v"(h1), [rk] "s"(rk), [rv] "s"(rv)
+      : "memory", "scc");
 }
 
-__device__ __forceinline__ void issue_stage(Stage *st, const LoadPlan &P, u4s rk, u4s rv,
-                                            uint32_t soff) {
-  soff = __builtin_amdgcn_readfirstlane(soff);
-  const uint32_t lk = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&st->k[0]));
-  const uint32_t lv = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&st->v[0]));
-#pragma unroll
-  for (int i = 0; i < 5; ++i) {
-    if (P.valid & (1u << i)) {
-      lds_dma16(lk + 1024u * i, P.voff[i], rk, soff);
-      lds_dma16(lv + 1024u * i, P.voff[i], rv, soff);
-    }
-  }
+// Stage this wave's KV head's 8 q rows (8 KB, contiguous in q) into LDS: eight
+// dwordx4 loads, lane l of load j moving bytes 1024 j + 16 l.
+__device__ __forceinline__ void issue_q(void *dst_lds, u4s rq, uint32_t lane16) {
+  const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)dst_lds));
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %[sv], m0\n\t"
+      "s_mov_b32 m0, %[d]\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o0], %[rq], 0 offen lds\n\t"
+      "s_add_u32 m0, %[d], 0x400\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o1], %[rq], 0 offen lds\n\t"
+      "s_add_u32 m0, %[d], 0x800\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o2], %[rq], 0 offen lds\n\t"
+      "s_add_u32 m0, %[d], 0xc00\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o3], %[rq], 0 offen lds\n\t"
+      "s_add_u32 m0, %[d], 0x1000\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o4], %[rq], 0 offen lds\n\t"
+      "s_add_u32 m0, %[d], 0x1400\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o5], %[rq], 0 offen lds\n\t"
+      "s_add_u32 m0, %[d], 0x1800\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o6], %[rq], 0 offen lds\n\t"
+      "s_add_u32 m0, %[d], 0x1c00\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o7], %[rq], 0 offen lds\n\t"
+      "s_mov_b32 m0, %[sv]"
+      : [sv] "=&s"(saved)
+      : [d] "s"(dst), [o0] "v"(lane16), [o1] "v"(lane16 + 1024u), [o2] "v"(lane16 + 2048u),
+        [o3] "v"(lane16 + 3072u), [o4] "v"(lane16 + 4096u), [o5] "v"(lane16 + 5120u),
+        [o6] "v"(lane16 + 6144u), [o7] "v"(lane16 + 7168u), [rq] "s"(rq)
+      : "memory", "scc");
 }
-
-// every lane issues exactly 10 loads per stage, so the count below is static
-__device__ __forceinline__ void wait_stage_ready() {
-  asm volatile("s_waitcnt vmcnt(20)" ::: "memory");  // the two younger stages may fly
-}
-
-
+constexpr int kLoadsQ = 8;
 
 struct WaveState {
   f4 acc[16];  // PV accumulators, tile T = 8h + 2*byte + hl
@@ -227,28 +287,29 @@ struct WaveState {
   float m_run, lsum;
 };
 
-// ---- per-block phases. The loop runs P(i) and Q(i+1) in one branch-free region so
-// the scheduler can overlap the MFMA chains, LDS reads and VALU work of two blocks.
 struct QKOut {
   f4 s1[2], s2[2];  // per 16-key tile: sum_e (n*sc)_e q_e and sum_j m_j qsum_j
 };
 
 // Phase Q: K rows of a staged block -> raw QK sums; per-key d, dmin into the tables.
+// Lane (r, g) feeds key kk(r) of tile t with sub-blocks 2g (low nibbles) and 2g+1
+// (high nibbles); its min codes m_2g, m_2g+1 form the A operand of the S2 product.
 __device__ __forceinline__ void phase_q(const Stage &st, WaveTab &T, const h8 *qb, h4 q2,
                                         float sl2, const Masks &MK, int lane, QKOut &o) {
   const int r = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int kk = 8 * (r >> 2) + 4 * t + (r & 3);
-    const int sl = row_slot(kk);
-    const u4 hd = st.k[sl];
-    const u4 q0 = st.k[sl + 1 + 2 * g], q1 = st.k[sl + 2 + 2 * g];
+    const int sw = swz(kk);
+    const u4 hd = st.k.hdr[kk];
+    const u4 q0 = st.k.nib[8 * kk + ((2 * g) ^ sw)];
+    const u4 q1 = st.k.nib[8 * kk + ((2 * g + 1) ^ sw)];
     // lanes of one key (g = 0..3) store the same values
     T.kd[kk] = h2f(hd.x & 0xFFFF) * sl2;
     T.kdm[kk] = h2f(hd.x >> 16) * sl2;
-    uint32_t sc0, sc1, mm;
-    scale_min(hd.y, hd.z, hd.w, 2 * g, sc0, mm);
-    scale_min(hd.y, hd.z, hd.w, 2 * g + 1, sc1, mm);
+    uint32_t sc0, sc1, m0, m1;
+    scale_min(hd.y, hd.z, hd.w, 2 * g, sc0, m0);
+    scale_min(hd.y, hd.z, hd.w, 2 * g + 1, sc1, m1);
     const _Float16 f0 = (_Float16)(float)sc0, f1 = (_Float16)((float)sc1 * 0.0625f);
     const _Float16 c0 = (_Float16)(-1024.0f * (float)sc0), c1 = (_Float16)(-64.0f * (float)sc1);
     const h2 SC0 = {f0, f0}, SC1 = {f1, f1}, C0 = {c0, c0}, C1 = {c1, c1};
@@ -275,13 +336,7 @@ __device__ __forceinline__ void phase_q(const Stage &st, WaveTab &T, const h8 *q
       s1 = mfma32(lo, qb[s], s1);
       s1 = mfma32(hi, qb[4 + s], s1);
     }
-    h4 a2;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      uint32_t scx, m;
-      scale_min(hd.y, hd.z, hd.w, (4 * g + jj) & 7, scx, m);
-      a2[jj] = g < 2 ? (_Float16)(float)m : (_Float16)0.0f;
-    }
+    const h4 a2 = {(_Float16)(float)m0, (_Float16)(float)m1, (_Float16)0.0f, (_Float16)0.0f};
     o.s1[t] = s1;
     o.s2[t] = mfma16(a2, q2, f4{0.f, 0.f, 0.f, 0.f});
   }
@@ -308,8 +363,9 @@ __device__ __forceinline__ float xmax32(float x) {  // max over lanes l and l ^ 
 }
 
 // Phase S: scores (log2 units) and the online softmax; p[k] for key 8g + k, head n % 8.
+// Keys at or past nvalid (only in a partial last block) are masked.
 __device__ __forceinline__ void phase_s(const QKOut &o, WaveState &S, const WaveTab &T,
-                                        int64_t key0, int64_t seq_k, int lane, float p[8]) {
+                                        int nvalid, int lane, float p[8]) {
   const int g = lane >> 4;
   float sc8[8];
 #pragma unroll
@@ -317,17 +373,21 @@ __device__ __forceinline__ void phase_s(const QKOut &o, WaveState &S, const Wave
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int kk = 8 * g + 4 * t + i;
-      const float v1 = o.s1[t][i] + ror8(o.s1[t][i]);
-      const float v2 = o.s2[t][i] + ror8(o.s2[t][i]);
-      float sc = T.kd[kk] * v1 - T.kdm[kk] * v2;
-      sc = fminf(fmaxf(sc, -kClampL2), kClampL2);
-      sc8[4 * t + i] = key0 + kk < seq_k ? sc : -INFINITY;
+      // this column's part (hi or lo of q); the other part sits 8 lanes away
+      const float part = T.kd[kk] * o.s1[t][i] - T.kdm[kk] * o.s2[t][i];
+      const float sc = part + ror8(part);
+      sc8[4 * t + i] = fminf(fmaxf(sc, -kClampL2), kClampL2);
     }
+  if (nvalid < kBlk) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (8 * g + k >= nvalid) sc8[k] = -INFINITY;
+  }
   float bm = sc8[0];
 #pragma unroll
   for (int k = 1; k < 8; ++k) bm = fmaxf(bm, sc8[k]);
   bm = xmax32(xmax16(bm));
-  if (__any(bm > S.m_run)) {
+  if (__any(bm > S.m_run + kLazy)) {
     const float m_new = fmaxf(S.m_run, bm);
     const float alpha = (S.m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(S.m_run - m_new);
     S.lsum *= alpha;
@@ -356,7 +416,7 @@ __device__ __forceinline__ void phase_p(const Stage &st, WaveState &S, WaveTab &
   // V header -> constant tables. Lane l handles key l % 32 and sub-blocks 4*(l/32)..+3.
   {
     const int kk = lane & 31, half = lane >> 5;
-    const u4 vh = st.v[row_slot(kk)];
+    const u4 vh = st.v.hdr[kk];
     int ed, em;
     float md, mm;
     split_scale(h2f(vh.x & 0xFFFF), ed, md);
@@ -373,15 +433,20 @@ __device__ __forceinline__ void phase_p(const Stage &st, WaveState &S, WaveTab &
       T.vm[j][kk] = (_Float16)__builtin_ldexpf((float)m, em);
     }
   }
-  // V rows, transposed: dword at qs byte 64h + 4n of keys 8g..8g+7
+  // V rows, transposed: dword n & 3 of nibble piece 4h + n / 4 of keys 8g..8g+7. Rows
+  // 2i and 2i+1 share their swizzle, so each pair is one ds_read2 (128 bytes apart).
   uint32_t vq[2][8];
-  const uint32_t *v32 = reinterpret_cast<const uint32_t *>(st.v);
+  const uint32_t *v32 = reinterpret_cast<const uint32_t *>(st.v.nib);
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int base = 4 * row_slot(8 * g + k) + 4 + n;
-    vq[0][k] = v32[base];
-    vq[1][k] = v32[base + 16];
-  }
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int k = 0; k < 8; k += 2) {
+      const int R = 8 * g + k;
+      const int piece = 4 * h + (n >> 2);
+      const int base = 4 * (8 * R + (piece ^ swz(R))) + (n & 3);
+      vq[h][k] = v32[base];
+      vq[h][k + 1] = v32[base + 32];
+    }
   // A: rows 0-7 p * mant(d), rows 8-15 p * mant(dmin)
   const float *mult = (n < 8) ? T.vmd : T.vmdm;
   h8 A;
@@ -427,257 +492,320 @@ __device__ __forceinline__ int tile_e(int T, int n) {
   return 64 * c + 32 * hl + 4 * (n & 7) + byte;
 }
 
+// Barrier of waves 0-3 only (the quantizing waves), through an LDS arrival counter, so
+// that waves 4-7 need not wait for the quantization. Every waiting wave is in this
+// workgroup, hence resident; the bound on the wait is only a safeguard.
+struct QuantWavesBarrier {
+  uint32_t *arrivals;
+  uint32_t target;
+  __device__ __forceinline__ void operator()() {
+    target += 4;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if ((threadIdx.x & 63) == 0)
+      __hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    for (int spin = 0; spin < (1 << 22); ++spin) {
+      if (__hip_atomic_load(arrivals, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target)
+        break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
+};
+
 __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   __shared__ Smem sm;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int kv = wave >> 1, wsub = wave & 1;
+  const int kv = wave & 1, wsub = wave >> 1;
   const int b = blockIdx.y, wg = blockIdx.x;
   const int n = lane & 15, g = lane >> 4;
 
-  // ---- fused append: workgroups past the main ones each quantize one new row and
-  // publish it dequantized for the combine step (which attends to the new key)
-  if (wg >= a.nwg_main) {
-    const int rowid = wg - a.nwg_main;  // 0: K kv0, 1: K kv1, 2: V kv0, 3: V kv1
-    const int p = rowid >> 1, kvr = rowid & 1;
-    const float *src = (p ? a.v_new : a.k_new) + ((int64_t)b * 2 + kvr) * 256;
-    uint8_t *dst = (p ? a.vw : a.kw) + b * a.rs_b + a.t_new * a.rs_t + kvr * a.rs_h;
-    float deq;
-    q4k_quantize_superblock_lanes(src[tid], dst, &sm.quant, tid, &deq);
-    a.dq[((int64_t)b * 4 + rowid) * 256 + tid] = deq;
-    return;
-  }
-
-  // ---- q operands (fp16 hi/lo, columns 0-7 hi, 8-15 lo) into LDS. q is staged in the
-  // (not yet used) table area with coalesced loads first.
-  {
-    float *qf = &sm.qsetup.qf[0][0];
-    float *qs = &sm.qsetup.qs[0][0];
-    const float4 *src4 = reinterpret_cast<const float4 *>(a.q + (int64_t)b * 16 * 256);
-    for (int x = tid; x < 16 * 256 / 4; x += kThreads) reinterpret_cast<float4 *>(qf)[x] = src4[x];
-    __syncthreads();
-    if (tid < 128) {
-      const float *qq = qf + (tid >> 3) * 256 + 32 * (tid & 7);
-      float sacc = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 32; ++e) sacc += qq[e];
-      qs[tid] = sacc;
-    }
-    __syncthreads();
-    constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-    for (int x = tid; x < 2 * 8 * 64; x += kThreads) {
-      const int ln = x & 63, st = (x >> 6) & 7, kvx = x >> 9;
-      const int nn = ln & 15, gg = ln >> 4;
-      const float *qrow = qf + (8 * kvx + (nn & 7)) * 256 + 64 * gg + 32 * (st >> 2) + 8 * (st & 3);
-      h8 val;
-#pragma unroll
-      for (int slot = 0; slot < 8; ++slot) {
-        const float qv = qrow[perm[slot]];
-        const _Float16 hi = (_Float16)qv;
-        val[slot] = (nn < 8) ? hi : (_Float16)(qv - (float)hi);
-      }
-      sm.qsetup.qb[kvx][st][ln] = val;
-    }
-    if (tid < 128) {
-      const int ln = tid & 63, kvx = tid >> 6;
-      const int nn = ln & 15, gg = ln >> 4;
-      h4 val = {0, 0, 0, 0};
-      if (gg < 2) {
-#pragma unroll
-        for (int slot = 0; slot < 4; ++slot) {
-          const float sv = qs[(8 * kvx + (nn & 7)) * 8 + 4 * gg + slot];
-          const _Float16 hi = (_Float16)sv;
-          val[slot] = (nn < 8) ? hi : (_Float16)(sv - (float)hi);
-        }
-      }
-      sm.qsetup.q2[kvx][ln] = val;
-    }
-  }
-  __syncthreads();
-  h8 qb[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) qb[s] = sm.qsetup.qb[kv][s][lane];
-  const h4 q2 = sm.qsetup.q2[kv][lane];
-  __syncthreads();  // the staging area becomes the wave tables
-
-  // ---- block range of this workgroup
+  // ---- blocks of this wave: b0 + wsub, b0 + wsub + 4, ... below b1
   const int b0 = wg * a.bpw;
   const int b1 = b0 + a.bpw < a.nblk ? b0 + a.bpw : a.nblk;
+  const int first = b0 + wsub;
+  const int nmine = first < b1 ? (b1 - first + 3) / 4 : 0;
+  const int kvu = __builtin_amdgcn_readfirstlane(kv);
+  const uint8_t *kbase = a.k + b * a.rs_b + kvu * a.rs_h;
+  const uint8_t *vbase = a.v + b * a.rs_b + kvu * a.rs_h;
+  const uint32_t rs_t = (uint32_t)a.rs_t;
+  // rows of keys [0, seq_k) of this head; loads past them return zeros (masked keys)
+  const uint32_t span = a.seq_k > 0 ? (uint32_t)(a.seq_k - 1) * rs_t + 144u : 0u;
+  const u4s rk = make_rsrc(kbase, span), rv = make_rsrc(vbase, span);
+  const LoadPlan P = make_plan(lane, rs_t);
+  const uint32_t bstep = 4u * kBlk * rs_t;  // byte distance between this wave's blocks
+  uint32_t boff = (uint32_t)first * kBlk * rs_t;
+
+  // Fused append: threads 0-255 (waves 0-3) of workgroups 0-3 quantize one new row each
+  // (further rows go round-robin when the grid is smaller) and publish it dequantized
+  // for the combine step, which attends to the new key. This runs while the first block
+  // streams in. The row is read before any staging load is issued, so the compiler's
+  // wait for it does not wait for the stage too.
+  const bool quant = a.k_new != nullptr && wg < 4 && tid < 256;
+  float xq = 0.0f;
+  if (quant) {
+    const int p = wg >> 1, kvr = wg & 1;
+    xq = (p ? a.v_new : a.k_new)[((int64_t)b * 2 + kvr) * 256 + tid];
+    asm volatile("" : "+v"(xq));
+  }
+  if (tid == 0) sm.run.t.quant.arrivals = 0u;
+
+  // ---- this wave's q rows, then its first block, into LDS. Every wave's q loads go out
+  // before any stage load (one barrier), so q returns ahead of the block data.
+  {
+    const u4s rq = make_rsrc(a.q + ((int64_t)b * 16 + 8 * kvu) * 256, 8 * 256 * 4);
+    issue_q(&sm.run.st1[wave], rq, 16u * lane);
+  }
+  __syncthreads();
+  if (nmine > 0) issue_stage(&sm.run.st0[wave], P, rk, rv, boff);
+
+  // QK B operands: lane (n, g) takes q of head n % 8, elements 64g + 32(s/4) + 8(s%4) +
+  // perm[slot], as the fp16 hi part (n < 8) or the lo remainder (n >= 8); S2 B operand:
+  // the sums of sub-blocks 2g and 2g+1 (elements 64g..64g+31, 64g+32..64g+63, in order).
+  // Built from the wave's own copy of q, so no workgroup barrier is needed.
+  h8 qb[8];
+  h4 q2 = {0, 0, 0, 0};
+  auto build_q = [&]() {
+    // q was issued before this wave's stage loads (12): once at most 12 loads are
+    // outstanding, q has landed
+    if (nmine > 0)
+      asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const float *qrow = reinterpret_cast<const float *>(&sm.run.st1[wave]) + (n & 7) * 256 + 64 * g;
+    constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    float qsum[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const float4 r0 = *reinterpret_cast<const float4 *>(qrow + 32 * (st >> 2) + 8 * (st & 3));
+      const float4 r1 = *reinterpret_cast<const float4 *>(qrow + 32 * (st >> 2) + 8 * (st & 3) + 4);
+      const float v8[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) qsum[st >> 2] += v8[k];
+#pragma unroll
+      for (int slot = 0; slot < 8; ++slot) {
+        const float qv = v8[perm[slot]];
+        const _Float16 hi = (_Float16)qv;
+        qb[st][slot] = (n < 8) ? hi : (_Float16)(qv - (float)hi);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const _Float16 hi = (_Float16)qsum[t];
+      q2[t] = (n < 8) ? hi : (_Float16)(qsum[t] - (float)hi);
+    }
+  };
+  static_assert(kLoadsPerStage == 12, "the vmcnt above counts one stage of loads");
+
+  if (quant) {
+    // the quantization delays this workgroup's blocks: it outranks the block loops of
+    // the waves sharing its SIMDs
+    __builtin_amdgcn_s_setprio(3);
+    QuantWavesBarrier bar{&sm.run.t.quant.arrivals, 0u};
+    for (int row = wg; row < 4; row += a.nwg_main) {
+      const int p = row >> 1, kvr = row & 1;  // 0: K kv0, 1: K kv1, 2: V kv0, 3: V kv1
+      if (row != wg) xq = (p ? a.v_new : a.k_new)[((int64_t)b * 2 + kvr) * 256 + tid];
+      uint8_t *dst = (p ? a.vw : a.kw) + b * a.rs_b + a.t_new * a.rs_t + kvr * a.rs_h;
+      float deq;
+      q4k_quantize_superblock_lanes(xq, dst, &sm.run.t.quant.scr, tid, &deq, bar);
+      bar.target += 12;  // the three barriers of that call
+      a.dq[((int64_t)b * 4 + row) * 256 + tid] = deq;
+    }
+    __builtin_amdgcn_s_setprio(0);
+  }
+  build_q();
+
   WaveState S;
 #pragma unroll
   for (int T2 = 0; T2 < 16; ++T2) S.acc[T2] = f4{0.f, 0.f, 0.f, 0.f};
   S.accm = f4{0.f, 0.f, 0.f, 0.f};
   S.m_run = -INFINITY;
   S.lsum = 0.0f;
-  WaveTab &T = sm.run.tab[wave];
-  const int kvu = __builtin_amdgcn_readfirstlane(kv);
-  const uint8_t *kbase = a.k + b * a.rs_b + kvu * a.rs_h;
-  const uint8_t *vbase = a.v + b * a.rs_b + kvu * a.rs_h;
-  const uint32_t rs_t = (uint32_t)a.rs_t;
-  // rows of keys [0, seq_k) of this head; loads past them return zeros (and are masked)
-  const uint32_t span = (uint32_t)(a.seq_k - 1) * rs_t + 144u;
-  const u4s rk = make_rsrc(kbase, span), rv = make_rsrc(vbase, span);
-  const LoadPlan P = make_plan(lane, rs_t);
-  const Masks MK = {vconst(0x000F000Fu), vconst(0x00F000F0u), vconst(0x64006400u)};
-  Stage *stages = reinterpret_cast<Stage *>(sm.run.stages) + wave * kStages;
-  // Three-stage pipeline: blocks first, first+2, first+4, ... of this wave are staged
-  // into LDS two ahead of the one being processed. Every iteration issues one stage
-  // (a block past the end reads out of range, which moves no data) so the wait count
-  // stays constant.
-  const int first = b0 + wsub;
-  const int nmine = first < b1 ? (b1 - first + 1) / 2 : 0;
-  auto soff_of = [&](int i) -> uint32_t {
-    return i < nmine ? (uint32_t)(first + 2 * i) * kBlk * rs_t : 0xFFFFFF00u;
-  };
+  WaveTab &T = sm.run.t.tab[wave];
+  Stage *const stg[2] = {&sm.run.st0[wave], &sm.run.st1[wave]};
   if (nmine > 0) {
-    issue_stage(&stages[0], P, rk, rv, soff_of(0));
-    issue_stage(&stages[1], P, rk, rv, soff_of(1));
-    issue_stage(&stages[2], P, rk, rv, soff_of(2));
-    asm volatile("s_waitcnt vmcnt(20)" ::: "memory");  // stage 0 landed
-    QKOut qo;
-    float pv[8];
-    phase_q(stages[0], T, qb, q2, a.sl2, MK, lane, qo);
-    phase_s(qo, S, T, (int64_t)first * kBlk, a.seq_k, lane, pv);
+    const Masks MK = {vconst(0x000F000Fu), vconst(0x00F000F0u), vconst(0x64006400u)};
     for (int i = 0; i < nmine; ++i) {
-      asm volatile("s_waitcnt vmcnt(10)" ::: "memory");  // stage i+1 landed
-      // P(i) and Q(i+1) form one straight-line region
-      phase_p(stages[i % kStages], S, T, pv, MK, lane);
-      phase_q(stages[(i + 1) % kStages], T, qb, q2, a.sl2, MK, lane, qo);
-      // stage i is refilled with block i+3 once its LDS reads have completed
+      // The two waves of a SIMD are issued oldest-first at equal priority, which lets
+      // the older one run ahead and leaves the younger to finish alone. Lowering the
+      // priority with each block done keeps the one behind first in line.
+      if (i == 0)
+        __builtin_amdgcn_s_setprio(2);
+      else if (i == 1)
+        __builtin_amdgcn_s_setprio(1);
+      else if (i == 2)
+        __builtin_amdgcn_s_setprio(0);
+      if (i + 1 < nmine) {  // block i+1 streams in while block i is processed
+        issue_stage(stg[(i + 1) & 1], P, rk, rv, boff + bstep);
+        asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      const Stage &st = *stg[i & 1];
+      QKOut qo;
+      float pv[8];
+      phase_q(st, T, qb, q2, a.sl2, MK, lane, qo);
+      phase_s(qo, S, T, (int)(a.seq_k - (int64_t)(first + 4 * i) * kBlk), lane, pv);
+      phase_p(st, S, T, pv, MK, lane);
+      // every LDS read of this stage has completed before it is refilled
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      issue_stage(&stages[i % kStages], P, rk, rv, soff_of(i + 3));
-      if (i + 1 < nmine) phase_s(qo, S, T, (int64_t)(first + 2 * (i + 1)) * kBlk, a.seq_k, lane, pv);
+      boff += bstep;
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_setprio(0);
   }
   // ---- per-wave reductions
   S.lsum += __shfl_xor(S.lsum, 16);
   S.lsum += __shfl_xor(S.lsum, 32);
-  __syncthreads();  // all waves done with sm.run before it is reused for merging
-  // min-term table per wave: accm rows 8 + 4(g-2) + i = head 4(g-2)+i, column j = n
+  // min term per [head][j] (accm rows 8 + 4(g-2) + i, column j = n) through this
+  // wave's own table area, then O'[head][e] = acc - cmin[head][e / 32] on lanes g < 2
+  // (rows 4g+i = head 4g+i)
+  float(*cmin)[8] = reinterpret_cast<float(*)[8]>(&T.kd[0]);
   if (g >= 2 && n < 8) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sm.merge.cmin[wave][4 * (g - 2) + i][n] = S.accm[i];
+    for (int i = 0; i < 4; ++i) cmin[4 * (g - 2) + i][n] = S.accm[i];
   }
-  __syncthreads();
-  // O'[head][e] = acc - cmin[head][e / 32] (lanes g < 2 hold rows 4g+i = head 4g+i)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   float o[16][4];
 #pragma unroll
   for (int T2 = 0; T2 < 16; ++T2) {
     const int e = tile_e(T2, n);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[T2][i] = S.acc[T2][i] - sm.merge.cmin[wave][(4 * g + i) & 7][e >> 5];
+    for (int i = 0; i < 4; ++i) o[T2][i] = S.acc[T2][i] - cmin[(4 * g + i) & 7][e >> 5];
   }
-  // ---- merge the two waves of each KV head through LDS
-  float mw = S.m_run;  // for head n % 8
-  float lw = S.lsum;
-  __syncthreads();
-  if (wsub == 1) {
-    if (g < 2) {
+  __syncthreads();  // every wave has left the loop: the st0 buffers become the merge area
+  // per-wave output in tile order: row head, index 16 T2 + n
+  if (g < 2) {
 #pragma unroll
-      for (int T2 = 0; T2 < 16; ++T2)
+    for (int T2 = 0; T2 < 16; ++T2)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sm.merge.o[kv][4 * g + i][tile_e(T2, n)] = o[T2][i];
-    }
-    if (g == 0 && n < 8) {
-      sm.merge.m[kv][n] = mw;
-      sm.merge.l[kv][n] = lw;
-    }
+      for (int i = 0; i < 4; ++i) sm.merge.o[wave][4 * g + i][16 * T2 + n] = o[T2][i];
+  }
+  if (g == 0 && n < 8) {
+    sm.merge.m[wave][n] = S.m_run;
+    sm.merge.l[wave][n] = S.lsum;
   }
   __syncthreads();
-  if (wsub == 0) {
-    const float mo = sm.merge.m[kv][n & 7], lo2 = sm.merge.l[kv][n & 7];
-    const float M = fmaxf(mw, mo);
-    const float fa = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-    const float fb = (mo == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mo - M);
-    float fai[4], fbi[4];
+  // ---- merge the four waves of each KV head into this workgroup's partial (tile order)
+  {
+    const int H = tid >> 5, hk = H >> 3, hh = H & 7, i0 = tid & 31;
+    float mw[4], M = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {  // o rows are head 4g+i: factors of heads 4(g&1)+i
-      fai[i] = __shfl(fa, 4 * (g & 1) + i);
-      fbi[i] = __shfl(fb, 4 * (g & 1) + i);
+    for (int s4 = 0; s4 < 4; ++s4) {
+      mw[s4] = sm.merge.m[2 * s4 + hk][hh];
+      M = fmaxf(M, mw[s4]);
     }
-    lw = lw * fa + lo2 * fb;
-    mw = M;
-    float *dst = a.part + ((int64_t)b * a.nwg_main + wg) * 16 * 258;
-    if (g < 2) {
+    float f[4], L = 0.0f;
 #pragma unroll
-      for (int T2 = 0; T2 < 16; ++T2) {
-        const int e = tile_e(T2, n);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          dst[(8 * kv + 4 * g + i) * 258 + e] =
-              o[T2][i] * fai[i] + sm.merge.o[kv][4 * g + i][e] * fbi[i];
-      }
+    for (int s4 = 0; s4 < 4; ++s4) {
+      f[s4] = (mw[s4] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw[s4] - M);
+      L += f[s4] * sm.merge.l[2 * s4 + hk][hh];
     }
-    if (g == 0 && n < 8) {
-      dst[(8 * kv + n) * 258 + 256] = mw;
-      dst[(8 * kv + n) * 258 + 257] = lw;
+    float *dst = a.part + ((int64_t)b * a.nwg_main + wg) * 16 * 258 + H * 258;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+      const int idx = i0 + 32 * x;
+      float acc = 0.0f;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) acc += f[s4] * sm.merge.o[2 * s4 + hk][hh][idx];
+      dst[idx] = acc;
+    }
+    if (i0 == 0) {
+      dst[256] = M;
+      dst[257] = L;
     }
   }
 }
 
-// out[b][h][e] = sum_w o_w 2^(m_w - M) / sum_w l_w 2^(m_w - M).
-// One workgroup per (head, 64-wide slice of e, batch); 4 thread groups split the partials.
-constexpr int kMaxPartials = 1024;
 // out[b][h][e] = (sum_w o_w 2^(m_w - M) + [new key]) / (sum_w l_w 2^(m_w - M) + [new key]).
-// One workgroup per (head, 64-wide slice of e, batch); 4 thread groups split the
-// partials. For a fused decode step the appended key enters here, from its exactly
-// dequantized K and V rows: score = clamp(q . k_new * scale), weight 2^(score - M).
+// One workgroup per (head, 32-entry slice of the tile-order row, batch): thread (ps, g4)
+// reads a float4 of entries and the (m, l) pair of every partial in slice ps of the
+// partials, all loads of a round issued before any is used. Slices keep their own
+// running max and merge through LDS. For a fused decode step the appended key enters
+// here, from its exactly dequantized K and V rows: score = clamp(q . k_new * scale),
+// weight 2^(score - M).
+constexpr int kMaxPartials = 1024;
+constexpr int kCombSlices = 32;  // partial slices (8 threads each)
+constexpr int kCombChunk = 8;    // partials per slice per round
 __global__ __launch_bounds__(256) void q4k_decode_combine_kernel(const float *part, int nwg,
                                                                  const float *q, const float *dq,
                                                                  float sl2, float *out) {
-  __shared__ float wts[kMaxPartials];
-  __shared__ float red[256];
-  __shared__ float acc4[4][64];
-  const int h = blockIdx.x >> 2, e0 = 64 * (blockIdx.x & 3), b = blockIdx.y;
-  const int tid = threadIdx.x;
+  __shared__ float dotp[4];
+  __shared__ float mx[kCombSlices], ls[kCombSlices];
+  __shared__ float4 accs[kCombSlices][8];
+  const int h = blockIdx.x >> 3, i0 = 32 * (blockIdx.x & 7), b = blockIdx.y;
+  const int tid = threadIdx.x, ps = tid >> 3, g4 = tid & 7;
   const float *P = part + (int64_t)b * nwg * 16 * 258 + h * 258;
-  // new key's score (log2 units), every thread gets it
-  float s_new = -INFINITY;
-  if (dq != nullptr) {
-    red[tid] = q[((int64_t)b * 16 + h) * 256 + tid] * dq[((int64_t)b * 4 + (h >> 3)) * 256 + tid];
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-      if (tid < o) red[tid] += red[tid + o];
-      __syncthreads();
+  // new key: q . k_new products (reduced below, after the partial loads are issued)
+  const float prod = dq != nullptr ? q[((int64_t)b * 16 + h) * 256 + tid] *
+                                         dq[((int64_t)b * 4 + (h >> 3)) * 256 + tid]
+                                   : 0.0f;
+  const int per = (nwg + kCombSlices - 1) / kCombSlices;
+  const int w0 = ps * per, w1 = w0 + per < nwg ? w0 + per : nwg;
+  float m_loc = -INFINITY, lacc = 0.0f;
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int w = w0; w < w1; w += kCombChunk) {
+    float2 mlv[kCombChunk];
+    float4 ov[kCombChunk];
+#pragma unroll
+    for (int x = 0; x < kCombChunk; ++x) {
+      const bool ok = w + x < w1;
+      const float *pw = P + (int64_t)(w + x) * 16 * 258;
+      mlv[x] = ok ? *reinterpret_cast<const float2 *>(pw + 256) : float2{-INFINITY, 0.0f};
+      ov[x] = ok ? *reinterpret_cast<const float4 *>(pw + i0 + 4 * g4) : float4{0.f, 0.f, 0.f, 0.f};
     }
-    s_new = fminf(fmaxf(red[0] * sl2, -kClampL2), kClampL2);
-    __syncthreads();
+    float mc = m_loc;
+#pragma unroll
+    for (int x = 0; x < kCombChunk; ++x) mc = fmaxf(mc, mlv[x].x);
+    if (mc != -INFINITY) {
+      const float r = (m_loc == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_loc - mc);
+      acc.x *= r;
+      acc.y *= r;
+      acc.z *= r;
+      acc.w *= r;
+      lacc *= r;
+#pragma unroll
+      for (int x = 0; x < kCombChunk; ++x) {
+        const float f = (mlv[x].x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mlv[x].x - mc);
+        acc.x += f * ov[x].x;
+        acc.y += f * ov[x].y;
+        acc.z += f * ov[x].z;
+        acc.w += f * ov[x].w;
+        lacc += f * mlv[x].y;
+      }
+      m_loc = mc;
+    }
   }
-  float M = s_new;
-  for (int w = tid; w < nwg; w += 256) M = fmaxf(M, P[(int64_t)w * 16 * 258 + 256]);
-  red[tid] = M;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if (tid < o) red[tid] = fmaxf(red[tid], red[tid + o]);
-    __syncthreads();
+  float d = prod;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) d += __shfl_xor(d, o, 64);
+  if ((tid & 63) == 0) dotp[tid >> 6] = d;
+  accs[ps][g4] = acc;
+  if (g4 == 0) {
+    mx[ps] = m_loc;
+    ls[ps] = lacc;
   }
-  M = red[0];
   __syncthreads();
-  float L = 0.0f;
-  for (int w = tid; w < nwg; w += 256) {
-    const float mw = P[(int64_t)w * 16 * 258 + 256];
-    const float f = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-    wts[w] = f;
-    L += f * P[(int64_t)w * 16 * 258 + 257];
-  }
-  red[tid] = L;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if (tid < o) red[tid] += red[tid + o];
-    __syncthreads();
-  }
-  const float f_new = (s_new == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_new - M);
-  L = red[0] + f_new;
-  const int e = tid & 63, r = tid >> 6;
-  float acc = 0.0f;
-#pragma unroll 8
-  for (int w = r; w < nwg; w += 4) acc += wts[w] * P[(int64_t)w * 16 * 258 + e0 + e];
-  acc4[r][e] = acc;
-  __syncthreads();
-  if (tid < 64) {
-    float sum = acc4[0][tid] + acc4[1][tid] + acc4[2][tid] + acc4[3][tid];
-    if (dq != nullptr) sum += f_new * dq[((int64_t)b * 4 + 2 + (h >> 3)) * 256 + e0 + tid];
-    out[((int64_t)b * 16 + h) * 256 + e0 + tid] = L > 0.0f ? sum / L : 0.0f;
+  if (tid < 32) {
+    const float s_new = dq != nullptr
+                            ? fminf(fmaxf((dotp[0] + dotp[1] + dotp[2] + dotp[3]) * sl2, -kClampL2), kClampL2)
+                            : -INFINITY;
+    float M = s_new;
+#pragma unroll
+    for (int x = 0; x < kCombSlices; ++x) M = fmaxf(M, mx[x]);
+    float sum = 0.0f, L = 0.0f;
+    const float *accf = reinterpret_cast<const float *>(&accs[0][0]);
+#pragma unroll
+    for (int x = 0; x < kCombSlices; ++x) {
+      const float f = (mx[x] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mx[x] - M);
+      sum += f * accf[32 * x + tid];
+      L += f * ls[x];
+    }
+    const int e = tile_e((i0 + tid) >> 4, (i0 + tid) & 15);
+    const float f_new = (s_new == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_new - M);
+    L += f_new;
+    if (dq != nullptr) sum += f_new * dq[((int64_t)b * 4 + 2 + (h >> 3)) * 256 + e];
+    out[((int64_t)b * 16 + h) * 256 + e] = L > 0.0f ? sum / L : 0.0f;
   }
 }
 
@@ -706,12 +834,14 @@ int launch_attend_mfma(const AttnArgs &a, const float *k_new, const float *v_new
   d.rs_h = a.rs.h;
   d.seq_k = fused ? a.seq_k - 1 : a.seq_k;  // old keys; the new one joins in the combine
   d.nblk = (int)((d.seq_k + kBlk - 1) / kBlk);
-  int nwg = (d.nblk + 1) / 2;
+  // 256 workgroups fill the CUs; each owns a multiple of 4 blocks (one or more per
+  // wave pair), so the split-K partials stay at <= 256 per batch row
+  int nwg = (d.nblk + 3) / 4;
   if (nwg > kMainWGs) nwg = kMainWGs;  // nwg <= kMaxPartials
   if (nwg < 1) nwg = 1;
   d.bpw = (d.nblk + nwg - 1) / nwg;
-  d.bpw = (d.bpw + 1) / 2 * 2;
-  if (d.bpw < 2) d.bpw = 2;
+  d.bpw = (d.bpw + 3) / 4 * 4;
+  if (d.bpw < 4) d.bpw = 4;
   nwg = (d.nblk + d.bpw - 1) / d.bpw;
   if (nwg < 1) nwg = 1;
   d.nwg_main = nwg;
@@ -725,10 +855,10 @@ int launch_attend_mfma(const AttnArgs &a, const float *k_new, const float *v_new
   if (rc) return rc;
   d.part = static_cast<float *>(ws.ptr);
   d.dq = d.part + part_floats;
-  hipLaunchKernelGGL(q4k_decode_kernel, dim3((unsigned)(nwg + (fused ? 4 : 0)), (unsigned)a.batch),
+  hipLaunchKernelGGL(q4k_decode_kernel, dim3((unsigned)nwg, (unsigned)a.batch),
                      dim3(kThreads), 0, s, d);
   PKV_HIP(hipGetLastError());
-  hipLaunchKernelGGL(q4k_decode_combine_kernel, dim3(64, (unsigned)a.batch), dim3(256), 0, s,
+  hipLaunchKernelGGL(q4k_decode_combine_kernel, dim3(16 * 8, (unsigned)a.batch), dim3(256), 0, s,
                      d.part, nwg, a.q, fused ? d.dq : nullptr, d.sl2, a.out);
   PKV_HIP(hipGetLastError());
   return PKV_OK;

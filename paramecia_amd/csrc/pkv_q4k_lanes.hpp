@@ -37,20 +37,41 @@ __device__ __forceinline__ float q4k_chain_sum_32(float *scr, int i, float term,
   return acc;
 }
 
+// All-reduce over the 32 lanes of each half-wave with DPP moves (within 16-lane rows)
+// and v_permlane16_swap (between the two rows of a half): a few VALU cycles per step
+// instead of an LDS round trip per __shfl_xor. Integer ops, so the order is immaterial.
+template <typename Op>
+__device__ __forceinline__ int32_t halfwave_allreduce(int32_t x, Op op) {
+  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x140, 0xF, 0xF, false));  // row_mirror
+  const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)x, (uint32_t)x, false, false);
+  const uint32_t r0 = r[0], r1 = r[1];  // scalar copies (see the decode kernel's note)
+  return op((int32_t)r0, (int32_t)r1);
+}
+
+// Barrier over the 256 threads of a quantization: by default the workgroup barrier.
+struct Q4kWorkgroupBarrier {
+  __device__ __forceinline__ void operator()() const { __syncthreads(); }
+};
+
 // x: this thread's element (tid = 32 * sub-block + element); blk: 144 output bytes.
-// Called by 256 threads of one workgroup together (contains __syncthreads()).
+// Called by 256 threads (four waves) together; `bar` synchronises exactly those four
+// waves (three times per call).
+template <typename Barrier = Q4kWorkgroupBarrier>
 static __device__ __forceinline__ void q4k_quantize_superblock_lanes(float x, uint8_t *blk,
                                                                    Q4kScratch *S, int tid,
-                                                                   float *deq = nullptr) {
+                                                                   float *deq = nullptr,
+                                                                   Barrier bar = Barrier()) {
 #pragma clang fp contract(off)
   const int j = tid >> 5, i = tid & 31;
   float *mine = S->scr + 32 * j;
-  int32_t kmin = total_key(x), kmax = kmin;
-#pragma unroll
-  for (int o = 16; o >= 1; o >>= 1) {
-    kmin = min(kmin, __shfl_xor(kmin, o, 32));
-    kmax = max(kmax, __shfl_xor(kmax, o, 32));
-  }
+  const auto imin = [](int32_t p, int32_t q) { return p < q ? p : q; };
+  const auto imax = [](int32_t p, int32_t q) { return p > q ? p : q; };
+  const auto iadd = [](int32_t p, int32_t q) { return p + q; };
+  const int32_t kmin = halfwave_allreduce(total_key(x), imin);
+  const int32_t kmax = halfwave_allreduce(total_key(x), imax);
   auto from_key = [](int32_t k) {
     return u2f((uint32_t)(k ^ (int32_t)(((uint32_t)(k >> 31)) >> 1)));
   };
@@ -67,9 +88,7 @@ static __device__ __forceinline__ void q4k_quantize_superblock_lanes(float x, ui
       const bool changed = (uint32_t)li != L;
       L = (uint32_t)li;
       const float sumlx = q4k_chain_sum_32(mine, i, (x - fmin) * (float)li, 0.0f);
-      int32_t l2 = li * li;
-#pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) l2 += __shfl_xor(l2, o, 32);
+      const int32_t l2 = halfwave_allreduce(li * li, iadd);
       scale = sumlx / (float)l2;
       const float sum = q4k_chain_sum_32(mine, i, x - scale * (float)L, -0.0f);
       fmin = sum / 32.0f;
@@ -86,7 +105,7 @@ static __device__ __forceinline__ void q4k_quantize_superblock_lanes(float x, ui
     S->red[0][j] = scale;
     S->red[1][j] = neg_min;
   }
-  __syncthreads();
+  bar();
   float max_scale = 0.0f, max_min = 0.0f;  // fold from +0, NaN-dropping maxNum
 #pragma unroll
   for (int jj = 0; jj < 8; ++jj) {
@@ -111,7 +130,7 @@ static __device__ __forceinline__ void q4k_quantize_superblock_lanes(float x, ui
   }
   if (i == 0) S->codes[j] = ls | (lm << 8);
   S->nib[tid] = (uint8_t)q;
-  __syncthreads();
+  bar();
   if (tid < 32) {  // qs[32c + l] = L_{2c}[l] | L_{2c+1}[l] << 4, 4 bytes per thread
     uint32_t w = 0;
 #pragma unroll
@@ -137,7 +156,7 @@ static __device__ __forceinline__ void q4k_quantize_superblock_lanes(float x, ui
     hd.w = (uint32_t)sc[8] | ((uint32_t)sc[9] << 8) | ((uint32_t)sc[10] << 16) | ((uint32_t)sc[11] << 24);
     *reinterpret_cast<uint4 *>(blk) = hd;
   }
-  __syncthreads();  // scratch is reused by the next call
+  bar();  // scratch is reused by the next call
 }
 
 }  // namespace pkv

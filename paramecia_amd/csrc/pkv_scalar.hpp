@@ -18,18 +18,18 @@ namespace pkv {
 PKV_HD uint32_t f2u(float x) { return __builtin_bit_cast(uint32_t, x); }
 PKV_HD float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
 
-// `v as i32` for an already-rounded v: saturating, NaN -> 0.
+// `v as i32` for an already-rounded v: saturating, NaN -> 0. Written as selects (no
+// branches) so that GPU code stays straight-line.
 PKV_HD int32_t rs_as_i32(float v) {
-  if (v != v) return 0;
-  if (v >= 2147483648.0f) return INT32_MAX;
-  if (v <= -2147483648.0f) return INT32_MIN;
-  return (int32_t)v;
+  const float c = v > -2147483648.0f ? (v < 2147483520.0f ? v : 2147483520.0f) : -2147483648.0f;
+  int32_t r = (int32_t)c;  // c is NaN-free only if v is; the selects below fix the rest
+  r = v >= 2147483648.0f ? INT32_MAX : r;
+  r = v != v ? 0 : r;
+  return r;
 }
 PKV_HD int32_t rs_as_i8(float v) {
-  if (v != v) return 0;
-  if (v >= 127.0f) return 127;
-  if (v <= -128.0f) return -128;
-  return (int32_t)v;
+  const float c = v > -128.0f ? (v < 127.0f ? v : 127.0f) : -128.0f;
+  return v != v ? 0 : (int32_t)c;
 }
 // candle's nearest_int: v.round() as i32.
 PKV_HD int32_t nearest_int(float v) { return rs_as_i32(__builtin_roundf(v)); }
@@ -41,54 +41,50 @@ PKV_HD int32_t total_key(float x) {
   return k;
 }
 // maxNum/minNum: a NaN operand loses; +0 beats -0 for max, -0 beats +0 for min.
+// Selects only (no branches).
 PKV_HD float fmax_rs(float a, float b) {
-  if (a != a) return b;
-  if (b != b) return a;
-  if (a > b) return a;
-  if (b > a) return b;
-  return (f2u(a) & 0x80000000u) ? b : a;
+  const float gt = a > b ? a : b;                        // a NaN -> b
+  const float eq = (f2u(a) & 0x80000000u) ? b : a;       // equal: prefer the non-negative
+  const float r = a == b ? eq : gt;
+  return a != a ? b : (b != b ? a : r);                   // a NaN -> b, else b NaN -> a
 }
 PKV_HD float fmin_rs(float a, float b) {
-  if (a != a) return b;
-  if (b != b) return a;
-  if (a < b) return a;
-  if (b < a) return b;
-  return (f2u(a) & 0x80000000u) ? a : b;
+  const float lt = a < b ? a : b;
+  const float eq = (f2u(a) & 0x80000000u) ? a : b;       // equal: prefer the negative
+  const float r = a == b ? eq : lt;
+  return a != a ? b : (b != b ? a : r);
 }
 
-// half::f16::from_f32 (round to nearest even, overflow -> inf, quiet NaN).
+// half::f16::from_f32 (round to nearest even, overflow -> inf, quiet NaN), computed
+// as selects over the normal, subnormal and special cases (no branches).
 PKV_HD uint16_t f32_to_f16(float value) {
-  uint32_t x = f2u(value);
-  uint32_t sign = x & 0x80000000u, exp = x & 0x7F800000u, man = x & 0x007FFFFFu;
-  if (exp == 0x7F800000u) {
-    uint32_t nan_bit = (man == 0) ? 0u : 0x0200u;
-    return (uint16_t)((sign >> 16) | 0x7C00u | nan_bit | (man >> 13));
-  }
-  uint32_t half_sign = sign >> 16;
-  int32_t half_exp = ((int32_t)(exp >> 23)) - 127 + 15;
-  if (half_exp >= 0x1F) return (uint16_t)(half_sign | 0x7C00u);
-  if (half_exp <= 0) {
-    if (14 - half_exp > 24) return (uint16_t)half_sign;
-    uint32_t m = man | 0x00800000u;
-    uint32_t shift = (uint32_t)(14 - half_exp);
-    uint32_t half_man = m >> shift;
-    uint32_t round_bit = 1u << (shift - 1);
-    if ((m & round_bit) != 0 && (m & (3u * round_bit - 1u)) != 0) half_man++;
-    return (uint16_t)(half_sign | half_man);
-  }
-  uint32_t out = half_sign | (((uint32_t)half_exp) << 10) | (man >> 13);
-  if ((x & 0x00001000u) != 0 && (x & 0x00002FFFu) != 0) out += 1u;
-  return (uint16_t)out;
+  const uint32_t x = f2u(value);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t exp = (x >> 23) & 0xFFu, man = x & 0x007FFFFFu;
+  const int32_t he = (int32_t)exp - 112;  // biased f16 exponent
+  // normal: truncate, then round to nearest even on the 13 dropped bits (a carry may
+  // ripple into the exponent, up to infinity)
+  const uint32_t nrm = (((uint32_t)(he & 0x1F) << 10) | (man >> 13)) +
+                       (((x & 0x1000u) != 0u && (x & 0x2FFFu) != 0u) ? 1u : 0u);
+  // subnormal (he <= 0): shift the implicit-1 mantissa right by 14 - he, same rounding
+  const int32_t sh_i = 14 - he;
+  const uint32_t sh = (uint32_t)(sh_i < 1 ? 1 : (sh_i > 31 ? 31 : sh_i));
+  const uint32_t m = man | 0x00800000u;
+  const uint32_t rb = 1u << (sh - 1u);
+  const uint32_t sub = (m >> sh) + (((m & rb) != 0u && (m & (3u * rb - 1u)) != 0u) ? 1u : 0u);
+  const uint32_t infnan = 0x7C00u | (man != 0u ? 0x0200u : 0u) | (man >> 13);
+  uint32_t out = he <= 0 ? (sh_i > 24 ? 0u : sub) : nrm;
+  out = he >= 0x1F ? 0x7C00u : out;
+  out = exp == 0xFFu ? infnan : out;
+  return (uint16_t)(sign | out);
 }
 PKV_HD float f16_to_f32(uint16_t h) {
-  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
-  uint32_t exp = (h >> 10) & 0x1Fu, man = h & 0x3FFu;
-  if (exp == 0) {
-    float v = (float)man * 5.9604644775390625e-08f;  // exact: man * 2^-24
-    return sign ? -v : v;
-  }
-  if (exp == 0x1F) return u2f(sign | 0x7F800000u | (man << 13));
-  return u2f(sign | ((exp + 112u) << 23) | (man << 13));
+  const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1Fu, man = h & 0x3FFu;
+  const float sub = u2f(sign | f2u((float)man * 5.9604644775390625e-08f));  // exact: man * 2^-24
+  const float spec = u2f(sign | 0x7F800000u | (man << 13));
+  const float nrm = u2f(sign | ((exp + 112u) << 23) | (man << 13));
+  return exp == 0u ? sub : (exp == 0x1Fu ? spec : nrm);
 }
 // half::bf16::from_f32 (round to nearest even, NaN keeps a quiet bit).
 PKV_HD uint16_t f32_to_bf16(float value) {
