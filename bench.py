@@ -11,6 +11,11 @@ Prints one JSON line. `value` is microseconds per 12-layer decode step (lower is
 better); `roofline` prices the dominant kernel against MI355X's 8 TB/s HBM peak;
 `cpu_baseline` times the CPU oracle's faithful restatement of the reference path
 (dequantize-all + repeat_kv + SDPA, qwen3_next.rs:2470-2605) on the host cores.
+
+`--config N` measures another workload of the path instead (one JSON line each;
+`--config all` prints all five): 1 Q8_0 decode over 4097 keys, 2 a 512-token Q4K
+prefill chunk over 16896 keys, 4 PrefixCache restore of 12 full + 36 linear layers plus
+a 1024-token suffix, 5 a 16-sequence batched decode step over 12 layers.
 """
 from __future__ import annotations
 
@@ -25,42 +30,61 @@ sys.path.insert(0, ROOT)
 
 METRIC = "Q4K decode-attn µs/step @128k ctx, 12 layers; achieved HBM GB/s & % of peak"
 HBM_PEAK_GBS = 8000.0
+FP16_DENSE_TFLOPS = 2500.0
 Q4K_ROW = 144
+Q8_ROW = 272
 
 
-def layer_bytes(keys: int) -> int:
+def layer_bytes(keys: int, row: int = Q4K_ROW) -> int:
     """Algorithmic HBM bytes of one layer's decode step: the K and V rows of every key
-    (2 KV heads x 144 B each), q in and out (16 x 256 f32 each), the new token's f32
+    (2 KV heads x `row` B each), q in and out (16 x 256 f32 each), the new token's f32
     k/v read and its 4 packed rows written."""
-    return keys * 2 * 2 * Q4K_ROW + 2 * 16 * 256 * 4 + 2 * 2 * 256 * 4 + 4 * Q4K_ROW
+    return keys * 2 * 2 * row + 2 * 16 * 256 * 4 + 2 * 2 * 256 * 4 + 4 * row
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cached", type=int, default=131072)
-    ap.add_argument("--layers", type=int, default=12)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=0)
-    ap.add_argument("--calib-copy-mib", type=int, default=0,
-                    help="after the timed runs, launch a plain elementwise copy of this many MiB "
-                         "(read N, write N) 3 times: the reference kernel that scales rocprofv3's "
-                         "FETCH_SIZE / WRITE_SIZE counters to bytes")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print("bench.py measures the single-GPU path only: every GPU box in this build has "
-              "one MI355X, and the KV-cache path needs no collectives (see DESIGN.md for how "
-              "it would shard). Run with --gpus 1.", file=sys.stderr)
-        return 2
+def cpu_model() -> str:
+    try:
+        return [l for l in open("/proc/cpuinfo") if l.startswith("model name")][0].split(":")[1].strip()
+    except Exception:
+        return "unknown"
 
+
+def event_time(torch, fn, steps, warmup):
+    """Milliseconds per call of fn: HIP events around `steps` calls after `warmup`."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def graph_time(torch, fn, steps, warmup):
+    """Capture fn once in a HIP graph (after an eager warm-up on the capture stream, which
+    sizes every workspace) and time its replays."""
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    return event_time(torch, graph.replay, steps, warmup)
+
+
+# ------------------------------------------------------------------ config 3 (headline)
+def run_config3(args):
     import torch
     import paramecia_amd as pk
     from paramecia_amd import workloads as W
 
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
     L, S = args.layers, args.cached
     cap = S + 1
     Q = pk.KvCacheQuantization.Q4K
@@ -100,40 +124,12 @@ def main() -> int:
             if events is not None:
                 events[l][1].record()
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-
     # eager: 12 ctypes launches per step from Python (host overhead included)
-    start.record()
-    for _ in range(args.steps):
-        step()
-    end.record()
-    torch.cuda.synchronize()
-    eager_ms = start.elapsed_time(end) / args.steps
-
+    eager_ms = event_time(torch, step, args.steps, args.warmup)
     # HIP graph of one 12-layer step, replayed (the serving-loop form)
-    graph = torch.cuda.CUDAGraph()
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        step()  # warm the workspace on the capture stream
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph, stream=side):
-            step()
-    torch.cuda.current_stream().wait_stream(side)
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(args.steps):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    ms = graph_time(torch, step, args.steps, args.warmup)
 
-    # per-launch duration of the layer kernel(s): the GPU is kept busy by a sleep kernel
+    # per-launch duration of the layer's kernels: the GPU is kept busy by a sleep kernel
     # while the host enqueues, so each event pair brackets device time only
     ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(L)] for _ in range(args.steps)]
@@ -172,7 +168,7 @@ def main() -> int:
         "step_hbm_gbs": round(step_bytes / (ms * 1e-3) / 1e9, 1),
         "step_pct_of_peak": round(100.0 * step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
         "roofline": {
-            "kernel": "pkv_append_attend (one layer: append + dequant-fused attention)",
+            "kernel": "pkv_append_attend (one layer: decode kernel + combine kernel)",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
             "bytes_per_launch": layer_bytes(keys),
@@ -181,7 +177,6 @@ def main() -> int:
         },
         "append_tokens_per_s": round(L * S / fill_s, 1),
     }
-
     if args.calib_copy_mib > 0:
         n = args.calib_copy_mib * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device=dev)
@@ -191,23 +186,21 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(caches[0], kn[0], vn[0], q[0], S, args.cpu_threads)
-    print(json.dumps(result), flush=True)
-    return 0
+        result["cpu_baseline"] = cpu_baseline_decode(
+            caches[0], kn[0], vn[0], q[0], S, args.cpu_threads, 3, 4, W.N_FULL)
+    return result
 
 
-def cpu_baseline(cache, kn, vn, q, S, threads):
+def cpu_baseline_decode(cache, kn, vn, q, S, threads, config, quant, layers):
     """The oracle's faithful restatement of the reference CPU path (CPU quantize of the new
     token, dequantize the whole cache, permute, repeat_kv, transposed-K copy, matmul,
-    clamp, softmax, matmul) on one layer, extrapolated to the 12-layer step."""
-    import numpy as np
-    import torch
+    clamp, softmax, matmul) on one layer, extrapolated to `layers` layers."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
     from paramecia_amd import workloads as W
 
-    nthreads = threads if threads > 0 else (os.cpu_count() or 1)
-    c = orc.Cache(orc.Q4K, 1, W.NUM_KV_HEADS, W.HEAD_DIM, S + 1)
+    nthreads = threads if threads > 0 else min(os.cpu_count() or 1, 16)
+    c = orc.Cache(quant, 1, W.NUM_KV_HEADS, W.HEAD_DIM, S + 1)
     cache.truncate(S)
     kb, vb = cache.raw_bytes()
     c.load_bytes(kb.cpu().numpy(), vb.cpu().numpy(), S)
@@ -216,16 +209,257 @@ def cpu_baseline(cache, kn, vn, q, S, threads):
     assert c.append_at(knp, vnp, S) == 0
     c.attend(qnp, W.SCALE, S, True, mode="faithful", threads=nthreads)
     dt = time.perf_counter() - t0
-    try:
-        model = [l for l in open("/proc/cpuinfo") if l.startswith("model name")][0].split(":")[1].strip()
-    except Exception:
-        model = "unknown"
     return {
-        "value": round(dt * W.N_FULL * 1e6, 1), "unit": "us/step", "cores": nthreads,
+        "value": round(dt * layers * 1e6, 1), "unit": "us/step", "cores": nthreads,
         "kind": "port",
-        "sample": f"1 of 12 layers, one decode step (append 1 token + attend {S + 1} keys) "
-                  f"timed once and multiplied by 12; {nthreads} OpenMP threads on {model}",
+        "sample": f"config {config}: 1 of {layers} layers, one decode step (append 1 token + "
+                  f"attend {S + 1} keys) timed once and multiplied by {layers}; {nthreads} "
+                  f"OpenMP threads on {cpu_model()}",
     }
+
+
+def base_result(config, metric, value, unit, hib, ms, args, workload, extra):
+    r = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps,
+         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": hib,
+         "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+         "data": "synthetic (seeded Philox N(0,1))",
+         "config": {"workload": workload, "index": config}}
+    r.update(extra)
+    return r
+
+
+# ------------------------------------------------------------------ config 1
+def run_config1(args):
+    """Q8_0, one layer, 4096 cached tokens: append one token and attend 4097 keys."""
+    import torch
+    import paramecia_amd as pk
+    from paramecia_amd import workloads as W
+
+    S = 4096
+    c = pk.PreallocatedQuantizedKvCache(1, 2, S + 1, 256, pk.KvCacheQuantization.Q8_0)
+    kb = torch.empty((1, 2, S, 256), device="cuda")
+    vb = torch.empty_like(kb)
+    pk.fill_normal(kb, W.SEED, W.stream_id(1, W.T_PREFILL_K))
+    pk.fill_normal(vb, W.SEED, W.stream_id(1, W.T_PREFILL_V))
+    c.append_quantized(kb, vb)
+    del kb, vb
+    q = torch.empty((1, 1, 16, 256), device="cuda")
+    kn = torch.empty((1, 2, 1, 256), device="cuda")
+    vn = torch.empty_like(kn)
+    pk.fill_normal(q, W.SEED, W.stream_id(1, W.T_Q))
+    pk.fill_normal(kn, W.SEED, W.stream_id(1, W.T_NEW_K))
+    pk.fill_normal(vn, W.SEED, W.stream_id(1, W.T_NEW_V))
+    step = lambda: c.append_attend(kn, vn, q, W.SCALE, offset=S)
+    ms = graph_time(torch, step, args.steps, args.warmup)
+    nbytes = layer_bytes(S + 1, Q8_ROW)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    r = base_result(1, "Q8_0 decode-attn µs/step @4097 keys, 1 layer", round(ms * 1000, 2),
+                    "us/step", False, ms, args,
+                    "config1: Q8_0 cache with 4096 tokens; step = quantize-append 1 token + "
+                    "attend 4097 keys (16 q heads, 2 kv heads, head_dim 256)",
+                    {"roofline": {"kernel": "pkv_append_attend (Q8_0)", "bound": "hbm",
+                                  "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": nbytes,
+                                  "traffic": None}})
+    if not args.no_cpu_baseline:
+        r["cpu_baseline"] = cpu_baseline_decode(c, kn, vn, q, S, args.cpu_threads, 1, 3, 1)
+    return r
+
+
+# ------------------------------------------------------------------ config 2
+def run_config2(args):
+    """Q4K, capacity 32768, 16384 cached: append a 512-token chunk and run its causal
+    attention over 16896 keys (q_offset 16384), as FullAttention::forward does for a
+    prefill chunk."""
+    import torch
+    import paramecia_amd as pk
+    from paramecia_amd import workloads as W
+
+    S, C, cap = 16384, 512, 32768
+    c = pk.PreallocatedQuantizedKvCache(1, 2, cap, 256, pk.KvCacheQuantization.Q4K)
+    kb = torch.empty((1, 2, S, 256), device="cuda")
+    vb = torch.empty_like(kb)
+    pk.fill_normal(kb, W.SEED, W.stream_id(2, W.T_PREFILL_K))
+    pk.fill_normal(vb, W.SEED, W.stream_id(2, W.T_PREFILL_V))
+    c.append_quantized(kb, vb)
+    del kb, vb
+    kc = torch.empty((1, 2, C, 256), device="cuda")
+    vc = torch.empty_like(kc)
+    qc = torch.empty((1, C, 16, 256), device="cuda")
+    pk.fill_normal(kc, W.SEED, W.stream_id(2, W.T_CHUNK_K))
+    pk.fill_normal(vc, W.SEED, W.stream_id(2, W.T_CHUNK_V))
+    pk.fill_normal(qc, W.SEED, W.stream_id(2, W.T_CHUNK_Q))
+
+    def step():
+        c.append_quantized(kc, vc, offset=S)
+        return c.attend(qc, W.SCALE, S, causal=True)
+
+    ms = graph_time(torch, step, args.steps, args.warmup)
+    flops = 16 * (C * S + C * (C + 1) // 2) * 256 * 2 * 2
+    tf = flops / (ms * 1e-3) / 1e12
+    return base_result(2, "Q4K prefill chunk µs (512 queries x 16896 keys, causal)",
+                       round(ms * 1000, 2), "us/chunk", False, ms, args,
+                       "config2: Q4K cache with 16384 tokens; step = quantize-append a 512-token "
+                       "chunk + causal attention of its 512 queries over 16896 keys",
+                       {"roofline": {"kernel": "pkv_append + pkv_attend (prefill chunk)",
+                                     "bound": "mfma", "achieved": round(tf, 2),
+                                     "peak": FP16_DENSE_TFLOPS, "unit": "TFLOP/s",
+                                     "frac": round(tf / FP16_DENSE_TFLOPS, 5), "flops": flops,
+                                     "traffic": None}})
+
+
+# ------------------------------------------------------------------ config 4
+def run_config4(args):
+    """PrefixCache restore: 12 full-attention layers x 65536 Q4K tokens and 36 Gated-
+    DeltaNet states in one batched copy, then a 1024-token suffix appended per layer."""
+    import torch
+    import paramecia_amd as pk
+    from paramecia_amd import workloads as W
+
+    S, SUF, cap = 65536, 1024, 131072
+    m = pk.ModelKvState(W.N_LAYERS, W.FULL_INTERVAL, W.NUM_HEADS, W.NUM_KV_HEADS, W.HEAD_DIM, cap)
+    kb = torch.empty((1, 2, S, 256), device="cuda")
+    vb = torch.empty_like(kb)
+    for i, l in enumerate(m.layers):
+        if isinstance(l, pk.FullAttentionKv):
+            pk.fill_normal(kb, W.SEED, W.stream_id(4, W.T_PREFILL_K, i))
+            pk.fill_normal(vb, W.SEED, W.stream_id(4, W.T_PREFILL_V, i))
+            l._ensure(1).append_quantized(kb, vb)
+        else:
+            ssm = torch.empty((1, W.DN_HEADS, W.DN_DK, W.DN_DV), device="cuda")
+            conv = torch.empty((1, W.DN_CONV_DIM, W.DN_CONV_K - 1), device="cuda")
+            gate = torch.empty((1, W.DN_HEADS), device="cuda")
+            pk.fill_normal(ssm, W.SEED, W.stream_id(4, W.T_SSM, i), 0.02)
+            pk.fill_normal(conv, W.SEED, W.stream_id(4, W.T_CONV, i))
+            pk.fill_normal(gate, W.SEED, W.stream_id(4, W.T_GATE, i))
+            l.recurrent_state = pk.RecurrentState(ssm, conv, gate)
+    del kb, vb
+    prefix = m.save_prefix_cache(list(range(S)))
+    ks = torch.empty((1, 2, SUF, 256), device="cuda")
+    vs = torch.empty_like(ks)
+    pk.fill_normal(ks, W.SEED, W.stream_id(4, W.T_SUFFIX_K))
+    pk.fill_normal(vs, W.SEED, W.stream_id(4, W.T_SUFFIX_V))
+    full = m.full_layers()
+
+    def restore():
+        m.restore_prefix_cache(prefix)
+
+    def step():
+        restore()
+        for l in full:
+            l.quantized_cache.append_quantized(ks, vs, offset=S)
+
+    ms_restore = event_time(torch, restore, args.steps, args.warmup)
+    ms = event_time(torch, step, args.steps, args.warmup)
+    full_bytes = len(full) * S * 2 * 2 * Q4K_ROW
+    lin_bytes = (W.N_LAYERS - len(full)) * 4 * (W.DN_HEADS * W.DN_DK * W.DN_DV +
+                                                W.DN_CONV_DIM * (W.DN_CONV_K - 1) + W.DN_HEADS)
+    moved = 2 * (full_bytes + lin_bytes)  # read + write
+    gbs = moved / (ms_restore * 1e-3) / 1e9
+    return base_result(4, "PrefixCache restore GB/s (12 x 65536-token Q4K layers + 36 DeltaNet "
+                          "states) and restore + 1024-token suffix µs",
+                       round(gbs, 1), "GB/s", True, ms, args,
+                       "config4: restore_prefix_cache of 12 full layers (65536 Q4K tokens each) "
+                       "and 36 linear layers in one batched copy; then append a 1024-token "
+                       "suffix to every full layer",
+                       {"restore_us": round(ms_restore * 1000, 2),
+                        "restore_plus_suffix_us": round(ms * 1000, 2),
+                        "restored_bytes": full_bytes + lin_bytes,
+                        "roofline": {"kernel": "copy_segments (restore)", "bound": "hbm",
+                                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                     "bytes_per_launch": moved, "traffic": None}})
+
+
+# ------------------------------------------------------------------ config 5
+def run_config5(args):
+    """16 independent sequences (cached lengths seeded in [1024, 65536], 5 outlier
+    channels x20 in K and V), 12 layers: one decode step appends a token to and attends
+    over every sequence of every layer."""
+    import torch
+    import paramecia_amd as pk
+    from paramecia_amd import workloads as W
+
+    lens = W.c5_lengths()
+    chans = W.c5_channels()
+    L, N = W.N_FULL, W.C5_SEQS
+    caches = [[None] * N for _ in range(L)]
+    for l in range(L):
+        for i, S in enumerate(lens):
+            c = pk.PreallocatedQuantizedKvCache(1, 2, S + 1, 256, pk.KvCacheQuantization.Q4K)
+            kb = torch.empty((1, 2, S, 256), device="cuda")
+            vb = torch.empty_like(kb)
+            pk.fill_normal(kb, W.SEED, W.stream_id(5, W.T_PREFILL_K, l, i))
+            pk.fill_normal(vb, W.SEED, W.stream_id(5, W.T_PREFILL_V, l, i))
+            pk.scale_channels(kb, chans, W.C5_OUTLIER_SCALE)
+            pk.scale_channels(vb, chans, W.C5_OUTLIER_SCALE)
+            c.append_quantized(kb, vb)
+            caches[l][i] = c
+            del kb, vb
+    q = torch.empty((L, N, 16, 256), device="cuda")
+    kn = torch.empty((L, N, 2, 256), device="cuda")
+    vn = torch.empty_like(kn)
+    for l in range(L):
+        pk.fill_normal(q[l], W.SEED, W.stream_id(5, W.T_Q, l))
+        pk.fill_normal(kn[l], W.SEED, W.stream_id(5, W.T_NEW_K, l))
+        pk.fill_normal(vn[l], W.SEED, W.stream_id(5, W.T_NEW_V, l))
+        pk.scale_channels(kn[l], chans, W.C5_OUTLIER_SCALE)
+        pk.scale_channels(vn[l], chans, W.C5_OUTLIER_SCALE)
+
+    def step():
+        for l in range(L):
+            for i, S in enumerate(lens):
+                caches[l][i].truncate(S)  # rewind the previous step's token
+            pk.append_attend_batched(caches[l], kn[l], vn[l], q[l], W.SCALE)
+
+    ms = graph_time(torch, step, args.steps, args.warmup)
+    nbytes = L * sum(layer_bytes(S + 1) for S in lens)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return base_result(5, "batched decode µs/step (16 sequences, 12 layers, Q4K)",
+                       round(ms * 1000, 2), "us/step", False, ms, args,
+                       "config5: 16 batch-1 Q4K caches per layer (seeded lengths 1024-65536, "
+                       "5 outlier channels x20), 12 layers; step = append 1 token + attend, "
+                       "every sequence of every layer",
+                       {"sequence_lengths": lens,
+                        "roofline": {"kernel": "pkv_append_attend_batched", "bound": "hbm",
+                                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                     "bytes_per_step": nbytes, "traffic": None}})
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="3", help="1, 2, 3 (headline, default), 4, 5 or all")
+    ap.add_argument("--cached", type=int, default=131072, help="config 3: cached tokens")
+    ap.add_argument("--layers", type=int, default=12, help="config 3: layers")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="config 3: after the timed runs, launch a plain elementwise copy of "
+                         "this many MiB (read N, write N) 3 times: the reference kernel that "
+                         "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures the single-GPU path only: every GPU box in this build has "
+              "one MI355X, and the KV-cache path needs no collectives (see DESIGN.md for how "
+              "it would shard). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+    torch.cuda.set_device(torch.device("cuda:0"))
+    runners = {"1": run_config1, "2": run_config2, "3": run_config3, "4": run_config4,
+               "5": run_config5}
+    which = list(runners) if args.config == "all" else [args.config]
+    for cfg in which:
+        if cfg not in runners:
+            print(f"unknown config {cfg}", file=sys.stderr)
+            return 2
+        print(json.dumps(runners[cfg](args)), flush=True)
+        torch.cuda.empty_cache()
+    return 0
 
 
 if __name__ == "__main__":
