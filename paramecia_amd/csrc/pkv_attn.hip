@@ -17,6 +17,8 @@ namespace pkv {
 int launch_attend_mfma(const AttnArgs &a, const float *k_new, const float *v_new,
                        uint8_t *kc, uint8_t *vc, int64_t t_new, Workspace &ws,
                        hipStream_t s);
+// Prefill chunk (l > 1) over Q4K rows of the Qwen3-Next shape (pkv_prefill_mfma.hip).
+int launch_prefill_mfma(const AttnArgs &a, Workspace &ws, hipStream_t s);
 
 namespace {
 
@@ -213,6 +215,8 @@ int launch_attend(const AttnArgs &a, Workspace &ws, hipStream_t s) {
   int rc = check_attn(a);
   if (rc) return rc;
   rc = launch_attend_mfma(a, nullptr, nullptr, nullptr, nullptr, -1, ws, s);
+  if (rc != PKV_ERR_UNSUPPORTED) return rc;
+  rc = launch_prefill_mfma(a, ws, s);
   if (rc != PKV_ERR_UNSUPPORTED) return rc;
   return launch_attend_generic(a, ws, s);
 }

@@ -25,26 +25,16 @@
 //   in, scores clamped to [-100, 100] (in natural-log units) as the reference does.
 //   The running max is raised only when a block exceeds it by 2^8 (p <= 256 is exact
 //   enough in fp16 and the f32 sums), so the accumulators are rarely rescaled.
-#include "pkv_internal.hpp"
-#include "pkv_scalar.hpp"
+#include "pkv_mfma_common.hpp"
 #include "pkv_q4k_lanes.hpp"
 
 namespace pkv {
 
 namespace {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;  // two waves per SIMD
-constexpr int kBlk = 32;
 constexpr int kMainWGs = 256;
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kClampL2 = 100.0f * 1.4426950408889634f;  // +-100 nats in log2 units
 constexpr float kLazy = 8.0f;  // log2 headroom of the running max before a rescale
 
 struct DecodeArgs {
@@ -60,78 +50,6 @@ struct DecodeArgs {
   float *part;  // [B][nwg_main][16][258]
   float *dq;    // [B][4][256] dequantized new rows (K kv0, K kv1, V kv0, V kv1)
 };
-
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
-  return (x & m) | o;
-}
-// Constants kept in VGPRs so that (x & mask) | magic is a single v_and_or_b32 (gfx9
-// VOP3 encodings take no literal operands).
-__device__ __forceinline__ uint32_t vconst(uint32_t c) {
-  uint32_t r;
-  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
-  return r;
-}
-struct Masks {
-  uint32_t lo, hi, magic;
-};
-__device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
-__device__ __forceinline__ uint32_t as_u(h2 x) { return __builtin_bit_cast(uint32_t, x); }
-__device__ __forceinline__ h2 pk_fma(h2 a, h2 b, h2 c) { return __builtin_elementwise_fma(a, b, c); }
-__device__ __forceinline__ float ror8(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x128,
-                                                            0xF, 0xF, false));
-}
-__device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
-}
-
-// 6-bit scale code and min code of sub-block j from the 12 packed bytes (s0 = bytes
-// 0-3, s1 = 4-7, s2 = 8-11), get_scale_min_k4.
-__device__ __forceinline__ void scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j,
-                                          uint32_t &sc, uint32_t &m) {
-  const int sh = 8 * (j & 3);
-  const uint32_t b_lo = (s0 >> sh) & 0xFF;   // byte j (j < 4) or j-4
-  const uint32_t b_mid = (s1 >> sh) & 0xFF;  // byte j+4 (j < 4) or j
-  const uint32_t b_hi = (s2 >> sh) & 0xFF;   // byte j+4 (j >= 4)
-  const uint32_t sc_lo = b_lo & 63, m_lo = b_mid & 63;
-  const uint32_t sc_hi = (b_hi & 0xF) | ((b_lo >> 6) << 4);
-  const uint32_t m_hi = (b_hi >> 4) | ((b_mid >> 6) << 4);
-  sc = j < 4 ? sc_lo : sc_hi;
-  m = j < 4 ? m_lo : m_hi;
-}
-
-// exact f16 -> f32 (hardware conversion)
-__device__ __forceinline__ float h2f(uint32_t bits16) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
-}
-
-// exponent e in [-20, 0] and mantissa d * 2^-e of a non-negative f16 scale
-__device__ __forceinline__ void split_scale(float d, int &e, float &mant) {
-  const int ex = (int)((f2u(d) >> 23) & 0xFF) - 127;  // d == 0 gives -127 -> -20, mant 0
-  e = ex < -20 ? -20 : (ex > 0 ? 0 : ex);
-  mant = __builtin_ldexpf(d, -e);
-}
-
-typedef uint32_t u4s __attribute__((ext_vector_type(4)));
-#define PKV_LDS __attribute__((address_space(3)))
-
-// ---- LDS staging of 32-key blocks. One tensor (K or V) of one KV head: the 16-byte
-// header of row R at hdr[R], and the row's eight 16-byte nibble pieces at
-// nib[8R + (piece ^ swz(R))]. The XOR swizzle makes the row-wise K reads of phase Q
-// conflict-free and keeps the transposed V reads of phase P at two ways.
-struct TensorStage {
-  u4 hdr[kBlk];
-  u4 nib[8 * kBlk];
-};
-struct Stage {
-  TensorStage k, v;
-};
-constexpr int kStages = 2;
-constexpr int kLoadsPerStage = 12;  // 4 x dwordx4 (pieces) + 2 x dword (headers), K and V
-__device__ __forceinline__ int swz(int R) { return ((R >> 1) & 1) | (((R >> 3) & 3) << 1); }
 
 // Per-wave tables rebuilt for every 32-key block.
 struct WaveTab {
@@ -169,86 +87,6 @@ static_assert(sizeof(float[kWaves][8][kMergeRow]) + 2 * sizeof(float[kWaves][8])
                   sizeof(Stage[kWaves]), "merge area within the st0 buffers");
 static_assert(sizeof(Smem) <= 160 * 1024, "LDS budget of one workgroup");
 
-// Buffer resource of a byte range (raw, stride 0; out-of-range loads return zero).
-__device__ __forceinline__ u4s make_rsrc(const void *base, uint32_t bytes) {
-  const uint64_t p = reinterpret_cast<uint64_t>(base);
-  u4s r;
-  r.x = __builtin_amdgcn_readfirstlane((uint32_t)p);
-  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32) & 0xFFFFu);
-  r.z = __builtin_amdgcn_readfirstlane(bytes);
-  r.w = 0x00020000u;
-  return r;
-}
-
-// One lane's part of staging a block, as byte offsets from the block's first row
-// (the same for K and V, whose rows share the stride). The block's own offset is
-// added in the voffset operand, so the buffer range check covers the whole address.
-struct LoadPlan {
-  uint32_t nib[4];  // dwordx4 load i: slot 64 i + lane
-  uint32_t hdr[2];  // dword load j: dword (lane & 3) of header 16 j + lane / 4
-};
-
-__device__ __forceinline__ LoadPlan make_plan(int lane, uint32_t rs_t) {
-  LoadPlan P;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int slot = 64 * i + lane, R = slot >> 3;
-    const int piece = (slot & 7) ^ swz(R);
-    P.nib[i] = (uint32_t)R * rs_t + 16u + 16u * (uint32_t)piece;
-  }
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-    P.hdr[j] = (uint32_t)(16 * j + (lane >> 2)) * rs_t + 4u * (uint32_t)(lane & 3);
-  return P;
-}
-
-// Stage one block (K and V) into LDS: 12 buffer_load ... lds, written from inline asm
-// so that the compiler's wait-count pass does not serialise later LDS reads behind
-// them; the kernel places its own s_waitcnt vmcnt before a stage is read. M0 holds
-// the LDS destination of each load (lane l writes M0 + 16 l, or M0 + 4 l for dwords);
-// one wait state separates an M0 write from the load that reads it.
-__device__ __forceinline__ void issue_stage(Stage *st, const LoadPlan &P, u4s rk, u4s rv,
-                                            uint32_t boff) {
-  const uint32_t kn = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&st->k.nib[0]));
-  const uint32_t kh = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&st->k.hdr[0]));
-  const uint32_t vn = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&st->v.nib[0]));
-  const uint32_t vh = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&st->v.hdr[0]));
-  const uint32_t o0 = P.nib[0] + boff, o1 = P.nib[1] + boff, o2 = P.nib[2] + boff,
-                 o3 = P.nib[3] + boff, h0 = P.hdr[0] + boff, h1 = P.hdr[1] + boff;
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %[sv], m0\n\t"
-      "s_mov_b32 m0, %[kn]\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o0], %[rk], 0 offen lds\n\t"
-      "s_add_u32 m0, %[kn], 0x400\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o1], %[rk], 0 offen lds\n\t"
-      "s_add_u32 m0, %[kn], 0x800\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o2], %[rk], 0 offen lds\n\t"
-      "s_add_u32 m0, %[kn], 0xc00\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o3], %[rk], 0 offen lds\n\t"
-      "s_mov_b32 m0, %[kh]\n\ts_nop 0\n\t"
-      "buffer_load_dword %[h0], %[rk], 0 offen lds\n\t"
-      "s_add_u32 m0, %[kh], 0x100\n\ts_nop 0\n\t"
-      "buffer_load_dword %[h1], %[rk], 0 offen lds\n\t"
-      "s_mov_b32 m0, %[vn]\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o0], %[rv], 0 offen lds\n\t"
-      "s_add_u32 m0, %[vn], 0x400\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o1], %[rv], 0 offen lds\n\t"
-      "s_add_u32 m0, %[vn], 0x800\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o2], %[rv], 0 offen lds\n\t"
-      "s_add_u32 m0, %[vn], 0xc00\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o3], %[rv], 0 offen lds\n\t"
-      "s_mov_b32 m0, %[vh]\n\ts_nop 0\n\t"
-      "buffer_load_dword %[h0], %[rv], 0 offen lds\n\t"
-      "s_add_u32 m0, %[vh], 0x100\n\ts_nop 0\n\t"
-      "buffer_load_dword %[h1], %[rv], 0 offen lds\n\t"
-      "s_mov_b32 m0, %[sv]"
-      : [sv] "=&s"(saved)
-      : [kn] "s"(kn), [kh] "s"(kh), [vn] "s"(vn), [vh] "s"(vh), [o0] "v"(o0), [o1] "v"(o1),
-        [o2] "v"(o2), [o3] "v"(o3), [h0] "v"(h0), [h1] "v"(h1), [rk] "s"(rk), [rv] "s"(rv)
-      : "memory", "scc");
-}
-
 // Stage this wave's KV head's 8 q rows (8 KB, contiguous in q) into LDS: eight
 // dwordx4 loads, lane l of load j moving bytes 1024 j + 16 l.
 __device__ __forceinline__ void issue_q(void *dst_lds, u4s rq, uint32_t lane16) {
@@ -279,7 +117,6 @@ __device__ __forceinline__ void issue_q(void *dst_lds, u4s rq, uint32_t lane16) 
         [o6] "v"(lane16 + 6144u), [o7] "v"(lane16 + 7168u), [rq] "s"(rq)
       : "memory", "scc");
 }
-constexpr int kLoadsQ = 8;
 
 struct WaveState {
   f4 acc[16];  // PV accumulators, tile T = 8h + 2*byte + hl
@@ -340,26 +177,6 @@ __device__ __forceinline__ void phase_q(const Stage &st, WaveTab &T, const h8 *q
     o.s1[t] = s1;
     o.s2[t] = mfma16(a2, q2, f4{0.f, 0.f, 0.f, 0.f});
   }
-}
-
-// Cross-lane max through v_permlane{16,32}_swap: with both operands x, the two results
-// hold x of lanes l and l ^ 16 (l ^ 32). The elements are copied to scalars before the
-// bit cast: __builtin_bit_cast of a vector element r[1] reads element 0 (clang lowers
-// it through the vector's address).
-__device__ __forceinline__ float max_pair(uint32_t a, uint32_t b) {
-  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
-}
-__device__ __forceinline__ float xmax16(float x) {  // max over lanes l and l ^ 16
-  const uint32_t u = __builtin_bit_cast(uint32_t, x);
-  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  const uint32_t r0 = r[0], r1 = r[1];
-  return max_pair(r0, r1);
-}
-__device__ __forceinline__ float xmax32(float x) {  // max over lanes l and l ^ 32
-  const uint32_t u = __builtin_bit_cast(uint32_t, x);
-  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  const uint32_t r0 = r[0], r1 = r[1];
-  return max_pair(r0, r1);
 }
 
 // Phase S: scores (log2 units) and the online softmax; p[k] for key 8g + k, head n % 8.
@@ -483,13 +300,6 @@ __device__ __forceinline__ void phase_p(const Stage &st, WaveState &S, WaveTab &
   const h8 Bm0 = *reinterpret_cast<const h8 *>(&T.vm[n & 7][8 * g]);
   const h8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
   S.accm = mfma32(A, n < 8 ? Bm0 : zero8, S.accm);
-}
-
-// e (0..255) of PV tile T at lane column n
-__device__ __forceinline__ int tile_e(int T, int n) {
-  const int h = T >> 3, byte = (T >> 1) & 3, hl = T & 1;
-  const int c = 2 * h + (n >> 3);
-  return 64 * c + 32 * hl + 4 * (n & 7) + byte;
 }
 
 // Barrier of waves 0-3 only (the quantizing waves), through an LDS arrival counter, so
@@ -724,7 +534,6 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
 // running max and merge through LDS. For a fused decode step the appended key enters
 // here, from its exactly dequantized K and V rows: score = clamp(q . k_new * scale),
 // weight 2^(score - M).
-constexpr int kMaxPartials = 1024;
 constexpr int kCombSlices = 32;  // partial slices (8 threads each)
 constexpr int kCombChunk = 8;    // partials per slice per round
 __global__ __launch_bounds__(256) void q4k_decode_combine_kernel(const float *part, int nwg,
@@ -837,7 +646,7 @@ int launch_attend_mfma(const AttnArgs &a, const float *k_new, const float *v_new
   // 256 workgroups fill the CUs; each owns a multiple of 4 blocks (one or more per
   // wave pair), so the split-K partials stay at <= 256 per batch row
   int nwg = (d.nblk + 3) / 4;
-  if (nwg > kMainWGs) nwg = kMainWGs;  // nwg <= kMaxPartials
+  if (nwg > kMainWGs) nwg = kMainWGs;
   if (nwg < 1) nwg = 1;
   d.bpw = (d.nblk + nwg - 1) / nwg;
   d.bpw = (d.bpw + 3) / 4 * 4;

@@ -1,0 +1,530 @@
+// MFMA prefill-chunk attention over a Q4K cache for the Qwen3-Next full-attention shape
+// (16 query heads, 2 KV heads, head_dim 256), gfx950.
+//
+// Role: FullAttention::forward for l > 1 (paramecia-model/src/qwen3_next.rs:2401-2605):
+// after a chunk of l tokens is appended, its l queries attend causally over every key
+// (query i sees key j iff j <= i + q_offset, q_offset = len - l), GQA group 8, scores
+// scaled, clamped to +-100, soft-maxed and applied to V.
+//
+// Work split: a workgroup owns one KV head, 16 query positions (128 rows = 16 positions
+// x 8 heads of the group) and one split of the keys. Its 8 waves each own 16 rows (two
+// positions); every 32-key block is dequantized ONCE into fp16 MFMA operand fragments
+// in LDS by waves 0-4 and then consumed by all eight waves, so the dequantization cost
+// is shared by 128 query rows. Key splits keep 256 workgroups busy; a small kernel
+// merges the splits' (m, l, o) partials.
+//
+// Arithmetic is the decode kernel's (exact fp16 operands, f32 accumulation):
+//   QK: A[key][e] = nibble * scale code (an integer <= 945, exact in fp16),
+//       B[e][row] = q as fp16 hi and lo parts (two MFMAs into one accumulator),
+//       score = d * S1 - dmin * S2 with S2 = sum_j m_j * qsum_j.
+//   PV: B[key][e] = nibble * scale code * 2^e_d (exact fp16), A[row][key] =
+//       p * mantissa(d) as fp16 hi and lo parts; the min term uses A' = p *
+//       mantissa(dmin) (hi and lo) against B'[key][j] = m_j * 2^e_dmin and is
+//       subtracted per (row, sub-block) at the end.
+#include "pkv_mfma_common.hpp"
+
+namespace pkv {
+
+namespace {
+
+constexpr int kPfWaves = 8;
+constexpr int kPfThreads = 64 * kPfWaves;
+constexpr int kPosPerWG = 16;  // query positions per workgroup, two per wave
+constexpr int kRaw = 3;        // raw Q4K block stages in flight
+constexpr int kPfTargetWGs = 256;
+constexpr float kPfLazy = 8.0f;
+
+struct PrefillArgs {
+  const float *q;  // [B][l][16][256]
+  const uint8_t *k, *v;
+  int64_t rs_b, rs_t, rs_h;
+  int64_t seq_k;     // keys in the cache
+  int64_t q_offset;  // query i sees key j iff !causal || j <= i + q_offset
+  int l, causal;
+  int ntiles, nsplit, bps;  // position tiles, key splits, blocks per split
+  float sl2;                // scale * log2(e)
+  float *part;  // [B * nsplit][2][l * 8][258] partials in tile order (nsplit > 1)
+  float *out;   // [B][l][16][256] (nsplit == 1)
+};
+
+// Fp16 operand fragments and tables of one 32-key block of one KV head.
+struct DqBlock {
+  h8 ka[2][8][64];  // QK A: [tile][step][lane], steps 0-3 low nibbles, 4-7 high
+  h4 ka2[2][64];    // S2 A: m codes of sub-blocks 2g, 2g+1
+  h8 vb[16][64];    // PV B: [tile T2 = 8h + 2 byte + hl][lane]
+  h8 vbm[64];       // min-term B: m_j * 2^e_dmin for columns j < 8
+  float kd[kBlk], kdm[kBlk];    // K: d * sl2, dmin * sl2
+  float vmd[kBlk], vmdm[kBlk];  // V: mantissas of d and dmin
+  _Float16 vsc[8][kBlk], vc[8][kBlk], vm[8][kBlk];  // V constants [j][key]
+};
+
+struct PfSmem {
+  Stage raw[kRaw];
+  DqBlock dq;
+  float cmin[kPfWaves][16][8];  // per wave: min term [row][j]
+};
+static_assert(sizeof(PfSmem) <= 160 * 1024, "LDS budget of one workgroup");
+
+// ---- dequantization of one staged block (waves 0-4)
+
+// Waves 0-1: QK A fragments of tile t (the layout of the decode kernel's phase Q).
+__device__ __forceinline__ void dq_keys(const Stage &st, DqBlock &D, float sl2, const Masks &MK,
+                                        int t, int lane) {
+  const int r = lane & 15, g = lane >> 4;
+  const int kk = 8 * (r >> 2) + 4 * t + (r & 3);
+  const int sw = swz(kk);
+  const u4 hd = st.k.hdr[kk];
+  const u4 q0 = st.k.nib[8 * kk + ((2 * g) ^ sw)];
+  const u4 q1 = st.k.nib[8 * kk + ((2 * g + 1) ^ sw)];
+  if (g == 0) {
+    D.kd[kk] = h2f(hd.x & 0xFFFF) * sl2;
+    D.kdm[kk] = h2f(hd.x >> 16) * sl2;
+  }
+  uint32_t sc0, sc1, m0, m1;
+  scale_min(hd.y, hd.z, hd.w, 2 * g, sc0, m0);
+  scale_min(hd.y, hd.z, hd.w, 2 * g + 1, sc1, m1);
+  const _Float16 f0 = (_Float16)(float)sc0, f1 = (_Float16)((float)sc1 * 0.0625f);
+  const _Float16 c0 = (_Float16)(-1024.0f * (float)sc0), c1 = (_Float16)(-64.0f * (float)sc1);
+  const h2 SC0 = {f0, f0}, SC1 = {f1, f1}, C0 = {c0, c0}, C1 = {c1, c1};
+  const uint32_t qd[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const uint32_t d0 = qd[2 * s], d1 = qd[2 * s + 1];
+    const uint32_t d0s = d0 >> 8, d1s = d1 >> 8;
+    const uint32_t lw[4] = {and_or(d0, MK.lo, MK.magic), and_or(d0s, MK.lo, MK.magic),
+                            and_or(d1, MK.lo, MK.magic), and_or(d1s, MK.lo, MK.magic)};
+    const uint32_t hw[4] = {and_or(d0, MK.hi, MK.magic), and_or(d0s, MK.hi, MK.magic),
+                            and_or(d1, MK.hi, MK.magic), and_or(d1s, MK.hi, MK.magic)};
+    h8 lo, hi;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const h2 l2 = pk_fma(as_h2(lw[w]), SC0, C0);
+      const h2 hh2 = pk_fma(as_h2(hw[w]), SC1, C1);
+      lo[2 * w] = l2[0];
+      lo[2 * w + 1] = l2[1];
+      hi[2 * w] = hh2[0];
+      hi[2 * w + 1] = hh2[1];
+    }
+    D.ka[t][s][lane] = lo;
+    D.ka[t][4 + s][lane] = hi;
+  }
+  D.ka2[t][lane] = h4{(_Float16)(float)m0, (_Float16)(float)m1, (_Float16)0.0f, (_Float16)0.0f};
+}
+
+// Waves 2-3: PV B fragments of e-half h (tiles T2 = 8h..8h+7), after their scale tables.
+__device__ __forceinline__ void dq_values(const Stage &st, DqBlock &D, const Masks &MK, int h,
+                                          int lane) {
+  {
+    // tables of sub-blocks 4h..4h+3: lane takes key lane % 32, sub-blocks 4h + 2 (lane /
+    // 32) + {0, 1}
+    const int kk = lane & 31, jp = lane >> 5;
+    const u4 vh = st.v.hdr[kk];
+    int ed;
+    float md;
+    split_scale(h2f(vh.x & 0xFFFF), ed, md);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 4 * h + 2 * jp + jj;
+      uint32_t sc, m;
+      scale_min(vh.y, vh.z, vh.w, j, sc, m);
+      const float scp = __builtin_ldexpf((float)sc, ed);
+      D.vsc[j][kk] = (_Float16)(jj ? scp * 0.0625f : scp);
+      D.vc[j][kk] = (_Float16)(jj ? -64.0f * scp : -1024.0f * scp);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int n = lane & 15, g = lane >> 4;
+  uint32_t vq[8];
+  const uint32_t *v32 = reinterpret_cast<const uint32_t *>(st.v.nib);
+#pragma unroll
+  for (int k = 0; k < 8; k += 2) {
+    const int R = 8 * g + k;
+    const int piece = 4 * h + (n >> 2);
+    const int base = 4 * (8 * R + (piece ^ swz(R))) + (n & 3);
+    vq[k] = v32[base];
+    vq[k + 1] = v32[base + 32];
+  }
+  const int c = 2 * h + (n >> 3);
+  const h8 SL = *reinterpret_cast<const h8 *>(&D.vsc[2 * c][8 * g]);
+  const h8 CL = *reinterpret_cast<const h8 *>(&D.vc[2 * c][8 * g]);
+  const h8 SH = *reinterpret_cast<const h8 *>(&D.vsc[2 * c + 1][8 * g]);
+  const h8 CH = *reinterpret_cast<const h8 *>(&D.vc[2 * c + 1][8 * g]);
+#pragma unroll
+  for (int byte = 0; byte < 4; ++byte) {
+    const uint32_t sel = (uint32_t)byte | (0x0Cu << 8) | ((uint32_t)(4 + byte) << 16) | (0x0Cu << 24);
+    h8 blo, bhi;
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      const uint32_t x = __builtin_amdgcn_perm(vq[2 * pp + 1], vq[2 * pp], sel);
+      const h2 lo = pk_fma(as_h2(and_or(x, MK.lo, MK.magic)), h2{SL[2 * pp], SL[2 * pp + 1]},
+                           h2{CL[2 * pp], CL[2 * pp + 1]});
+      const h2 hi = pk_fma(as_h2(and_or(x, MK.hi, MK.magic)), h2{SH[2 * pp], SH[2 * pp + 1]},
+                           h2{CH[2 * pp], CH[2 * pp + 1]});
+      blo[2 * pp] = lo[0];
+      blo[2 * pp + 1] = lo[1];
+      bhi[2 * pp] = hi[0];
+      bhi[2 * pp + 1] = hi[1];
+    }
+    D.vb[8 * h + 2 * byte][lane] = blo;
+    D.vb[8 * h + 2 * byte + 1][lane] = bhi;
+  }
+}
+
+// Wave 4: V mantissas and the min-term B fragment.
+__device__ __forceinline__ void dq_value_mins(const Stage &st, DqBlock &D, int lane) {
+  {
+    const int kk = lane & 31, half = lane >> 5;
+    const u4 vh = st.v.hdr[kk];
+    int ed, em;
+    float md, mm;
+    split_scale(h2f(vh.x & 0xFFFF), ed, md);
+    split_scale(h2f(vh.x >> 16), em, mm);
+    (half ? D.vmdm : D.vmd)[kk] = half ? mm : md;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int j = 4 * half + jj;
+      uint32_t sc, m;
+      scale_min(vh.y, vh.z, vh.w, j, sc, m);
+      D.vm[j][kk] = (_Float16)__builtin_ldexpf((float)m, em);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int n = lane & 15, g = lane >> 4;
+  const h8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  const h8 bm = *reinterpret_cast<const h8 *>(&D.vm[n & 7][8 * g]);
+  D.vbm[lane] = n < 8 ? bm : zero8;
+}
+
+// The 6 loads of one tensor of one block: issued by one wave, so that its vmcnt counts
+// exactly its own loads.
+__device__ __forceinline__ void issue_tensor(TensorStage *ts, const LoadPlan &P, u4s rsrc,
+                                             uint32_t boff) {
+  const uint32_t n0 = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&ts->nib[0]));
+  const uint32_t h0 = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&ts->hdr[0]));
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %[sv], m0\n\t"
+      "s_mov_b32 m0, %[n0]\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o0], %[rs], 0 offen lds\n\t"
+      "s_add_u32 m0, %[n0], 0x400\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o1], %[rs], 0 offen lds\n\t"
+      "s_add_u32 m0, %[n0], 0x800\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o2], %[rs], 0 offen lds\n\t"
+      "s_add_u32 m0, %[n0], 0xc00\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o3], %[rs], 0 offen lds\n\t"
+      "s_mov_b32 m0, %[h0]\n\ts_nop 0\n\t"
+      "buffer_load_dword %[p0], %[rs], 0 offen lds\n\t"
+      "s_add_u32 m0, %[h0], 0x100\n\ts_nop 0\n\t"
+      "buffer_load_dword %[p1], %[rs], 0 offen lds\n\t"
+      "s_mov_b32 m0, %[sv]"
+      : [sv] "=&s"(saved)
+      : [n0] "s"(n0), [h0] "s"(h0), [o0] "v"(P.nib[0] + boff), [o1] "v"(P.nib[1] + boff),
+        [o2] "v"(P.nib[2] + boff), [o3] "v"(P.nib[3] + boff), [p0] "v"(P.hdr[0] + boff),
+        [p1] "v"(P.hdr[1] + boff), [rs] "s"(rsrc)
+      : "memory", "scc");
+}
+
+__global__ __launch_bounds__(kPfThreads) void q4k_prefill_kernel(PrefillArgs a) {
+  __shared__ PfSmem sm;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int tile = blockIdx.x, kvg = blockIdx.y;
+  const int split = blockIdx.z % a.nsplit, b = blockIdx.z / a.nsplit;
+  const int p0 = tile * kPosPerWG;
+  const int pw = p0 + 2 * wave;  // this wave's first position; row n -> pw + n / 8
+
+  // ---- key blocks of this workgroup: its split, cut at the last key any of its queries
+  // may see
+  int64_t kend = a.seq_k;
+  if (a.causal) {
+    const int64_t plast = (p0 + kPosPerWG - 1 < a.l ? p0 + kPosPerWG - 1 : a.l - 1);
+    const int64_t lim = plast + a.q_offset + 1;
+    if (lim < kend) kend = lim;
+  }
+  const int nblk_all = (int)((kend + kBlk - 1) / kBlk);
+  const int kb0 = split * a.bps;
+  const int kb1 = kb0 + a.bps < nblk_all ? kb0 + a.bps : nblk_all;
+  const int nb = kb1 > kb0 ? kb1 - kb0 : 0;
+
+  const uint8_t *kbase = a.k + b * a.rs_b + kvg * a.rs_h;
+  const uint8_t *vbase = a.v + b * a.rs_b + kvg * a.rs_h;
+  const uint32_t rs_t = (uint32_t)a.rs_t;
+  const uint32_t span = a.seq_k > 0 ? (uint32_t)(a.seq_k - 1) * rs_t + 144u : 0u;
+  const u4s rk = make_rsrc(kbase, span), rv = make_rsrc(vbase, span);
+  const LoadPlan P = make_plan(lane, rs_t);
+  const uint32_t bbytes = kBlk * rs_t;
+  const bool loader = wave == 5 || wave == 6;
+  auto issue = [&](int i) {  // raw block i of this workgroup into stage i % kRaw
+    if (wave == 5) issue_tensor(&sm.raw[i % kRaw].k, P, rk, (uint32_t)(kb0 + i) * bbytes);
+    if (wave == 6) issue_tensor(&sm.raw[i % kRaw].v, P, rv, (uint32_t)(kb0 + i) * bbytes);
+  };
+  if (loader) {
+    if (nb > 0) issue(0);
+    if (nb > 1) issue(1);
+  }
+
+  // ---- q operands of this wave's 16 rows (row n: position pw + n / 8, head 8 kvg + n % 8)
+  h8 qbh[8], qbl[8];
+  h4 q2h = {0, 0, 0, 0}, q2l = {0, 0, 0, 0};
+  {
+    const int pos = pw + (n >> 3);
+    const bool ok = pos < a.l;
+    const float *qrow = a.q + (((int64_t)b * a.l + (ok ? pos : 0)) * 16 + 8 * kvg + (n & 7)) * 256 + 64 * g;
+    constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    float qsum[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      // rows past the chunk read position 0 and are never stored
+      const float4 r0 = *reinterpret_cast<const float4 *>(qrow + 32 * (st >> 2) + 8 * (st & 3));
+      const float4 r1 = *reinterpret_cast<const float4 *>(qrow + 32 * (st >> 2) + 8 * (st & 3) + 4);
+      const float v8[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) qsum[st >> 2] += v8[k];
+#pragma unroll
+      for (int slot = 0; slot < 8; ++slot) {
+        const float qv = v8[perm[slot]];
+        const _Float16 hi = (_Float16)qv;
+        qbh[st][slot] = hi;
+        qbl[st][slot] = (_Float16)(qv - (float)hi);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const _Float16 hi = (_Float16)qsum[t];
+      q2h[t] = hi;
+      q2l[t] = (_Float16)(qsum[t] - (float)hi);
+    }
+  }
+
+  f4 acc[16];
+#pragma unroll
+  for (int T2 = 0; T2 < 16; ++T2) acc[T2] = f4{0.f, 0.f, 0.f, 0.f};
+  f4 accm = {0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, lsum = 0.0f;
+  const Masks MK = {vconst(0x000F000Fu), vconst(0x00F000F0u), vconst(0x64006400u)};
+  DqBlock &D = sm.dq;
+  // position of this lane's row (n): the causal limit of its keys
+  const int64_t myq = (int64_t)pw + (n >> 3);
+  const int64_t klim = a.causal ? myq + a.q_offset : (int64_t)1 << 62;
+
+  for (int i = 0; i < nb; ++i) {
+    if (loader) {  // block i landed (block i+1 may still fly)
+      if (i + 1 < nb)  // the 6 loads of block i + 1 may stay in flight
+        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();  // raw block i visible; the previous block's operands are consumed
+    if (loader && i + 2 < nb) issue(i + 2);
+    const Stage &st = sm.raw[i % kRaw];
+    if (wave < 2)
+      dq_keys(st, D, a.sl2, MK, wave, lane);
+    else if (wave < 4)
+      dq_values(st, D, MK, wave - 2, lane);
+    else if (wave == 4)
+      dq_value_mins(st, D, lane);
+    __syncthreads();  // operands of block i ready
+
+    // ---- QK (two tiles of 16 keys), rows = this wave's 16 query rows
+    const int64_t key0 = (int64_t)(kb0 + i) * kBlk;
+    float sc8[8];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      f4 s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const h8 A = D.ka[t][s][lane];
+        s1 = mfma32(A, qbh[s], s1);
+        s1 = mfma32(A, qbl[s], s1);
+      }
+      const h4 A2 = D.ka2[t][lane];
+      f4 s2 = mfma16(A2, q2h, f4{0.f, 0.f, 0.f, 0.f});
+      s2 = mfma16(A2, q2l, s2);
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int kk = 8 * g + 4 * t + ii;
+        float sc = D.kd[kk] * s1[ii] - D.kdm[kk] * s2[ii];
+        sc = fminf(fmaxf(sc, -kClampL2), kClampL2);
+        const int64_t key = key0 + kk;
+        sc8[4 * t + ii] = (key < a.seq_k && key <= klim) ? sc : -INFINITY;
+      }
+    }
+    // ---- online softmax per row (lanes n, n+16, n+32, n+48 hold row n's 32 keys)
+    float bm = sc8[0];
+#pragma unroll
+    for (int k = 1; k < 8; ++k) bm = fmaxf(bm, sc8[k]);
+    bm = xmax32(xmax16(bm));
+    if (__any(bm > m_run + kPfLazy)) {
+      const float m_new = fmaxf(m_run, bm);
+      const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      lsum *= alpha;
+      m_run = m_new;
+      float ai[4];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) ai[ii] = __shfl(alpha, 4 * g + ii);  // rows 4g+ii
+#pragma unroll
+      for (int T2 = 0; T2 < 16; ++T2)
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) acc[T2][ii] *= ai[ii];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) accm[ii] *= ai[ii];
+    }
+    float p[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      // a row with no visible key so far keeps m_run = -inf: its p are 0
+      p[k] = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sc8[k] - m_run);
+      lsum += p[k];
+    }
+    // ---- PV: A rows = query rows, keys 8g..8g+7. The weights p * mantissa enter as
+    // fp16 hi and lo parts (~22 bits): one fp16 rounding of a weight (2^-12 relative)
+    // times a value of an outlier channel would exceed the attention tolerance.
+    h8 A, Al, Am, Aml;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float x = p[k] * D.vmd[8 * g + k], xm = p[k] * D.vmdm[8 * g + k];
+      A[k] = (_Float16)x;
+      Al[k] = (_Float16)(x - (float)A[k]);
+      Am[k] = (_Float16)xm;
+      Aml[k] = (_Float16)(xm - (float)Am[k]);
+    }
+#pragma unroll
+    for (int T2 = 0; T2 < 16; ++T2) {
+      const h8 B = D.vb[T2][lane];
+      acc[T2] = mfma32(A, B, acc[T2]);
+      acc[T2] = mfma32(Al, B, acc[T2]);
+    }
+    const h8 Bm = D.vbm[lane];
+    accm = mfma32(Am, Bm, accm);
+    accm = mfma32(Aml, Bm, accm);
+  }
+
+  // ---- epilogue: row sums, min-term subtraction, then output or partial
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+  float(*cmin)[8] = sm.cmin[wave];
+  if (n < 8) {
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) cmin[4 * g + ii][n] = accm[ii];  // rows 4g+ii, column j=n
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float lrow[4], mrow[4];
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) {  // m and l of row 4g+ii live in lane 4g+ii (any g)
+    lrow[ii] = __shfl(lsum, 4 * g + ii);
+    mrow[ii] = __shfl(m_run, 4 * g + ii);
+  }
+  if (a.nsplit == 1) {
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const int row = 4 * g + ii;
+      const int pos = pw + (row >> 3);
+      if (pos >= a.l) continue;
+      float *orow = a.out + (((int64_t)b * a.l + pos) * 16 + 8 * kvg + (row & 7)) * 256;
+      const float inv = lrow[ii] > 0.0f ? 1.0f / lrow[ii] : 0.0f;
+#pragma unroll
+      for (int T2 = 0; T2 < 16; ++T2) {
+        const int e = tile_e(T2, n);
+        orow[e] = (acc[T2][ii] - cmin[row][e >> 5]) * inv;
+      }
+    }
+  } else {
+    float *pz = a.part + (((int64_t)(b * a.nsplit + split) * 2 + kvg) * a.l * 8) * 258;
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const int row = 4 * g + ii;
+      const int pos = pw + (row >> 3);
+      if (pos >= a.l) continue;
+      float *prow = pz + ((int64_t)pos * 8 + (row & 7)) * 258;
+#pragma unroll
+      for (int T2 = 0; T2 < 16; ++T2) {
+        const int e = tile_e(T2, n);
+        prow[16 * T2 + n] = acc[T2][ii] - cmin[row][e >> 5];
+      }
+      if (n == 0) {
+        prow[256] = mrow[ii];
+        prow[257] = lrow[ii];
+      }
+    }
+  }
+}
+
+// Merge the key splits: out[b][pos][8 kvg + hh][e] = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
+// One workgroup of 256 threads per (row, batch); thread = tile-order index.
+__global__ __launch_bounds__(256) void q4k_prefill_merge_kernel(const float *part, int nsplit,
+                                                                int l, float *out) {
+  const int row = blockIdx.x, b = blockIdx.y;  // row = kvg * l * 8 + pos * 8 + hh
+  const int kvg = row / (l * 8), rr = row % (l * 8), pos = rr >> 3, hh = rr & 7;
+  const int idx = threadIdx.x;
+  float M = -INFINITY;
+  for (int s = 0; s < nsplit; ++s)
+    M = fmaxf(M, part[(((int64_t)(b * nsplit + s) * 2 + kvg) * l * 8 + rr) * 258 + 256]);
+  float acc = 0.0f, L = 0.0f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float *pr = part + (((int64_t)(b * nsplit + s) * 2 + kvg) * l * 8 + rr) * 258;
+    const float ms = pr[256];
+    const float f = (ms == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+    acc += f * pr[idx];
+    L += f * pr[257];
+  }
+  const int e = tile_e(idx >> 4, idx & 15);
+  out[(((int64_t)b * l + pos) * 16 + 8 * kvg + hh) * 256 + e] = L > 0.0f ? acc / L : 0.0f;
+}
+
+}  // namespace
+
+int launch_prefill_mfma(const AttnArgs &a, Workspace &ws, hipStream_t s) {
+  if (a.quant != PKV_QUANT_Q4K || a.head_dim != 256 || a.num_heads != 16 ||
+      a.num_kv_heads != 2 || a.l < 2)
+    return PKV_ERR_UNSUPPORTED;
+  if (a.rs.t >= (1 << 24) || a.seq_k >= (1 << 24) ||
+      (uint64_t)a.seq_k * (uint64_t)a.rs.t >= (1ull << 32))
+    return PKV_ERR_UNSUPPORTED;
+  PrefillArgs d;
+  d.q = a.q;
+  d.k = a.k;
+  d.v = a.v;
+  d.rs_b = a.rs.b;
+  d.rs_t = a.rs.t;
+  d.rs_h = a.rs.h;
+  d.seq_k = a.seq_k;
+  d.q_offset = a.q_offset;
+  d.l = a.l;
+  d.causal = a.causal ? 1 : 0;
+  d.sl2 = a.scale * kLog2e;
+  d.ntiles = (a.l + kPosPerWG - 1) / kPosPerWG;
+  const int nblk = (int)((a.seq_k + kBlk - 1) / kBlk);
+  const int base = d.ntiles * 2 * a.batch;
+  int nsplit = (kPfTargetWGs + base - 1) / base;
+  if (nsplit > 16) nsplit = 16;
+  if (nsplit > nblk) nsplit = nblk > 0 ? nblk : 1;
+  if (nsplit < 1) nsplit = 1;
+  d.bps = (nblk + nsplit - 1) / nsplit;
+  if (d.bps < 1) d.bps = 1;
+  d.nsplit = nsplit;
+  d.out = a.out;
+  d.part = nullptr;
+  if (nsplit > 1) {
+    const size_t need = (size_t)a.batch * nsplit * 2 * a.l * 8 * 258 * sizeof(float);
+    const int rc = ws.reserve(need);
+    if (rc) return rc;
+    d.part = static_cast<float *>(ws.ptr);
+  }
+  hipLaunchKernelGGL(q4k_prefill_kernel, dim3((unsigned)d.ntiles, 2u, (unsigned)(nsplit * a.batch)),
+                     dim3(kPfThreads), 0, s, d);
+  PKV_HIP(hipGetLastError());
+  if (nsplit > 1) {
+    hipLaunchKernelGGL(q4k_prefill_merge_kernel, dim3((unsigned)(2 * a.l * 8), (unsigned)a.batch),
+                       dim3(256), 0, s, d.part, nsplit, a.l, a.out);
+    PKV_HIP(hipGetLastError());
+  }
+  return PKV_OK;
+}
+
+}  // namespace pkv
