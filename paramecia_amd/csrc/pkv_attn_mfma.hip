@@ -58,16 +58,18 @@ struct WaveTab {
   _Float16 vsc[8][kBlk], vc[8][kBlk], vm[8][kBlk];  // V: fp16 constants [j][key]
 };
 
-// LDS of one workgroup. Each wave owns stage buffers st0/st1 and a table area; before
-// its first refill of st1 a wave stages its KV head's q rows there, and the quantizer
-// scratch of the quantizing waves 0-3 overlaps their tables. The merge area reuses the
-// st0 buffers once every wave has left the loop.
+// LDS of one workgroup. Each wave owns stage buffers st[0]/st[1] and a table area;
+// before its first refill of st[1] a wave stages its KV head's q rows there, and the
+// quantizer scratch of the quantizing waves 0-3 overlaps their tables. The merge area
+// reuses the st[0] buffers once every wave has left the loop. Stages are always addressed by
+// indexing this array: a pointer chosen at run time between two stages loses its LDS
+// address space, and the generic (flat) loads it then compiles to wait on every
+// outstanding buffer load, including the prefetch of the next block.
 constexpr int kMergeRow = 264;  // padded row of a wave's per-head output in tile order
 struct Smem {
   union {
     struct {
-      Stage st0[kWaves];
-      Stage st1[kWaves];
+      Stage st[2][kWaves];
       union {
         WaveTab tab[kWaves];
         struct {
@@ -84,7 +86,7 @@ struct Smem {
 };
 static_assert(sizeof(Q4kScratch) + 4 <= sizeof(WaveTab), "quantizer scratch within wave 0's tables");
 static_assert(sizeof(float[kWaves][8][kMergeRow]) + 2 * sizeof(float[kWaves][8]) <=
-                  sizeof(Stage[kWaves]), "merge area within the st0 buffers");
+                  sizeof(Stage[kWaves]), "merge area within the st[0] buffers");
 static_assert(sizeof(Smem) <= 160 * 1024, "LDS budget of one workgroup");
 
 // Stage this wave's KV head's 8 q rows (8 KB, contiguous in q) into LDS: eight
@@ -363,10 +365,10 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   // before any stage load (one barrier), so q returns ahead of the block data.
   {
     const u4s rq = make_rsrc(a.q + ((int64_t)b * 16 + 8 * kvu) * 256, 8 * 256 * 4);
-    issue_q(&sm.run.st1[wave], rq, 16u * lane);
+    issue_q(&sm.run.st[1][wave], rq, 16u * lane);
   }
   __syncthreads();
-  if (nmine > 0) issue_stage(&sm.run.st0[wave], P, rk, rv, boff);
+  if (nmine > 0) issue_stage(&sm.run.st[0][wave], P, rk, rv, boff);
 
   // QK B operands: lane (n, g) takes q of head n % 8, elements 64g + 32(s/4) + 8(s%4) +
   // perm[slot], as the fp16 hi part (n < 8) or the lo remainder (n >= 8); S2 B operand:
@@ -381,7 +383,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
       asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
     else
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    const float *qrow = reinterpret_cast<const float *>(&sm.run.st1[wave]) + (n & 7) * 256 + 64 * g;
+    const float *qrow = reinterpret_cast<const float *>(&sm.run.st[1][wave]) + (n & 7) * 256 + 64 * g;
     constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
     float qsum[2] = {0.0f, 0.0f};
 #pragma unroll
@@ -431,7 +433,6 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   S.m_run = -INFINITY;
   S.lsum = 0.0f;
   WaveTab &T = sm.run.t.tab[wave];
-  Stage *const stg[2] = {&sm.run.st0[wave], &sm.run.st1[wave]};
   if (nmine > 0) {
     const Masks MK = {vconst(0x000F000Fu), vconst(0x00F000F0u), vconst(0x64006400u)};
     for (int i = 0; i < nmine; ++i) {
@@ -445,12 +446,12 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
       else if (i == 2)
         __builtin_amdgcn_s_setprio(0);
       if (i + 1 < nmine) {  // block i+1 streams in while block i is processed
-        issue_stage(stg[(i + 1) & 1], P, rk, rv, boff + bstep);
+        issue_stage(&sm.run.st[(i + 1) & 1][wave], P, rk, rv, boff + bstep);
         asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
       } else {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
-      const Stage &st = *stg[i & 1];
+      const Stage &st = sm.run.st[i & 1][wave];
       QKOut qo;
       float pv[8];
       phase_q(st, T, qb, q2, a.sl2, MK, lane, qo);
@@ -483,7 +484,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[T2][i] = S.acc[T2][i] - cmin[(4 * g + i) & 7][e >> 5];
   }
-  __syncthreads();  // every wave has left the loop: the st0 buffers become the merge area
+  __syncthreads();  // every wave has left the loop: the st[0] buffers become the merge area
   // per-wave output in tile order: row head, index 16 T2 + n
   if (g < 2) {
 #pragma unroll
