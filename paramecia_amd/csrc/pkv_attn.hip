@@ -17,6 +17,10 @@ namespace pkv {
 int launch_attend_mfma(const AttnArgs &a, const float *k_new, const float *v_new,
                        uint8_t *kc, uint8_t *vc, int64_t t_new, Workspace &ws,
                        hipStream_t s);
+int launch_append_attend_batched_mfma(int quant, const SeqDesc *seqs, int n, const float *k,
+                                      const float *v, const float *q, int num_heads,
+                                      int num_kv_heads, int head_dim, float scale, float *out,
+                                      Workspace &ws, hipStream_t s);
 // Prefill chunk (l > 1) over Q4K rows of the Qwen3-Next shape (pkv_prefill_mfma.hip).
 int launch_prefill_mfma(const AttnArgs &a, Workspace &ws, hipStream_t s);
 
@@ -238,6 +242,10 @@ int launch_append_attend_batched(int quant, const SeqDesc *seqs, int n, const fl
                                  const float *v, const float *q, int num_heads,
                                  int num_kv_heads, int head_dim, float scale, float *out,
                                  Workspace &ws, hipStream_t s) {
+  // one launch for every sequence when an MFMA kernel covers the shape
+  const int rc0 = launch_append_attend_batched_mfma(quant, seqs, n, k, v, q, num_heads,
+                                                    num_kv_heads, head_dim, scale, out, ws, s);
+  if (rc0 != PKV_ERR_UNSUPPORTED) return rc0;
   const size_t kv_stride = (size_t)num_kv_heads * head_dim;
   const size_t q_stride = (size_t)num_heads * head_dim;
   const int64_t bpr = (int64_t)row_bytes(quant, head_dim);

@@ -19,12 +19,14 @@
 //       group's 8 heads, 8-15 the lo parts, so hi+lo recover q to ~22 bits.
 //       score = d * S1 - dmin * S2 with S2 = sum_j m_j * qsum_j (a 16x16x16 MFMA).
 //   PV: B[key][e] = nibble * scale code * 2^e_d (exact fp16, e_d = exponent of d),
-//       A[head][key] = p * mantissa(d) in fp16; rows 8-15 of A carry p * mantissa(dmin)
-//       and feed the min-term MFMA against B'[key][j] = m_j * 2^e_dmin.
+//       A[head][key] = p * mantissa(d): rows 0-7 its fp16 hi part, rows 8-15 the lo
+//       remainder (rows h and 8 + h are summed after the loop, ~22 bits). The min term
+//       A'[head][key] = p * mantissa(dmin) (hi and lo rows alike) against
+//       B'[key][j] = m_j * 2^e_dmin.
 //   All accumulation is f32. Softmax runs in base 2 with the 1/sqrt(d) scale folded
 //   in, scores clamped to [-100, 100] (in natural-log units) as the reference does.
-//   The running max is raised only when a block exceeds it by 2^8 (p <= 256 is exact
-//   enough in fp16 and the f32 sums), so the accumulators are rarely rescaled.
+//   The running max is raised only when a block exceeds it by 2^8, so the
+//   accumulators are rarely rescaled.
 #include "pkv_mfma_common.hpp"
 #include "pkv_q4k_lanes.hpp"
 
@@ -37,18 +39,30 @@ constexpr int kThreads = 64 * kWaves;  // two waves per SIMD
 constexpr int kMainWGs = 256;
 constexpr float kLazy = 8.0f;  // log2 headroom of the running max before a rescale
 
+// One launch serves up to kMaxSegs segments: the batch rows of one cache, or the
+// sequences of a batched decode step (each with its own cache and length). Segment s
+// owns workgroups [wg0, next wg0); every workgroup writes one split-K partial, indexed
+// by its workgroup id.
+constexpr int kMaxSegs = 32;
+struct DecodeSeg {
+  uint8_t *k, *v;  // K and V rows of token 0, KV head 0 (rows of head 1 follow at rs_h)
+  int64_t seq_k;   // keys held in the cache before this step's append (all attended)
+  int64_t t_new;   // row the fused step writes
+  int nblk, wg0;
+};
+struct DecodeSegIn {
+  uint8_t *k, *v;
+  int64_t seq_k;  // keys after the append (fused) or in the cache
+};
 struct DecodeArgs {
-  const float *q;  // [B][16][256]
-  const uint8_t *k, *v;
-  uint8_t *kw, *vw;
-  int64_t rs_b, rs_t, rs_h;
-  int64_t seq_k;  // keys held in the cache before this step's append (all attended)
-  int nblk, nwg_main, bpw;
-  float sl2;  // scale * log2(e)
-  const float *k_new, *v_new;  // [B][2][256] or null (fused decode step)
-  int64_t t_new;
-  float *part;  // [B][nwg_main][16][258]
-  float *dq;    // [B][4][256] dequantized new rows (K kv0, K kv1, V kv0, V kv1)
+  DecodeSeg seg[kMaxSegs];
+  int nseg, nwg, bpw;
+  int64_t rs_t, rs_h;
+  float sl2;                   // scale * log2(e)
+  const float *q;              // [nseg][16][256]
+  const float *k_new, *v_new;  // [nseg][2][256] or null (fused decode step)
+  float *part;                 // [nwg][16][258]
+  float *dq;  // [nseg][4][256] dequantized new rows (K kv0, K kv1, V kv0, V kv1)
 };
 
 // Per-wave tables rebuilt for every 32-key block.
@@ -266,11 +280,19 @@ __device__ __forceinline__ void phase_p(const Stage &st, WaveState &S, WaveTab &
       vq[h][k] = v32[base];
       vq[h][k + 1] = v32[base + 32];
     }
-  // A: rows 0-7 p * mant(d), rows 8-15 p * mant(dmin)
-  const float *mult = (n < 8) ? T.vmd : T.vmdm;
-  h8 A;
+  // A: rows 0-7 the fp16 hi parts of p * mant(d), rows 8-15 the lo remainders (the two
+  // row halves are summed after the loop); Am likewise for p * mant(dmin). One fp16
+  // rounding of a weight (2^-12 relative) times a value of an outlier channel would
+  // exceed the attention tolerance; hi + lo keeps ~22 bits.
+  const bool lo_row = n >= 8;
+  h8 A, Am;
 #pragma unroll
-  for (int k = 0; k < 8; ++k) A[k] = (_Float16)(p[k] * mult[8 * g + k]);
+  for (int k = 0; k < 8; ++k) {
+    const float x = p[k] * T.vmd[8 * g + k], xm = p[k] * T.vmdm[8 * g + k];
+    const _Float16 xh = (_Float16)x, xmh = (_Float16)xm;
+    A[k] = lo_row ? (_Float16)(x - (float)xh) : xh;
+    Am[k] = lo_row ? (_Float16)(xm - (float)xmh) : xmh;
+  }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int c = 2 * h + (n >> 3);
@@ -298,10 +320,10 @@ __device__ __forceinline__ void phase_p(const Stage &st, WaveState &S, WaveTab &
       S.acc[8 * h + 2 * byte + 1] = mfma32(A, bhi, S.acc[8 * h + 2 * byte + 1]);
     }
   }
-  // min term: C'[8 + head][j] += sum_k p * mant(dmin) * m_kj * 2^e_dmin
+  // min term: C'[row][j] += sum_k Am[row][k] * m_kj * 2^e_dmin (columns j < 8)
   const h8 Bm0 = *reinterpret_cast<const h8 *>(&T.vm[n & 7][8 * g]);
   const h8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
-  S.accm = mfma32(A, n < 8 ? Bm0 : zero8, S.accm);
+  S.accm = mfma32(Am, n < 8 ? Bm0 : zero8, S.accm);
 }
 
 // Barrier of waves 0-3 only (the quantizing waves), through an LDS arrival counter, so
@@ -328,35 +350,40 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   __shared__ Smem sm;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kv = wave & 1, wsub = wave >> 1;
-  const int b = blockIdx.y, wg = blockIdx.x;
+  const int wg = blockIdx.x;
   const int n = lane & 15, g = lane >> 4;
+  int b = 0;  // segment of this workgroup
+  while (b + 1 < a.nseg && wg >= a.seg[b + 1].wg0) ++b;
+  const DecodeSeg &sg = a.seg[b];
 
   // ---- blocks of this wave: b0 + wsub, b0 + wsub + 4, ... below b1
-  const int b0 = wg * a.bpw;
-  const int b1 = b0 + a.bpw < a.nblk ? b0 + a.bpw : a.nblk;
+  const int b0 = (wg - sg.wg0) * a.bpw;
+  const int b1 = b0 + a.bpw < sg.nblk ? b0 + a.bpw : sg.nblk;
   const int first = b0 + wsub;
   const int nmine = first < b1 ? (b1 - first + 3) / 4 : 0;
   const int kvu = __builtin_amdgcn_readfirstlane(kv);
-  const uint8_t *kbase = a.k + b * a.rs_b + kvu * a.rs_h;
-  const uint8_t *vbase = a.v + b * a.rs_b + kvu * a.rs_h;
+  const uint8_t *kbase = sg.k + kvu * a.rs_h;
+  const uint8_t *vbase = sg.v + kvu * a.rs_h;
   const uint32_t rs_t = (uint32_t)a.rs_t;
+  const int64_t seq_k = sg.seq_k;
   // rows of keys [0, seq_k) of this head; loads past them return zeros (masked keys)
-  const uint32_t span = a.seq_k > 0 ? (uint32_t)(a.seq_k - 1) * rs_t + 144u : 0u;
+  const uint32_t span = seq_k > 0 ? (uint32_t)(seq_k - 1) * rs_t + 144u : 0u;
   const u4s rk = make_rsrc(kbase, span), rv = make_rsrc(vbase, span);
   const LoadPlan P = make_plan(lane, rs_t);
   const uint32_t bstep = 4u * kBlk * rs_t;  // byte distance between this wave's blocks
   uint32_t boff = (uint32_t)first * kBlk * rs_t;
 
-  // Fused append: threads 0-255 (waves 0-3) of workgroups 0-3 quantize one new row each
-  // (further rows go round-robin when the grid is smaller) and publish it dequantized
-  // for the combine step, which attends to the new key. This runs while the first block
-  // streams in. The row is read before any staging load is issued, so the compiler's
-  // wait for it does not wait for the stage too.
-  const bool quant = a.k_new != nullptr && wg < 4 && tid < 256;
+  // Fused append: threads 0-255 (waves 0-3) of workgroup r quantize new row r (row
+  // 4s + 2p + kv: segment s, K (p = 0) or V (p = 1), KV head kv; further rows go
+  // round-robin when the grid is smaller) and publish it dequantized for the combine
+  // step, which attends to the new key. This runs while the first block streams in.
+  // The row is read before any staging load is issued, so the compiler's wait for it
+  // does not wait for the stage too.
+  const bool quant = a.k_new != nullptr && wg < 4 * a.nseg && tid < 256;
   float xq = 0.0f;
   if (quant) {
-    const int p = wg >> 1, kvr = wg & 1;
-    xq = (p ? a.v_new : a.k_new)[((int64_t)b * 2 + kvr) * 256 + tid];
+    const int p = (wg >> 1) & 1, kvr = wg & 1;
+    xq = (p ? a.v_new : a.k_new)[((int64_t)(wg >> 2) * 2 + kvr) * 256 + tid];
     asm volatile("" : "+v"(xq));
   }
   if (tid == 0) sm.run.t.quant.arrivals = 0u;
@@ -413,14 +440,15 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
     // the waves sharing its SIMDs
     __builtin_amdgcn_s_setprio(3);
     QuantWavesBarrier bar{&sm.run.t.quant.arrivals, 0u};
-    for (int row = wg; row < 4; row += a.nwg_main) {
-      const int p = row >> 1, kvr = row & 1;  // 0: K kv0, 1: K kv1, 2: V kv0, 3: V kv1
-      if (row != wg) xq = (p ? a.v_new : a.k_new)[((int64_t)b * 2 + kvr) * 256 + tid];
-      uint8_t *dst = (p ? a.vw : a.kw) + b * a.rs_b + a.t_new * a.rs_t + kvr * a.rs_h;
+    for (int row = wg; row < 4 * a.nseg; row += a.nwg) {
+      const int rs = row >> 2, p = (row >> 1) & 1, kvr = row & 1;
+      if (row != wg) xq = (p ? a.v_new : a.k_new)[((int64_t)rs * 2 + kvr) * 256 + tid];
+      const DecodeSeg &rg = a.seg[rs];
+      uint8_t *dst = (p ? rg.v : rg.k) + rg.t_new * a.rs_t + kvr * a.rs_h;
       float deq;
       q4k_quantize_superblock_lanes(xq, dst, &sm.run.t.quant.scr, tid, &deq, bar);
       bar.target += 12;  // the three barriers of that call
-      a.dq[((int64_t)b * 4 + row) * 256 + tid] = deq;
+      a.dq[(int64_t)row * 256 + tid] = deq;
     }
     __builtin_amdgcn_s_setprio(0);
   }
@@ -455,7 +483,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
       QKOut qo;
       float pv[8];
       phase_q(st, T, qb, q2, a.sl2, MK, lane, qo);
-      phase_s(qo, S, T, (int)(a.seq_k - (int64_t)(first + 4 * i) * kBlk), lane, pv);
+      phase_s(qo, S, T, (int)(seq_k - (int64_t)(first + 4 * i) * kBlk), lane, pv);
       phase_p(st, S, T, pv, MK, lane);
       // every LDS read of this stage has completed before it is refilled
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -466,13 +494,19 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   // ---- per-wave reductions
   S.lsum += __shfl_xor(S.lsum, 16);
   S.lsum += __shfl_xor(S.lsum, 32);
-  // min term per [head][j] (accm rows 8 + 4(g-2) + i, column j = n) through this
-  // wave's own table area, then O'[head][e] = acc - cmin[head][e / 32] on lanes g < 2
-  // (rows 4g+i = head 4g+i)
-  float(*cmin)[8] = reinterpret_cast<float(*)[8]>(&T.kd[0]);
-  if (g >= 2 && n < 8) {
+  // hi rows 4g+i (lanes g < 2) plus lo rows 8+4g+i (lanes g + 2, 32 lanes up)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) cmin[4 * (g - 2) + i][n] = S.accm[i];
+  for (int T2 = 0; T2 < 16; ++T2)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) S.acc[T2][i] = xsum32(S.acc[T2][i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) S.accm[i] = xsum32(S.accm[i]);
+  // min term per [head][j] (accm row 4g+i, column j = n) through this wave's own table
+  // area, then O'[head][e] = acc - cmin[head][e / 32] on lanes g < 2 (row 4g+i = head)
+  float(*cmin)[8] = reinterpret_cast<float(*)[8]>(&T.kd[0]);
+  if (g < 2 && n < 8) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cmin[4 * g + i][n] = S.accm[i];
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -512,7 +546,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
       f[s4] = (mw[s4] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw[s4] - M);
       L += f[s4] * sm.merge.l[2 * s4 + hk][hh];
     }
-    float *dst = a.part + ((int64_t)b * a.nwg_main + wg) * 16 * 258 + H * 258;
+    float *dst = a.part + (int64_t)wg * 16 * 258 + H * 258;
 #pragma unroll
     for (int x = 0; x < 8; ++x) {
       const int idx = i0 + 32 * x;
@@ -537,15 +571,24 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
 // weight 2^(score - M).
 constexpr int kCombSlices = 32;  // partial slices (8 threads each)
 constexpr int kCombChunk = 8;    // partials per slice per round
-__global__ __launch_bounds__(256) void q4k_decode_combine_kernel(const float *part, int nwg,
-                                                                 const float *q, const float *dq,
-                                                                 float sl2, float *out) {
+struct CombineArgs {
+  const float *part;      // [wg][16][258]
+  const float *q, *dq;    // [nseg][16][256], [nseg][4][256] or null
+  float *out;             // [nseg][16][256]
+  float sl2;
+  int wg0[kMaxSegs + 1];  // segment s owns partials [wg0[s], wg0[s + 1])
+};
+__global__ __launch_bounds__(256) void q4k_decode_combine_kernel(CombineArgs c) {
   __shared__ float dotp[4];
   __shared__ float mx[kCombSlices], ls[kCombSlices];
   __shared__ float4 accs[kCombSlices][8];
   const int h = blockIdx.x >> 3, i0 = 32 * (blockIdx.x & 7), b = blockIdx.y;
   const int tid = threadIdx.x, ps = tid >> 3, g4 = tid & 7;
-  const float *P = part + (int64_t)b * nwg * 16 * 258 + h * 258;
+  const float *q = c.q, *dq = c.dq;
+  const float sl2 = c.sl2;
+  float *out = c.out;
+  const int nwg = c.wg0[b + 1] - c.wg0[b];
+  const float *P = c.part + (int64_t)c.wg0[b] * 16 * 258 + h * 258;
   // new key: q . k_new products (reduced below, after the partial loads are issued)
   const float prod = dq != nullptr ? q[((int64_t)b * 16 + h) * 256 + tid] *
                                          dq[((int64_t)b * 4 + (h >> 3)) * 256 + tid]
@@ -621,6 +664,86 @@ __global__ __launch_bounds__(256) void q4k_decode_combine_kernel(const float *pa
 
 }  // namespace
 
+// Plan and launch the decode and combine kernels over n <= kMaxSegs segments.
+static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
+                                  const float *k_new, const float *v_new, float *out,
+                                  int64_t rs_t, int64_t rs_h, float scale, Workspace &ws,
+                                  hipStream_t s) {
+  DecodeArgs d;
+  const bool fused = k_new != nullptr;
+  for (int i = 0; i < n; ++i) {
+    d.seg[i].k = in[i].k;
+    d.seg[i].v = in[i].v;
+    d.seg[i].seq_k = fused ? in[i].seq_k - 1 : in[i].seq_k;  // the new key joins in the combine
+    d.seg[i].t_new = in[i].seq_k - 1;
+    d.seg[i].nblk = (int)((d.seg[i].seq_k + kBlk - 1) / kBlk);
+  }
+  // Blocks per workgroup, a multiple of 4 (one or more per wave pair). One segment:
+  // spread over at most kMainWGs workgroups, one per CU. Several: the multiple that
+  // minimises the estimated makespan, ceil(workgroups / 256) rounds of (bpw / 4 blocks
+  // per wave + a per-workgroup overhead of about 1.3 blocks).
+  int bpw;
+  if (n == 1) {
+    int nwg = (d.seg[0].nblk + 3) / 4;
+    if (nwg > kMainWGs) nwg = kMainWGs;
+    if (nwg < 1) nwg = 1;
+    bpw = (d.seg[0].nblk + nwg - 1) / nwg;
+    bpw = (bpw + 3) / 4 * 4;
+    if (bpw < 4) bpw = 4;
+  } else {
+    bpw = 4;
+    double best = 1e30;
+    for (int cand = 4; cand <= 64; cand += 4) {
+      int64_t w = 0;
+      for (int i = 0; i < n; ++i) w += d.seg[i].nblk > 0 ? (d.seg[i].nblk + cand - 1) / cand : 1;
+      const double cost = (double)((w + kMainWGs - 1) / kMainWGs) * (cand / 4.0 + 1.3);
+      if (cost < best) {
+        best = cost;
+        bpw = cand;
+      }
+    }
+  }
+  CombineArgs c;
+  int wg = 0;
+  for (int i = 0; i < n; ++i) {
+    d.seg[i].wg0 = wg;
+    c.wg0[i] = wg;
+    const int w = d.seg[i].nblk > 0 ? (d.seg[i].nblk + bpw - 1) / bpw : 1;
+    wg += w;
+  }
+  c.wg0[n] = wg;
+  d.nseg = n;
+  d.nwg = wg;
+  d.bpw = bpw;
+  d.rs_t = rs_t;
+  d.rs_h = rs_h;
+  d.sl2 = scale * kLog2e;
+  d.q = q;
+  d.k_new = k_new;
+  d.v_new = v_new;
+  const size_t part_floats = (size_t)wg * 16 * 258;
+  const size_t need = (part_floats + (size_t)n * 4 * 256) * sizeof(float);
+  int rc = ws.reserve(need);
+  if (rc) return rc;
+  d.part = static_cast<float *>(ws.ptr);
+  d.dq = d.part + part_floats;
+  hipLaunchKernelGGL(q4k_decode_kernel, dim3((unsigned)wg), dim3(kThreads), 0, s, d);
+  PKV_HIP(hipGetLastError());
+  c.part = d.part;
+  c.q = q;
+  c.dq = fused ? d.dq : nullptr;
+  c.out = out;
+  c.sl2 = d.sl2;
+  hipLaunchKernelGGL(q4k_decode_combine_kernel, dim3(16 * 8, (unsigned)n), dim3(256), 0, s, c);
+  PKV_HIP(hipGetLastError());
+  return PKV_OK;
+}
+
+// Rows are addressed with 32-bit offsets (key * row stride) from a per-head base.
+static bool decode_rows_fit(int64_t seq_k, int64_t rs_t) {
+  return rs_t < (1 << 24) && seq_k < (1 << 24) && (uint64_t)seq_k * (uint64_t)rs_t < (1ull << 32);
+}
+
 int launch_attend_mfma(const AttnArgs &a, const float *k_new, const float *v_new, uint8_t *kc,
                        uint8_t *vc, int64_t t_new, Workspace &ws, hipStream_t s) {
   if (a.quant != PKV_QUANT_Q4K || a.head_dim != 256 || a.num_heads != 16 ||
@@ -629,48 +752,48 @@ int launch_attend_mfma(const AttnArgs &a, const float *k_new, const float *v_new
   // decode only: the single query sees every key
   if (a.causal && a.q_offset + 1 < a.seq_k) return PKV_ERR_UNSUPPORTED;
   const bool fused = k_new != nullptr;
-  // rows are addressed with 32-bit offsets (key * row stride) from a per-head base
-  if (a.rs.t >= (1 << 24) || a.seq_k >= (1 << 24) ||
-      (uint64_t)a.seq_k * (uint64_t)a.rs.t >= (1ull << 32))
+  // the fused step writes the new row into the cache being read, at its last row
+  if (fused && (kc != a.k || vc != a.v || t_new != a.seq_k - 1)) return PKV_ERR_UNSUPPORTED;
+  if (!decode_rows_fit(a.seq_k, a.rs.t)) return PKV_ERR_UNSUPPORTED;
+  for (int b0 = 0; b0 < a.batch; b0 += kMaxSegs) {
+    const int nb = a.batch - b0 < kMaxSegs ? a.batch - b0 : kMaxSegs;
+    DecodeSegIn in[kMaxSegs];
+    for (int i = 0; i < nb; ++i) {
+      in[i].k = const_cast<uint8_t *>(a.k) + (int64_t)(b0 + i) * a.rs.b;
+      in[i].v = const_cast<uint8_t *>(a.v) + (int64_t)(b0 + i) * a.rs.b;
+      in[i].seq_k = a.seq_k;
+    }
+    const int64_t qo = (int64_t)b0 * 16 * 256, ko = (int64_t)b0 * 2 * 256;
+    const int rc = launch_decode_segments(in, nb, a.q + qo, fused ? k_new + ko : nullptr,
+                                          fused ? v_new + ko : nullptr, a.out + qo, a.rs.t,
+                                          a.rs.h, a.scale, ws, s);
+    if (rc) return rc;
+  }
+  return PKV_OK;
+}
+
+int launch_append_attend_batched_mfma(int quant, const SeqDesc *seqs, int n, const float *k,
+                                      const float *v, const float *q, int num_heads,
+                                      int num_kv_heads, int head_dim, float scale, float *out,
+                                      Workspace &ws, hipStream_t s) {
+  if (quant != PKV_QUANT_Q4K || head_dim != 256 || num_heads != 16 || num_kv_heads != 2)
     return PKV_ERR_UNSUPPORTED;
-  DecodeArgs d;
-  d.q = a.q;
-  d.k = a.k;
-  d.v = a.v;
-  d.kw = kc;
-  d.vw = vc;
-  d.rs_b = a.rs.b;
-  d.rs_t = a.rs.t;
-  d.rs_h = a.rs.h;
-  d.seq_k = fused ? a.seq_k - 1 : a.seq_k;  // old keys; the new one joins in the combine
-  d.nblk = (int)((d.seq_k + kBlk - 1) / kBlk);
-  // 256 workgroups fill the CUs; each owns a multiple of 4 blocks (one or more per
-  // wave pair), so the split-K partials stay at <= 256 per batch row
-  int nwg = (d.nblk + 3) / 4;
-  if (nwg > kMainWGs) nwg = kMainWGs;
-  if (nwg < 1) nwg = 1;
-  d.bpw = (d.nblk + nwg - 1) / nwg;
-  d.bpw = (d.bpw + 3) / 4 * 4;
-  if (d.bpw < 4) d.bpw = 4;
-  nwg = (d.nblk + d.bpw - 1) / d.bpw;
-  if (nwg < 1) nwg = 1;
-  d.nwg_main = nwg;
-  d.sl2 = a.scale * kLog2e;
-  d.k_new = k_new;
-  d.v_new = v_new;
-  d.t_new = t_new;
-  const size_t part_floats = (size_t)a.batch * nwg * 16 * 258;
-  const size_t need = (part_floats + (size_t)a.batch * 4 * 256) * sizeof(float);
-  int rc = ws.reserve(need);
-  if (rc) return rc;
-  d.part = static_cast<float *>(ws.ptr);
-  d.dq = d.part + part_floats;
-  hipLaunchKernelGGL(q4k_decode_kernel, dim3((unsigned)nwg, (unsigned)a.batch),
-                     dim3(kThreads), 0, s, d);
-  PKV_HIP(hipGetLastError());
-  hipLaunchKernelGGL(q4k_decode_combine_kernel, dim3(16 * 8, (unsigned)a.batch), dim3(256), 0, s,
-                     d.part, nwg, a.q, fused ? d.dq : nullptr, d.sl2, a.out);
-  PKV_HIP(hipGetLastError());
+  const int64_t rs_t = 2 * 144, rs_h = 144;
+  for (int i = 0; i < n; ++i)
+    if (seqs[i].len < 1 || !decode_rows_fit(seqs[i].len, rs_t)) return PKV_ERR_UNSUPPORTED;
+  for (int b0 = 0; b0 < n; b0 += kMaxSegs) {
+    const int nb = n - b0 < kMaxSegs ? n - b0 : kMaxSegs;
+    DecodeSegIn in[kMaxSegs];
+    for (int i = 0; i < nb; ++i) {
+      in[i].k = seqs[b0 + i].k;
+      in[i].v = seqs[b0 + i].v;
+      in[i].seq_k = seqs[b0 + i].len;
+    }
+    const int64_t qo = (int64_t)b0 * 16 * 256, ko = (int64_t)b0 * 2 * 256;
+    const int rc = launch_decode_segments(in, nb, q + qo, k + ko, v + ko, out + qo, rs_t, rs_h,
+                                          scale, ws, s);
+    if (rc) return rc;
+  }
   return PKV_OK;
 }
 

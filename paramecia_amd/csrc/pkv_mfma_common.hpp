@@ -190,6 +190,13 @@ __device__ __forceinline__ float xmax32(float x) {  // max over lanes l and l ^ 
   return max_pair(r0, r1);
 }
 
+__device__ __forceinline__ float xsum32(float x) {  // x of lanes l and l ^ 32, summed
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
+
 // e (0..255) of PV tile T at lane column n
 __device__ __forceinline__ int tile_e(int T, int n) {
   const int h = T >> 3, byte = (T >> 1) & 3, hl = T & 1;

@@ -129,3 +129,65 @@ def test_decode_full_size_layer(pk, orc):
     err = np.abs(out - ref)
     say(f"full-size layer: max|diff| = {err.max():.3e}")
     np.testing.assert_allclose(out, ref, atol=ATOL, rtol=RTOL)
+
+
+def run_batched(pk, orc, lens, seed, chans=None):
+    """One batched decode step over len(lens) caches of different lengths: each gets a
+    new token appended (bit-exact bytes) and its query attends over all its keys."""
+    rng = np.random.default_rng(seed)
+    caches, oracles = [], []
+    for S in lens:
+        g = pk.PreallocatedQuantizedKvCache(1, 2, S + 1, 256, pk.KvCacheQuantization.Q4K)
+        c = orc.Cache(Q4K, 1, 2, 256, S + 1)
+        if S > 0:
+            k = rng.standard_normal((1, 2, S, 256)).astype(np.float32)
+            v = rng.standard_normal((1, 2, S, 256)).astype(np.float32)
+            if chans is not None:
+                k[..., chans] *= 20.0
+                v[..., chans] *= 20.0
+            g.append_quantized(dev(k), dev(v))
+            assert c.append(k, v) == 0
+        caches.append(g)
+        oracles.append(c)
+    n = len(lens)
+    kn = rng.standard_normal((n, 2, 256)).astype(np.float32)
+    vn = rng.standard_normal((n, 2, 256)).astype(np.float32)
+    if chans is not None:
+        kn[..., chans] *= 20.0
+        vn[..., chans] *= 20.0
+    q = rng.standard_normal((n, 16, 256)).astype(np.float32)
+    out = host(pk.append_attend_batched(caches, dev(kn), dev(vn), dev(q), 1 / 16))
+    worst = 0.0
+    for i, (g, c, S) in enumerate(zip(caches, oracles, lens)):
+        assert c.append(kn[i][None, :, None], vn[i][None, :, None]) == 0
+        ref = c.attend(q[i][None, None], 1 / 16, S, True, mode="f32")[0, 0]
+        np.testing.assert_allclose(out[i], ref, atol=ATOL, rtol=RTOL)
+        worst = max(worst, float(np.abs(out[i] - ref).max()))
+        assert g.seq_len == S + 1
+        gk, gv = g.raw_bytes()
+        ok, ov = c.valid_bytes()
+        assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
+    return worst
+
+
+def test_batched_varlen_edges(pk, orc):
+    """Empty, single-token and block-boundary caches in one launch."""
+    say("batched decode, edge lengths")
+    run_batched(pk, orc, [0, 1, 31, 32, 33, 127, 128, 129, 1000, 4095], seed=20)
+
+
+def test_batched_over_segment_limit(pk, orc):
+    """More sequences than one launch takes (32): the call splits into launches."""
+    say("batched decode, 40 sequences")
+    lens = [int(x) for x in np.random.default_rng(21).integers(1, 700, size=40)]
+    run_batched(pk, orc, lens, seed=21)
+
+
+def test_batched_outliers_config5_shape(pk, orc):
+    """16 sequences of seeded lengths with the config-5 outlier channels (x20), at
+    lengths cut to 1/8 of config 5's so the oracle stays fast."""
+    say("batched decode, config-5 shape (lengths / 8)")
+    from paramecia_amd import workloads as W
+    lens = [max(1, S // 8) for S in W.c5_lengths()]
+    worst = run_batched(pk, orc, lens, seed=22, chans=W.c5_channels())
+    say(f"batched decode, config-5 shape: max|diff| = {worst:.3e}")
