@@ -63,9 +63,13 @@ def event_time(torch, fn, steps, warmup):
     return a.elapsed_time(b) / steps
 
 
-def graph_time(torch, fn, steps, warmup):
-    """Capture fn once in a HIP graph (after an eager warm-up on the capture stream, which
-    sizes every workspace) and time its replays."""
+def graph_time(torch, fn, steps, warmup, reps=1):
+    """Milliseconds per call of fn, run from a HIP graph: fn is captured `reps` times in a
+    row into one graph (after an eager warm-up on the capture stream, which sizes every
+    workspace), the graph is replayed, and the time of a replay is divided by `reps`.
+    With reps > 1 the graph launch is shared by several steps, as it is in a serving
+    loop whose graph holds the whole forward pass; every captured step does all of its
+    work."""
     graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -73,9 +77,11 @@ def graph_time(torch, fn, steps, warmup):
         fn()
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=side):
-            fn()
+            for _ in range(reps):
+                fn()
     torch.cuda.current_stream().wait_stream(side)
-    return event_time(torch, graph.replay, steps, warmup)
+    replays = max(1, steps // reps)  # steps timed: replays * reps (== steps when reps | steps)
+    return event_time(torch, graph.replay, replays, max(1, warmup // reps)) / reps
 
 
 # ------------------------------------------------------------------ config 3 (headline)
@@ -126,8 +132,11 @@ def run_config3(args):
 
     # eager: 12 ctypes launches per step from Python (host overhead included)
     eager_ms = event_time(torch, step, args.steps, args.warmup)
-    # HIP graph of one 12-layer step, replayed (the serving-loop form)
-    ms = graph_time(torch, step, args.steps, args.warmup)
+    # HIP graph of args.graph_reps 12-layer steps (default one), replayed (the
+    # serving-loop form), and a graph of a single step for reference
+    reps = args.graph_reps if args.graph_reps > 0 else 1
+    ms = graph_time(torch, step, args.steps, args.warmup, reps)
+    ms_1 = graph_time(torch, step, args.steps, args.warmup, 1)
 
     # per-launch duration of the layer's kernels: the GPU is kept busy by a sleep kernel
     # while the host enqueues, so each event pair brackets device time only
@@ -153,6 +162,8 @@ def run_config3(args):
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
         "eager_us_per_step": round(eager_ms * 1000.0, 2),
+        "graph_steps_per_replay": reps,
+        "one_step_graph_us_per_step": round(ms_1 * 1000.0, 2),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -250,14 +261,18 @@ def run_config1(args):
     pk.fill_normal(kn, W.SEED, W.stream_id(1, W.T_NEW_K))
     pk.fill_normal(vn, W.SEED, W.stream_id(1, W.T_NEW_V))
     step = lambda: c.append_attend(kn, vn, q, W.SCALE, offset=S)
-    ms = graph_time(torch, step, args.steps, args.warmup)
+    reps = args.graph_reps if args.graph_reps > 0 else 20
+    ms = graph_time(torch, step, args.steps, args.warmup, reps)
+    ms_1 = graph_time(torch, step, args.steps, args.warmup, 1)
     nbytes = layer_bytes(S + 1, Q8_ROW)
     gbs = nbytes / (ms * 1e-3) / 1e9
     r = base_result(1, "Q8_0 decode-attn µs/step @4097 keys, 1 layer", round(ms * 1000, 2),
                     "us/step", False, ms, args,
                     "config1: Q8_0 cache with 4096 tokens; step = quantize-append 1 token + "
                     "attend 4097 keys (16 q heads, 2 kv heads, head_dim 256)",
-                    {"roofline": {"kernel": "pkv_append_attend (Q8_0)", "bound": "hbm",
+                    {"graph_steps_per_replay": reps,
+                     "one_step_graph_us_per_step": round(ms_1 * 1000, 2),
+                     "roofline": {"kernel": "pkv_append_attend (Q8_0)", "bound": "hbm",
                                   "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                   "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": nbytes,
                                   "traffic": None}})
@@ -290,18 +305,37 @@ def run_config2(args):
     pk.fill_normal(vc, W.SEED, W.stream_id(2, W.T_CHUNK_V))
     pk.fill_normal(qc, W.SEED, W.stream_id(2, W.T_CHUNK_Q))
 
+    q1 = torch.empty((1, 1, 16, 256), device="cuda")
+    k1 = torch.empty((1, 2, 1, 256), device="cuda")
+    v1 = torch.empty_like(k1)
+    pk.fill_normal(q1, W.SEED, W.stream_id(2, W.T_Q))
+    pk.fill_normal(k1, W.SEED, W.stream_id(2, W.T_NEW_K))
+    pk.fill_normal(v1, W.SEED, W.stream_id(2, W.T_NEW_V))
+
     def step():
         c.append_quantized(kc, vc, offset=S)
-        return c.attend(qc, W.SCALE, S, causal=True)
+        c.attend(qc, W.SCALE, S, causal=True)
+        return c.append_attend(k1, v1, q1, W.SCALE, offset=S + C)
 
-    ms = graph_time(torch, step, args.steps, args.warmup)
+    reps = args.graph_reps if args.graph_reps > 0 else 1
+    ms = graph_time(torch, step, args.steps, args.warmup, reps)
+    ms_1 = graph_time(torch, step, args.steps, args.warmup, 1)
+    # the prefill attention alone (the MFMA kernel's roofline)
+    ms_attn = graph_time(torch, lambda: c.attend(qc, W.SCALE, S, causal=True), args.steps,
+                         args.warmup, reps)
     flops = 16 * (C * S + C * (C + 1) // 2) * 256 * 2 * 2
-    tf = flops / (ms * 1e-3) / 1e12
-    return base_result(2, "Q4K prefill chunk µs (512 queries x 16896 keys, causal)",
-                       round(ms * 1000, 2), "us/chunk", False, ms, args,
+    tf = flops / (ms_attn * 1e-3) / 1e12
+    return base_result(2, "Q4K prefill chunk + decode µs (512-token append, 512 x 16896 causal "
+                       "attention, 1-token decode over 16897 keys)",
+                       round(ms * 1000, 2), "us/step", False, ms, args,
                        "config2: Q4K cache with 16384 tokens; step = quantize-append a 512-token "
-                       "chunk + causal attention of its 512 queries over 16896 keys",
-                       {"roofline": {"kernel": "pkv_append + pkv_attend (prefill chunk)",
+                       "chunk + causal attention of its 512 queries over 16896 keys + one decode "
+                       "step (append 1 token, attend 16897 keys)",
+                       {"graph_steps_per_replay": reps,
+                        "one_step_graph_us_per_step": round(ms_1 * 1000, 2),
+                        "prefill_attention_us": round(ms_attn * 1000, 2),
+                        "roofline": {"kernel": "pkv_attend prefill chunk (q4k_prefill_kernel + "
+                                     "split merge)",
                                      "bound": "mfma", "achieved": round(tf, 2),
                                      "peak": FP16_DENSE_TFLOPS, "unit": "TFLOP/s",
                                      "frac": round(tf / FP16_DENSE_TFLOPS, 5), "flops": flops,
@@ -412,7 +446,8 @@ def run_config5(args):
                 caches[l][i].truncate(S)  # rewind the previous step's token
             pk.append_attend_batched(caches[l], kn[l], vn[l], q[l], W.SCALE)
 
-    ms = graph_time(torch, step, args.steps, args.warmup)
+    reps = args.graph_reps if args.graph_reps > 0 else 1
+    ms = graph_time(torch, step, args.steps, args.warmup, reps)
     nbytes = L * sum(layer_bytes(S + 1) for S in lens)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return base_result(5, "batched decode µs/step (16 sequences, 12 layers, Q4K)",
@@ -420,7 +455,7 @@ def run_config5(args):
                        "config5: 16 batch-1 Q4K caches per layer (seeded lengths 1024-65536, "
                        "5 outlier channels x20), 12 layers; step = append 1 token + attend, "
                        "every sequence of every layer",
-                       {"sequence_lengths": lens,
+                       {"sequence_lengths": lens, "graph_steps_per_replay": reps,
                         "roofline": {"kernel": "pkv_append_attend_batched", "bound": "hbm",
                                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -436,6 +471,8 @@ def main() -> int:
     ap.add_argument("--cached", type=int, default=131072, help="config 3: cached tokens")
     ap.add_argument("--layers", type=int, default=12, help="config 3: layers")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph-reps", type=int, default=0,
+                    help="steps captured per HIP graph replay (0: per-config default)")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="config 3: after the timed runs, launch a plain elementwise copy of "

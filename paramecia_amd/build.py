@@ -28,6 +28,7 @@ SOURCES = {
     "pkv_attn.hip": [],
     "pkv_attn_mfma.hip": [],
     "pkv_prefill_mfma.hip": [],
+    "pkv_q8_decode.hip": [],
     "pkv_util.hip": [],
     "pkv_api.cpp": ["-x", "hip"],
 }

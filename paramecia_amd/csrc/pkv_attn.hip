@@ -21,6 +21,13 @@ int launch_append_attend_batched_mfma(int quant, const SeqDesc *seqs, int n, con
                                       const float *v, const float *q, int num_heads,
                                       int num_kv_heads, int head_dim, float scale, float *out,
                                       Workspace &ws, hipStream_t s);
+// Q8_0 decode for the Qwen3-Next shape (pkv_q8_decode.hip).
+int launch_attend_q8(const AttnArgs &a, const float *k_new, const float *v_new, uint8_t *kc,
+                     uint8_t *vc, int64_t t_new, Workspace &ws, hipStream_t s);
+int launch_append_attend_batched_q8(int quant, const SeqDesc *seqs, int n, const float *k,
+                                    const float *v, const float *q, int num_heads,
+                                    int num_kv_heads, int head_dim, float scale, float *out,
+                                    Workspace &ws, hipStream_t s);
 // Prefill chunk (l > 1) over Q4K rows of the Qwen3-Next shape (pkv_prefill_mfma.hip).
 int launch_prefill_mfma(const AttnArgs &a, Workspace &ws, hipStream_t s);
 
@@ -220,6 +227,8 @@ int launch_attend(const AttnArgs &a, Workspace &ws, hipStream_t s) {
   if (rc) return rc;
   rc = launch_attend_mfma(a, nullptr, nullptr, nullptr, nullptr, -1, ws, s);
   if (rc != PKV_ERR_UNSUPPORTED) return rc;
+  rc = launch_attend_q8(a, nullptr, nullptr, nullptr, nullptr, -1, ws, s);
+  if (rc != PKV_ERR_UNSUPPORTED) return rc;
   rc = launch_prefill_mfma(a, ws, s);
   if (rc != PKV_ERR_UNSUPPORTED) return rc;
   return launch_attend_generic(a, ws, s);
@@ -231,6 +240,8 @@ int launch_append_attend(const AttnArgs &a, const float *k_new, const float *v_n
   int rc = check_attn(a);
   if (rc) return rc;
   rc = launch_attend_mfma(a, k_new, v_new, kc, vc, t_new, ws, s);
+  if (rc != PKV_ERR_UNSUPPORTED) return rc;
+  rc = launch_attend_q8(a, k_new, v_new, kc, vc, t_new, ws, s);
   if (rc != PKV_ERR_UNSUPPORTED) return rc;
   rc = launch_append(a.quant, k_new, v_new, kc, vc, a.batch, a.num_kv_heads, a.head_dim, 1,
                      t_new, s);
@@ -246,6 +257,9 @@ int launch_append_attend_batched(int quant, const SeqDesc *seqs, int n, const fl
   const int rc0 = launch_append_attend_batched_mfma(quant, seqs, n, k, v, q, num_heads,
                                                     num_kv_heads, head_dim, scale, out, ws, s);
   if (rc0 != PKV_ERR_UNSUPPORTED) return rc0;
+  const int rc1 = launch_append_attend_batched_q8(quant, seqs, n, k, v, q, num_heads,
+                                                  num_kv_heads, head_dim, scale, out, ws, s);
+  if (rc1 != PKV_ERR_UNSUPPORTED) return rc1;
   const size_t kv_stride = (size_t)num_kv_heads * head_dim;
   const size_t q_stride = (size_t)num_heads * head_dim;
   const int64_t bpr = (int64_t)row_bytes(quant, head_dim);

@@ -27,6 +27,7 @@
 //   in, scores clamped to [-100, 100] (in natural-log units) as the reference does.
 //   The running max is raised only when a block exceeds it by 2^8, so the
 //   accumulators are rarely rescaled.
+#include "pkv_decode_split.hpp"
 #include "pkv_mfma_common.hpp"
 #include "pkv_q4k_lanes.hpp"
 
@@ -39,21 +40,6 @@ constexpr int kThreads = 64 * kWaves;  // two waves per SIMD
 constexpr int kMainWGs = 256;
 constexpr float kLazy = 8.0f;  // log2 headroom of the running max before a rescale
 
-// One launch serves up to kMaxSegs segments: the batch rows of one cache, or the
-// sequences of a batched decode step (each with its own cache and length). Segment s
-// owns workgroups [wg0, next wg0); every workgroup writes one split-K partial, indexed
-// by its workgroup id.
-constexpr int kMaxSegs = 32;
-struct DecodeSeg {
-  uint8_t *k, *v;  // K and V rows of token 0, KV head 0 (rows of head 1 follow at rs_h)
-  int64_t seq_k;   // keys held in the cache before this step's append (all attended)
-  int64_t t_new;   // row the fused step writes
-  int nblk, wg0;
-};
-struct DecodeSegIn {
-  uint8_t *k, *v;
-  int64_t seq_k;  // keys after the append (fused) or in the cache
-};
 struct DecodeArgs {
   DecodeSeg seg[kMaxSegs];
   int nseg, nwg, bpw;
@@ -79,7 +65,8 @@ struct WaveTab {
 // indexing this array: a pointer chosen at run time between two stages loses its LDS
 // address space, and the generic (flat) loads it then compiles to wait on every
 // outstanding buffer load, including the prefetch of the next block.
-constexpr int kMergeRow = 264;  // padded row of a wave's per-head output in tile order
+constexpr int kMergeRow = 268;  // padded row of a wave's per-head output in tile order: rows
+                                // 4 apart (lane groups g, g + 1) start 16 banks apart
 struct Smem {
   union {
     struct {
@@ -104,7 +91,11 @@ static_assert(sizeof(float[kWaves][8][kMergeRow]) + 2 * sizeof(float[kWaves][8])
 static_assert(sizeof(Smem) <= 160 * 1024, "LDS budget of one workgroup");
 
 // Stage this wave's KV head's 8 q rows (8 KB, contiguous in q) into LDS: eight
-// dwordx4 loads, lane l of load j moving bytes 1024 j + 16 l.
+// dwordx4 loads, lane l of load j moving bytes 1024 j + 16 l of q to LDS byte
+// kQRow j + 16 l. The 16-byte pad per row puts the rows' reads in build_q (one row per
+// lane, same column) on different banks.
+constexpr int kQRow = 1040;  // bytes per staged q row (256 floats + 16 bytes of pad)
+static_assert(8 * kQRow <= (int)sizeof(Stage), "q rows fit one stage");
 __device__ __forceinline__ void issue_q(void *dst_lds, u4s rq, uint32_t lane16) {
   const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)dst_lds));
   uint32_t saved;
@@ -112,19 +103,19 @@ __device__ __forceinline__ void issue_q(void *dst_lds, u4s rq, uint32_t lane16) 
       "s_mov_b32 %[sv], m0\n\t"
       "s_mov_b32 m0, %[d]\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o0], %[rq], 0 offen lds\n\t"
-      "s_add_u32 m0, %[d], 0x400\n\ts_nop 0\n\t"
+      "s_add_u32 m0, %[d], 0x410\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o1], %[rq], 0 offen lds\n\t"
-      "s_add_u32 m0, %[d], 0x800\n\ts_nop 0\n\t"
+      "s_add_u32 m0, %[d], 0x820\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o2], %[rq], 0 offen lds\n\t"
-      "s_add_u32 m0, %[d], 0xc00\n\ts_nop 0\n\t"
+      "s_add_u32 m0, %[d], 0xc30\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o3], %[rq], 0 offen lds\n\t"
-      "s_add_u32 m0, %[d], 0x1000\n\ts_nop 0\n\t"
+      "s_add_u32 m0, %[d], 0x1040\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o4], %[rq], 0 offen lds\n\t"
-      "s_add_u32 m0, %[d], 0x1400\n\ts_nop 0\n\t"
+      "s_add_u32 m0, %[d], 0x1450\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o5], %[rq], 0 offen lds\n\t"
-      "s_add_u32 m0, %[d], 0x1800\n\ts_nop 0\n\t"
+      "s_add_u32 m0, %[d], 0x1860\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o6], %[rq], 0 offen lds\n\t"
-      "s_add_u32 m0, %[d], 0x1c00\n\ts_nop 0\n\t"
+      "s_add_u32 m0, %[d], 0x1c70\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o7], %[rq], 0 offen lds\n\t"
       "s_mov_b32 m0, %[sv]"
       : [sv] "=&s"(saved)
@@ -410,7 +401,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
       asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
     else
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    const float *qrow = reinterpret_cast<const float *>(&sm.run.st[1][wave]) + (n & 7) * 256 + 64 * g;
+    const float *qrow = reinterpret_cast<const float *>(&sm.run.st[1][wave]) + (n & 7) * (kQRow / 4) + 64 * g;
     constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
     float qsum[2] = {0.0f, 0.0f};
 #pragma unroll
@@ -562,106 +553,6 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   }
 }
 
-// out[b][h][e] = (sum_w o_w 2^(m_w - M) + [new key]) / (sum_w l_w 2^(m_w - M) + [new key]).
-// One workgroup per (head, 32-entry slice of the tile-order row, batch): thread (ps, g4)
-// reads a float4 of entries and the (m, l) pair of every partial in slice ps of the
-// partials, all loads of a round issued before any is used. Slices keep their own
-// running max and merge through LDS. For a fused decode step the appended key enters
-// here, from its exactly dequantized K and V rows: score = clamp(q . k_new * scale),
-// weight 2^(score - M).
-constexpr int kCombSlices = 32;  // partial slices (8 threads each)
-constexpr int kCombChunk = 8;    // partials per slice per round
-struct CombineArgs {
-  const float *part;      // [wg][16][258]
-  const float *q, *dq;    // [nseg][16][256], [nseg][4][256] or null
-  float *out;             // [nseg][16][256]
-  float sl2;
-  int wg0[kMaxSegs + 1];  // segment s owns partials [wg0[s], wg0[s + 1])
-};
-__global__ __launch_bounds__(256) void q4k_decode_combine_kernel(CombineArgs c) {
-  __shared__ float dotp[4];
-  __shared__ float mx[kCombSlices], ls[kCombSlices];
-  __shared__ float4 accs[kCombSlices][8];
-  const int h = blockIdx.x >> 3, i0 = 32 * (blockIdx.x & 7), b = blockIdx.y;
-  const int tid = threadIdx.x, ps = tid >> 3, g4 = tid & 7;
-  const float *q = c.q, *dq = c.dq;
-  const float sl2 = c.sl2;
-  float *out = c.out;
-  const int nwg = c.wg0[b + 1] - c.wg0[b];
-  const float *P = c.part + (int64_t)c.wg0[b] * 16 * 258 + h * 258;
-  // new key: q . k_new products (reduced below, after the partial loads are issued)
-  const float prod = dq != nullptr ? q[((int64_t)b * 16 + h) * 256 + tid] *
-                                         dq[((int64_t)b * 4 + (h >> 3)) * 256 + tid]
-                                   : 0.0f;
-  const int per = (nwg + kCombSlices - 1) / kCombSlices;
-  const int w0 = ps * per, w1 = w0 + per < nwg ? w0 + per : nwg;
-  float m_loc = -INFINITY, lacc = 0.0f;
-  float4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int w = w0; w < w1; w += kCombChunk) {
-    float2 mlv[kCombChunk];
-    float4 ov[kCombChunk];
-#pragma unroll
-    for (int x = 0; x < kCombChunk; ++x) {
-      const bool ok = w + x < w1;
-      const float *pw = P + (int64_t)(w + x) * 16 * 258;
-      mlv[x] = ok ? *reinterpret_cast<const float2 *>(pw + 256) : float2{-INFINITY, 0.0f};
-      ov[x] = ok ? *reinterpret_cast<const float4 *>(pw + i0 + 4 * g4) : float4{0.f, 0.f, 0.f, 0.f};
-    }
-    float mc = m_loc;
-#pragma unroll
-    for (int x = 0; x < kCombChunk; ++x) mc = fmaxf(mc, mlv[x].x);
-    if (mc != -INFINITY) {
-      const float r = (m_loc == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_loc - mc);
-      acc.x *= r;
-      acc.y *= r;
-      acc.z *= r;
-      acc.w *= r;
-      lacc *= r;
-#pragma unroll
-      for (int x = 0; x < kCombChunk; ++x) {
-        const float f = (mlv[x].x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mlv[x].x - mc);
-        acc.x += f * ov[x].x;
-        acc.y += f * ov[x].y;
-        acc.z += f * ov[x].z;
-        acc.w += f * ov[x].w;
-        lacc += f * mlv[x].y;
-      }
-      m_loc = mc;
-    }
-  }
-  float d = prod;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) d += __shfl_xor(d, o, 64);
-  if ((tid & 63) == 0) dotp[tid >> 6] = d;
-  accs[ps][g4] = acc;
-  if (g4 == 0) {
-    mx[ps] = m_loc;
-    ls[ps] = lacc;
-  }
-  __syncthreads();
-  if (tid < 32) {
-    const float s_new = dq != nullptr
-                            ? fminf(fmaxf((dotp[0] + dotp[1] + dotp[2] + dotp[3]) * sl2, -kClampL2), kClampL2)
-                            : -INFINITY;
-    float M = s_new;
-#pragma unroll
-    for (int x = 0; x < kCombSlices; ++x) M = fmaxf(M, mx[x]);
-    float sum = 0.0f, L = 0.0f;
-    const float *accf = reinterpret_cast<const float *>(&accs[0][0]);
-#pragma unroll
-    for (int x = 0; x < kCombSlices; ++x) {
-      const float f = (mx[x] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mx[x] - M);
-      sum += f * accf[32 * x + tid];
-      L += f * ls[x];
-    }
-    const int e = tile_e((i0 + tid) >> 4, (i0 + tid) & 15);
-    const float f_new = (s_new == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_new - M);
-    L += f_new;
-    if (dq != nullptr) sum += f_new * dq[((int64_t)b * 4 + 2 + (h >> 3)) * 256 + e];
-    out[((int64_t)b * 16 + h) * 256 + e] = L > 0.0f ? sum / L : 0.0f;
-  }
-}
-
 }  // namespace
 
 // Plan and launch the decode and combine kernels over n <= kMaxSegs segments.
@@ -734,14 +625,9 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
   c.dq = fused ? d.dq : nullptr;
   c.out = out;
   c.sl2 = d.sl2;
-  hipLaunchKernelGGL(q4k_decode_combine_kernel, dim3(16 * 8, (unsigned)n), dim3(256), 0, s, c);
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(16 * 8, (unsigned)n), dim3(256), 0, s, c);
   PKV_HIP(hipGetLastError());
   return PKV_OK;
-}
-
-// Rows are addressed with 32-bit offsets (key * row stride) from a per-head base.
-static bool decode_rows_fit(int64_t seq_k, int64_t rs_t) {
-  return rs_t < (1 << 24) && seq_k < (1 << 24) && (uint64_t)seq_k * (uint64_t)rs_t < (1ull << 32);
 }
 
 int launch_attend_mfma(const AttnArgs &a, const float *k_new, const float *v_new, uint8_t *kc,

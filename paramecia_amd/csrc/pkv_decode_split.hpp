@@ -1,0 +1,153 @@
+// Split-K decode plumbing shared by the decode kernels (Q4K MFMA, Q8_0): the segment
+// table of one launch, and the kernel that merges the per-workgroup partials of each
+// segment and adds the appended key of a fused decode step. Include-only; every
+// symbol has internal linkage.
+//
+// Partial layout: part[wg][16 heads][258]: entries 0-255 the un-normalised output in
+// tile order (entry 16 T + n holds element tile_e(T, n)), then the running max m (log2
+// units) and the sum l of 2^(score - m).
+#pragma once
+#include "pkv_internal.hpp"
+
+namespace pkv {
+namespace {
+
+constexpr float kSplitClampL2 = 100.0f * 1.4426950408889634f;  // +-100 nats in log2 units
+
+// e (0..255) of tile-order entry 16 T + n
+__device__ __forceinline__ int tile_e(int T, int n) {
+  const int h = T >> 3, byte = (T >> 1) & 3, hl = T & 1;
+  const int c = 2 * h + (n >> 3);
+  return 64 * c + 32 * hl + 4 * (n & 7) + byte;
+}
+// tile-order entry of element e (the inverse of tile_e)
+__host__ __device__ __forceinline__ int tile_index(int e) {
+  const int c = e >> 6, hl = (e >> 5) & 1, r = e & 31;
+  const int n = 8 * (c & 1) + (r >> 2), T = 8 * (c >> 1) + 2 * (r & 3) + hl;
+  return 16 * T + n;
+}
+
+// One launch serves up to kMaxSegs segments: the batch rows of one cache, or the
+// sequences of a batched decode step (each with its own cache and length). Segment s
+// owns workgroups [wg0, next wg0); every workgroup writes one split-K partial, indexed
+// by its workgroup id.
+constexpr int kMaxSegs = 32;
+struct DecodeSeg {
+  uint8_t *k, *v;  // K and V rows of token 0, KV head 0 (rows of head 1 follow at rs_h)
+  int64_t seq_k;   // keys held in the cache before this step's append (all attended)
+  int64_t t_new;   // row the fused step writes
+  int nblk, wg0;
+};
+struct DecodeSegIn {
+  uint8_t *k, *v;
+  int64_t seq_k;  // keys after the append (fused) or in the cache
+};
+// out[b][h][e] = (sum_w o_w 2^(m_w - M) + [new key]) / (sum_w l_w 2^(m_w - M) + [new key]).
+// One workgroup per (head, 32-entry slice of the tile-order row, batch): thread (ps, g4)
+// reads a float4 of entries and the (m, l) pair of every partial in slice ps of the
+// partials, all loads of a round issued before any is used. Slices keep their own
+// running max and merge through LDS. For a fused decode step the appended key enters
+// here, from its exactly dequantized K and V rows: score = clamp(q . k_new * scale),
+// weight 2^(score - M).
+constexpr int kCombSlices = 32;  // partial slices (8 threads each)
+constexpr int kCombChunk = 8;    // partials per slice per round
+struct CombineArgs {
+  const float *part;      // [wg][16][258]
+  const float *q, *dq;    // [nseg][16][256], [nseg][4][256] or null
+  float *out;             // [nseg][16][256]
+  float sl2;
+  int wg0[kMaxSegs + 1];  // segment s owns partials [wg0[s], wg0[s + 1])
+};
+__global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs c) {
+  __shared__ float dotp[4];
+  __shared__ float mx[kCombSlices], ls[kCombSlices];
+  __shared__ float4 accs[kCombSlices][8];
+  const int h = blockIdx.x >> 3, i0 = 32 * (blockIdx.x & 7), b = blockIdx.y;
+  const int tid = threadIdx.x, ps = tid >> 3, g4 = tid & 7;
+  const float *q = c.q, *dq = c.dq;
+  const float sl2 = c.sl2;
+  float *out = c.out;
+  const int nwg = c.wg0[b + 1] - c.wg0[b];
+  const float *P = c.part + (int64_t)c.wg0[b] * 16 * 258 + h * 258;
+  // new key: q . k_new products (reduced below, after the partial loads are issued)
+  const float prod = dq != nullptr ? q[((int64_t)b * 16 + h) * 256 + tid] *
+                                         dq[((int64_t)b * 4 + (h >> 3)) * 256 + tid]
+                                   : 0.0f;
+  const int per = (nwg + kCombSlices - 1) / kCombSlices;
+  const int w0 = ps * per, w1 = w0 + per < nwg ? w0 + per : nwg;
+  float m_loc = -INFINITY, lacc = 0.0f;
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int w = w0; w < w1; w += kCombChunk) {
+    float2 mlv[kCombChunk];
+    float4 ov[kCombChunk];
+#pragma unroll
+    for (int x = 0; x < kCombChunk; ++x) {
+      const bool ok = w + x < w1;
+      const float *pw = P + (int64_t)(w + x) * 16 * 258;
+      mlv[x] = ok ? *reinterpret_cast<const float2 *>(pw + 256) : float2{-INFINITY, 0.0f};
+      ov[x] = ok ? *reinterpret_cast<const float4 *>(pw + i0 + 4 * g4) : float4{0.f, 0.f, 0.f, 0.f};
+    }
+    float mc = m_loc;
+#pragma unroll
+    for (int x = 0; x < kCombChunk; ++x) mc = fmaxf(mc, mlv[x].x);
+    if (mc != -INFINITY) {
+      const float r = (m_loc == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_loc - mc);
+      acc.x *= r;
+      acc.y *= r;
+      acc.z *= r;
+      acc.w *= r;
+      lacc *= r;
+#pragma unroll
+      for (int x = 0; x < kCombChunk; ++x) {
+        const float f = (mlv[x].x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mlv[x].x - mc);
+        acc.x += f * ov[x].x;
+        acc.y += f * ov[x].y;
+        acc.z += f * ov[x].z;
+        acc.w += f * ov[x].w;
+        lacc += f * mlv[x].y;
+      }
+      m_loc = mc;
+    }
+  }
+  float d = prod;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) d += __shfl_xor(d, o, 64);
+  if ((tid & 63) == 0) dotp[tid >> 6] = d;
+  accs[ps][g4] = acc;
+  if (g4 == 0) {
+    mx[ps] = m_loc;
+    ls[ps] = lacc;
+  }
+  __syncthreads();
+  if (tid < 32) {
+    const float s_new = dq != nullptr
+                            ? fminf(fmaxf((dotp[0] + dotp[1] + dotp[2] + dotp[3]) * sl2, -kSplitClampL2), kSplitClampL2)
+                            : -INFINITY;
+    float M = s_new;
+#pragma unroll
+    for (int x = 0; x < kCombSlices; ++x) M = fmaxf(M, mx[x]);
+    float sum = 0.0f, L = 0.0f;
+    const float *accf = reinterpret_cast<const float *>(&accs[0][0]);
+#pragma unroll
+    for (int x = 0; x < kCombSlices; ++x) {
+      const float f = (mx[x] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mx[x] - M);
+      sum += f * accf[32 * x + tid];
+      L += f * ls[x];
+    }
+    const int e = tile_e((i0 + tid) >> 4, (i0 + tid) & 15);
+    const float f_new = (s_new == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_new - M);
+    L += f_new;
+    if (dq != nullptr) sum += f_new * dq[((int64_t)b * 4 + 2 + (h >> 3)) * 256 + e];
+    out[((int64_t)b * 16 + h) * 256 + e] = L > 0.0f ? sum / L : 0.0f;
+  }
+}
+
+
+}  // namespace
+
+// Rows are addressed with 32-bit offsets (key * row stride) from a per-head base.
+static inline bool decode_rows_fit(int64_t seq_k, int64_t rs_t) {
+  return rs_t < (1 << 24) && seq_k < (1 << 24) && (uint64_t)seq_k * (uint64_t)rs_t < (1ull << 32);
+}
+
+}  // namespace pkv

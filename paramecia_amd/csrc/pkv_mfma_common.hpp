@@ -3,6 +3,7 @@
 // staging layout of 32-key blocks with its buffer_load ... lds issue, and cross-lane
 // reductions. Include-only; every symbol has internal linkage.
 #pragma once
+#include "pkv_decode_split.hpp"
 #include "pkv_internal.hpp"
 #include "pkv_scalar.hpp"
 
@@ -197,12 +198,6 @@ __device__ __forceinline__ float xsum32(float x) {  // x of lanes l and l ^ 32, 
   return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
 }
 
-// e (0..255) of PV tile T at lane column n
-__device__ __forceinline__ int tile_e(int T, int n) {
-  const int h = T >> 3, byte = (T >> 1) & 3, hl = T & 1;
-  const int c = 2 * h + (n >> 3);
-  return 64 * c + 32 * hl + 4 * (n & 7) + byte;
-}
 
 }  // namespace
 }  // namespace pkv

@@ -1,0 +1,328 @@
+// Decode attention over a Q8_0 cache for the Qwen3-Next full-attention shape (16 query
+// heads, 2 KV heads, head_dim 256), gfx950.
+//
+// Role: the reference's only GPU attention over quantized K/V, flash_attn_q8
+// (paramecia-model/src/ops.rs:756-792, called at qwen3_next.rs:2531-2561), for a decode
+// step (one query that sees every key), and the CPU SDPA it replaces
+// (qwen3_next.rs:2580-2605). A Q8_0 row is 8 blocks of {f16 d, 32 x int8}: element e is
+// int8 * d of block e / 32 (BlockQ8_0::to_float).
+//
+// Work split: a workgroup of 512 threads owns a contiguous key range of one segment
+// (one cache's batch row, or one sequence of a batched decode step) and both KV heads;
+// threads 0-255 take KV head 0, threads 256-511 head 1. The range streams through LDS
+// in chunks of 32 keys (K and V rows of both heads, 34.8 KB): QK with one thread per
+// (query head, key), an online softmax per query head over the chunk, then PV with one
+// thread per output element e for the group's 8 query heads. Each workgroup writes one
+// split-K partial in tile order; decode_combine_kernel merges them (and the new key of
+// a fused step). Dequantization is exact (int8 * d in f32, as the reference's to_float),
+// all products and sums f32.
+//
+// Fused append: workgroups 0 .. 4 * segments - 1 first quantize one new row each
+// (BlockQ8_0::from_float, bit-exact) and publish it dequantized for the combine.
+#include "pkv_decode_split.hpp"
+#include "pkv_scalar.hpp"
+
+namespace pkv {
+namespace {
+
+constexpr int kQ8Row = 272;    // bytes of one head's row: 8 blocks x 34
+constexpr int kQ8Chunk = 32;   // keys per LDS chunk
+constexpr int kQ8Threads = 512;
+constexpr int kQ8RowWords = kQ8Row / 4;  // 68 dwords, 16-byte aligned rows (272 = 17 x 16)
+
+struct Q8Args {
+  DecodeSeg seg[kMaxSegs];
+  int nseg, nwg, kpw;  // segments, workgroups, keys per workgroup (a multiple of 32)
+  int64_t rs_t, rs_h;
+  float sl2;
+  const float *q;              // [nseg][16][256]
+  const float *k_new, *v_new;  // [nseg][2][256] or null
+  float *part;                 // [nwg][16][258]
+  float *dq;                   // [nseg][4][256]
+};
+
+struct Q8Smem {
+  uint32_t k[2][kQ8Chunk][kQ8RowWords];  // [kv][key][dword]
+  uint32_t v[2][kQ8Chunk][kQ8RowWords];
+  float q[16][256];
+  float p[2][kQ8Chunk][8];  // weights [kv][key][head of the group]
+  float alpha[2][8];        // rescale of the running sums for this chunk
+};
+
+// BlockQ8_0::from_float of one 256-element row by 256 threads (thread e owns element
+// e): d = amax / 127 of its 32-block, q = round(x / d) saturated to i8, d stored as
+// f16. Returns the dequantized element (q * f16(d), the reference's to_float).
+__device__ float q8_quantize_row_lanes(float x, uint8_t *row, int e) {
+#pragma clang fp contract(off)
+  float amax = __builtin_fabsf(x);
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) amax = fmax_rs(amax, __shfl_xor(amax, o, 32));
+  // amax: maxNum fold from +0 of |x| over the block; the order does not matter for
+  // maxNum, so the butterfly equals the sequential fold.
+  amax = fmax_rs(amax, 0.0f);
+  const float d = amax / 127.0f;
+  const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+  const int32_t qv = rs_as_i8(__builtin_roundf(x * id));
+  const uint16_t dh = f32_to_f16(d);
+  uint8_t *blk = row + (e >> 5) * 34;
+  blk[2 + (e & 31)] = (uint8_t)qv;
+  if ((e & 31) == 0) {
+    blk[0] = (uint8_t)(dh & 0xFF);
+    blk[1] = (uint8_t)(dh >> 8);
+  }
+  return (float)qv * f16_to_f32(dh);
+}
+
+// exact f16 -> f32 of the low (hi = 0) or high half of a dword (hardware conversion)
+__device__ __forceinline__ float h16(uint32_t w, int hi) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? (w >> 16) : (w & 0xFFFF)));
+}
+
+__global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
+  __shared__ Q8Smem sm;
+  const int tid = threadIdx.x, half = tid >> 8, t = tid & 255;
+  const int wg = blockIdx.x;
+  int b = 0;
+  while (b + 1 < a.nseg && wg >= a.seg[b + 1].wg0) ++b;
+  const DecodeSeg &sg = a.seg[b];
+  const int64_t k0 = (int64_t)(wg - sg.wg0) * a.kpw;
+  const int64_t k1 = k0 + a.kpw < sg.seq_k ? k0 + a.kpw : sg.seq_k;
+
+  // ---- fused append: new row r = 4 s + 2 p + kv (K p = 0, V p = 1), one per workgroup
+  if (a.k_new != nullptr && half == 0) {
+    for (int row = wg; row < 4 * a.nseg; row += a.nwg) {
+      const int rs = row >> 2, p = (row >> 1) & 1, kvr = row & 1;
+      const float x = (p ? a.v_new : a.k_new)[((int64_t)rs * 2 + kvr) * 256 + t];
+      const DecodeSeg &rg = a.seg[rs];
+      uint8_t *dst = (p ? rg.v : rg.k) + rg.t_new * a.rs_t + kvr * a.rs_h;
+      a.dq[(int64_t)row * 256 + t] = q8_quantize_row_lanes(x, dst, t);
+    }
+  }
+
+  // ---- q of the 16 heads into LDS
+  {
+    const float4 *q4 = reinterpret_cast<const float4 *>(a.q + (int64_t)b * 16 * 256);
+    float4 *s4 = reinterpret_cast<float4 *>(&sm.q[0][0]);
+    s4[tid] = q4[tid];
+    s4[tid + 512] = q4[tid + 512];
+  }
+
+  // QK role: (head hh of the group, key kk of the chunk); PV role: element e = t
+  const int hh = t >> 5, kk = t & 31;
+  float m_run = -INFINITY, l_run = 0.0f;  // QK role: this thread's head
+  float acc[8];
+#pragma unroll
+  for (int h = 0; h < 8; ++h) acc[h] = 0.0f;
+
+  for (int64_t c0 = k0; c0 < k1; c0 += kQ8Chunk) {
+    const int nk = (int)(k1 - c0 < kQ8Chunk ? k1 - c0 : kQ8Chunk);
+    __syncthreads();  // the previous chunk's readers are done
+    // ---- stage the chunk: K and V rows of both heads, 2 x 2 x 32 x 68 dwords
+    {
+      constexpr int kWords = 2 * kQ8Chunk * kQ8RowWords;  // per tensor
+      constexpr int kPer = (kWords + kQ8Threads - 1) / kQ8Threads;
+      uint32_t kv_[2][kPer];
+#pragma unroll
+      for (int x = 0; x < kPer; ++x) {
+        const int i = tid + x * kQ8Threads;
+        const int kvh = i / (kQ8Chunk * kQ8RowWords), r = i % (kQ8Chunk * kQ8RowWords);
+        const int key = r / kQ8RowWords, w = r % kQ8RowWords;
+        const bool ok = i < kWords && key < nk;
+        const int64_t off = (c0 + (ok ? key : 0)) * a.rs_t + kvh * a.rs_h + 4 * w;
+        kv_[0][x] = ok ? *reinterpret_cast<const uint32_t *>(sg.k + off) : 0u;
+        kv_[1][x] = ok ? *reinterpret_cast<const uint32_t *>(sg.v + off) : 0u;
+      }
+#pragma unroll
+      for (int x = 0; x < kPer; ++x) {
+        const int i = tid + x * kQ8Threads;
+        if (i < kWords) {
+          (&sm.k[0][0][0])[i] = kv_[0][x];
+          (&sm.v[0][0][0])[i] = kv_[1][x];
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- QK: score of (head 8 half + hh, key kk) = sum_j d_j sum_i q8 * q
+    {
+      const uint32_t *krow = sm.k[half][kk];
+      const float *qh = sm.q[8 * half + hh];
+      float s = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        // block j: bytes 34 j .. 34 j + 33 of the row (d, then 32 int8)
+        const int o = 34 * j;
+        const float d = h16(krow[o >> 2], (o >> 1) & 1);
+        float part = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          const int ob = o + 2 + i;
+          const int8_t qb = (int8_t)(krow[ob >> 2] >> (8 * (ob & 3)));
+          part += (float)qb * qh[32 * j + i];
+        }
+        s += part * d;
+      }
+      // log2 units, clamped at +-100 nats; keys past the chunk are masked
+      float s2 = fminf(fmaxf(s * a.sl2, -kSplitClampL2), kSplitClampL2);
+      if (kk >= nk) s2 = -INFINITY;
+      float mc = s2;
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) mc = fmaxf(mc, __shfl_xor(mc, o, 32));
+      const float m_new = fmaxf(m_run, mc);
+      const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      const float p = (s2 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s2 - m_new);
+      float ps = p;
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) ps += __shfl_xor(ps, o, 32);
+      l_run = l_run * alpha + ps;
+      m_run = m_new;
+      sm.p[half][kk][hh] = p;
+      if (kk == 0) sm.alpha[half][hh] = alpha;
+    }
+    __syncthreads();
+
+    // ---- PV: element e = t of the 8 heads: acc = acc * alpha + sum_k p * (d_j * q8)
+    {
+      const int e = t, j = e >> 5, ob = 34 * j + 2 + (e & 31);
+#pragma unroll
+      for (int h = 0; h < 8; ++h) acc[h] *= sm.alpha[half][h];
+      for (int key = 0; key < nk; ++key) {
+        const uint32_t *vrow = sm.v[half][key];
+        const float d = h16(vrow[(34 * j) >> 2], ((34 * j) >> 1) & 1);
+        const int8_t qb = (int8_t)(vrow[ob >> 2] >> (8 * (ob & 3)));
+        const float vv = (float)qb * d;
+        const float4 p0 = *reinterpret_cast<const float4 *>(&sm.p[half][key][0]);
+        const float4 p1 = *reinterpret_cast<const float4 *>(&sm.p[half][key][4]);
+        acc[0] += p0.x * vv;
+        acc[1] += p0.y * vv;
+        acc[2] += p0.z * vv;
+        acc[3] += p0.w * vv;
+        acc[4] += p1.x * vv;
+        acc[5] += p1.y * vv;
+        acc[6] += p1.z * vv;
+        acc[7] += p1.w * vv;
+      }
+    }
+  }
+
+  // ---- partial of this workgroup (tile order), m and l per head
+  float *P = a.part + (int64_t)wg * 16 * 258;
+  const int idx = tile_index(t);
+#pragma unroll
+  for (int h = 0; h < 8; ++h) P[(8 * half + h) * 258 + idx] = acc[h];
+  if (kk == 0) {
+    P[(8 * half + hh) * 258 + 256] = m_run;
+    P[(8 * half + hh) * 258 + 257] = l_run;
+  }
+}
+
+}  // namespace
+
+// Plan and launch the Q8_0 decode and the combine over n <= kMaxSegs segments.
+static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, const float *k_new,
+                              const float *v_new, float *out, int64_t rs_t, int64_t rs_h,
+                              float scale, Workspace &ws, hipStream_t s) {
+  Q8Args d;
+  const bool fused = k_new != nullptr;
+  int64_t longest = 0;
+  for (int i = 0; i < n; ++i) {
+    d.seg[i].k = in[i].k;
+    d.seg[i].v = in[i].v;
+    d.seg[i].seq_k = fused ? in[i].seq_k - 1 : in[i].seq_k;
+    d.seg[i].t_new = in[i].seq_k - 1;
+    d.seg[i].nblk = 0;
+    if (d.seg[i].seq_k > longest) longest = d.seg[i].seq_k;
+  }
+  // keys per workgroup: one 32-key chunk while that keeps <= 512 partials per
+  // segment, more chunks per workgroup for longer caches
+  int64_t kpw = (longest + 511) / 512;
+  kpw = (kpw + kQ8Chunk - 1) / kQ8Chunk * kQ8Chunk;
+  if (kpw < kQ8Chunk) kpw = kQ8Chunk;
+  CombineArgs c;
+  int wg = 0;
+  for (int i = 0; i < n; ++i) {
+    d.seg[i].wg0 = wg;
+    c.wg0[i] = wg;
+    const int64_t w = d.seg[i].seq_k > 0 ? (d.seg[i].seq_k + kpw - 1) / kpw : 1;
+    wg += (int)w;
+  }
+  c.wg0[n] = wg;
+  d.nseg = n;
+  d.nwg = wg;
+  d.kpw = (int)kpw;
+  d.rs_t = rs_t;
+  d.rs_h = rs_h;
+  d.sl2 = scale * 1.4426950408889634f;
+  d.q = q;
+  d.k_new = k_new;
+  d.v_new = v_new;
+  const size_t part_floats = (size_t)wg * 16 * 258;
+  const size_t need = (part_floats + (size_t)n * 4 * 256) * sizeof(float);
+  int rc = ws.reserve(need);
+  if (rc) return rc;
+  d.part = static_cast<float *>(ws.ptr);
+  d.dq = d.part + part_floats;
+  hipLaunchKernelGGL(q8_decode_kernel, dim3((unsigned)wg), dim3(kQ8Threads), 0, s, d);
+  PKV_HIP(hipGetLastError());
+  c.part = d.part;
+  c.q = q;
+  c.dq = fused ? d.dq : nullptr;
+  c.out = out;
+  c.sl2 = d.sl2;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(16 * 8, (unsigned)n), dim3(256), 0, s, c);
+  PKV_HIP(hipGetLastError());
+  return PKV_OK;
+}
+
+int launch_attend_q8(const AttnArgs &a, const float *k_new, const float *v_new, uint8_t *kc,
+                     uint8_t *vc, int64_t t_new, Workspace &ws, hipStream_t s) {
+  if (a.quant != PKV_QUANT_Q8_0 || a.head_dim != 256 || a.num_heads != 16 ||
+      a.num_kv_heads != 2 || a.l != 1)
+    return PKV_ERR_UNSUPPORTED;
+  if (a.causal && a.q_offset + 1 < a.seq_k) return PKV_ERR_UNSUPPORTED;
+  const bool fused = k_new != nullptr;
+  if (fused && (kc != a.k || vc != a.v || t_new != a.seq_k - 1)) return PKV_ERR_UNSUPPORTED;
+  if (a.rs.h != kQ8Row || !decode_rows_fit(a.seq_k, a.rs.t)) return PKV_ERR_UNSUPPORTED;
+  for (int b0 = 0; b0 < a.batch; b0 += kMaxSegs) {
+    const int nb = a.batch - b0 < kMaxSegs ? a.batch - b0 : kMaxSegs;
+    DecodeSegIn in[kMaxSegs];
+    for (int i = 0; i < nb; ++i) {
+      in[i].k = const_cast<uint8_t *>(a.k) + (int64_t)(b0 + i) * a.rs.b;
+      in[i].v = const_cast<uint8_t *>(a.v) + (int64_t)(b0 + i) * a.rs.b;
+      in[i].seq_k = a.seq_k;
+    }
+    const int64_t qo = (int64_t)b0 * 16 * 256, ko = (int64_t)b0 * 2 * 256;
+    const int rc = launch_q8_segments(in, nb, a.q + qo, fused ? k_new + ko : nullptr,
+                                      fused ? v_new + ko : nullptr, a.out + qo, a.rs.t, a.rs.h,
+                                      a.scale, ws, s);
+    if (rc) return rc;
+  }
+  return PKV_OK;
+}
+
+int launch_append_attend_batched_q8(int quant, const SeqDesc *seqs, int n, const float *k,
+                                    const float *v, const float *q, int num_heads,
+                                    int num_kv_heads, int head_dim, float scale, float *out,
+                                    Workspace &ws, hipStream_t s) {
+  if (quant != PKV_QUANT_Q8_0 || head_dim != 256 || num_heads != 16 || num_kv_heads != 2)
+    return PKV_ERR_UNSUPPORTED;
+  const int64_t rs_t = 2 * kQ8Row, rs_h = kQ8Row;
+  for (int i = 0; i < n; ++i)
+    if (seqs[i].len < 1 || !decode_rows_fit(seqs[i].len, rs_t)) return PKV_ERR_UNSUPPORTED;
+  for (int b0 = 0; b0 < n; b0 += kMaxSegs) {
+    const int nb = n - b0 < kMaxSegs ? n - b0 : kMaxSegs;
+    DecodeSegIn in[kMaxSegs];
+    for (int i = 0; i < nb; ++i) {
+      in[i].k = seqs[b0 + i].k;
+      in[i].v = seqs[b0 + i].v;
+      in[i].seq_k = seqs[b0 + i].len;
+    }
+    const int64_t qo = (int64_t)b0 * 16 * 256, ko = (int64_t)b0 * 2 * 256;
+    const int rc = launch_q8_segments(in, nb, q + qo, k + ko, v + ko, out + qo, rs_t, rs_h,
+                                      scale, ws, s);
+    if (rc) return rc;
+  }
+  return PKV_OK;
+}
+
+}  // namespace pkv

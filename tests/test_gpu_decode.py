@@ -191,3 +191,85 @@ def test_batched_outliers_config5_shape(pk, orc):
     lens = [max(1, S // 8) for S in W.c5_lengths()]
     worst = run_batched(pk, orc, lens, seed=22, chans=W.c5_channels())
     say(f"batched decode, config-5 shape: max|diff| = {worst:.3e}")
+
+
+# ---- Q8_0 decode (the flash_attn_q8 role): same shape, 272-byte rows
+Q8_0 = 3
+
+
+def run_decode_q8(pk, orc, S, B=1, fused=True, seed=0, chans=None):
+    rng = np.random.default_rng(seed)
+    g = pk.PreallocatedQuantizedKvCache(B, 2, S + 1, 256, pk.KvCacheQuantization.Q8_0)
+    c = orc.Cache(Q8_0, B, 2, 256, S + 1)
+    k = rng.standard_normal((B, 2, S, 256)).astype(np.float32)
+    v = rng.standard_normal((B, 2, S, 256)).astype(np.float32)
+    q = rng.standard_normal((B, 1, 16, 256)).astype(np.float32)
+    kn = rng.standard_normal((B, 2, 1, 256)).astype(np.float32)
+    vn = rng.standard_normal((B, 2, 1, 256)).astype(np.float32)
+    if chans is not None:
+        for x in (k, v, kn, vn):
+            x[..., chans] *= 20.0
+    if S > 0:
+        g.append_quantized(dev(k), dev(v))
+        assert c.append(k, v) == 0
+    if fused:
+        out = g.append_attend(dev(kn), dev(vn), dev(q), 1 / 16)
+        assert c.append(kn, vn) == 0
+        seq = S + 1
+    else:
+        out = g.attend(dev(q), 1 / 16, S - 1, True)
+        seq = S
+    ref = c.attend(q, 1 / 16, seq - 1, True, mode="f32")
+    got = host(out)
+    np.testing.assert_allclose(got, ref, atol=ATOL, rtol=RTOL)
+    gk, gv = g.raw_bytes()
+    ok, ov = c.valid_bytes()
+    assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
+    return np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("S", [0, 1, 31, 32, 33, 511, 512, 513, 4096, 20000])
+def test_q8_decode_fused(pk, orc, S):
+    say(f"Q8_0 fused decode S={S}")
+    run_decode_q8(pk, orc, S, fused=True, seed=300 + S)
+
+
+@pytest.mark.parametrize("S", [1, 64, 4097])
+def test_q8_decode_attend_only(pk, orc, S):
+    say(f"Q8_0 attend-only decode S={S}")
+    run_decode_q8(pk, orc, S, fused=False, seed=400 + S)
+
+
+def test_q8_decode_batch2_outliers(pk, orc):
+    say("Q8_0 decode batch 2, outlier channels")
+    from paramecia_amd import workloads as W
+    run_decode_q8(pk, orc, 3000, B=2, seed=500, chans=W.c5_channels())
+
+
+def test_q8_batched_varlen(pk, orc):
+    say("Q8_0 batched decode, varied lengths")
+    rng = np.random.default_rng(23)
+    lens = [0, 1, 33, 700, 2500]
+    caches, oracles = [], []
+    for S in lens:
+        g = pk.PreallocatedQuantizedKvCache(1, 2, S + 1, 256, pk.KvCacheQuantization.Q8_0)
+        c = orc.Cache(Q8_0, 1, 2, 256, S + 1)
+        if S > 0:
+            k = rng.standard_normal((1, 2, S, 256)).astype(np.float32)
+            v = rng.standard_normal((1, 2, S, 256)).astype(np.float32)
+            g.append_quantized(dev(k), dev(v))
+            assert c.append(k, v) == 0
+        caches.append(g)
+        oracles.append(c)
+    n = len(lens)
+    kn = rng.standard_normal((n, 2, 256)).astype(np.float32)
+    vn = rng.standard_normal((n, 2, 256)).astype(np.float32)
+    q = rng.standard_normal((n, 16, 256)).astype(np.float32)
+    out = host(pk.append_attend_batched(caches, dev(kn), dev(vn), dev(q), 1 / 16))
+    for i, (g, c, S) in enumerate(zip(caches, oracles, lens)):
+        assert c.append(kn[i][None, :, None], vn[i][None, :, None]) == 0
+        ref = c.attend(q[i][None, None], 1 / 16, S, True, mode="f32")[0, 0]
+        np.testing.assert_allclose(out[i], ref, atol=ATOL, rtol=RTOL)
+        gk, gv = g.raw_bytes()
+        ok, ov = c.valid_bytes()
+        assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
