@@ -65,8 +65,6 @@ struct WaveTab {
 // indexing this array: a pointer chosen at run time between two stages loses its LDS
 // address space, and the generic (flat) loads it then compiles to wait on every
 // outstanding buffer load, including the prefetch of the next block.
-constexpr int kMergeRow = 268;  // padded row of a wave's per-head output in tile order: rows
-                                // 4 apart (lane groups g, g + 1) start 16 banks apart
 struct Smem {
   union {
     struct {
@@ -80,14 +78,14 @@ struct Smem {
       } t;
     } run;
     struct {
-      float o[kWaves][8][kMergeRow];
-      float m[kWaves][8], l[kWaves][8];
+      float4 o[kWaves][16][2][16];  // [wave][T2][row group g][n]: rows 4g..4g+3, scaled
     } merge;
   };
 };
 static_assert(sizeof(Q4kScratch) + 4 <= sizeof(WaveTab), "quantizer scratch within wave 0's tables");
-static_assert(sizeof(float[kWaves][8][kMergeRow]) + 2 * sizeof(float[kWaves][8]) <=
-                  sizeof(Stage[kWaves]), "merge area within the st[0] buffers");
+static_assert(sizeof(float4[kWaves][16][2][16]) <= sizeof(Stage[kWaves]),
+              "merge area within the st[0] buffers");
+static_assert(24 <= kBlk, "m, l and f * l of 8 heads fit a wave's vmd table");
 static_assert(sizeof(Smem) <= 160 * 1024, "LDS budget of one workgroup");
 
 // Stage this wave's KV head's 8 q rows (8 KB, contiguous in q) into LDS: eight
@@ -404,6 +402,9 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
     const float *qrow = reinterpret_cast<const float *>(&sm.run.st[1][wave]) + (n & 7) * (kQRow / 4) + 64 * g;
     constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
     float qsum[2] = {0.0f, 0.0f};
+    // hi lanes (n < 8) take fp16(q), lo lanes fp16(q - fp16(q)): both are fp16(q - c)
+    // with c = fp16(q) masked to zero on the hi lanes
+    const uint32_t lo_mask = n < 8 ? 0u : 0xFFFFFFFFu;
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
       const float4 r0 = *reinterpret_cast<const float4 *>(qrow + 32 * (st >> 2) + 8 * (st & 3));
@@ -411,12 +412,15 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
       const float v8[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
 #pragma unroll
       for (int k = 0; k < 8; ++k) qsum[st >> 2] += v8[k];
+      uint32_t w[4];
 #pragma unroll
-      for (int slot = 0; slot < 8; ++slot) {
-        const float qv = v8[perm[slot]];
-        const _Float16 hi = (_Float16)qv;
-        qb[st][slot] = (n < 8) ? hi : (_Float16)(qv - (float)hi);
+      for (int pp = 0; pp < 4; ++pp) {
+        const float a0 = v8[perm[2 * pp]], a1 = v8[perm[2 * pp + 1]];
+        const h2 h = {(_Float16)a0, (_Float16)a1};
+        const uint32_t c = as_u(h) & lo_mask;
+        w[pp] = mix_sub_hi(mix_sub_lo(a0, c), a1, c);
       }
+      qb[st] = __builtin_bit_cast(h8, u4{w[0], w[1], w[2], w[3]});
     }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -482,7 +486,8 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
     }
     __builtin_amdgcn_s_setprio(0);
   }
-  // ---- per-wave reductions
+  // ---- epilogue: per-wave reductions, then the four waves of each KV head merged into
+  // this workgroup's partial
   S.lsum += __shfl_xor(S.lsum, 16);
   S.lsum += __shfl_xor(S.lsum, 32);
   // hi rows 4g+i (lanes g < 2) plus lo rows 8+4g+i (lanes g + 2, 32 lanes up)
@@ -492,64 +497,78 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
     for (int i = 0; i < 4; ++i) S.acc[T2][i] = xsum32(S.acc[T2][i]);
 #pragma unroll
   for (int i = 0; i < 4; ++i) S.accm[i] = xsum32(S.accm[i]);
-  // min term per [head][j] (accm row 4g+i, column j = n) through this wave's own table
-  // area, then O'[head][e] = acc - cmin[head][e / 32] on lanes g < 2 (row 4g+i = head)
+  // Exchange through this wave's own table area (no other wave reads it before the
+  // barrier): min term cmin[head][j] (accm row 4g+i, column j = n), and ml = {m of
+  // heads 0-7, l of heads 0-7, f * l of heads 0-7}.
   float(*cmin)[8] = reinterpret_cast<float(*)[8]>(&T.kd[0]);
+  float *ml = T.vmd;
   if (g < 2 && n < 8) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) cmin[4 * g + i][n] = S.accm[i];
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  float o[16][4];
-#pragma unroll
-  for (int T2 = 0; T2 < 16; ++T2) {
-    const int e = tile_e(T2, n);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[T2][i] = S.acc[T2][i] - cmin[(4 * g + i) & 7][e >> 5];
+  if (g == 0 && n < 8) {
+    ml[n] = S.m_run;
+    ml[8 + n] = S.lsum;
   }
   __syncthreads();  // every wave has left the loop: the st[0] buffers become the merge area
-  // per-wave output in tile order: row head, index 16 T2 + n
+  // weights f = 2^(m - M) of this wave's rows against the four waves of its KV head
+  auto weight = [&](int h) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) M = fmaxf(M, sm.run.t.tab[2 * s4 + kv].vmd[h]);
+    const float mine = ml[h];
+    return (mine == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mine - M);
+  };
   if (g < 2) {
+    float fr[4];
 #pragma unroll
-    for (int T2 = 0; T2 < 16; ++T2)
+    for (int i = 0; i < 4; ++i) fr[i] = weight(4 * g + i);
+    // scaled output rows 4g..4g+3: (acc - cmin[row][e / 32]) * f, one float4 per tile
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sm.merge.o[wave][4 * g + i][16 * T2 + n] = o[T2][i];
+    for (int T2 = 0; T2 < 16; ++T2) {
+      const int j = tile_e(T2, n) >> 5;
+      float4 v;
+      v.x = (S.acc[T2][0] - cmin[4 * g + 0][j]) * fr[0];
+      v.y = (S.acc[T2][1] - cmin[4 * g + 1][j]) * fr[1];
+      v.z = (S.acc[T2][2] - cmin[4 * g + 2][j]) * fr[2];
+      v.w = (S.acc[T2][3] - cmin[4 * g + 3][j]) * fr[3];
+      sm.merge.o[wave][T2][g][n] = v;
+    }
   }
-  if (g == 0 && n < 8) {
-    sm.merge.m[wave][n] = S.m_run;
-    sm.merge.l[wave][n] = S.lsum;
-  }
+  if (g == 0 && n < 8) ml[16 + n] = weight(n) * ml[8 + n];
   __syncthreads();
-  // ---- merge the four waves of each KV head into this workgroup's partial (tile order)
-  {
-    const int H = tid >> 5, hk = H >> 3, hh = H & 7, i0 = tid & 31;
-    float mw[4], M = -INFINITY;
+  // ---- merge: item (kv, T2, g2, n) sums rows 4 g2 .. 4 g2 + 3 of KV head kv over its four
+  // waves and stores them at tile-order entry 16 T2 + n of heads 8 kv + 4 g2 + i
+  float *dst = a.part + (int64_t)wg * 16 * 258;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int item = tid + kThreads * it;
+    const int n2 = item & 15, g2 = (item >> 4) & 1, T2 = (item >> 5) & 15, kv2 = item >> 9;
+    float4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
-      mw[s4] = sm.merge.m[2 * s4 + hk][hh];
-      M = fmaxf(M, mw[s4]);
+      const float4 v = sm.merge.o[2 * s4 + kv2][T2][g2][n2];
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
     }
-    float f[4], L = 0.0f;
+    float *d0 = dst + (8 * kv2 + 4 * g2) * 258 + 16 * T2 + n2;
+    __builtin_nontemporal_store(acc.x, d0);
+    __builtin_nontemporal_store(acc.y, d0 + 258);
+    __builtin_nontemporal_store(acc.z, d0 + 2 * 258);
+    __builtin_nontemporal_store(acc.w, d0 + 3 * 258);
+  }
+  if (tid < 16) {
+    const int kv2 = tid >> 3, h = tid & 7;
+    float M = -INFINITY, L = 0.0f;
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
-      f[s4] = (mw[s4] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw[s4] - M);
-      L += f[s4] * sm.merge.l[2 * s4 + hk][hh];
+      M = fmaxf(M, sm.run.t.tab[2 * s4 + kv2].vmd[h]);
+      L += sm.run.t.tab[2 * s4 + kv2].vmd[16 + h];
     }
-    float *dst = a.part + (int64_t)wg * 16 * 258 + H * 258;
-#pragma unroll
-    for (int x = 0; x < 8; ++x) {
-      const int idx = i0 + 32 * x;
-      float acc = 0.0f;
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) acc += f[s4] * sm.merge.o[2 * s4 + hk][hh][idx];
-      dst[idx] = acc;
-    }
-    if (i0 == 0) {
-      dst[256] = M;
-      dst[257] = L;
-    }
+    __builtin_nontemporal_store(M, dst + tid * 258 + 256);
+    __builtin_nontemporal_store(L, dst + tid * 258 + 257);
   }
 }
 

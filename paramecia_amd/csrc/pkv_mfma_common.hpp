@@ -40,6 +40,20 @@ __device__ __forceinline__ float ror8(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x128,
                                                             0xF, 0xF, false));
 }
+// fp16(a - c) into the low (mix_sub_lo) or high (mix_sub_hi, low half of d kept) half
+// of a dword: v_fma_mix computes a * 1.0 - c in f32 (exact for c = fp16(a) or 0) and
+// rounds once to fp16; c is the low / high fp16 half of cw.
+__device__ __forceinline__ uint32_t mix_sub_lo(float a, uint32_t cw) {
+  uint32_t d;
+  asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]" : "=v"(d) : "v"(a), "v"(cw));
+  return d;
+}
+__device__ __forceinline__ uint32_t mix_sub_hi(uint32_t d, float a, uint32_t cw) {
+  asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+      : "+v"(d)
+      : "v"(a), "v"(cw));
+  return d;
+}
 __device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
