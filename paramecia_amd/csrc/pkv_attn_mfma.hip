@@ -47,7 +47,7 @@ struct DecodeArgs {
   float sl2;                   // scale * log2(e)
   const float *q;              // [nseg][16][256]
   const float *k_new, *v_new;  // [nseg][2][256] or null (fused decode step)
-  float *part;                 // [nwg][16][258]
+  float *part;                 // [nwg][16][kPartRow]
   float *dq;  // [nseg][4][256] dequantized new rows (K kv0, K kv1, V kv0, V kv1)
 };
 
@@ -539,7 +539,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   __syncthreads();
   // ---- merge: item (kv, T2, g2, n) sums rows 4 g2 .. 4 g2 + 3 of KV head kv over its four
   // waves and stores them at tile-order entry 16 T2 + n of heads 8 kv + 4 g2 + i
-  float *dst = a.part + (int64_t)wg * 16 * 258;
+  float *dst = a.part + (int64_t)wg * 16 * kPartRow;
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
     const int item = tid + kThreads * it;
@@ -553,11 +553,11 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
       acc.z += v.z;
       acc.w += v.w;
     }
-    float *d0 = dst + (8 * kv2 + 4 * g2) * 258 + 16 * T2 + n2;
+    float *d0 = dst + (8 * kv2 + 4 * g2) * kPartRow + 16 * T2 + n2;
     __builtin_nontemporal_store(acc.x, d0);
-    __builtin_nontemporal_store(acc.y, d0 + 258);
-    __builtin_nontemporal_store(acc.z, d0 + 2 * 258);
-    __builtin_nontemporal_store(acc.w, d0 + 3 * 258);
+    __builtin_nontemporal_store(acc.y, d0 + kPartRow);
+    __builtin_nontemporal_store(acc.z, d0 + 2 * kPartRow);
+    __builtin_nontemporal_store(acc.w, d0 + 3 * kPartRow);
   }
   if (tid < 16) {
     const int kv2 = tid >> 3, h = tid & 7;
@@ -567,8 +567,8 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
       M = fmaxf(M, sm.run.t.tab[2 * s4 + kv2].vmd[h]);
       L += sm.run.t.tab[2 * s4 + kv2].vmd[16 + h];
     }
-    __builtin_nontemporal_store(M, dst + tid * 258 + 256);
-    __builtin_nontemporal_store(L, dst + tid * 258 + 257);
+    __builtin_nontemporal_store(M, dst + tid * kPartRow + 256);
+    __builtin_nontemporal_store(L, dst + tid * kPartRow + 257);
   }
 }
 
@@ -631,7 +631,7 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
   d.q = q;
   d.k_new = k_new;
   d.v_new = v_new;
-  const size_t part_floats = (size_t)wg * 16 * 258;
+  const size_t part_floats = (size_t)wg * 16 * kPartRow;
   const size_t need = (part_floats + (size_t)n * 4 * 256) * sizeof(float);
   int rc = ws.reserve(need);
   if (rc) return rc;

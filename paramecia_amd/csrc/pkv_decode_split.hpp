@@ -3,9 +3,10 @@
 // segment and adds the appended key of a fused decode step. Include-only; every
 // symbol has internal linkage.
 //
-// Partial layout: part[wg][16 heads][258]: entries 0-255 the un-normalised output in
+// Partial layout: part[wg][16 heads][kPartRow]: entries 0-255 the un-normalised output in
 // tile order (entry 16 T + n holds element tile_e(T, n)), then the running max m (log2
-// units) and the sum l of 2^(score - m).
+// units) and the sum l of 2^(score - m). Rows are padded to 288 floats (1152 bytes, a
+// multiple of 128) so that the combine's 32-entry slices each fill one 128-byte line.
 #pragma once
 #include "pkv_internal.hpp"
 
@@ -13,6 +14,7 @@ namespace pkv {
 namespace {
 
 constexpr float kSplitClampL2 = 100.0f * 1.4426950408889634f;  // +-100 nats in log2 units
+constexpr int kPartRow = 288;  // floats per partial row: 256 entries, m, l, pad
 
 // e (0..255) of tile-order entry 16 T + n
 __device__ __forceinline__ int tile_e(int T, int n) {
@@ -52,7 +54,7 @@ struct DecodeSegIn {
 constexpr int kCombSlices = 32;  // partial slices (8 threads each)
 constexpr int kCombChunk = 8;    // partials per slice per round
 struct CombineArgs {
-  const float *part;      // [wg][16][258]
+  const float *part;      // [wg][16][kPartRow]
   const float *q, *dq;    // [nseg][16][256], [nseg][4][256] or null
   float *out;             // [nseg][16][256]
   float sl2;
@@ -68,7 +70,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs c) {
   const float sl2 = c.sl2;
   float *out = c.out;
   const int nwg = c.wg0[b + 1] - c.wg0[b];
-  const float *P = c.part + (int64_t)c.wg0[b] * 16 * 258 + h * 258;
+  const float *P = c.part + (int64_t)c.wg0[b] * 16 * kPartRow + h * kPartRow;
   // new key: q . k_new products (reduced below, after the partial loads are issued)
   const float prod = dq != nullptr ? q[((int64_t)b * 16 + h) * 256 + tid] *
                                          dq[((int64_t)b * 4 + (h >> 3)) * 256 + tid]
@@ -83,7 +85,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs c) {
 #pragma unroll
     for (int x = 0; x < kCombChunk; ++x) {
       const bool ok = w + x < w1;
-      const float *pw = P + (int64_t)(w + x) * 16 * 258;
+      const float *pw = P + (int64_t)(w + x) * 16 * kPartRow;
       mlv[x] = ok ? *reinterpret_cast<const float2 *>(pw + 256) : float2{-INFINITY, 0.0f};
       ov[x] = ok ? *reinterpret_cast<const float4 *>(pw + i0 + 4 * g4) : float4{0.f, 0.f, 0.f, 0.f};
     }

@@ -37,7 +37,7 @@ struct Q8Args {
   float sl2;
   const float *q;              // [nseg][16][256]
   const float *k_new, *v_new;  // [nseg][2][256] or null
-  float *part;                 // [nwg][16][258]
+  float *part;                 // [nwg][16][kPartRow]
   float *dq;                   // [nseg][4][256]
 };
 
@@ -206,13 +206,13 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
   }
 
   // ---- partial of this workgroup (tile order), m and l per head
-  float *P = a.part + (int64_t)wg * 16 * 258;
+  float *P = a.part + (int64_t)wg * 16 * kPartRow;
   const int idx = tile_index(t);
 #pragma unroll
-  for (int h = 0; h < 8; ++h) P[(8 * half + h) * 258 + idx] = acc[h];
+  for (int h = 0; h < 8; ++h) P[(8 * half + h) * kPartRow + idx] = acc[h];
   if (kk == 0) {
-    P[(8 * half + hh) * 258 + 256] = m_run;
-    P[(8 * half + hh) * 258 + 257] = l_run;
+    P[(8 * half + hh) * kPartRow + 256] = m_run;
+    P[(8 * half + hh) * kPartRow + 257] = l_run;
   }
 }
 
@@ -256,7 +256,7 @@ static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, cons
   d.q = q;
   d.k_new = k_new;
   d.v_new = v_new;
-  const size_t part_floats = (size_t)wg * 16 * 258;
+  const size_t part_floats = (size_t)wg * 16 * kPartRow;
   const size_t need = (part_floats + (size_t)n * 4 * 256) * sizeof(float);
   int rc = ws.reserve(need);
   if (rc) return rc;
