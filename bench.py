@@ -33,6 +33,20 @@ HBM_PEAK_GBS = 8000.0
 FP16_DENSE_TFLOPS = 2500.0
 Q4K_ROW = 144
 Q8_ROW = 272
+# HBM bytes per launch of each config's roofline kernel(s), from the two calibrated
+# rocprofv3 --pmc runs (FETCH_SIZE x2.0, WRITE_SIZE x1.0) summarised in profiles/; the
+# profiling step cannot run inside bench.py itself. Refreshed with the profiles.
+MEASURED_TRAFFIC = {
+    3: (92_460_000, "profiles/q4k_decode_config3.md: decode + combine per layer"),
+    1: (12_880_000, "profiles/q8_decode_config1.md: decode + combine"),
+    2: (170_180_000, "profiles/q4k_prefill_config2.md: prefill kernel + split merge"),
+    5: (424_550_000, "profiles/q4k_batched_decode_config5.md: decode + combine per layer"),
+}
+
+
+def traffic(config):
+    t = MEASURED_TRAFFIC.get(config)
+    return None if t is None else t[0]
 
 
 def layer_bytes(keys: int, row: int = Q4K_ROW) -> int:
@@ -184,7 +198,8 @@ def run_config3(args):
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
             "bytes_per_launch": layer_bytes(keys),
             "avg_launch_us": round(per_launch_ms * 1000.0, 2),
-            "traffic": None,
+            "traffic": traffic(3),
+            "traffic_source": MEASURED_TRAFFIC[3][1],
         },
         "append_tokens_per_s": round(L * S / fill_s, 1),
     }
@@ -275,7 +290,7 @@ def run_config1(args):
                      "roofline": {"kernel": "pkv_append_attend (Q8_0)", "bound": "hbm",
                                   "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                   "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": nbytes,
-                                  "traffic": None}})
+                                  "traffic": traffic(1)}})
     if not args.no_cpu_baseline:
         r["cpu_baseline"] = cpu_baseline_decode(c, kn, vn, q, S, args.cpu_threads, 1, 3, 1)
     return r
@@ -339,7 +354,7 @@ def run_config2(args):
                                      "bound": "mfma", "achieved": round(tf, 2),
                                      "peak": FP16_DENSE_TFLOPS, "unit": "TFLOP/s",
                                      "frac": round(tf / FP16_DENSE_TFLOPS, 5), "flops": flops,
-                                     "traffic": None}})
+                                     "traffic": traffic(2)}})
 
 
 # ------------------------------------------------------------------ config 4
@@ -459,7 +474,8 @@ def run_config5(args):
                         "roofline": {"kernel": "pkv_append_attend_batched", "bound": "hbm",
                                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                                     "bytes_per_step": nbytes, "traffic": None}})
+                                     "bytes_per_step": nbytes,
+                                     "traffic_per_layer": traffic(5)}})
 
 
 def main() -> int:
