@@ -60,7 +60,7 @@ struct DqBlock {
 
 struct PfSmem {
   Stage raw[kRaw];
-  DqBlock dq;
+  DqBlock dq[2];  // block i's operands in dq[i & 1] while block i + 1's are built
   float cmin[kPfWaves][16][8];  // per wave: min term [row][j]
 };
 static_assert(sizeof(PfSmem) <= 160 * 1024, "LDS budget of one workgroup");
@@ -306,28 +306,47 @@ __global__ __launch_bounds__(kPfThreads) void q4k_prefill_kernel(PrefillArgs a) 
   f4 accm = {0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, lsum = 0.0f;
   const Masks MK = {vconst(0x000F000Fu), vconst(0x00F000F0u), vconst(0x64006400u)};
-  DqBlock &D = sm.dq;
   // position of this lane's row (n): the causal limit of its keys
   const int64_t myq = (int64_t)pw + (n >> 3);
   const int64_t klim = a.causal ? myq + a.q_offset : (int64_t)1 << 62;
 
-  for (int i = 0; i < nb; ++i) {
-    if (loader) {  // block i landed (block i+1 may still fly)
-      if (i + 1 < nb)  // the 6 loads of block i + 1 may stay in flight
+  // Waves 0-4 build the fp16 operands of block i + 1 while every wave runs the MFMAs of
+  // block i: one barrier per block. Raw stages rotate over kRaw = 3 (blocks i + 1 and
+  // i + 2 in flight or landed while block i + 3 is issued).
+  auto dequant = [&](int blk) {
+    const Stage &st = sm.raw[blk % kRaw];
+    DqBlock &Dn = sm.dq[blk & 1];
+    if (wave < 2)
+      dq_keys(st, Dn, a.sl2, MK, wave, lane);
+    else if (wave < 4)
+      dq_values(st, Dn, MK, wave - 2, lane);
+    else if (wave == 4)
+      dq_value_mins(st, Dn, lane);
+  };
+  if (nb > 0) {
+    if (loader) {  // block 0 landed (block 1 may still fly)
+      if (nb > 1)
         asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
       else
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-    __syncthreads();  // raw block i visible; the previous block's operands are consumed
-    if (loader && i + 2 < nb) issue(i + 2);
-    const Stage &st = sm.raw[i % kRaw];
-    if (wave < 2)
-      dq_keys(st, D, a.sl2, MK, wave, lane);
-    else if (wave < 4)
-      dq_values(st, D, MK, wave - 2, lane);
-    else if (wave == 4)
-      dq_value_mins(st, D, lane);
-    __syncthreads();  // operands of block i ready
+    __syncthreads();
+    if (loader && nb > 2) issue(2);
+    dequant(0);
+  }
+  for (int i = 0; i < nb; ++i) {
+    if (loader && i + 1 < nb) {  // block i + 1 landed (block i + 2 may still fly)
+      if (i + 2 < nb)  // the 6 loads of block i + 2 may stay in flight
+        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    // operands of block i ready; raw block i + 1 visible; block i - 1's operands and
+    // block i's raw stage no longer read
+    __syncthreads();
+    if (loader && i + 3 < nb) issue(i + 3);
+    if (i + 1 < nb) dequant(i + 1);
+    const DqBlock &D = sm.dq[i & 1];
 
     // ---- QK (two tiles of 16 keys), rows = this wave's 16 query rows
     const int64_t key0 = (int64_t)(kb0 + i) * kBlk;
