@@ -246,6 +246,48 @@ def test_prefix_restore_bytes_and_requantize(pk, orc):
         m2.restore_prefix_cache(pc)
 
 
+def test_prefix_restore_many_segments(pk):
+    """A 64-layer model (16 full, 48 linear layers: 176 copy segments, more than the
+    kernel-argument table holds) restores through the device-side segment table; odd
+    segment sizes exercise the unaligned tail copy."""
+    say("prefix restore, 176 segments")
+    m = pk.ModelKvState(64, 4, 16, 2, 256, 256, pk.KvCacheQuantization.Q4K)
+    full = m.full_layers()
+    for l in full:
+        l._ensure(1).append_quantized(torch.randn(1, 2, 37, 256, device="cuda"),
+                                      torch.randn(1, 2, 37, 256, device="cuda"))
+    states = []
+    for l in m.layers:
+        if isinstance(l, pk.LinearAttentionState):
+            s = pk.RecurrentState(torch.randn(1, 3, 5, 7, device="cuda"),
+                                  torch.randn(1, 11, 3, device="cuda"),
+                                  torch.randn(1, 3, device="cuda"))
+            l.recurrent_state = s
+            states.append(tuple(host(x).copy() for x in (s.ssm_state, s.conv_state,
+                                                        s.gate_cumsum_offset)))
+    snap = [tuple(host(x).copy() for x in l.quantized_cache.raw_bytes()) for l in full]
+    pc = m.save_prefix_cache(list(range(37)))
+    for l in full:
+        l.quantized_cache.append_quantized(torch.randn(1, 2, 5, 256, device="cuda"),
+                                           torch.randn(1, 2, 5, 256, device="cuda"), offset=10)
+    for l in m.layers:  # diverge the recurrent states in place
+        if isinstance(l, pk.LinearAttentionState):
+            for x in (l.recurrent_state.ssm_state, l.recurrent_state.conv_state,
+                      l.recurrent_state.gate_cumsum_offset):
+                x.fill_(5.0)
+    m.clear_kv_cache()
+    assert m.restore_prefix_cache(pc) == 37
+    for l, (kb, vb) in zip(full, snap):
+        gk, gv = l.quantized_cache.raw_bytes()
+        assert np.array_equal(host(gk), kb) and np.array_equal(host(gv), vb)
+    lin = [l for l in m.layers if isinstance(l, pk.LinearAttentionState)]
+    for l, (ss, cs, gs) in zip(lin, states):
+        st = l.recurrent_state
+        assert np.array_equal(host(st.ssm_state), ss)
+        assert np.array_equal(host(st.conv_state), cs)
+        assert np.array_equal(host(st.gate_cumsum_offset), gs)
+
+
 def test_batched_decode_matches_per_sequence(pk, orc):
     say("batched decode")
     rng = np.random.default_rng(10)
