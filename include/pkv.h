@@ -126,7 +126,8 @@ int pkv_flash_attn(int quant, const float *q, const void *k_bytes, const void *v
 
 /* Batched decode over independent sequences (serving loop): caches[i] is a batch-1
  * cache; appends one token to each (k, v: [n, n_kv_heads, head_dim]) then attends
- * (q, out: [n, num_heads, head_dim]) in one launch. All caches share geometry. */
+ * (q, out: [n, num_heads, head_dim]). All caches share geometry. For the Qwen3-Next
+ * shape (Q4K or Q8_0) up to 32 sequences share one decode + combine launch pair. */
 int pkv_append_attend_batched(pkv_cache *const *caches, int n, const float *k,
                               const float *v, const float *q, int num_heads, float scale,
                               float *out, pkv_stream stream);
