@@ -348,28 +348,41 @@ __global__ __launch_bounds__(kPfThreads) void q4k_prefill_kernel(PrefillArgs a) 
     if (i + 1 < nb) dequant(i + 1);
     const DqBlock &D = sm.dq[i & 1];
 
-    // ---- QK (two tiles of 16 keys), rows = this wave's 16 query rows
+    // ---- QK (two tiles of 16 keys), rows = this wave's 16 query rows; keys kk of the
+    // block at or past nlim are masked (past the cache, or past this row's causal limit)
     const int64_t key0 = (int64_t)(kb0 + i) * kBlk;
+    int64_t lim = a.seq_k < klim + 1 ? a.seq_k : klim + 1;
+    lim -= key0;
+    const int nlim = lim < 0 ? 0 : (lim > kBlk ? kBlk : (int)lim);
     float sc8[8];
+    // four independent accumulator chains (tile x q part), interleaved so that the
+    // MFMA pipe never waits for the previous result of the same chain
+    f4 s1h[2], s1l[2], s2[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) s1h[t] = s1l[t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const h8 A = D.ka[t][s][lane];
+        s1h[t] = mfma32(A, qbh[s], s1h[t]);
+        s1l[t] = mfma32(A, qbl[s], s1l[t]);
+      }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      f4 s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const h8 A = D.ka[t][s][lane];
-        s1 = mfma32(A, qbh[s], s1);
-        s1 = mfma32(A, qbl[s], s1);
-      }
       const h4 A2 = D.ka2[t][lane];
-      f4 s2 = mfma16(A2, q2h, f4{0.f, 0.f, 0.f, 0.f});
-      s2 = mfma16(A2, q2l, s2);
+      s2[t] = mfma16(A2, q2h, f4{0.f, 0.f, 0.f, 0.f});
+      s2[t] = mfma16(A2, q2l, s2[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const f4 s1 = s1h[t] + s1l[t];
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const int kk = 8 * g + 4 * t + ii;
-        float sc = D.kd[kk] * s1[ii] - D.kdm[kk] * s2[ii];
+        float sc = D.kd[kk] * s1[ii] - D.kdm[kk] * s2[t][ii];
         sc = fminf(fmaxf(sc, -kClampL2), kClampL2);
-        const int64_t key = key0 + kk;
-        sc8[4 * t + ii] = (key < a.seq_k && key <= klim) ? sc : -INFINITY;
+        sc8[4 * t + ii] = kk < nlim ? sc : -INFINITY;
       }
     }
     // ---- online softmax per row (lanes n, n+16, n+32, n+48 hold row n's 32 keys)
@@ -402,15 +415,22 @@ __global__ __launch_bounds__(kPfThreads) void q4k_prefill_kernel(PrefillArgs a) 
     // ---- PV: A rows = query rows, keys 8g..8g+7. The weights p * mantissa enter as
     // fp16 hi and lo parts (~22 bits): one fp16 rounding of a weight (2^-12 relative)
     // times a value of an outlier channel would exceed the attention tolerance.
-    h8 A, Al, Am, Aml;
+    uint32_t wa[4], wl[4], wm[4], wml[4];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float x = p[k] * D.vmd[8 * g + k], xm = p[k] * D.vmdm[8 * g + k];
-      A[k] = (_Float16)x;
-      Al[k] = (_Float16)(x - (float)A[k]);
-      Am[k] = (_Float16)xm;
-      Aml[k] = (_Float16)(xm - (float)Am[k]);
+    for (int k2 = 0; k2 < 4; ++k2) {
+      const float x0 = p[2 * k2] * D.vmd[8 * g + 2 * k2];
+      const float x1 = p[2 * k2 + 1] * D.vmd[8 * g + 2 * k2 + 1];
+      const float y0 = p[2 * k2] * D.vmdm[8 * g + 2 * k2];
+      const float y1 = p[2 * k2 + 1] * D.vmdm[8 * g + 2 * k2 + 1];
+      wa[k2] = as_u(h2{(_Float16)x0, (_Float16)x1});
+      wl[k2] = mix_sub_hi(mix_sub_lo(x0, wa[k2]), x1, wa[k2]);
+      wm[k2] = as_u(h2{(_Float16)y0, (_Float16)y1});
+      wml[k2] = mix_sub_hi(mix_sub_lo(y0, wm[k2]), y1, wm[k2]);
     }
+    const h8 A = __builtin_bit_cast(h8, u4{wa[0], wa[1], wa[2], wa[3]});
+    const h8 Al = __builtin_bit_cast(h8, u4{wl[0], wl[1], wl[2], wl[3]});
+    const h8 Am = __builtin_bit_cast(h8, u4{wm[0], wm[1], wm[2], wm[3]});
+    const h8 Aml = __builtin_bit_cast(h8, u4{wml[0], wml[1], wml[2], wml[3]});
 #pragma unroll
     for (int T2 = 0; T2 < 16; ++T2) {
       const h8 B = D.vb[T2][lane];
