@@ -53,22 +53,23 @@ struct DecodeArgs {
 
 // Per-wave tables rebuilt for every 32-key block.
 struct WaveTab {
-  float kd[kBlk], kdm[kBlk];                        // K: d*sl2, dmin*sl2
+  float kd[kBlk], kdm[kBlk];                        // epilogue exchange (cmin)
   float vmd[kBlk], vmdm[kBlk];                      // V: mantissas of d and dmin
   _Float16 vsc[8][kBlk], vc[8][kBlk], vm[8][kBlk];  // V: fp16 constants [j][key]
 };
 
-// LDS of one workgroup. Each wave owns stage buffers st[0]/st[1] and a table area;
-// before its first refill of st[1] a wave stages its KV head's q rows there, and the
+// LDS of one workgroup. Each wave owns stage buffers st[w][0], st[w][1] (adjacent, so
+// both are reached from one base register with immediate offsets) and a table area;
+// before its first refill of st[w][1] a wave stages its KV head's q rows there, and the
 // quantizer scratch of the quantizing waves 0-3 overlaps their tables. The merge area
-// reuses the st[0] buffers once every wave has left the loop. Stages are always addressed by
+// reuses the first stage buffers once every wave has left the loop. Stages are always addressed by
 // indexing this array: a pointer chosen at run time between two stages loses its LDS
 // address space, and the generic (flat) loads it then compiles to wait on every
 // outstanding buffer load, including the prefetch of the next block.
 struct Smem {
   union {
     struct {
-      Stage st[2][kWaves];
+      Stage st[kWaves][2];
       union {
         WaveTab tab[kWaves];
         struct {
@@ -84,7 +85,7 @@ struct Smem {
 };
 static_assert(sizeof(Q4kScratch) + 4 <= sizeof(WaveTab), "quantizer scratch within wave 0's tables");
 static_assert(sizeof(float4[kWaves][16][2][16]) <= sizeof(Stage[kWaves]),
-              "merge area within the st[0] buffers");
+              "merge area within the first stage buffers");
 static_assert(24 <= kBlk, "m, l and f * l of 8 heads fit a wave's vmd table");
 static_assert(sizeof(Smem) <= 160 * 1024, "LDS budget of one workgroup");
 
@@ -133,28 +134,66 @@ struct QKOut {
   f4 s1[2], s2[2];  // per 16-key tile: sum_e (n*sc)_e q_e and sum_j m_j qsum_j
 };
 
-// Phase Q: K rows of a staged block -> raw QK sums; per-key d, dmin into the tables.
+// Lane constants of the K scale decode. Lane group g uses sub-blocks 2g and 2g + 1,
+// whose 6-bit scale and min codes sit in bytes 2(g & 1), 2(g & 1) + 1 of the header's
+// words s0 (scales 0-3), s1 (mins 0-3) and, for sub-blocks 4-7, s2 (low 4 bits) with
+// the top two bits in s0 / s1 (get_scale_min_k4). v_perm puts header byte b of s2 (or
+// s0 / s1 for g < 2) in the low byte and byte b of s0 / s1 in the high byte of each
+// 16-bit half; the masks then keep the code's low bits in place and move bits 6-7 of
+// the high byte down to bits 4-5, and the 0x6400 exponent makes each half the fp16
+// value 1024 + code.
+struct KScaleSel {
+  uint32_t perm;  // v_perm selector: S0 = s0 or s1, S1 = s2
+  uint32_t lo;    // low code bits kept in place: 0x3F (g < 2) or 0x0F per half
+  uint32_t up;    // bits 4-5 taken from bits 14-15 of each half (g >= 2)
+  uint32_t msh;   // right shift of the min codes' low bits: 0 (g < 2) or 4
+};
+__device__ __forceinline__ KScaleSel make_kscale_sel(int g) {
+  const uint32_t b = 2u * (uint32_t)(g & 1);
+  KScaleSel s;
+  if (g < 2) {
+    s.perm = (4u + b) | (0x0Cu << 8) | ((5u + b) << 16) | (0x0Cu << 24);
+    s.lo = 0x003F003Fu;
+    s.up = 0u;
+    s.msh = 0u;
+  } else {
+    s.perm = b | ((4u + b) << 8) | ((b + 1u) << 16) | ((5u + b) << 24);
+    s.lo = 0x000F000Fu;
+    s.up = 0x00300030u;
+    s.msh = 4u;
+  }
+  return s;
+}
+// {1024 + code(2g), 1024 + code(2g + 1)} as fp16 halves: the scale codes from (s0, s2),
+// the min codes from (s1, s2)
+__device__ __forceinline__ uint32_t kcode_pair(uint32_t sx, uint32_t s2, uint32_t sh,
+                                               const KScaleSel &ks, uint32_t magic) {
+  const uint32_t P = __builtin_amdgcn_perm(sx, s2, ks.perm);
+  return and_or(P >> sh, ks.lo, and_or(P >> 10, ks.up, magic));
+}
+
+// Phase Q: K rows of a staged block -> raw QK sums.
 // Lane (r, g) feeds key kk(r) of tile t with sub-blocks 2g (low nibbles) and 2g+1
 // (high nibbles); its min codes m_2g, m_2g+1 form the A operand of the S2 product.
-__device__ __forceinline__ void phase_q(const Stage &st, WaveTab &T, const h8 *qb, h4 q2,
-                                        float sl2, const Masks &MK, int lane, QKOut &o) {
-  const int r = lane & 15, g = lane >> 4;
+__device__ __forceinline__ void phase_q(const Stage &st, const h8 *qb, h4 q2, const Masks &MK,
+                                        const KScaleSel &ks, int lane, QKOut &o) {
+  const int r = lane & 15;
+  // pk_fma constants: {1024 + sc0, 1024 + sc1} -> {sc0, sc1 / 16}; then the offsets
+  // {-1024 sc0, -64 sc1} of the two nibble forms (1024 + n, 1024 + 16 n)
+  const h2 ksc = {(_Float16)1.0f, (_Float16)0.0625f}, kcc = {(_Float16)-1024.0f, (_Float16)-64.0f};
+  const h2 kneg = {(_Float16)-1024.0f, (_Float16)-1024.0f};
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int kk = 8 * (r >> 2) + 4 * t + (r & 3);
     const int sw = swz(kk);
     const u4 hd = st.k.hdr[kk];
-    const u4 q0 = st.k.nib[8 * kk + ((2 * g) ^ sw)];
-    const u4 q1 = st.k.nib[8 * kk + ((2 * g + 1) ^ sw)];
-    // lanes of one key (g = 0..3) store the same values
-    T.kd[kk] = h2f(hd.x & 0xFFFF) * sl2;
-    T.kdm[kk] = h2f(hd.x >> 16) * sl2;
-    uint32_t sc0, sc1, m0, m1;
-    scale_min(hd.y, hd.z, hd.w, 2 * g, sc0, m0);
-    scale_min(hd.y, hd.z, hd.w, 2 * g + 1, sc1, m1);
-    const _Float16 f0 = (_Float16)(float)sc0, f1 = (_Float16)((float)sc1 * 0.0625f);
-    const _Float16 c0 = (_Float16)(-1024.0f * (float)sc0), c1 = (_Float16)(-64.0f * (float)sc1);
-    const h2 SC0 = {f0, f0}, SC1 = {f1, f1}, C0 = {c0, c0}, C1 = {c1, c1};
+    const u4 q0 = st.k.nib[8 * kk + ((2 * (lane >> 4)) ^ sw)];
+    const u4 q1 = st.k.nib[8 * kk + ((2 * (lane >> 4) + 1) ^ sw)];
+    const h2 SC = pk_fma(as_h2(kcode_pair(hd.y, hd.w, 0u, ks, MK.magic)), ksc, kcc);
+    const h2 CC = SC * kneg;
+    const h2 MM = as_h2(kcode_pair(hd.z, hd.w, ks.msh, ks, MK.magic)) + kneg;
+    const h2 SC0 = __builtin_shufflevector(SC, SC, 0, 0), SC1 = __builtin_shufflevector(SC, SC, 1, 1);
+    const h2 C0 = __builtin_shufflevector(CC, CC, 0, 0), C1 = __builtin_shufflevector(CC, CC, 1, 1);
     const uint32_t qd[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
     f4 s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -178,27 +217,43 @@ __device__ __forceinline__ void phase_q(const Stage &st, WaveTab &T, const h8 *q
       s1 = mfma32(lo, qb[s], s1);
       s1 = mfma32(hi, qb[4 + s], s1);
     }
-    const h4 a2 = {(_Float16)(float)m0, (_Float16)(float)m1, (_Float16)0.0f, (_Float16)0.0f};
+    const h4 a2 = {MM[0], MM[1], (_Float16)0.0f, (_Float16)0.0f};
     o.s1[t] = s1;
     o.s2[t] = mfma16(a2, q2, f4{0.f, 0.f, 0.f, 0.f});
   }
 }
 
+// d * s1 - dmin * s2 with the fp16 pair {d, dmin} of a header dword: two v_fma_mix
+__device__ __forceinline__ float hdr_dot(uint32_t hx, float s1, float s2) {
+  float t, r;
+  asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(t) : "v"(hx), "v"(s1));
+  asm("v_fma_mix_f32 %0, -%1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "=v"(r)
+      : "v"(hx), "v"(s2), "v"(t));
+  return r;
+}
+
 // Phase S: scores (log2 units) and the online softmax; p[k] for key 8g + k, head n % 8.
 // Keys at or past nvalid (only in a partial last block) are masked.
-__device__ __forceinline__ void phase_s(const QKOut &o, WaveState &S, const WaveTab &T,
-                                        int nvalid, int lane, float p[8]) {
+// Scores stay in q.k units here (the running max too); sl2 = scale * log2(e) enters
+// the exponents, and clamp / lazy are the +-100-nat clamp and the rescale headroom in
+// those units.
+__device__ __forceinline__ void phase_s(const Stage &st, const QKOut &o, WaveState &S,
+                                        int nvalid, float sl2, float clamp, float lazy, int lane,
+                                        float p[8]) {
   const int g = lane >> 4;
+  const uint32_t *hdr32 = reinterpret_cast<const uint32_t *>(st.k.hdr);
   float sc8[8];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int kk = 8 * g + 4 * t + i;
-      // this column's part (hi or lo of q); the other part sits 8 lanes away
-      const float part = T.kd[kk] * o.s1[t][i] - T.kdm[kk] * o.s2[t][i];
+      // this column's part (hi or lo of q); the other part sits 8 lanes away. d and
+      // dmin enter as fp16 (v_fma_mix).
+      const float part = hdr_dot(hdr32[4 * kk], o.s1[t][i], o.s2[t][i]);
       const float sc = part + ror8(part);
-      sc8[4 * t + i] = fminf(fmaxf(sc, -kClampL2), kClampL2);
+      sc8[4 * t + i] = fminf(fmaxf(sc, -clamp), clamp);
     }
   if (nvalid < kBlk) {
 #pragma unroll
@@ -209,9 +264,9 @@ __device__ __forceinline__ void phase_s(const QKOut &o, WaveState &S, const Wave
 #pragma unroll
   for (int k = 1; k < 8; ++k) bm = fmaxf(bm, sc8[k]);
   bm = xmax32(xmax16(bm));
-  if (__any(bm > S.m_run + kLazy)) {
+  if (__any(bm > S.m_run + lazy)) {
     const float m_new = fmaxf(S.m_run, bm);
-    const float alpha = (S.m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(S.m_run - m_new);
+    const float alpha = (S.m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((S.m_run - m_new) * sl2);
     S.lsum *= alpha;
     S.m_run = m_new;
     float ai[4];
@@ -224,36 +279,69 @@ __device__ __forceinline__ void phase_s(const QKOut &o, WaveState &S, const Wave
 #pragma unroll
     for (int i = 0; i < 4; ++i) S.accm[i] *= ai[i];
   }
+  const float nm = -S.m_run * sl2;  // finite: every block has a valid key
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    p[k] = __builtin_amdgcn_exp2f(sc8[k] - S.m_run);
+    p[k] = __builtin_amdgcn_exp2f(fmaf(sc8[k], sl2, nm));
     S.lsum += p[k];
   }
 }
 
+// Lane constants of the V table build: lane l takes key l % 32 and sub-blocks
+// 4u..4u+3 (u = l / 32), whose codes are bytes 0-3 of s0 / s1 (u = 0) or the low 4 bits
+// of s2 with bits 6-7 of s0 / s1 above them (u = 1, get_scale_min_k4).
+struct VScaleSel {
+  uint32_t sh, ma, mb;
+};
+__device__ __forceinline__ VScaleSel make_vscale_sel(int lane) {
+  const bool u = lane >= 32;
+  return VScaleSel{u ? 2u : 0u, u ? 0x30303030u : 0x3F3F3F3Fu, u ? 0x0F0F0F0Fu : 0u};
+}
+
 // Phase P: V header tables, PV A/B operands and MFMAs, min term.
 __device__ __forceinline__ void phase_p(const Stage &st, WaveState &S, WaveTab &T,
-                                        const float p[8], const Masks &MK, int lane) {
+                                        const float p[8], const Masks &MK, const VScaleSel &vs,
+                                        int lane) {
   const int n = lane & 15, g = lane >> 4;
-  // V header -> constant tables. Lane l handles key l % 32 and sub-blocks 4*(l/32)..+3.
+  // V header -> constant tables. The four codes of a lane come out as bytes; the pairs
+  // (4u, 4u+2) and (4u+1, 4u+3) become fp16 1024 + code, and one v_pk_fma each gives
+  // sc * 2^e_d (sc * 2^(e_d - 4) for the high-nibble sub-blocks), exact in fp16 for
+  // e_d in [-20, 0]; the offsets are -1024 times those.
   {
-    const int kk = lane & 31, half = lane >> 5;
+    const int kk = lane & 31, u = lane >> 5;
     const u4 vh = st.v.hdr[kk];
     int ed, em;
     float md, mm;
     split_scale(h2f(vh.x & 0xFFFF), ed, md);
     split_scale(h2f(vh.x >> 16), em, mm);
-    (half ? T.vmdm : T.vmd)[kk] = half ? mm : md;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int j = 4 * half + jj;
-      uint32_t sc, m;
-      scale_min(vh.y, vh.z, vh.w, j, sc, m);
-      const float scp = __builtin_ldexpf((float)sc, ed);
-      T.vsc[j][kk] = (_Float16)((jj & 1) ? scp * 0.0625f : scp);
-      T.vc[j][kk] = (_Float16)((jj & 1) ? -64.0f * scp : -1024.0f * scp);
-      T.vm[j][kk] = (_Float16)__builtin_ldexpf((float)m, em);
-    }
+    (u ? T.vmdm : T.vmd)[kk] = u ? mm : md;
+    const uint32_t sc4 = and_or(vh.y >> vs.sh, vs.ma, vh.w & vs.mb);
+    const uint32_t m4 = and_or(vh.z >> vs.sh, vs.ma, (vh.w >> 4) & vs.mb);
+    const _Float16 e1 = __builtin_amdgcn_ldexph((_Float16)1.0f, ed);
+    const _Float16 n1 = __builtin_amdgcn_ldexph((_Float16)-1024.0f, ed);
+    const _Float16 e4 = __builtin_amdgcn_ldexph((_Float16)0.0625f, ed);
+    const _Float16 n4 = __builtin_amdgcn_ldexph((_Float16)-64.0f, ed);
+    const _Float16 em1 = __builtin_amdgcn_ldexph((_Float16)1.0f, em);
+    const _Float16 nm1 = __builtin_amdgcn_ldexph((_Float16)-1024.0f, em);
+    const h2 kneg = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const h2 se = pk_fma(as_h2(and_or(sc4, 0x00FF00FFu, MK.magic)), h2{e1, e1}, h2{n1, n1});
+    const h2 so = pk_fma(as_h2(and_or(sc4 >> 8, 0x00FF00FFu, MK.magic)), h2{e4, e4}, h2{n4, n4});
+    const h2 me = pk_fma(as_h2(and_or(m4, 0x00FF00FFu, MK.magic)), h2{em1, em1}, h2{nm1, nm1});
+    const h2 mo = pk_fma(as_h2(and_or(m4 >> 8, 0x00FF00FFu, MK.magic)), h2{em1, em1}, h2{nm1, nm1});
+    const h2 ce = se * kneg, co = so * kneg;
+    const int j = 4 * u;
+    T.vsc[j][kk] = se[0];
+    T.vsc[j + 2][kk] = se[1];
+    T.vsc[j + 1][kk] = so[0];
+    T.vsc[j + 3][kk] = so[1];
+    T.vc[j][kk] = ce[0];
+    T.vc[j + 2][kk] = ce[1];
+    T.vc[j + 1][kk] = co[0];
+    T.vc[j + 3][kk] = co[1];
+    T.vm[j][kk] = me[0];
+    T.vm[j + 2][kk] = me[1];
+    T.vm[j + 1][kk] = mo[0];
+    T.vm[j + 3][kk] = mo[1];
   }
   // V rows, transposed: dword n & 3 of nibble piece 4h + n / 4 of keys 8g..8g+7. Rows
   // 2i and 2i+1 share their swizzle, so each pair is one ds_read2 (128 bytes apart).
@@ -273,15 +361,20 @@ __device__ __forceinline__ void phase_p(const Stage &st, WaveState &S, WaveTab &
   // row halves are summed after the loop); Am likewise for p * mant(dmin). One fp16
   // rounding of a weight (2^-12 relative) times a value of an outlier channel would
   // exceed the attention tolerance; hi + lo keeps ~22 bits.
-  const bool lo_row = n >= 8;
-  h8 A, Am;
+  // Both parts are fp16(x - c) with c = fp16(x) masked to zero on the hi rows.
+  const uint32_t lo_mask = n >= 8 ? 0xFFFFFFFFu : 0u;
+  uint32_t aw[4], amw[4];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const float x = p[k] * T.vmd[8 * g + k], xm = p[k] * T.vmdm[8 * g + k];
-    const _Float16 xh = (_Float16)x, xmh = (_Float16)xm;
-    A[k] = lo_row ? (_Float16)(x - (float)xh) : xh;
-    Am[k] = lo_row ? (_Float16)(xm - (float)xmh) : xmh;
+  for (int kp = 0; kp < 4; ++kp) {
+    const float x0 = p[2 * kp] * T.vmd[8 * g + 2 * kp], x1 = p[2 * kp + 1] * T.vmd[8 * g + 2 * kp + 1];
+    const float y0 = p[2 * kp] * T.vmdm[8 * g + 2 * kp], y1 = p[2 * kp + 1] * T.vmdm[8 * g + 2 * kp + 1];
+    const uint32_t cx = as_u(h2{(_Float16)x0, (_Float16)x1}) & lo_mask;
+    const uint32_t cy = as_u(h2{(_Float16)y0, (_Float16)y1}) & lo_mask;
+    aw[kp] = mix_sub_hi(mix_sub_lo(x0, cx), x1, cx);
+    amw[kp] = mix_sub_hi(mix_sub_lo(y0, cy), y1, cy);
   }
+  const h8 A = __builtin_bit_cast(h8, u4{aw[0], aw[1], aw[2], aw[3]});
+  const h8 Am = __builtin_bit_cast(h8, u4{amw[0], amw[1], amw[2], amw[3]});
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int c = 2 * h + (n >> 3);
@@ -348,8 +441,9 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   // ---- blocks of this wave: b0 + wsub, b0 + wsub + 4, ... below b1
   const int b0 = (wg - sg.wg0) * a.bpw;
   const int b1 = b0 + a.bpw < sg.nblk ? b0 + a.bpw : sg.nblk;
-  const int first = b0 + wsub;
-  const int nmine = first < b1 ? (b1 - first + 3) / 4 : 0;
+  // wave-uniform: loop control and the key mask stay scalar
+  const int first = __builtin_amdgcn_readfirstlane(b0 + wsub);
+  const int nmine = __builtin_amdgcn_readfirstlane(first < b1 ? (b1 - first + 3) / 4 : 0);
   const int kvu = __builtin_amdgcn_readfirstlane(kv);
   const uint8_t *kbase = sg.k + kvu * a.rs_h;
   const uint8_t *vbase = sg.v + kvu * a.rs_h;
@@ -360,7 +454,10 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   const u4s rk = make_rsrc(kbase, span), rv = make_rsrc(vbase, span);
   const LoadPlan P = make_plan(lane, rs_t);
   const uint32_t bstep = 4u * kBlk * rs_t;  // byte distance between this wave's blocks
-  uint32_t boff = (uint32_t)first * kBlk * rs_t;
+  uint32_t boff = __builtin_amdgcn_readfirstlane((uint32_t)first * kBlk * rs_t);
+  // LDS byte addresses of this wave's two stages
+  const uint32_t st_lds0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(size_t)((PKV_LDS void *)&sm.run.st[wave][0]));
 
   // Fused append: threads 0-255 (waves 0-3) of workgroup r quantize new row r (row
   // 4s + 2p + kv: segment s, K (p = 0) or V (p = 1), KV head kv; further rows go
@@ -381,10 +478,11 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   // before any stage load (one barrier), so q returns ahead of the block data.
   {
     const u4s rq = make_rsrc(a.q + ((int64_t)b * 16 + 8 * kvu) * 256, 8 * 256 * 4);
-    issue_q(&sm.run.st[1][wave], rq, 16u * lane);
+    issue_q(&sm.run.st[wave][1], rq, 16u * lane);
   }
   __syncthreads();
-  if (nmine > 0) issue_stage(&sm.run.st[0][wave], P, rk, rv, boff);
+  // every issued block has its first key below seq_k, so its offset is inside the range
+  if (nmine > 0) issue_stage_at(st_lds0, P, rsrc_advance(rk, boff), rsrc_advance(rv, boff));
 
   // QK B operands: lane (n, g) takes q of head n % 8, elements 64g + 32(s/4) + 8(s%4) +
   // perm[slot], as the fp16 hi part (n < 8) or the lo remainder (n >= 8); S2 B operand:
@@ -399,7 +497,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
       asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
     else
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    const float *qrow = reinterpret_cast<const float *>(&sm.run.st[1][wave]) + (n & 7) * (kQRow / 4) + 64 * g;
+    const float *qrow = reinterpret_cast<const float *>(&sm.run.st[wave][1]) + (n & 7) * (kQRow / 4) + 64 * g;
     constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
     float qsum[2] = {0.0f, 0.0f};
     // hi lanes (n < 8) take fp16(q), lo lanes fp16(q - fp16(q)): both are fp16(q - c)
@@ -458,7 +556,11 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   WaveTab &T = sm.run.t.tab[wave];
   if (nmine > 0) {
     const Masks MK = {vconst(0x000F000Fu), vconst(0x00F000F0u), vconst(0x64006400u)};
+    const KScaleSel ks = make_kscale_sel(g);
+    const float clamp_raw = kClampL2 / a.sl2, lazy_raw = kLazy / a.sl2;
+    const VScaleSel vs = make_vscale_sel(lane);
     for (int i = 0; i < nmine; ++i) {
+      const int si = i & 1;  // block i uses stage i % 2
       // The two waves of a SIMD are issued oldest-first at equal priority, which lets
       // the older one run ahead and leaves the younger to finish alone. Lowering the
       // priority with each block done keeps the one behind first in line.
@@ -469,17 +571,19 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
       else if (i == 2)
         __builtin_amdgcn_s_setprio(0);
       if (i + 1 < nmine) {  // block i+1 streams in while block i is processed
-        issue_stage(&sm.run.st[(i + 1) & 1][wave], P, rk, rv, boff + bstep);
+        issue_stage_at(st_lds0 + (uint32_t)(1 - si) * (uint32_t)sizeof(Stage), P,
+                       rsrc_advance(rk, boff + bstep), rsrc_advance(rv, boff + bstep));
         asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
       } else {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
-      const Stage &st = sm.run.st[i & 1][wave];
+      const Stage &st = sm.run.st[wave][si];
       QKOut qo;
       float pv[8];
-      phase_q(st, T, qb, q2, a.sl2, MK, lane, qo);
-      phase_s(qo, S, T, (int)(seq_k - (int64_t)(first + 4 * i) * kBlk), lane, pv);
-      phase_p(st, S, T, pv, MK, lane);
+      phase_q(st, qb, q2, MK, ks, lane, qo);
+      phase_s(st, qo, S, (int)(seq_k - (int64_t)(first + 4 * i) * kBlk), a.sl2, clamp_raw,
+              lazy_raw, lane, pv);
+      phase_p(st, S, T, pv, MK, vs, lane);
       // every LDS read of this stage has completed before it is refilled
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       boff += bstep;
@@ -490,27 +594,28 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
   // this workgroup's partial
   S.lsum += __shfl_xor(S.lsum, 16);
   S.lsum += __shfl_xor(S.lsum, 32);
-  // hi rows 4g+i (lanes g < 2) plus lo rows 8+4g+i (lanes g + 2, 32 lanes up)
+  // Row halves: the hi rows 0-7 sit in lanes g < 2 and the lo rows 8-15 of the same
+  // heads 32 lanes up. One v_permlane32_swap sums them for two tiles at once: afterwards
+  // lanes 0-31 hold tile T2 and lanes 32-63 tile T2 + 8, both for rows (heads)
+  // 4 (g & 1) + i.
+  const int gr = g & 1, gh = g >> 1;
+  f4 hs[8];
 #pragma unroll
-  for (int T2 = 0; T2 < 16; ++T2)
+  for (int T2 = 0; T2 < 8; ++T2)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) S.acc[T2][i] = xsum32(S.acc[T2][i]);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) S.accm[i] = xsum32(S.accm[i]);
-  // Exchange through this wave's own table area (no other wave reads it before the
-  // barrier): min term cmin[head][j] (accm row 4g+i, column j = n), and ml = {m of
-  // heads 0-7, l of heads 0-7, f * l of heads 0-7}.
+    for (int i = 0; i < 4; ++i) hs[T2][i] = pair_sum32(S.acc[T2][i], S.acc[T2 + 8][i]);
+  // min term, paired alike: cm0 is row 4 (g & 1) + g / 2, cm1 row 4 (g & 1) + 2 + g / 2
+  // (column j = n)
+  const float cm0 = pair_sum32(S.accm[0], S.accm[1]), cm1 = pair_sum32(S.accm[2], S.accm[3]);
+  // Exchange through this wave's own table area: ml = {m of heads 0-7 (log2 units), l,
+  // f * l}, read by the other waves after the barrier; then cmin[head][j] * f.
   float(*cmin)[8] = reinterpret_cast<float(*)[8]>(&T.kd[0]);
   float *ml = T.vmd;
-  if (g < 2 && n < 8) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) cmin[4 * g + i][n] = S.accm[i];
-  }
   if (g == 0 && n < 8) {
-    ml[n] = S.m_run;
+    ml[n] = S.m_run * a.sl2;
     ml[8 + n] = S.lsum;
   }
-  __syncthreads();  // every wave has left the loop: the st[0] buffers become the merge area
+  __syncthreads();  // every wave has left the loop: the stage buffers become the merge area
   // weights f = 2^(m - M) of this wave's rows against the four waves of its KV head
   auto weight = [&](int h) {
     float M = -INFINITY;
@@ -519,21 +624,25 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
     const float mine = ml[h];
     return (mine == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mine - M);
   };
-  if (g < 2) {
-    float fr[4];
+  float fr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fr[i] = weight(4 * g + i);
-    // scaled output rows 4g..4g+3: (acc - cmin[row][e / 32]) * f, one float4 per tile
+  for (int i = 0; i < 4; ++i) fr[i] = weight(4 * gr + i);
+  // cmin * f, written and read back by this wave only (its LDS operations stay in order)
+  if (n < 8) {
+    cmin[4 * gr + gh][n] = cm0 * (gh ? fr[1] : fr[0]);
+    cmin[4 * gr + 2 + gh][n] = cm1 * (gh ? fr[3] : fr[2]);
+  }
+  // scaled output rows: acc * f - cmin[row][e / 32] * f, one float4 per tile
 #pragma unroll
-    for (int T2 = 0; T2 < 16; ++T2) {
-      const int j = tile_e(T2, n) >> 5;
-      float4 v;
-      v.x = (S.acc[T2][0] - cmin[4 * g + 0][j]) * fr[0];
-      v.y = (S.acc[T2][1] - cmin[4 * g + 1][j]) * fr[1];
-      v.z = (S.acc[T2][2] - cmin[4 * g + 2][j]) * fr[2];
-      v.w = (S.acc[T2][3] - cmin[4 * g + 3][j]) * fr[3];
-      sm.merge.o[wave][T2][g][n] = v;
-    }
+  for (int T2 = 0; T2 < 8; ++T2) {
+    const int Tt = T2 + 8 * gh;
+    const int j = tile_e(Tt, n) >> 5;
+    float4 v;
+    v.x = fmaf(hs[T2][0], fr[0], -cmin[4 * gr + 0][j]);
+    v.y = fmaf(hs[T2][1], fr[1], -cmin[4 * gr + 1][j]);
+    v.z = fmaf(hs[T2][2], fr[2], -cmin[4 * gr + 2][j]);
+    v.w = fmaf(hs[T2][3], fr[3], -cmin[4 * gr + 3][j]);
+    sm.merge.o[wave][Tt][gr][n] = v;
   }
   if (g == 0 && n < 8) ml[16 + n] = weight(n) * ml[8 + n];
   __syncthreads();

@@ -185,6 +185,58 @@ __device__ __forceinline__ void issue_stage(Stage *st, const LoadPlan &P, u4s rk
       : "memory", "scc");
 }
 
+// The resource r advanced by off <= its record count: base + off and the records past
+// the new base, so that a lane's voffset alone is range checked. Plain scalar
+// arithmetic (a saturating subtract would be a vector instruction).
+__device__ __forceinline__ u4s rsrc_advance(u4s r, uint32_t off) {
+  const uint64_t b = (((uint64_t)r.y << 32) | r.x) + off;  // r.y: address bits 32-47, stride 0
+  u4s o;
+  o.x = (uint32_t)b;
+  o.y = (uint32_t)(b >> 32);
+  o.z = r.z - off;
+  o.w = r.w;
+  return o;
+}
+
+// issue_stage with a wave-uniform LDS byte address of the Stage and the block's offset
+// already in the resources: no vector work per issue. K: headers at +0, pieces at
+// +0x200; V: headers at +0x1200, pieces at +0x1400.
+__device__ __forceinline__ void issue_stage_at(uint32_t base, const LoadPlan &P, u4s rk, u4s rv) {
+  static_assert(sizeof(TensorStage) == 0x1200 && sizeof(Stage) == 0x2400, "stage layout");
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %[sv], m0\n\t"
+      "s_add_u32 m0, %[b], 0x200\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o0], %[rk], 0 offen lds\n\t"
+      "s_add_u32 m0, %[b], 0x600\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o1], %[rk], 0 offen lds\n\t"
+      "s_add_u32 m0, %[b], 0xa00\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o2], %[rk], 0 offen lds\n\t"
+      "s_add_u32 m0, %[b], 0xe00\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o3], %[rk], 0 offen lds\n\t"
+      "s_mov_b32 m0, %[b]\n\ts_nop 0\n\t"
+      "buffer_load_dword %[h0], %[rk], 0 offen lds\n\t"
+      "s_add_u32 m0, %[b], 0x100\n\ts_nop 0\n\t"
+      "buffer_load_dword %[h1], %[rk], 0 offen lds\n\t"
+      "s_add_u32 m0, %[b], 0x1400\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o0], %[rv], 0 offen lds\n\t"
+      "s_add_u32 m0, %[b], 0x1800\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o1], %[rv], 0 offen lds\n\t"
+      "s_add_u32 m0, %[b], 0x1c00\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o2], %[rv], 0 offen lds\n\t"
+      "s_add_u32 m0, %[b], 0x2000\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %[o3], %[rv], 0 offen lds\n\t"
+      "s_add_u32 m0, %[b], 0x1200\n\ts_nop 0\n\t"
+      "buffer_load_dword %[h0], %[rv], 0 offen lds\n\t"
+      "s_add_u32 m0, %[b], 0x1300\n\ts_nop 0\n\t"
+      "buffer_load_dword %[h1], %[rv], 0 offen lds\n\t"
+      "s_mov_b32 m0, %[sv]"
+      : [sv] "=&s"(saved)
+      : [b] "s"(base), [o0] "v"(P.nib[0]), [o1] "v"(P.nib[1]), [o2] "v"(P.nib[2]),
+        [o3] "v"(P.nib[3]), [h0] "v"(P.hdr[0]), [h1] "v"(P.hdr[1]), [rk] "s"(rk), [rv] "s"(rv)
+      : "memory", "scc");
+}
+
 // Cross-lane max through v_permlane{16,32}_swap: with both operands x, the two results
 // hold x of lanes l and l ^ 16 (l ^ 32). The elements are copied to scalars before the
 // bit cast: __builtin_bit_cast of a vector element r[1] reads element 0 (clang lowers
@@ -203,6 +255,15 @@ __device__ __forceinline__ float xmax32(float x) {  // max over lanes l and l ^ 
   const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
   const uint32_t r0 = r[0], r1 = r[1];
   return max_pair(r0, r1);
+}
+
+// Sum over lanes l and l ^ 32 of x (lanes 0-31) and of y (lanes 32-63) with one swap:
+// v_permlane32_swap(x, y) exchanges x's upper 32 lanes with y's lower 32 lanes.
+__device__ __forceinline__ float pair_sum32(float x, float y) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
+                                                  __builtin_bit_cast(uint32_t, y), false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
 }
 
 __device__ __forceinline__ float xsum32(float x) {  // x of lanes l and l ^ 32, summed
