@@ -172,23 +172,42 @@ __device__ __forceinline__ uint32_t kcode_pair(uint32_t sx, uint32_t s2, uint32_
   return and_or(P >> sh, ks.lo, and_or(P >> 10, ks.up, magic));
 }
 
+// K words of a staged block, read together at the start of the block so that their
+// latencies overlap instead of each one stalling its phase. The V words are read later,
+// in phase P: the stage's V rows are its last loads, and LDS reads issued right after
+// the vmcnt wait have been seen to return stale bytes for them, while reads a phase
+// later have not.
+struct BlockWords {
+  u4 khd[2], kq0[2], kq1[2];  // phase Q: header and nibble pieces of key kk(r) per tile
+  uint32_t hx[8];             // phase S: {d, dmin} of keys 8g..8g+7
+};
+__device__ __forceinline__ void load_block_words(const Stage &st, int lane, BlockWords &W) {
+  const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int kk = 8 * (r >> 2) + 4 * t + (r & 3);
+    const int sw = swz(kk);
+    W.khd[t] = st.k.hdr[kk];
+    W.kq0[t] = st.k.nib[8 * kk + ((2 * g) ^ sw)];
+    W.kq1[t] = st.k.nib[8 * kk + ((2 * g + 1) ^ sw)];
+  }
+  const uint32_t *hdr32 = reinterpret_cast<const uint32_t *>(st.k.hdr);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) W.hx[k] = hdr32[4 * (8 * g + k)];
+}
+
 // Phase Q: K rows of a staged block -> raw QK sums.
 // Lane (r, g) feeds key kk(r) of tile t with sub-blocks 2g (low nibbles) and 2g+1
 // (high nibbles); its min codes m_2g, m_2g+1 form the A operand of the S2 product.
-__device__ __forceinline__ void phase_q(const Stage &st, const h8 *qb, h4 q2, const Masks &MK,
-                                        const KScaleSel &ks, int lane, QKOut &o) {
-  const int r = lane & 15;
+__device__ __forceinline__ void phase_q(const BlockWords &W, const h8 *qb, h4 q2, const Masks &MK,
+                                        const KScaleSel &ks, QKOut &o) {
   // pk_fma constants: {1024 + sc0, 1024 + sc1} -> {sc0, sc1 / 16}; then the offsets
   // {-1024 sc0, -64 sc1} of the two nibble forms (1024 + n, 1024 + 16 n)
   const h2 ksc = {(_Float16)1.0f, (_Float16)0.0625f}, kcc = {(_Float16)-1024.0f, (_Float16)-64.0f};
   const h2 kneg = {(_Float16)-1024.0f, (_Float16)-1024.0f};
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int kk = 8 * (r >> 2) + 4 * t + (r & 3);
-    const int sw = swz(kk);
-    const u4 hd = st.k.hdr[kk];
-    const u4 q0 = st.k.nib[8 * kk + ((2 * (lane >> 4)) ^ sw)];
-    const u4 q1 = st.k.nib[8 * kk + ((2 * (lane >> 4) + 1) ^ sw)];
+    const u4 hd = W.khd[t], q0 = W.kq0[t], q1 = W.kq1[t];
     const h2 SC = pk_fma(as_h2(kcode_pair(hd.y, hd.w, 0u, ks, MK.magic)), ksc, kcc);
     const h2 CC = SC * kneg;
     const h2 MM = as_h2(kcode_pair(hd.z, hd.w, ks.msh, ks, MK.magic)) + kneg;
@@ -238,20 +257,18 @@ __device__ __forceinline__ float hdr_dot(uint32_t hx, float s1, float s2) {
 // Scores stay in q.k units here (the running max too); sl2 = scale * log2(e) enters
 // the exponents, and clamp / lazy are the +-100-nat clamp and the rescale headroom in
 // those units.
-__device__ __forceinline__ void phase_s(const Stage &st, const QKOut &o, WaveState &S,
+__device__ __forceinline__ void phase_s(const BlockWords &W, const QKOut &o, WaveState &S,
                                         int nvalid, float sl2, float clamp, float lazy, int lane,
                                         float p[8]) {
   const int g = lane >> 4;
-  const uint32_t *hdr32 = reinterpret_cast<const uint32_t *>(st.k.hdr);
   float sc8[8];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int kk = 8 * g + 4 * t + i;
-      // this column's part (hi or lo of q); the other part sits 8 lanes away. d and
-      // dmin enter as fp16 (v_fma_mix).
-      const float part = hdr_dot(hdr32[4 * kk], o.s1[t][i], o.s2[t][i]);
+      // key 8g + 4t + i: this column's part (hi or lo of q); the other part sits 8 lanes
+      // away. d and dmin enter as fp16 (v_fma_mix).
+      const float part = hdr_dot(W.hx[4 * t + i], o.s1[t][i], o.s2[t][i]);
       const float sc = part + ror8(part);
       sc8[4 * t + i] = fminf(fmaxf(sc, -clamp), clamp);
     }
@@ -299,9 +316,9 @@ __device__ __forceinline__ VScaleSel make_vscale_sel(int lane) {
 }
 
 // Phase P: V header tables, PV A/B operands and MFMAs, min term.
-__device__ __forceinline__ void phase_p(const Stage &st, WaveState &S, WaveTab &T,
-                                        const float p[8], const Masks &MK, const VScaleSel &vs,
-                                        int lane) {
+__device__ __forceinline__ void phase_p(const Stage &st, const BlockWords &W, WaveState &S,
+                                        WaveTab &T, const float p[8], const Masks &MK,
+                                        const VScaleSel &vs, int lane) {
   const int n = lane & 15, g = lane >> 4;
   // V header -> constant tables. The four codes of a lane come out as bytes; the pairs
   // (4u, 4u+2) and (4u+1, 4u+3) become fp16 1024 + code, and one v_pk_fma each gives
@@ -578,12 +595,15 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
       const Stage &st = sm.run.st[wave][si];
+      BlockWords W;
+      load_block_words(st, lane, W);
+      __builtin_amdgcn_sched_barrier(0);  // keep the K reads ahead of their phases
       QKOut qo;
       float pv[8];
-      phase_q(st, qb, q2, MK, ks, lane, qo);
-      phase_s(st, qo, S, (int)(seq_k - (int64_t)(first + 4 * i) * kBlk), a.sl2, clamp_raw,
+      phase_q(W, qb, q2, MK, ks, qo);
+      phase_s(W, qo, S, (int)(seq_k - (int64_t)(first + 4 * i) * kBlk), a.sl2, clamp_raw,
               lazy_raw, lane, pv);
-      phase_p(st, S, T, pv, MK, vs, lane);
+      phase_p(st, W, S, T, pv, MK, vs, lane);
       // every LDS read of this stage has completed before it is refilled
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       boff += bstep;

@@ -200,12 +200,18 @@ __device__ __forceinline__ u4s rsrc_advance(u4s r, uint32_t off) {
 
 // issue_stage with a wave-uniform LDS byte address of the Stage and the block's offset
 // already in the resources: no vector work per issue. K: headers at +0, pieces at
-// +0x200; V: headers at +0x1200, pieces at +0x1400.
+// +0x200; V: headers at +0x1200, pieces at +0x1400. The loads go out in the order the
+// block is read (K headers, K pieces, V headers, V pieces), so the data read first has
+// landed longest when the stage's vmcnt wait completes.
 __device__ __forceinline__ void issue_stage_at(uint32_t base, const LoadPlan &P, u4s rk, u4s rv) {
   static_assert(sizeof(TensorStage) == 0x1200 && sizeof(Stage) == 0x2400, "stage layout");
   uint32_t saved;
   asm volatile(
       "s_mov_b32 %[sv], m0\n\t"
+      "s_mov_b32 m0, %[b]\n\ts_nop 0\n\t"
+      "buffer_load_dword %[h0], %[rk], 0 offen lds\n\t"
+      "s_add_u32 m0, %[b], 0x100\n\ts_nop 0\n\t"
+      "buffer_load_dword %[h1], %[rk], 0 offen lds\n\t"
       "s_add_u32 m0, %[b], 0x200\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o0], %[rk], 0 offen lds\n\t"
       "s_add_u32 m0, %[b], 0x600\n\ts_nop 0\n\t"
@@ -214,10 +220,10 @@ __device__ __forceinline__ void issue_stage_at(uint32_t base, const LoadPlan &P,
       "buffer_load_dwordx4 %[o2], %[rk], 0 offen lds\n\t"
       "s_add_u32 m0, %[b], 0xe00\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o3], %[rk], 0 offen lds\n\t"
-      "s_mov_b32 m0, %[b]\n\ts_nop 0\n\t"
-      "buffer_load_dword %[h0], %[rk], 0 offen lds\n\t"
-      "s_add_u32 m0, %[b], 0x100\n\ts_nop 0\n\t"
-      "buffer_load_dword %[h1], %[rk], 0 offen lds\n\t"
+      "s_add_u32 m0, %[b], 0x1200\n\ts_nop 0\n\t"
+      "buffer_load_dword %[h0], %[rv], 0 offen lds\n\t"
+      "s_add_u32 m0, %[b], 0x1300\n\ts_nop 0\n\t"
+      "buffer_load_dword %[h1], %[rv], 0 offen lds\n\t"
       "s_add_u32 m0, %[b], 0x1400\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o0], %[rv], 0 offen lds\n\t"
       "s_add_u32 m0, %[b], 0x1800\n\ts_nop 0\n\t"
@@ -226,10 +232,6 @@ __device__ __forceinline__ void issue_stage_at(uint32_t base, const LoadPlan &P,
       "buffer_load_dwordx4 %[o2], %[rv], 0 offen lds\n\t"
       "s_add_u32 m0, %[b], 0x2000\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o3], %[rv], 0 offen lds\n\t"
-      "s_add_u32 m0, %[b], 0x1200\n\ts_nop 0\n\t"
-      "buffer_load_dword %[h0], %[rv], 0 offen lds\n\t"
-      "s_add_u32 m0, %[b], 0x1300\n\ts_nop 0\n\t"
-      "buffer_load_dword %[h1], %[rv], 0 offen lds\n\t"
       "s_mov_b32 m0, %[sv]"
       : [sv] "=&s"(saved)
       : [b] "s"(base), [o0] "v"(P.nib[0]), [o1] "v"(P.nib[1]), [o2] "v"(P.nib[2]),
