@@ -270,7 +270,7 @@ __device__ __forceinline__ void phase_s(const BlockWords &W, const QKOut &o, Wav
       // away. d and dmin enter as fp16 (v_fma_mix).
       const float part = hdr_dot(W.hx[4 * t + i], o.s1[t][i], o.s2[t][i]);
       const float sc = part + ror8(part);
-      sc8[4 * t + i] = fminf(fmaxf(sc, -clamp), clamp);
+      sc8[4 * t + i] = __builtin_amdgcn_fmed3f(sc, -clamp, clamp);
     }
   if (nvalid < kBlk) {
 #pragma unroll
