@@ -37,10 +37,10 @@ Q8_ROW = 272
 # rocprofv3 --pmc runs (FETCH_SIZE x2.0, WRITE_SIZE x1.0) summarised in profiles/; the
 # profiling step cannot run inside bench.py itself. Refreshed with the profiles.
 MEASURED_TRAFFIC = {
-    3: (92_460_000, "profiles/q4k_decode_config3.md: decode + combine per layer"),
-    1: (12_880_000, "profiles/q8_decode_config1.md: decode + combine"),
-    2: (170_180_000, "profiles/q4k_prefill_config2.md: prefill kernel + split merge"),
-    5: (424_550_000, "profiles/q4k_batched_decode_config5.md: decode + combine per layer"),
+    3: (88_890_000, "profiles/q4k_decode_config3.md: decode + combine per layer"),
+    1: (11_460_000, "profiles/q8_decode_config1.md: decode + combine"),
+    2: (170_260_000, "profiles/q4k_prefill_config2.md: prefill kernel + split merge"),
+    5: (418_800_000, "profiles/q4k_batched_decode_config5.md: decode + combine per layer"),
 }
 
 
