@@ -8,6 +8,8 @@
 // units) and the sum l of 2^(score - m). Rows are padded to 288 floats (1152 bytes, a
 // multiple of 128) so that the combine's 32-entry slices each fill one 128-byte line.
 #pragma once
+#include <type_traits>
+
 #include "pkv_internal.hpp"
 
 namespace pkv {
@@ -51,6 +53,34 @@ struct DecodeSegIn {
 // running max and merge through LDS. For a fused decode step the appended key enters
 // here, from its exactly dequantized K and V rows: score = clamp(q . k_new * scale),
 // weight 2^(score - M).
+// Sum over the 64 lanes of a wave, every lane getting it: DPP moves within rows of 16,
+// then v_permlane16_swap and v_permlane32_swap across them (no LDS round trips).
+__device__ __forceinline__ float wave_sum(float x) {
+  auto dpp = [](float v, auto ctrl) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v),
+                                                                __builtin_bit_cast(int, v),
+                                                                decltype(ctrl)::value, 0xF, 0xF,
+                                                                false));
+  };
+  x += dpp(x, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+  x += dpp(x, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+  x += dpp(x, std::integral_constant<int, 0x141>{});  // row_half_mirror
+  x += dpp(x, std::integral_constant<int, 0x140>{});  // row_mirror
+  {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    x = __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+  }
+  {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    x = __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+  }
+  return x;
+}
+
 constexpr int kCombSlices = 32;  // partial slices (8 threads each)
 constexpr int kCombChunk = 8;    // partials per slice per round
 struct CombineArgs {
@@ -111,9 +141,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs c) {
       m_loc = mc;
     }
   }
-  float d = prod;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) d += __shfl_xor(d, o, 64);
+  const float d = wave_sum(prod);
   if ((tid & 63) == 0) dotp[tid >> 6] = d;
   accs[ps][g4] = acc;
   if (g4 == 0) {
