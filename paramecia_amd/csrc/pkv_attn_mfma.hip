@@ -281,7 +281,10 @@ __device__ __forceinline__ void phase_s(const BlockWords &W, const QKOut &o, Wav
 #pragma unroll
   for (int k = 1; k < 8; ++k) bm = fmaxf(bm, sc8[k]);
   bm = xmax32(xmax16(bm));
-  if (__any(bm > S.m_run + lazy)) {
+  if (S.m_run == -INFINITY) {
+    // first block with a valid key: nothing accumulated yet, no rescale
+    S.m_run = bm;
+  } else if (__any(bm > S.m_run + lazy)) {
     const float m_new = fmaxf(S.m_run, bm);
     const float alpha = (S.m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((S.m_run - m_new) * sl2);
     S.lsum *= alpha;
