@@ -47,7 +47,10 @@ struct Segment {
 // here (6.5 TB/s read + write, against 5.3-5.9 TB/s for 64-256 KB chunks or cached
 // accesses, and 5.3 TB/s for hipMemcpyAsync).
 constexpr uint64_t kChunk = 16 * 1024;
-constexpr int kCopyWGs = 2048;  // workgroups; each walks chunks c = wg, wg + 2048, ...
+// One workgroup per chunk (the hardware dispatcher keeps every CU fed; a persistent grid
+// of 2048 workgroups walking the chunks measured 7% slower on a 532 MB restore). Larger
+// copies loop: workgroup wg takes chunks wg, wg + grid, ...
+constexpr int kCopyWGs = 1 << 20;
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
