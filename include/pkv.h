@@ -132,6 +132,46 @@ int pkv_append_attend_batched(pkv_cache *const *caches, int n, const float *k,
                               const float *v, const float *q, int num_heads, float scale,
                               float *out, pkv_stream stream);
 
+/* ---- q/k preparation fused into the append (FullAttention::forward qn:2369-2399) ----
+ * RotaryEmbedding (qn:866-940): cos/sin tables [max_pos][n_rot/2] f32, built on the host
+ * as RotaryEmbedding::new does (inv_freq = 1/theta^(2i/n_rot), f32 cos/sin of t*inv_freq)
+ * and kept on the device; one table serves every layer (the reference shares it). */
+typedef struct pkv_rope pkv_rope;
+/* The tables alone, into host memory (no device work). */
+int pkv_rope_tables_host(int n_rot, int64_t max_pos, double theta, float *cos_out,
+                         float *sin_out);
+int pkv_rope_create(int n_rot, int64_t max_pos, double theta, pkv_rope **out);
+int pkv_rope_destroy(pkv_rope *r);
+int pkv_rope_geometry(const pkv_rope *r, int *n_rot, int64_t *max_pos, const float **cos_tab,
+                      const float **sin_tab);
+
+/* One layer's q/k preparation: the RmsNorm alphas of attn_q_norm / attn_k_norm (device f32
+ * [head_dim], qn:2297-2306), rms_norm_eps, and the shared rope. */
+typedef struct {
+  const float *q_alpha;
+  const float *k_alpha;
+  float eps;
+  const pkv_rope *rope;
+} pkv_qk_prep;
+
+/* q_norm, k_norm, the [b,l,h,d] -> [b,h,l,d] transposes, rope (qn:2369-2399) and
+ * append_quantized (qn:2442) in one launch. Inputs are the projection outputs as the
+ * reference reshapes them: q [batch, n, num_heads, head_dim] (may be NULL, with q_out),
+ * k, v [batch, n, n_kv_heads, head_dim]. q_out (same layout as q) receives the normalised,
+ * rotated q; K rows are normalised and rotated, V rows taken as given, both encoded at
+ * the cache's position. Token t sits at rope position offset + t (len + t for
+ * offset = -1); positions past the rope table -> PKV_ERR_ARG before anything changes.
+ * Offset, overflow and error rules otherwise as pkv_append. */
+int pkv_append_prep(pkv_cache *h, const pkv_qk_prep *prep, const float *q, int num_heads,
+                    float *q_out, const float *k, const float *v, int64_t n, int64_t offset);
+
+/* A decode step from the projection outputs: pkv_append_prep of one token (its q into
+ * the handle's scratch), then attention of the prepared q over all len+1 keys.
+ * q, out: [batch, 1, num_heads, head_dim]; k, v: [batch, 1, n_kv_heads, head_dim]. */
+int pkv_append_attend_prep(pkv_cache *h, const pkv_qk_prep *prep, const float *q,
+                           const float *k, const float *v, int num_heads, float scale,
+                           int64_t offset, float *out);
+
 /* ---- PrefixCache (qn:834-864, 2780-2884, 4066-4132, 5702-5750) ---- */
 int pkv_prefix_create(const uint32_t *prefix_tokens, size_t n_tokens, int n_layers,
                       pkv_prefix **out);

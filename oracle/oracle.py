@@ -89,6 +89,14 @@ def _declare(L: ctypes.CDLL) -> None:
                                  ctypes.c_int, _dp]
     L.orc_attend_faithful.argtypes = [cp, _fp, ctypes.c_int, ctypes.c_int, ctypes.c_float, i64,
                                       ctypes.c_int, _fp, ctypes.c_int]
+    _i64p = ctypes.POINTER(ctypes.c_int64)
+    L.orc_rope_tables.argtypes = [ctypes.c_int, i64, ctypes.c_double, _fp, _fp]
+    L.orc_rms_norm.argtypes = [_fp, _fp, ctypes.c_float, sz, ctypes.c_int, _fp]
+    L.orc_rms_norm.restype = None
+    L.orc_rope_rows.argtypes = [_fp, sz, ctypes.c_int, ctypes.c_int, _i64p, _fp, _fp]
+    L.orc_qk_prep.argtypes = [_fp, _fp] + [ctypes.c_int] * 5 + [_fp, _fp, ctypes.c_float,
+                                                                 ctypes.c_int, _fp, _fp, i64,
+                                                                 _fp, _fp]
 
 
 def _f(a: np.ndarray):
@@ -174,6 +182,64 @@ def normal(n: int, seed: int, stream: int, scale: float = 1.0) -> np.ndarray:
 
 def bytes_per_row(quant: int, head_dim: int) -> int:
     return lib().orc_bytes_per_row(quant, head_dim)
+
+
+# ---------------------------------------------------------------- q/k preparation
+def rope_tables(n_rot: int, max_pos: int, theta: float):
+    """RotaryEmbedding::new tables (qwen3_next.rs:878-904): cos, sin [max_pos, n_rot/2]."""
+    half = n_rot // 2
+    c = np.zeros((max_pos, half), dtype=np.float32)
+    s = np.zeros((max_pos, half), dtype=np.float32)
+    rc = lib().orc_rope_tables(n_rot, max_pos, theta, _f(c), _f(s))
+    if rc != OK:
+        raise ValueError(f"orc_rope_tables failed ({rc})")
+    return c, s
+
+
+def rms_norm(x: np.ndarray, alpha: np.ndarray, eps: float) -> np.ndarray:
+    """candle_nn::ops::rms_norm over the last axis (qwen3_next.rs:2369, 2389)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    a = np.ascontiguousarray(alpha, dtype=np.float32)
+    d = x.shape[-1]
+    y = np.empty_like(x)
+    lib().orc_rms_norm(_f(x), _f(a), eps, x.size // d, d, _f(y))
+    return y
+
+
+def rope_rows(x: np.ndarray, pos: np.ndarray, n_rot: int, cos: np.ndarray,
+              sin: np.ndarray) -> np.ndarray:
+    """candle rope on x[..., :n_rot]; pos gives each row's position (flattened rows)."""
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    d = y.shape[-1]
+    p = np.ascontiguousarray(pos, dtype=np.int64).reshape(-1)
+    assert p.size == y.size // d
+    rc = lib().orc_rope_rows(_f(y), p.size, d, n_rot, p.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                             _f(np.ascontiguousarray(cos)), _f(np.ascontiguousarray(sin)))
+    if rc != OK:
+        raise ValueError(f"orc_rope_rows failed ({rc})")
+    return y
+
+
+def qk_prep(q, k, q_alpha, k_alpha, eps: float, n_rot: int, cos, sin, offset: int):
+    """q [b, l, H, d], k [b, l, Hkv, d] -> (q_norm + rope, k_norm + rope) at positions
+    offset + t (FullAttention::forward, qwen3_next.rs:2369-2399). Either may be None."""
+    ref = q if q is not None else k
+    b, l, _, d = ref.shape
+    qa = np.ascontiguousarray(q, dtype=np.float32) if q is not None else None
+    ka = np.ascontiguousarray(k, dtype=np.float32) if k is not None else None
+    qo = np.empty_like(qa) if qa is not None else None
+    ko = np.empty_like(ka) if ka is not None else None
+    nul = ctypes.cast(None, _fp)
+    rc = lib().orc_qk_prep(
+        _f(qa) if qa is not None else nul, _f(ka) if ka is not None else nul, b, l,
+        qa.shape[2] if qa is not None else 0, ka.shape[2] if ka is not None else 0, d,
+        _f(np.ascontiguousarray(q_alpha, dtype=np.float32)) if qa is not None else nul,
+        _f(np.ascontiguousarray(k_alpha, dtype=np.float32)) if ka is not None else nul,
+        eps, n_rot, _f(np.ascontiguousarray(cos)), _f(np.ascontiguousarray(sin)), offset,
+        _f(qo) if qo is not None else nul, _f(ko) if ko is not None else nul)
+    if rc != OK:
+        raise ValueError(f"orc_qk_prep failed ({rc})")
+    return qo, ko
 
 
 # ---------------------------------------------------------------- cache

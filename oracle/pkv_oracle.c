@@ -693,3 +693,85 @@ int orc_attend_faithful(const orc_cache *c, const float *q, int l, int num_heads
   free(Vr);
   return ORC_OK;
 }
+
+/* ------------------------------------------------------------------ */
+/* q/k preparation: RMSNorm + partial RoPE (qwen3_next.rs:2369-2399)     */
+/* ------------------------------------------------------------------ */
+
+/* RotaryEmbedding::new, qwen3_next.rs:878-904. */
+int orc_rope_tables(int n_rot, int64_t max_pos, double theta, float *cos_out, float *sin_out) {
+  if (n_rot <= 0 || (n_rot & 1) || max_pos < 0) return ORC_ERR_ARG;
+  const int half = n_rot / 2;
+  float *inv = (float *)malloc((size_t)half * sizeof(float));
+  for (int i = 0; i < half; ++i) {
+    /* (0..n_rot).step_by(2): exponent (2i as f64) / (n_rot as f64) */
+    const float p = (float)pow(theta, (double)(2 * i) / (double)n_rot);
+    inv[i] = 1.0f / p;
+  }
+  for (int64_t t = 0; t < max_pos; ++t)
+    for (int i = 0; i < half; ++i) {
+      const float f = (float)t * inv[i]; /* t.matmul(inv_freq): one product */
+      cos_out[(size_t)t * half + i] = cosf(f);
+      sin_out[(size_t)t * half + i] = sinf(f);
+    }
+  free(inv);
+  return ORC_OK;
+}
+
+/* candle_nn::ops::rms_norm (CPU): qwen3_next.rs:2369 (q_norm), 2389 (k_norm). */
+void orc_rms_norm(const float *x, const float *alpha, float eps, size_t rows, int d, float *y) {
+  for (size_t r = 0; r < rows; ++r) {
+    const float *s = x + r * (size_t)d;
+    float *o = y + r * (size_t)d;
+    float sum2 = -0.0f; /* Sum for f32 folds from -0.0; same result for any x here */
+    for (int e = 0; e < d; ++e) sum2 += s[e] * s[e];
+    const float m = sqrtf(sum2 / (float)d + eps);
+    for (int e = 0; e < d; ++e) o[e] = s[e] / m * alpha[e];
+  }
+}
+
+/* candle_nn::rotary_emb::rope on x[.., :n_rot] (RotaryEmbedding::apply, qwen3_next.rs:919-939). */
+int orc_rope_rows(float *x, size_t rows, int d, int n_rot, const int64_t *pos,
+                  const float *cos_tab, const float *sin_tab) {
+  if (n_rot <= 0 || (n_rot & 1) || n_rot > d) return ORC_ERR_ARG;
+  const int half = n_rot / 2;
+  for (size_t r = 0; r < rows; ++r) {
+    float *v = x + r * (size_t)d;
+    const float *c = cos_tab + (size_t)pos[r] * half, *s = sin_tab + (size_t)pos[r] * half;
+    for (int i = 0; i < half; ++i) {
+      const float a = v[i], b = v[i + half];
+      v[i] = a * c[i] - b * s[i];
+      v[i + half] = a * s[i] + b * c[i];
+    }
+  }
+  return ORC_OK;
+}
+
+static int prep_rows(const float *x, int batch, int l, int heads, int d, const float *alpha,
+                     float eps, int n_rot, const float *cos_tab, const float *sin_tab,
+                     int64_t offset, float *out) {
+  const size_t rows = (size_t)batch * l * heads;
+  orc_rms_norm(x, alpha, eps, rows, d, out);
+  int64_t *pos = (int64_t *)malloc((rows + 1) * sizeof(int64_t));
+  for (size_t r = 0; r < rows; ++r) pos[r] = offset + (int64_t)((r / (size_t)heads) % (size_t)l);
+  const int rc = orc_rope_rows(out, rows, d, n_rot, pos, cos_tab, sin_tab);
+  free(pos);
+  return rc;
+}
+
+/* FullAttention::forward, qwen3_next.rs:2369 (q_norm), 2389 (k_norm), 2399 (rope). */
+int orc_qk_prep(const float *q, const float *k, int batch, int l, int n_heads, int n_kv_heads,
+                int d, const float *q_alpha, const float *k_alpha, float eps, int n_rot,
+                const float *cos_tab, const float *sin_tab, int64_t offset, float *q_out,
+                float *k_out) {
+  if (batch < 0 || l < 0 || d <= 0 || offset < 0) return ORC_ERR_ARG;
+  if (q != NULL) {
+    const int rc = prep_rows(q, batch, l, n_heads, d, q_alpha, eps, n_rot, cos_tab, sin_tab,
+                             offset, q_out);
+    if (rc != ORC_OK) return rc;
+  }
+  if (k != NULL)
+    return prep_rows(k, batch, l, n_kv_heads, d, k_alpha, eps, n_rot, cos_tab, sin_tab,
+                     offset, k_out);
+  return ORC_OK;
+}

@@ -41,6 +41,20 @@
  *                               independent numpy softmax(QK^T)V on small shapes.
  *   RNG ....................... pinned: Philox4x32-10 known-answer vectors from
  *                               Salmon et al. (SC'11) / Random123.
+ *   rope tables ............... pinned: closed form inv_freq = theta^(-2i/n_rot)
+ *                               against float64, position 0 -> (1, 0) exactly,
+ *                               cos^2 + sin^2 = 1, and transformers' independent
+ *                               Qwen3-Next rotary module (partial_rotary_factor).
+ *   rms_norm .................. pinned: closed forms (constant row, one-hot row),
+ *                               per-element alpha, float64 restatement, and
+ *                               transformers' Qwen3NextRMSNorm (weight 1 + w).
+ *   rope (half-split) ......... pinned: unit-vector rotations (sign and pairing
+ *                               (i, i + n_rot/2)), position 0 = identity, pass-through
+ *                               of dims >= n_rot, float64 complex rotation, and
+ *                               transformers' apply_rotary_pos_emb.
+ *   The last ulp of these three follows candle's CPU kernels (rms_norm,
+ *   rotary_emb::rope) and the host libm's powf/sinf/cosf, restated; the candle fork
+ *   is absent, so bit-level agreement with it is UNPINNED (tolerance-level pinned).
  */
 #ifndef PKV_ORACLE_H
 #define PKV_ORACLE_H
@@ -119,6 +133,27 @@ int orc_attend_f64(const orc_cache *c, const float *q, int l, int num_heads, dou
  * cache, permute copy, repeat_kv copy, transposed-K copy, matmul, softmax, matmul). */
 int orc_attend_faithful(const orc_cache *c, const float *q, int l, int num_heads,
                         float scale, int64_t q_offset, int causal, float *out, int threads);
+
+/* ---- q/k preparation ahead of the cache (FullAttention::forward, qwen3_next.rs:2369-2399) ----
+ * RotaryEmbedding::new (qwen3_next.rs:878-904): inv_freq[i] = 1 / (f32)(theta^(2i / n_rot))
+ * with the power in f64, freqs[p][i] = (f32)p * inv_freq[i], cos/sin in f32 (libm cosf,
+ * sinf). Tables are [max_pos][n_rot / 2]. n_rot must be even and positive. */
+int orc_rope_tables(int n_rot, int64_t max_pos, double theta, float *cos_out, float *sin_out);
+/* candle_nn::ops::rms_norm on the CPU: per row of d values, sum2 = sequential f32 sum of
+ * x*x, m = sqrtf(sum2 / d + eps), y = x / m * alpha (qwen3_next.rs:2369, 2389). */
+void orc_rms_norm(const float *x, const float *alpha, float eps, size_t rows, int d, float *y);
+/* candle_nn::rotary_emb::rope (half-split pairs (i, i + n_rot/2)) on the first n_rot
+ * values of each row of d values, in place; row r sits at position pos[r]
+ * (RotaryEmbedding::apply, qwen3_next.rs:906-940). */
+int orc_rope_rows(float *x, size_t rows, int d, int n_rot, const int64_t *pos,
+                  const float *cos_tab, const float *sin_tab);
+/* q: [batch, l, n_heads, d] -> q_norm then rope; k: [batch, l, n_kv_heads, d] -> k_norm
+ * then rope; token t sits at position offset + t. Outputs keep the input layout. Either
+ * of q / k may be NULL (with its output). */
+int orc_qk_prep(const float *q, const float *k, int batch, int l, int n_heads, int n_kv_heads,
+                int d, const float *q_alpha, const float *k_alpha, float eps, int n_rot,
+                const float *cos_tab, const float *sin_tab, int64_t offset, float *q_out,
+                float *k_out);
 
 #ifdef __cplusplus
 }

@@ -7,6 +7,6 @@ from ._lib import PkvError, lib  # noqa: F401
 from .kv_cache import (  # noqa: F401
     EmptyCacheError, FullAttentionKv, KvCacheError, KvCacheOffsetMismatch, KvCacheOverflow,
     KvCacheQuantization, LinearAttentionState, ModelKvState, PreallocatedQuantizedKvCache,
-    PrefixCache, PrefixCacheEntry, PrefixLayerMismatch, RecurrentState, append_attend_batched,
-    fill_normal, flash_attn, scale_channels,
+    PrefixCache, PrefixCacheEntry, PrefixLayerMismatch, QkPrep, RecurrentState, RotaryEmbedding,
+    append_attend_batched, fill_normal, flash_attn, scale_channels,
 )

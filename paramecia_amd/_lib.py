@@ -28,6 +28,8 @@ SYMBOLS = (
     "pkv_prefix_num_layers", "pkv_prefix_entry_kind", "pkv_prefix_save_full",
     "pkv_prefix_save_linear", "pkv_prefix_linear_sizes", "pkv_prefix_full_len",
     "pkv_prefix_restore", "pkv_fill_normal", "pkv_scale_channels", "pkv_copy_segments",
+    "pkv_rope_tables_host", "pkv_rope_create", "pkv_rope_destroy", "pkv_rope_geometry",
+    "pkv_append_prep", "pkv_append_attend_prep",
 )
 
 
@@ -44,6 +46,16 @@ class LayerTarget(ctypes.Structure):
         ("conv", ctypes.c_void_p),
         ("gate_offset", ctypes.c_void_p),
         ("state_valid", ctypes.POINTER(ctypes.c_int)),
+    ]
+
+
+class QkPrep(ctypes.Structure):
+    """pkv_qk_prep: one layer's q_norm / k_norm alphas, eps and the shared rope."""
+    _fields_ = [
+        ("q_alpha", ctypes.c_void_p),
+        ("k_alpha", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("rope", ctypes.c_void_p),
     ]
 
 
@@ -104,6 +116,12 @@ def _declare(L: ctypes.CDLL) -> None:
         "pkv_fill_normal": ([vp, c_sz, c_u64, c_u64, fl, vp], c_int),
         "pkv_scale_channels": ([vp, c_sz, c_int, P(c_int), c_int, fl, vp], c_int),
         "pkv_copy_segments": ([P(vp), P(vp), P(c_sz), c_int, vp], c_int),
+        "pkv_rope_tables_host": ([c_int, c_i64, ctypes.c_double, vp, vp], c_int),
+        "pkv_rope_create": ([c_int, c_i64, ctypes.c_double, P(vp)], c_int),
+        "pkv_rope_destroy": ([vp], c_int),
+        "pkv_rope_geometry": ([vp, P(c_int), P(c_i64), P(vp), P(vp)], c_int),
+        "pkv_append_prep": ([vp, P(QkPrep), vp, c_int, vp, vp, vp, c_i64, c_i64], c_int),
+        "pkv_append_attend_prep": ([vp, P(QkPrep), vp, vp, vp, c_int, fl, c_i64, vp], c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

@@ -2,6 +2,7 @@
 // checking around the kernels. The reference behaviour each function mirrors is cited
 // in include/pkv.h; error codes stand in for the reference's bail! strings.
 #include <ctype.h>
+#include <math.h>
 #include <string.h>
 
 #include <string>
@@ -368,6 +369,163 @@ int pkv_flash_attn(int quant, const float *q, const void *k_bytes, const void *v
   a.causal = causal;
   a.out = out;
   return launch_attend(a, util_workspace(), static_cast<hipStream_t>(stream));
+}
+
+// ---- q/k preparation (FullAttention::forward, qwen3_next.rs:2369-2399) ----
+
+// RotaryEmbedding::new (qwen3_next.rs:878-904): inv_freq[i] = 1f32 / (theta^(2i/n_rot) as
+// f32) with the power in f64, freqs = (t as f32) * inv_freq[i] (a [max_pos, 1] x
+// [1, n_rot/2] matmul: one rounded product), then f32 cos and sin (libm cosf / sinf).
+int pkv_rope_tables_host(int n_rot, int64_t max_pos, double theta, float *cos_out,
+                         float *sin_out) {
+  if (n_rot <= 0 || (n_rot & 1) || max_pos < 0 || (max_pos > 0 && (!cos_out || !sin_out)))
+    return set_error(PKV_ERR_ARG, "n_rot must be even and positive, max_pos >= 0");
+  const int half = n_rot / 2;
+  std::vector<float> inv(half);
+  for (int i = 0; i < half; ++i)
+    inv[i] = 1.0f / (float)::pow(theta, (double)(2 * i) / (double)n_rot);
+  for (int64_t t = 0; t < max_pos; ++t) {
+    const float ft = (float)t;
+    for (int i = 0; i < half; ++i) {
+      const float f = ft * inv[i];
+      cos_out[t * half + i] = ::cosf(f);
+      sin_out[t * half + i] = ::sinf(f);
+    }
+  }
+  return PKV_OK;
+}
+
+int pkv_rope_create(int n_rot, int64_t max_pos, double theta, pkv_rope **out) {
+  if (!out) return set_error(PKV_ERR_ARG, "null argument");
+  *out = nullptr;
+  if (max_pos <= 0) return set_error(PKV_ERR_ARG, "max_pos must be positive");
+  if (n_rot <= 0 || (n_rot & 1)) return set_error(PKV_ERR_ARG, "n_rot must be even and positive");
+  const size_t n = (size_t)max_pos * (size_t)(n_rot / 2);
+  std::vector<float> c(n), sn(n);
+  int rc = pkv_rope_tables_host(n_rot, max_pos, theta, c.data(), sn.data());
+  if (rc) return rc;
+  pkv_rope *r = new pkv_rope{n_rot, max_pos, nullptr, nullptr};
+  hipError_t e = hipMalloc(&r->cos, n * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&r->sin, n * sizeof(float));
+  if (e == hipSuccess) e = hipMemcpy(r->cos, c.data(), n * sizeof(float), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(r->sin, sn.data(), n * sizeof(float), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    pkv_rope_destroy(r);
+    return hip_error(e, "pkv_rope_create");
+  }
+  *out = r;
+  return PKV_OK;
+}
+
+int pkv_rope_destroy(pkv_rope *r) {
+  if (!r) return PKV_OK;
+  if (r->cos) (void)hipFree(r->cos);
+  if (r->sin) (void)hipFree(r->sin);
+  delete r;
+  return PKV_OK;
+}
+
+int pkv_rope_geometry(const pkv_rope *r, int *n_rot, int64_t *max_pos, const float **cos_tab,
+                      const float **sin_tab) {
+  if (!r) return set_error(PKV_ERR_ARG, "null argument");
+  if (n_rot) *n_rot = r->n_rot;
+  if (max_pos) *max_pos = r->max_pos;
+  if (cos_tab) *cos_tab = r->cos;
+  if (sin_tab) *sin_tab = r->sin;
+  return PKV_OK;
+}
+
+// Checks shared by the two prepared appends; fills everything but q/q_out/k/v/t0/l.
+static int prep_setup(const pkv_cache *h, const pkv_qk_prep *prep, bool with_q, int num_heads,
+                      int64_t n, int64_t offset, PrepArgs &a) {
+  if (!h || !prep || !prep->rope || !prep->k_alpha)
+    return set_error(PKV_ERR_ARG, "null argument");
+  if (with_q && (!prep->q_alpha || num_heads <= 0))
+    return set_error(PKV_ERR_ARG, "q needs q_alpha and num_heads > 0");
+  if (n < 0 || n >= (1ll << 31)) return set_error(PKV_ERR_ARG, "n out of range");
+  const pkv_rope *r = prep->rope;
+  if (r->n_rot > h->head_dim) return set_error(PKV_ERR_ARG, "n_rot exceeds head_dim");
+  if (h->head_dim > 512) return set_error(PKV_ERR_UNSUPPORTED, "head_dim > 512");
+  // RotaryEmbedding::apply narrows the tables at [offset, offset + n) (qwen3_next.rs:921)
+  const int64_t first = offset >= 0 ? offset : h->seq_len;
+  if (first + n > r->max_pos)
+    return set_error(PKV_ERR_ARG, "positions " + std::to_string(first) + ".." +
+                                      std::to_string(first + n) + " exceed the rope table (" +
+                                      std::to_string(r->max_pos) + ")");
+  a = PrepArgs{};
+  a.kc = h->k;
+  a.vc = h->v;
+  a.q_alpha = prep->q_alpha;
+  a.k_alpha = prep->k_alpha;
+  a.cos_tab = r->cos;
+  a.sin_tab = r->sin;
+  a.eps = prep->eps;
+  a.quant = h->quant;
+  a.batch = h->batch;
+  a.l = (int)n;
+  a.num_heads = with_q ? num_heads : 0;
+  a.kv_heads = h->n_kv_heads;
+  a.head_dim = h->head_dim;
+  a.padded = h->padded;
+  a.n_rot = r->n_rot;
+  a.bpr = (int64_t)h->bpr;
+  a.q_rows = with_q ? (int64_t)h->batch * n * num_heads : 0;
+  a.kv_rows = (int64_t)h->batch * n * h->n_kv_heads;
+  return PKV_OK;
+}
+
+int pkv_append_prep(pkv_cache *h, const pkv_qk_prep *prep, const float *q, int num_heads,
+                    float *q_out, const float *k, const float *v, int64_t n, int64_t offset) {
+  if ((q == nullptr) != (q_out == nullptr))
+    return set_error(PKV_ERR_ARG, "q and q_out go together");
+  if (n > 0 && (!k || !v)) return set_error(PKV_ERR_ARG, "null argument");
+  PrepArgs a;
+  int rc = prep_setup(h, prep, q != nullptr, num_heads, n, offset, a);
+  if (rc) return rc;
+  rc = position_for_append(h, n, offset);
+  if (rc) return rc;
+  a.q = q;
+  a.q_out = q_out;
+  a.k = k;
+  a.v = v;
+  a.t0 = h->seq_len;
+  rc = launch_prep_append(a, h->stream);
+  if (rc) return rc;
+  h->seq_len += n;
+  return PKV_OK;
+}
+
+int pkv_append_attend_prep(pkv_cache *h, const pkv_qk_prep *prep, const float *q,
+                           const float *k, const float *v, int num_heads, float scale,
+                           int64_t offset, float *out) {
+  if (!q || !k || !v || !out) return set_error(PKV_ERR_ARG, "null argument");
+  if (h && (num_heads <= 0 || num_heads % h->n_kv_heads))
+    return set_error(PKV_ERR_ARG, "num_heads must be a multiple of num_kv_heads");
+  PrepArgs a;
+  int rc = prep_setup(h, prep, true, num_heads, 1, offset, a);
+  if (rc) return rc;
+  rc = h->qws.reserve((size_t)h->batch * num_heads * h->head_dim * sizeof(float));
+  if (rc) return rc;
+  const int64_t saved = h->seq_len;
+  rc = position_for_append(h, 1, offset);
+  if (rc) return rc;
+  const int64_t t_new = h->seq_len;
+  float *qp = static_cast<float *>(h->qws.ptr);
+  a.q = q;
+  a.q_out = qp;
+  a.k = k;
+  a.v = v;
+  a.t0 = t_new;
+  rc = launch_prep_append(a, h->stream);
+  if (!rc)
+    rc = launch_attend(cache_args(h, qp, 1, num_heads, scale, t_new + 1, t_new, 1, out), h->ws,
+                       h->stream);
+  if (rc) {
+    if (rc != PKV_ERR_HIP) h->seq_len = saved;
+    return rc;
+  }
+  h->seq_len = t_new + 1;
+  return PKV_OK;
 }
 
 int pkv_append_attend_batched(pkv_cache *const *caches, int n, const float *k, const float *v,

@@ -61,6 +61,12 @@ struct Workspace {
 
 }  // namespace pkv
 
+struct pkv_rope {
+  int n_rot;
+  int64_t max_pos;
+  float *cos, *sin;  // device [max_pos][n_rot / 2]
+};
+
 struct pkv_cache {
   int quant, batch, n_kv_heads, head_dim, padded;
   int64_t max_seq_len, seq_len;
@@ -68,6 +74,7 @@ struct pkv_cache {
   uint8_t *k, *v;
   hipStream_t stream;
   pkv::Workspace ws;
+  pkv::Workspace qws;  // prepared q of a decode step with q/k preparation
   pkv::RowStrides strides() const {
     return {(int64_t)n_kv_heads * (int64_t)bpr, (int64_t)batch * n_kv_heads * (int64_t)bpr,
             (int64_t)bpr};
@@ -84,6 +91,22 @@ int launch_append(int quant, const float *k, const float *v, uint8_t *kc, uint8_
 // Dequantize rows [0, S) to f32 [batch, heads, S, head_dim].
 int launch_dequant(int quant, const uint8_t *kc, const uint8_t *vc, float *ko, float *vo,
                    int batch, int heads, int head_dim, int64_t S, hipStream_t s);
+
+// ---- launcher (pkv_prep.hip) ----
+// One launch: q rows [b, l, num_heads, d] -> q_norm + rope -> q_out; K rows
+// [b, l, kv_heads, d] -> k_norm + rope -> encoded at cache token t0 + t; V rows encoded.
+// Token t sits at position t0 + t of the rope tables.
+struct PrepArgs {
+  const float *q, *k, *v;  // q may be null (q_rows = 0)
+  float *q_out;
+  uint8_t *kc, *vc;
+  const float *q_alpha, *k_alpha;   // [head_dim]
+  const float *cos_tab, *sin_tab;   // [max_pos][n_rot / 2]
+  float eps;
+  int quant, batch, l, num_heads, kv_heads, head_dim, padded, n_rot;
+  int64_t t0, bpr, q_rows, kv_rows;
+};
+int launch_prep_append(const PrepArgs &a, hipStream_t s);
 
 // ---- launchers (pkv_attn.hip) ----
 struct AttnArgs {

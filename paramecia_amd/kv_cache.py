@@ -217,6 +217,33 @@ class PreallocatedQuantizedKvCache:
                                       offset, _ptr(out)))
         return out
 
+    def append_prep(self, q: Optional[torch.Tensor], new_k: torch.Tensor, new_v: torch.Tensor,
+                    prep: "QkPrep", offset: int = -1) -> Optional[torch.Tensor]:
+        """q_norm / k_norm, rope and append_quantized in one launch (qwen3_next.rs:2369-2442).
+        q: [batch, n, num_heads, d] or None; new_k, new_v: [batch, n, num_kv_heads, d], the
+        projection outputs before the transpose. Returns the prepared q (same layout)."""
+        self._follow_stream()
+        k, v = _f32(new_k, "new_k"), _f32(new_v, "new_v")
+        if k.shape != v.shape or k.dim() != 4:
+            raise KvCacheError("new_k/new_v must both be [batch, n, heads, head_dim]")
+        qq = _f32(q, "q") if q is not None else None
+        q_out = torch.empty_like(qq) if qq is not None else None
+        H = qq.shape[2] if qq is not None else 0
+        _call(lib().pkv_append_prep(self._h, ctypes.byref(prep.c), _ptr(qq), H, _ptr(q_out),
+                                    _ptr(k), _ptr(v), k.shape[1], offset))
+        return q_out
+
+    def append_attend_prep(self, q: torch.Tensor, new_k: torch.Tensor, new_v: torch.Tensor,
+                           prep: "QkPrep", scale: float, offset: int = -1) -> torch.Tensor:
+        """Decode step from the projection outputs: prepare q and k, append, attend.
+        q: [batch, 1, num_heads, d]; new_k, new_v: [batch, 1, num_kv_heads, d]."""
+        self._follow_stream()
+        k, v, qq = _f32(new_k, "new_k"), _f32(new_v, "new_v"), _f32(q, "q")
+        out = torch.empty_like(qq)
+        _call(lib().pkv_append_attend_prep(self._h, ctypes.byref(prep.c), _ptr(qq), _ptr(k),
+                                           _ptr(v), qq.shape[2], scale, offset, _ptr(out)))
+        return out
+
     def clear(self) -> None:
         check(lib().pkv_clear(self._h))
 
@@ -270,6 +297,64 @@ def scale_channels(t: torch.Tensor, channels: Sequence[int], factor: float) -> t
     return t
 
 
+# ------------------------------------------------------------------ q/k preparation
+class RotaryEmbedding:
+    """RotaryEmbedding (qwen3_next.rs:866-940): cos/sin tables [max_pos, n_rot/2] built on
+    the host as RotaryEmbedding::new does, kept on the device, shared by every layer."""
+
+    def __init__(self, n_rot: int, max_position_embeddings: int, rope_theta: float):
+        h = ctypes.c_void_p()
+        _call(lib().pkv_rope_create(n_rot, max_position_embeddings, rope_theta, ctypes.byref(h)))
+        self._h = h
+        self.n_rot, self.max_pos, self.theta = n_rot, max_position_embeddings, rope_theta
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            lib().pkv_rope_destroy(h)
+            self._h = None
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    @staticmethod
+    def host_tables(n_rot: int, max_pos: int, rope_theta: float):
+        """(cos, sin) [max_pos, n_rot/2] CPU float32 tensors from the library's host code
+        (no device work)."""
+        half = max(n_rot // 2, 1)
+        c = torch.zeros((max_pos, half), dtype=torch.float32)
+        s = torch.zeros((max_pos, half), dtype=torch.float32)
+        _call(lib().pkv_rope_tables_host(n_rot, max_pos, rope_theta,
+                                         ctypes.c_void_p(c.data_ptr()),
+                                         ctypes.c_void_p(s.data_ptr())))
+        return c, s
+
+    def tables(self):
+        """The device tables as [max_pos, n_rot/2] float32 tensors (copies)."""
+        cp, sp = ctypes.c_void_p(), ctypes.c_void_p()
+        _call(lib().pkv_rope_geometry(self._h, None, None, ctypes.byref(cp), ctypes.byref(sp)))
+        n = self.max_pos * (self.n_rot // 2) * 4
+        shape = (self.max_pos, self.n_rot // 2)
+        c = torch.as_tensor(_DeviceBytes(cp.value, n), device="cuda").clone().view(torch.float32)
+        s = torch.as_tensor(_DeviceBytes(sp.value, n), device="cuda").clone().view(torch.float32)
+        return c.view(shape), s.view(shape)
+
+
+class QkPrep:
+    """One full-attention layer's q_norm / k_norm (RmsNorm alphas attn_q_norm.weight /
+    attn_k_norm.weight, qwen3_next.rs:2297-2306) and the shared rope."""
+
+    def __init__(self, q_alpha: torch.Tensor, k_alpha: torch.Tensor, eps: float,
+                 rope: RotaryEmbedding):
+        self.q_alpha = _f32(q_alpha, "q_alpha")
+        self.k_alpha = _f32(k_alpha, "k_alpha")
+        self.rope = rope
+        self.eps = float(eps)
+        self.c = _lib.QkPrep(self.q_alpha.data_ptr(), self.k_alpha.data_ptr(), self.eps,
+                             rope.handle.value)
+
+
 # ------------------------------------------------------------------ FullAttention's cache block
 class FullAttentionKv:
     """The KV-cache half of FullAttention::forward (qwen3_next.rs:2401-2561): lazy cache
@@ -300,6 +385,20 @@ class FullAttentionKv:
             cache.append_quantized(k, v, offset)
             seq_k = cache.seq_len
             out = cache.attend(q, self.scale, seq_k - l, causal=True)
+        return out.reshape(b, l, self.num_heads * self.head_dim)
+
+    def forward_projected(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, offset: int,
+                          prep: QkPrep) -> torch.Tensor:
+        """From the projection outputs (qwen3_next.rs:2369-2561): q [b, l, num_heads, d],
+        k, v [b, l, num_kv_heads, d], before q_norm / k_norm / rope. Returns [b, l, H*d]."""
+        b, l = q.shape[0], q.shape[1]
+        cache = self._ensure(b)
+        if l == 1:
+            out = cache.append_attend_prep(q, k, v, prep, self.scale, offset)
+        else:
+            qp = cache.append_prep(q, k, v, prep, offset)
+            seq_k = cache.seq_len
+            out = cache.attend(qp, self.scale, seq_k - l, causal=True)
         return out.reshape(b, l, self.num_heads * self.head_dim)
 
     def cache_seq_len(self) -> int:

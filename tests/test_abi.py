@@ -41,3 +41,24 @@ def test_host_side_helpers():
     assert L.pkv_bytes_per_row(4, 256) == 144 and L.pkv_bytes_per_row(3, 256) == 272
     assert L.pkv_bytes_per_row(3, 100) == 4 * 34 and L.pkv_bytes_per_row(1, 256) == 512
     assert L.pkv_quant_is_ggml(4) == 1 and L.pkv_quant_is_ggml(1) == 0
+
+
+def test_rope_host_tables_match_oracle_bit_exactly(orc):
+    """The library's RotaryEmbedding::new restatement (host code, no device work) against
+    the oracle's, for the Qwen3-Next shape and an odd theta."""
+    import numpy as np
+    from paramecia_amd import RotaryEmbedding
+    for n_rot, n, theta in [(64, 4096, 1.0e7), (256, 300, 10000.0), (2, 70000, 500000.0)]:
+        c, s = RotaryEmbedding.host_tables(n_rot, n, theta)
+        oc, os_ = orc.rope_tables(n_rot, n, theta)
+        assert np.array_equal(c.numpy().view(np.uint32), oc.view(np.uint32))
+        assert np.array_equal(s.numpy().view(np.uint32), os_.view(np.uint32))
+
+
+def test_rope_host_table_errors():
+    import pytest
+    from paramecia_amd import KvCacheError, RotaryEmbedding
+    with pytest.raises(KvCacheError):
+        RotaryEmbedding.host_tables(63, 4, 1e7)
+    with pytest.raises(KvCacheError):
+        RotaryEmbedding.host_tables(0, 4, 1e7)
