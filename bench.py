@@ -133,9 +133,10 @@ def run_config3(args):
         pk.fill_normal(kn[l], W.SEED, W.stream_id(3, W.T_NEW_K, l))
         pk.fill_normal(vn[l], W.SEED, W.stream_id(3, W.T_NEW_V, l))
     outs = [torch.empty_like(q[l]) for l in range(L)]
+    preps = make_preps(torch, pk, W, L, cap) if args.prep else None
     torch.cuda.synchronize()
 
-    def step(events=None):
+    def step_plain(events=None):
         for l in range(L):
             if events is not None:
                 events[l][0].record()
@@ -143,6 +144,20 @@ def run_config3(args):
             outs[l] = caches[l].append_attend(kn[l], vn[l], q[l], W.SCALE, offset=S)
             if events is not None:
                 events[l][1].record()
+
+    def step_prep(events=None):
+        # q, k, v as projection outputs ([b, l, h, d]; for one token the new k / v rows
+        # have the same memory layout): q_norm, k_norm and rope run inside the step
+        for l in range(L):
+            if events is not None:
+                events[l][0].record()
+            outs[l] = caches[l].append_attend_prep(q[l], kn[l].view(1, 1, W.NUM_KV_HEADS, W.HEAD_DIM),
+                                                   vn[l].view(1, 1, W.NUM_KV_HEADS, W.HEAD_DIM),
+                                                   preps[l], W.SCALE, offset=S)
+            if events is not None:
+                events[l][1].record()
+
+    step = step_prep if args.prep else step_plain
 
     # eager: 12 ctypes launches per step from Python (host overhead included)
     eager_ms = event_time(torch, step, args.steps, args.warmup)
@@ -167,6 +182,12 @@ def run_config3(args):
     keys = S + 1
     step_bytes = L * layer_bytes(keys)
     achieved = layer_bytes(keys) / (per_launch_ms * 1e-3) / 1e9
+    workload = ("config3: 12 Qwen3-Next full-attention layers, batch 1, Q4K KV cache "
+                f"with {S} cached tokens; step = per layer quantize-append 1 token + "
+                f"attend over {keys} keys (16 q heads, 2 kv heads, head_dim 256)")
+    if args.prep:
+        workload += ("; inputs are the q/k/v projection outputs: q_norm, k_norm and the "
+                     "64-dim rope (theta 1e7) run inside the step (pkv_append_attend_prep)")
     result = {
         "metric": METRIC,
         "value": round(ms * 1000.0, 2),
@@ -184,16 +205,17 @@ def run_config3(args):
         "dtype": "f32",
         "data": "synthetic (seeded Philox N(0,1), bit-identical to the CPU oracle's generator)",
         "config": {
-            "workload": "config3: 12 Qwen3-Next full-attention layers, batch 1, Q4K KV cache "
-                        f"with {S} cached tokens; step = per layer quantize-append 1 token + "
-                        f"attend over {keys} keys (16 q heads, 2 kv heads, head_dim 256)",
+            "workload": workload,
             "layers": L, "cached_tokens": S, "keys": keys, "kv_quant": "Q4K",
             "num_heads": 16, "num_kv_heads": 2, "head_dim": 256, "batch": 1,
+            "qk_prep": bool(args.prep),
         },
         "step_hbm_gbs": round(step_bytes / (ms * 1e-3) / 1e9, 1),
         "step_pct_of_peak": round(100.0 * step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
         "roofline": {
-            "kernel": "pkv_append_attend (one layer: decode kernel + combine kernel)",
+            "kernel": ("pkv_append_attend_prep (one layer: prep-append kernel + decode "
+                       "kernel + combine kernel)") if args.prep else
+                      "pkv_append_attend (one layer: decode kernel + combine kernel)",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
             "bytes_per_launch": layer_bytes(keys),
@@ -203,6 +225,9 @@ def run_config3(args):
         },
         "append_tokens_per_s": round(L * S / fill_s, 1),
     }
+    if args.prep:
+        result["unprepared_us_per_step"] = round(
+            graph_time(torch, step_plain, args.steps, args.warmup, reps) * 1000.0, 2)
     if args.calib_copy_mib > 0:
         n = args.calib_copy_mib * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device=dev)
@@ -215,6 +240,20 @@ def run_config3(args):
         result["cpu_baseline"] = cpu_baseline_decode(
             caches[0], kn[0], vn[0], q[0], S, args.cpu_threads, 3, 4, W.N_FULL)
     return result
+
+
+def make_preps(torch, pk, W, layers, max_pos):
+    """Per-layer q_norm / k_norm alphas (seeded, around 1 as trained RMSNorm weights are)
+    and one rope shared by every layer, as the model loads them."""
+    rope = pk.RotaryEmbedding(W.N_ROT, max_pos, W.ROPE_THETA)
+    preps = []
+    for l in range(layers):
+        qa = torch.empty(W.HEAD_DIM, dtype=torch.float32, device="cuda")
+        ka = torch.empty_like(qa)
+        pk.fill_normal(qa, W.SEED, W.stream_id(6, W.T_Q, l), 0.1)
+        pk.fill_normal(ka, W.SEED, W.stream_id(6, W.T_NEW_K, l), 0.1)
+        preps.append(pk.QkPrep(qa + 1.0, ka + 1.0, W.RMS_EPS, rope))
+    return preps
 
 
 def cpu_baseline_decode(cache, kn, vn, q, S, threads, config, quant, layers):
@@ -327,10 +366,24 @@ def run_config2(args):
     pk.fill_normal(k1, W.SEED, W.stream_id(2, W.T_NEW_K))
     pk.fill_normal(v1, W.SEED, W.stream_id(2, W.T_NEW_V))
 
-    def step():
+    def step_plain():
         c.append_quantized(kc, vc, offset=S)
         c.attend(qc, W.SCALE, S, causal=True)
         return c.append_attend(k1, v1, q1, W.SCALE, offset=S + C)
+
+    if args.prep:
+        prep = make_preps(torch, pk, W, 1, cap)[0]
+        # projection-output layout [b, l, h, d] of the same values
+        kcp = kc.transpose(1, 2).contiguous()
+        vcp = vc.transpose(1, 2).contiguous()
+
+        def step():
+            qp = c.append_prep(qc, kcp, vcp, prep, offset=S)
+            c.attend(qp, W.SCALE, S, causal=True)
+            return c.append_attend_prep(q1, k1.view(1, 1, 2, 256), v1.view(1, 1, 2, 256), prep,
+                                        W.SCALE, offset=S + C)
+    else:
+        step = step_plain
 
     reps = args.graph_reps if args.graph_reps > 0 else 1
     ms = graph_time(torch, step, args.steps, args.warmup, reps)
@@ -340,13 +393,26 @@ def run_config2(args):
                          args.warmup, reps)
     flops = 16 * (C * S + C * (C + 1) // 2) * 256 * 2 * 2
     tf = flops / (ms_attn * 1e-3) / 1e12
+    workload = ("config2: Q4K cache with 16384 tokens; step = quantize-append a 512-token "
+                "chunk + causal attention of its 512 queries over 16896 keys + one decode "
+                "step (append 1 token, attend 16897 keys)")
+    extra = {}
+    if args.prep:
+        workload += ("; inputs are the q/k/v projection outputs: q_norm, k_norm and the "
+                     "64-dim rope run inside the appends (pkv_append_prep, "
+                     "pkv_append_attend_prep)")
+        extra["unprepared_us_per_step"] = round(
+            graph_time(torch, step_plain, args.steps, args.warmup, reps) * 1000, 2)
+        extra["prep_append_chunk_us"] = round(graph_time(
+            torch, lambda: c.append_prep(qc, kcp, vcp, prep, offset=S), args.steps,
+            args.warmup, reps) * 1000, 2)
+        extra["append_chunk_us"] = round(graph_time(
+            torch, lambda: c.append_quantized(kc, vc, offset=S), args.steps, args.warmup,
+            reps) * 1000, 2)
     return base_result(2, "Q4K prefill chunk + decode µs (512-token append, 512 x 16896 causal "
                        "attention, 1-token decode over 16897 keys)",
-                       round(ms * 1000, 2), "us/step", False, ms, args,
-                       "config2: Q4K cache with 16384 tokens; step = quantize-append a 512-token "
-                       "chunk + causal attention of its 512 queries over 16896 keys + one decode "
-                       "step (append 1 token, attend 16897 keys)",
-                       {"graph_steps_per_replay": reps,
+                       round(ms * 1000, 2), "us/step", False, ms, args, workload,
+                       {**extra, "graph_steps_per_replay": reps,
                         "one_step_graph_us_per_step": round(ms_1 * 1000, 2),
                         "prefill_attention_us": round(ms_attn * 1000, 2),
                         "roofline": {"kernel": "pkv_attend prefill chunk (q4k_prefill_kernel + "
@@ -497,6 +563,9 @@ def main() -> int:
     ap.add_argument("--graph-reps", type=int, default=0,
                     help="steps captured per HIP graph replay (0: per-config default)")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--prep", action="store_true",
+                    help="configs 2 and 3: start from the q/k/v projection outputs, so q_norm, "
+                         "k_norm and rope run inside the step (the fused preparation)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="config 3: after the timed runs, launch a plain elementwise copy of "
                          "this many MiB (read N, write N) 3 times: the reference kernel that "

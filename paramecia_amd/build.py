@@ -27,6 +27,7 @@ SOURCES = {
     "pkv_quant.hip": ["-ffp-contract=off"],
     "pkv_attn.hip": [],
     "pkv_attn_mfma.hip": [],
+    "pkv_attn_mfma_prep.hip": [],
     "pkv_prefill_mfma.hip": [],
     "pkv_q8_decode.hip": [],
     "pkv_util.hip": [],

@@ -504,22 +504,30 @@ int pkv_append_attend_prep(pkv_cache *h, const pkv_qk_prep *prep, const float *q
   PrepArgs a;
   int rc = prep_setup(h, prep, true, num_heads, 1, offset, a);
   if (rc) return rc;
-  rc = h->qws.reserve((size_t)h->batch * num_heads * h->head_dim * sizeof(float));
-  if (rc) return rc;
   const int64_t saved = h->seq_len;
   rc = position_for_append(h, 1, offset);
   if (rc) return rc;
   const int64_t t_new = h->seq_len;
-  float *qp = static_cast<float *>(h->qws.ptr);
-  a.q = q;
-  a.q_out = qp;
-  a.k = k;
-  a.v = v;
-  a.t0 = t_new;
-  rc = launch_prep_append(a, h->stream);
-  if (!rc)
-    rc = launch_attend(cache_args(h, qp, 1, num_heads, scale, t_new + 1, t_new, 1, out), h->ws,
-                       h->stream);
+  // Q4K at the Qwen3-Next shape: the decode kernel prepares q and the new k itself
+  const DecodePrep dp{prep->q_alpha, prep->k_alpha, prep->rope->cos, prep->rope->sin,
+                      prep->eps, prep->rope->n_rot};
+  rc = launch_append_attend_prep_mfma(
+      cache_args(h, q, 1, num_heads, scale, t_new + 1, t_new, 1, out), k, v, h->k, h->v, t_new,
+      dp, h->ws, h->stream);
+  if (rc == PKV_ERR_UNSUPPORTED) {
+    // otherwise: the prep-append kernel (q into the handle's scratch), then attention
+    rc = h->qws.reserve((size_t)h->batch * num_heads * h->head_dim * sizeof(float));
+    float *qp = static_cast<float *>(h->qws.ptr);
+    a.q = q;
+    a.q_out = qp;
+    a.k = k;
+    a.v = v;
+    a.t0 = t_new;
+    if (!rc) rc = launch_prep_append(a, h->stream);
+    if (!rc)
+      rc = launch_attend(cache_args(h, qp, 1, num_heads, scale, t_new + 1, t_new, 1, out),
+                         h->ws, h->stream);
+  }
   if (rc) {
     if (rc != PKV_ERR_HIP) h->seq_len = saved;
     return rc;

@@ -1,785 +1,8 @@
-// MFMA decode attention over a Q4K cache for the Qwen3-Next full-attention shape
-// (16 query heads, 2 KV heads, head_dim 256), gfx950.
-//
-// Role: the dequant-fused attention of the reference's flash_attn_q8 path
-// (paramecia-model/src/ops.rs:756-792, called at qwen3_next.rs:2531-2561) and the CPU
-// SDPA it falls back to (qwen3_next.rs:2580-2605), for a decode step (one query).
-//
-// Work split: split-K over 32-key blocks. A workgroup of 8 waves (two per SIMD, so each
-// SIMD always has a second wave to issue while one waits) owns a contiguous block
-// range; waves 2s and 2s+1 take KV heads 0 and 1 of the same blocks, so the two halves
-// of a token's 288-byte K (and V) rows are read together. Each wave streams its blocks
-// through two LDS stages with buffer_load ... lds. Extra workgroups past the main ones
-// quantize the new token's rows for a fused decode step (bit-exact Q4K).
-//
-// Arithmetic (per KV head, per 16 keys, MFMA f32_16x16x32_f16):
-//   QK: A[key][e] = nibble * sub-block scale code, an integer <= 945 built exactly in
-//       fp16 from the packed byte with the 1024-offset trick and one v_pk_fma;
-//       B[e][col] = q split into fp16 hi/lo parts: columns 0-7 are the hi parts of the
-//       group's 8 heads, 8-15 the lo parts, so hi+lo recover q to ~22 bits.
-//       score = d * S1 - dmin * S2 with S2 = sum_j m_j * qsum_j (a 16x16x16 MFMA).
-//   PV: B[key][e] = nibble * scale code * 2^e_d (exact fp16, e_d = exponent of d),
-//       A[head][key] = p * mantissa(d): rows 0-7 its fp16 hi part, rows 8-15 the lo
-//       remainder (rows h and 8 + h are summed after the loop, ~22 bits). The min term
-//       A'[head][key] = p * mantissa(dmin) (hi and lo rows alike) against
-//       B'[key][j] = m_j * 2^e_dmin.
-//   All accumulation is f32. Softmax runs in base 2 with the 1/sqrt(d) scale folded
-//   in, scores clamped to [-100, 100] (in natural-log units) as the reference does.
-//   The running max is raised only when a block exceeds it by 2^8, so the
-//   accumulators are rarely rescaled.
-#include "pkv_decode_split.hpp"
-#include "pkv_mfma_common.hpp"
-#include "pkv_q4k_lanes.hpp"
+// Q4K MFMA decode launchers (decode kernel without q/k preparation); the kernel, its
+// helpers and the launch plan are in pkv_q4k_decode.hpp.
+#include "pkv_q4k_decode.hpp"
 
 namespace pkv {
-
-namespace {
-
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;  // two waves per SIMD
-constexpr int kMainWGs = 256;
-constexpr float kLazy = 8.0f;  // log2 headroom of the running max before a rescale
-
-struct DecodeArgs {
-  DecodeSeg seg[kMaxSegs];
-  int nseg, nwg, bpw;
-  int64_t rs_t, rs_h;
-  float sl2;                   // scale * log2(e)
-  const float *q;              // [nseg][16][256]
-  const float *k_new, *v_new;  // [nseg][2][256] or null (fused decode step)
-  float *part;                 // [nwg][16][kPartRow]
-  float *dq;  // [nseg][4][256] dequantized new rows (K kv0, K kv1, V kv0, V kv1)
-};
-
-// Per-wave tables rebuilt for every 32-key block.
-struct WaveTab {
-  float kd[kBlk], kdm[kBlk];                        // epilogue exchange (cmin)
-  float vmd[kBlk], vmdm[kBlk];                      // V: mantissas of d and dmin
-  _Float16 vsc[8][kBlk], vc[8][kBlk], vm[8][kBlk];  // V: fp16 constants [j][key]
-};
-
-// LDS of one workgroup. Each wave owns stage buffers st[w][0], st[w][1] (adjacent, so
-// both are reached from one base register with immediate offsets) and a table area;
-// before its first refill of st[w][1] a wave stages its KV head's q rows there, and the
-// quantizer scratch of the quantizing waves 0-3 overlaps their tables. The merge area
-// reuses the first stage buffers once every wave has left the loop. Stages are always addressed by
-// indexing this array: a pointer chosen at run time between two stages loses its LDS
-// address space, and the generic (flat) loads it then compiles to wait on every
-// outstanding buffer load, including the prefetch of the next block.
-struct Smem {
-  union {
-    struct {
-      Stage st[kWaves][2];
-      union {
-        WaveTab tab[kWaves];
-        struct {
-          Q4kScratch scr;
-          uint32_t arrivals;  // barrier counter of the quantizing waves 0-3
-        } quant;
-      } t;
-    } run;
-    struct {
-      float4 o[kWaves][16][2][16];  // [wave][T2][row group g][n]: rows 4g..4g+3, scaled
-    } merge;
-  };
-};
-static_assert(sizeof(Q4kScratch) + 4 <= sizeof(WaveTab), "quantizer scratch within wave 0's tables");
-static_assert(sizeof(float4[kWaves][16][2][16]) <= sizeof(Stage[kWaves]),
-              "merge area within the first stage buffers");
-static_assert(24 <= kBlk, "m, l and f * l of 8 heads fit a wave's vmd table");
-static_assert(sizeof(Smem) <= 160 * 1024, "LDS budget of one workgroup");
-
-// Stage this wave's KV head's 8 q rows (8 KB, contiguous in q) into LDS: eight
-// dwordx4 loads, lane l of load j moving bytes 1024 j + 16 l of q to LDS byte
-// kQRow j + 16 l. The 16-byte pad per row puts the rows' reads in build_q (one row per
-// lane, same column) on different banks.
-constexpr int kQRow = 1040;  // bytes per staged q row (256 floats + 16 bytes of pad)
-static_assert(8 * kQRow <= (int)sizeof(Stage), "q rows fit one stage");
-__device__ __forceinline__ void issue_q(void *dst_lds, u4s rq, uint32_t lane16) {
-  const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)dst_lds));
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %[sv], m0\n\t"
-      "s_mov_b32 m0, %[d]\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o0], %[rq], 0 offen lds\n\t"
-      "s_add_u32 m0, %[d], 0x410\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o1], %[rq], 0 offen lds\n\t"
-      "s_add_u32 m0, %[d], 0x820\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o2], %[rq], 0 offen lds\n\t"
-      "s_add_u32 m0, %[d], 0xc30\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o3], %[rq], 0 offen lds\n\t"
-      "s_add_u32 m0, %[d], 0x1040\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o4], %[rq], 0 offen lds\n\t"
-      "s_add_u32 m0, %[d], 0x1450\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o5], %[rq], 0 offen lds\n\t"
-      "s_add_u32 m0, %[d], 0x1860\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o6], %[rq], 0 offen lds\n\t"
-      "s_add_u32 m0, %[d], 0x1c70\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %[o7], %[rq], 0 offen lds\n\t"
-      "s_mov_b32 m0, %[sv]"
-      : [sv] "=&s"(saved)
-      : [d] "s"(dst), [o0] "v"(lane16), [o1] "v"(lane16 + 1024u), [o2] "v"(lane16 + 2048u),
-        [o3] "v"(lane16 + 3072u), [o4] "v"(lane16 + 4096u), [o5] "v"(lane16 + 5120u),
-        [o6] "v"(lane16 + 6144u), [o7] "v"(lane16 + 7168u), [rq] "s"(rq)
-      : "memory", "scc");
-}
-
-struct WaveState {
-  f4 acc[16];  // PV accumulators, tile T = 8h + 2*byte + hl
-  f4 accm;     // min-term accumulator
-  float m_run, lsum;
-};
-
-struct QKOut {
-  f4 s1[2], s2[2];  // per 16-key tile: sum_e (n*sc)_e q_e and sum_j m_j qsum_j
-};
-
-// Lane constants of the K scale decode. Lane group g uses sub-blocks 2g and 2g + 1,
-// whose 6-bit scale and min codes sit in bytes 2(g & 1), 2(g & 1) + 1 of the header's
-// words s0 (scales 0-3), s1 (mins 0-3) and, for sub-blocks 4-7, s2 (low 4 bits) with
-// the top two bits in s0 / s1 (get_scale_min_k4). v_perm puts header byte b of s2 (or
-// s0 / s1 for g < 2) in the low byte and byte b of s0 / s1 in the high byte of each
-// 16-bit half; the masks then keep the code's low bits in place and move bits 6-7 of
-// the high byte down to bits 4-5, and the 0x6400 exponent makes each half the fp16
-// value 1024 + code.
-struct KScaleSel {
-  uint32_t perm;  // v_perm selector: S0 = s0 or s1, S1 = s2
-  uint32_t lo;    // low code bits kept in place: 0x3F (g < 2) or 0x0F per half
-  uint32_t up;    // bits 4-5 taken from bits 14-15 of each half (g >= 2)
-  uint32_t msh;   // right shift of the min codes' low bits: 0 (g < 2) or 4
-};
-__device__ __forceinline__ KScaleSel make_kscale_sel(int g) {
-  const uint32_t b = 2u * (uint32_t)(g & 1);
-  KScaleSel s;
-  if (g < 2) {
-    s.perm = (4u + b) | (0x0Cu << 8) | ((5u + b) << 16) | (0x0Cu << 24);
-    s.lo = 0x003F003Fu;
-    s.up = 0u;
-    s.msh = 0u;
-  } else {
-    s.perm = b | ((4u + b) << 8) | ((b + 1u) << 16) | ((5u + b) << 24);
-    s.lo = 0x000F000Fu;
-    s.up = 0x00300030u;
-    s.msh = 4u;
-  }
-  return s;
-}
-// {1024 + code(2g), 1024 + code(2g + 1)} as fp16 halves: the scale codes from (s0, s2),
-// the min codes from (s1, s2)
-__device__ __forceinline__ uint32_t kcode_pair(uint32_t sx, uint32_t s2, uint32_t sh,
-                                               const KScaleSel &ks, uint32_t magic) {
-  const uint32_t P = __builtin_amdgcn_perm(sx, s2, ks.perm);
-  return and_or(P >> sh, ks.lo, and_or(P >> 10, ks.up, magic));
-}
-
-// K words of a staged block, read together at the start of the block so that their
-// latencies overlap instead of each one stalling its phase. The V words are read later,
-// in phase P: the stage's V rows are its last loads, and LDS reads issued right after
-// the vmcnt wait have been seen to return stale bytes for them, while reads a phase
-// later have not.
-struct BlockWords {
-  u4 khd[2], kq0[2], kq1[2];  // phase Q: header and nibble pieces of key kk(r) per tile
-  uint32_t hx[8];             // phase S: {d, dmin} of keys 8g..8g+7
-};
-__device__ __forceinline__ void load_block_words(const Stage &st, int lane, BlockWords &W) {
-  const int r = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int kk = 8 * (r >> 2) + 4 * t + (r & 3);
-    const int sw = swz(kk);
-    W.khd[t] = st.k.hdr[kk];
-    W.kq0[t] = st.k.nib[8 * kk + ((2 * g) ^ sw)];
-    W.kq1[t] = st.k.nib[8 * kk + ((2 * g + 1) ^ sw)];
-  }
-  const uint32_t *hdr32 = reinterpret_cast<const uint32_t *>(st.k.hdr);
-#pragma unroll
-  for (int k = 0; k < 8; ++k) W.hx[k] = hdr32[4 * (8 * g + k)];
-}
-
-// Phase Q: K rows of a staged block -> raw QK sums.
-// Lane (r, g) feeds key kk(r) of tile t with sub-blocks 2g (low nibbles) and 2g+1
-// (high nibbles); its min codes m_2g, m_2g+1 form the A operand of the S2 product.
-__device__ __forceinline__ void phase_q(const BlockWords &W, const h8 *qb, h4 q2, const Masks &MK,
-                                        const KScaleSel &ks, QKOut &o) {
-  // pk_fma constants: {1024 + sc0, 1024 + sc1} -> {sc0, sc1 / 16}; then the offsets
-  // {-1024 sc0, -64 sc1} of the two nibble forms (1024 + n, 1024 + 16 n)
-  const h2 ksc = {(_Float16)1.0f, (_Float16)0.0625f}, kcc = {(_Float16)-1024.0f, (_Float16)-64.0f};
-  const h2 kneg = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const u4 hd = W.khd[t], q0 = W.kq0[t], q1 = W.kq1[t];
-    const h2 SC = pk_fma(as_h2(kcode_pair(hd.y, hd.w, 0u, ks, MK.magic)), ksc, kcc);
-    const h2 CC = SC * kneg;
-    const h2 MM = as_h2(kcode_pair(hd.z, hd.w, ks.msh, ks, MK.magic)) + kneg;
-    const h2 SC0 = __builtin_shufflevector(SC, SC, 0, 0), SC1 = __builtin_shufflevector(SC, SC, 1, 1);
-    const h2 C0 = __builtin_shufflevector(CC, CC, 0, 0), C1 = __builtin_shufflevector(CC, CC, 1, 1);
-    const uint32_t qd[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    f4 s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const uint32_t d0 = qd[2 * s], d1 = qd[2 * s + 1];
-      const uint32_t d0s = d0 >> 8, d1s = d1 >> 8;
-      const uint32_t lw[4] = {and_or(d0, MK.lo, MK.magic), and_or(d0s, MK.lo, MK.magic),
-                              and_or(d1, MK.lo, MK.magic), and_or(d1s, MK.lo, MK.magic)};
-      const uint32_t hw[4] = {and_or(d0, MK.hi, MK.magic), and_or(d0s, MK.hi, MK.magic),
-                              and_or(d1, MK.hi, MK.magic), and_or(d1s, MK.hi, MK.magic)};
-      h8 lo, hi;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const h2 l2 = pk_fma(as_h2(lw[w]), SC0, C0);
-        const h2 hh2 = pk_fma(as_h2(hw[w]), SC1, C1);
-        lo[2 * w] = l2[0];
-        lo[2 * w + 1] = l2[1];
-        hi[2 * w] = hh2[0];
-        hi[2 * w + 1] = hh2[1];
-      }
-      s1 = mfma32(lo, qb[s], s1);
-      s1 = mfma32(hi, qb[4 + s], s1);
-    }
-    const h4 a2 = {MM[0], MM[1], (_Float16)0.0f, (_Float16)0.0f};
-    o.s1[t] = s1;
-    o.s2[t] = mfma16(a2, q2, f4{0.f, 0.f, 0.f, 0.f});
-  }
-}
-
-// d * s1 - dmin * s2 with the fp16 pair {d, dmin} of a header dword: two v_fma_mix
-__device__ __forceinline__ float hdr_dot(uint32_t hx, float s1, float s2) {
-  float t, r;
-  asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(t) : "v"(hx), "v"(s1));
-  asm("v_fma_mix_f32 %0, -%1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-      : "=v"(r)
-      : "v"(hx), "v"(s2), "v"(t));
-  return r;
-}
-
-// Phase S: scores (log2 units) and the online softmax; p[k] for key 8g + k, head n % 8.
-// Keys at or past nvalid (only in a partial last block) are masked.
-// Scores stay in q.k units here (the running max too); sl2 = scale * log2(e) enters
-// the exponents, and clamp / lazy are the +-100-nat clamp and the rescale headroom in
-// those units.
-__device__ __forceinline__ void phase_s(const BlockWords &W, const QKOut &o, WaveState &S,
-                                        int nvalid, float sl2, float clamp, float lazy, int lane,
-                                        float p[8]) {
-  const int g = lane >> 4;
-  float sc8[8];
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // key 8g + 4t + i: this column's part (hi or lo of q); the other part sits 8 lanes
-      // away. d and dmin enter as fp16 (v_fma_mix).
-      const float part = hdr_dot(W.hx[4 * t + i], o.s1[t][i], o.s2[t][i]);
-      const float sc = part + ror8(part);
-      sc8[4 * t + i] = __builtin_amdgcn_fmed3f(sc, -clamp, clamp);
-    }
-  if (nvalid < kBlk) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (8 * g + k >= nvalid) sc8[k] = -INFINITY;
-  }
-  float bm = sc8[0];
-#pragma unroll
-  for (int k = 1; k < 8; ++k) bm = fmaxf(bm, sc8[k]);
-  bm = xmax32(xmax16(bm));
-  if (S.m_run == -INFINITY) {
-    // first block with a valid key: nothing accumulated yet, no rescale
-    S.m_run = bm;
-  } else if (__any(bm > S.m_run + lazy)) {
-    const float m_new = fmaxf(S.m_run, bm);
-    const float alpha = (S.m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((S.m_run - m_new) * sl2);
-    S.lsum *= alpha;
-    S.m_run = m_new;
-    float ai[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ai[i] = __shfl(alpha, 4 * (g & 1) + i);
-#pragma unroll
-    for (int T2 = 0; T2 < 16; ++T2)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) S.acc[T2][i] *= ai[i];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) S.accm[i] *= ai[i];
-  }
-  const float nm = -S.m_run * sl2;  // finite: every block has a valid key
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    p[k] = __builtin_amdgcn_exp2f(fmaf(sc8[k], sl2, nm));
-    S.lsum += p[k];
-  }
-}
-
-// Lane constants of the V table build: lane l takes key l % 32 and sub-blocks
-// 4u..4u+3 (u = l / 32), whose codes are bytes 0-3 of s0 / s1 (u = 0) or the low 4 bits
-// of s2 with bits 6-7 of s0 / s1 above them (u = 1, get_scale_min_k4).
-struct VScaleSel {
-  uint32_t sh, ma, mb;
-};
-__device__ __forceinline__ VScaleSel make_vscale_sel(int lane) {
-  const bool u = lane >= 32;
-  return VScaleSel{u ? 2u : 0u, u ? 0x30303030u : 0x3F3F3F3Fu, u ? 0x0F0F0F0Fu : 0u};
-}
-
-// Phase P: V header tables, PV A/B operands and MFMAs, min term.
-__device__ __forceinline__ void phase_p(const Stage &st, const BlockWords &W, WaveState &S,
-                                        WaveTab &T, const float p[8], const Masks &MK,
-                                        const VScaleSel &vs, int lane) {
-  const int n = lane & 15, g = lane >> 4;
-  // V header -> constant tables. The four codes of a lane come out as bytes; the pairs
-  // (4u, 4u+2) and (4u+1, 4u+3) become fp16 1024 + code, and one v_pk_fma each gives
-  // sc * 2^e_d (sc * 2^(e_d - 4) for the high-nibble sub-blocks), exact in fp16 for
-  // e_d in [-20, 0]; the offsets are -1024 times those.
-  {
-    const int kk = lane & 31, u = lane >> 5;
-    const u4 vh = st.v.hdr[kk];
-    int ed, em;
-    float md, mm;
-    split_scale(h2f(vh.x & 0xFFFF), ed, md);
-    split_scale(h2f(vh.x >> 16), em, mm);
-    (u ? T.vmdm : T.vmd)[kk] = u ? mm : md;
-    const uint32_t sc4 = and_or(vh.y >> vs.sh, vs.ma, vh.w & vs.mb);
-    const uint32_t m4 = and_or(vh.z >> vs.sh, vs.ma, (vh.w >> 4) & vs.mb);
-    const _Float16 e1 = __builtin_amdgcn_ldexph((_Float16)1.0f, ed);
-    const _Float16 n1 = __builtin_amdgcn_ldexph((_Float16)-1024.0f, ed);
-    const _Float16 e4 = __builtin_amdgcn_ldexph((_Float16)0.0625f, ed);
-    const _Float16 n4 = __builtin_amdgcn_ldexph((_Float16)-64.0f, ed);
-    const _Float16 em1 = __builtin_amdgcn_ldexph((_Float16)1.0f, em);
-    const _Float16 nm1 = __builtin_amdgcn_ldexph((_Float16)-1024.0f, em);
-    const h2 kneg = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-    const h2 se = pk_fma(as_h2(and_or(sc4, 0x00FF00FFu, MK.magic)), h2{e1, e1}, h2{n1, n1});
-    const h2 so = pk_fma(as_h2(and_or(sc4 >> 8, 0x00FF00FFu, MK.magic)), h2{e4, e4}, h2{n4, n4});
-    const h2 me = pk_fma(as_h2(and_or(m4, 0x00FF00FFu, MK.magic)), h2{em1, em1}, h2{nm1, nm1});
-    const h2 mo = pk_fma(as_h2(and_or(m4 >> 8, 0x00FF00FFu, MK.magic)), h2{em1, em1}, h2{nm1, nm1});
-    const h2 ce = se * kneg, co = so * kneg;
-    const int j = 4 * u;
-    T.vsc[j][kk] = se[0];
-    T.vsc[j + 2][kk] = se[1];
-    T.vsc[j + 1][kk] = so[0];
-    T.vsc[j + 3][kk] = so[1];
-    T.vc[j][kk] = ce[0];
-    T.vc[j + 2][kk] = ce[1];
-    T.vc[j + 1][kk] = co[0];
-    T.vc[j + 3][kk] = co[1];
-    T.vm[j][kk] = me[0];
-    T.vm[j + 2][kk] = me[1];
-    T.vm[j + 1][kk] = mo[0];
-    T.vm[j + 3][kk] = mo[1];
-  }
-  // V rows, transposed: dword n & 3 of nibble piece 4h + n / 4 of keys 8g..8g+7. Rows
-  // 2i and 2i+1 share their swizzle, so each pair is one ds_read2 (128 bytes apart).
-  uint32_t vq[2][8];
-  const uint32_t *v32 = reinterpret_cast<const uint32_t *>(st.v.nib);
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int k = 0; k < 8; k += 2) {
-      const int R = 8 * g + k;
-      const int piece = 4 * h + (n >> 2);
-      const int base = 4 * (8 * R + (piece ^ swz(R))) + (n & 3);
-      vq[h][k] = v32[base];
-      vq[h][k + 1] = v32[base + 32];
-    }
-  // A: rows 0-7 the fp16 hi parts of p * mant(d), rows 8-15 the lo remainders (the two
-  // row halves are summed after the loop); Am likewise for p * mant(dmin). One fp16
-  // rounding of a weight (2^-12 relative) times a value of an outlier channel would
-  // exceed the attention tolerance; hi + lo keeps ~22 bits.
-  // Both parts are fp16(x - c) with c = fp16(x) masked to zero on the hi rows.
-  const uint32_t lo_mask = n >= 8 ? 0xFFFFFFFFu : 0u;
-  uint32_t aw[4], amw[4];
-#pragma unroll
-  for (int kp = 0; kp < 4; ++kp) {
-    const float x0 = p[2 * kp] * T.vmd[8 * g + 2 * kp], x1 = p[2 * kp + 1] * T.vmd[8 * g + 2 * kp + 1];
-    const float y0 = p[2 * kp] * T.vmdm[8 * g + 2 * kp], y1 = p[2 * kp + 1] * T.vmdm[8 * g + 2 * kp + 1];
-    const uint32_t cx = as_u(h2{(_Float16)x0, (_Float16)x1}) & lo_mask;
-    const uint32_t cy = as_u(h2{(_Float16)y0, (_Float16)y1}) & lo_mask;
-    aw[kp] = mix_sub_hi(mix_sub_lo(x0, cx), x1, cx);
-    amw[kp] = mix_sub_hi(mix_sub_lo(y0, cy), y1, cy);
-  }
-  const h8 A = __builtin_bit_cast(h8, u4{aw[0], aw[1], aw[2], aw[3]});
-  const h8 Am = __builtin_bit_cast(h8, u4{amw[0], amw[1], amw[2], amw[3]});
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int c = 2 * h + (n >> 3);
-    const h8 SL = *reinterpret_cast<const h8 *>(&T.vsc[2 * c][8 * g]);
-    const h8 CL = *reinterpret_cast<const h8 *>(&T.vc[2 * c][8 * g]);
-    const h8 SH = *reinterpret_cast<const h8 *>(&T.vsc[2 * c + 1][8 * g]);
-    const h8 CH = *reinterpret_cast<const h8 *>(&T.vc[2 * c + 1][8 * g]);
-#pragma unroll
-    for (int byte = 0; byte < 4; ++byte) {
-      const uint32_t sel = (uint32_t)byte | (0x0Cu << 8) | ((uint32_t)(4 + byte) << 16) | (0x0Cu << 24);
-      h8 blo, bhi;
-#pragma unroll
-      for (int pp = 0; pp < 4; ++pp) {
-        const uint32_t x = __builtin_amdgcn_perm(vq[h][2 * pp + 1], vq[h][2 * pp], sel);
-        const h2 lo = pk_fma(as_h2(and_or(x, MK.lo, MK.magic)),
-                             h2{SL[2 * pp], SL[2 * pp + 1]}, h2{CL[2 * pp], CL[2 * pp + 1]});
-        const h2 hi = pk_fma(as_h2(and_or(x, MK.hi, MK.magic)),
-                             h2{SH[2 * pp], SH[2 * pp + 1]}, h2{CH[2 * pp], CH[2 * pp + 1]});
-        blo[2 * pp] = lo[0];
-        blo[2 * pp + 1] = lo[1];
-        bhi[2 * pp] = hi[0];
-        bhi[2 * pp + 1] = hi[1];
-      }
-      S.acc[8 * h + 2 * byte] = mfma32(A, blo, S.acc[8 * h + 2 * byte]);
-      S.acc[8 * h + 2 * byte + 1] = mfma32(A, bhi, S.acc[8 * h + 2 * byte + 1]);
-    }
-  }
-  // min term: C'[row][j] += sum_k Am[row][k] * m_kj * 2^e_dmin (columns j < 8)
-  const h8 Bm0 = *reinterpret_cast<const h8 *>(&T.vm[n & 7][8 * g]);
-  const h8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
-  S.accm = mfma32(Am, n < 8 ? Bm0 : zero8, S.accm);
-}
-
-// Barrier of waves 0-3 only (the quantizing waves), through an LDS arrival counter, so
-// that waves 4-7 need not wait for the quantization. Every waiting wave is in this
-// workgroup, hence resident; the bound on the wait is only a safeguard.
-struct QuantWavesBarrier {
-  uint32_t *arrivals;
-  uint32_t target;
-  __device__ __forceinline__ void operator()() {
-    target += 4;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    if ((threadIdx.x & 63) == 0)
-      __hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    for (int spin = 0; spin < (1 << 22); ++spin) {
-      if (__hip_atomic_load(arrivals, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target)
-        break;
-      __builtin_amdgcn_s_sleep(1);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  }
-};
-
-__global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
-  __shared__ Smem sm;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int kv = wave & 1, wsub = wave >> 1;
-  const int wg = blockIdx.x;
-  const int n = lane & 15, g = lane >> 4;
-  int b = 0;  // segment of this workgroup
-  while (b + 1 < a.nseg && wg >= a.seg[b + 1].wg0) ++b;
-  const DecodeSeg &sg = a.seg[b];
-
-  // ---- blocks of this wave: b0 + wsub, b0 + wsub + 4, ... below b1
-  const int b0 = (wg - sg.wg0) * a.bpw;
-  const int b1 = b0 + a.bpw < sg.nblk ? b0 + a.bpw : sg.nblk;
-  // wave-uniform: loop control and the key mask stay scalar
-  const int first = __builtin_amdgcn_readfirstlane(b0 + wsub);
-  const int nmine = __builtin_amdgcn_readfirstlane(first < b1 ? (b1 - first + 3) / 4 : 0);
-  const int kvu = __builtin_amdgcn_readfirstlane(kv);
-  const uint8_t *kbase = sg.k + kvu * a.rs_h;
-  const uint8_t *vbase = sg.v + kvu * a.rs_h;
-  const uint32_t rs_t = (uint32_t)a.rs_t;
-  const int64_t seq_k = sg.seq_k;
-  // rows of keys [0, seq_k) of this head; loads past them return zeros (masked keys)
-  const uint32_t span = seq_k > 0 ? (uint32_t)(seq_k - 1) * rs_t + 144u : 0u;
-  const u4s rk = make_rsrc(kbase, span), rv = make_rsrc(vbase, span);
-  const LoadPlan P = make_plan(lane, rs_t);
-  const uint32_t bstep = 4u * kBlk * rs_t;  // byte distance between this wave's blocks
-  uint32_t boff = __builtin_amdgcn_readfirstlane((uint32_t)first * kBlk * rs_t);
-  // LDS byte addresses of this wave's two stages
-  const uint32_t st_lds0 = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(size_t)((PKV_LDS void *)&sm.run.st[wave][0]));
-
-  // Fused append: threads 0-255 (waves 0-3) of workgroup r quantize new row r (row
-  // 4s + 2p + kv: segment s, K (p = 0) or V (p = 1), KV head kv; further rows go
-  // round-robin when the grid is smaller) and publish it dequantized for the combine
-  // step, which attends to the new key. This runs while the first block streams in.
-  // The row is read before any staging load is issued, so the compiler's wait for it
-  // does not wait for the stage too.
-  const bool quant = a.k_new != nullptr && wg < 4 * a.nseg && tid < 256;
-  float xq = 0.0f;
-  if (quant) {
-    const int p = (wg >> 1) & 1, kvr = wg & 1;
-    xq = (p ? a.v_new : a.k_new)[((int64_t)(wg >> 2) * 2 + kvr) * 256 + tid];
-    asm volatile("" : "+v"(xq));
-  }
-  if (tid == 0) sm.run.t.quant.arrivals = 0u;
-
-  // ---- this wave's q rows, then its first block, into LDS. Every wave's q loads go out
-  // before any stage load (one barrier), so q returns ahead of the block data.
-  {
-    const u4s rq = make_rsrc(a.q + ((int64_t)b * 16 + 8 * kvu) * 256, 8 * 256 * 4);
-    issue_q(&sm.run.st[wave][1], rq, 16u * lane);
-  }
-  __syncthreads();
-  // every issued block has its first key below seq_k, so its offset is inside the range
-  if (nmine > 0) issue_stage_at(st_lds0, P, rsrc_advance(rk, boff), rsrc_advance(rv, boff));
-
-  // QK B operands: lane (n, g) takes q of head n % 8, elements 64g + 32(s/4) + 8(s%4) +
-  // perm[slot], as the fp16 hi part (n < 8) or the lo remainder (n >= 8); S2 B operand:
-  // the sums of sub-blocks 2g and 2g+1 (elements 64g..64g+31, 64g+32..64g+63, in order).
-  // Built from the wave's own copy of q, so no workgroup barrier is needed.
-  h8 qb[8];
-  h4 q2 = {0, 0, 0, 0};
-  auto build_q = [&]() {
-    // q was issued before this wave's stage loads (12): once at most 12 loads are
-    // outstanding, q has landed
-    if (nmine > 0)
-      asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    const float *qrow = reinterpret_cast<const float *>(&sm.run.st[wave][1]) + (n & 7) * (kQRow / 4) + 64 * g;
-    constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-    float qsum[2] = {0.0f, 0.0f};
-    // hi lanes (n < 8) take fp16(q), lo lanes fp16(q - fp16(q)): both are fp16(q - c)
-    // with c = fp16(q) masked to zero on the hi lanes
-    const uint32_t lo_mask = n < 8 ? 0u : 0xFFFFFFFFu;
-#pragma unroll
-    for (int st = 0; st < 8; ++st) {
-      const float4 r0 = *reinterpret_cast<const float4 *>(qrow + 32 * (st >> 2) + 8 * (st & 3));
-      const float4 r1 = *reinterpret_cast<const float4 *>(qrow + 32 * (st >> 2) + 8 * (st & 3) + 4);
-      const float v8[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-#pragma unroll
-      for (int k = 0; k < 8; ++k) qsum[st >> 2] += v8[k];
-      uint32_t w[4];
-#pragma unroll
-      for (int pp = 0; pp < 4; ++pp) {
-        const float a0 = v8[perm[2 * pp]], a1 = v8[perm[2 * pp + 1]];
-        const h2 h = {(_Float16)a0, (_Float16)a1};
-        const uint32_t c = as_u(h) & lo_mask;
-        w[pp] = mix_sub_hi(mix_sub_lo(a0, c), a1, c);
-      }
-      qb[st] = __builtin_bit_cast(h8, u4{w[0], w[1], w[2], w[3]});
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const _Float16 hi = (_Float16)qsum[t];
-      q2[t] = (n < 8) ? hi : (_Float16)(qsum[t] - (float)hi);
-    }
-  };
-  static_assert(kLoadsPerStage == 12, "the vmcnt above counts one stage of loads");
-
-  if (quant) {
-    // the quantization delays this workgroup's blocks: it outranks the block loops of
-    // the waves sharing its SIMDs
-    __builtin_amdgcn_s_setprio(3);
-    QuantWavesBarrier bar{&sm.run.t.quant.arrivals, 0u};
-    for (int row = wg; row < 4 * a.nseg; row += a.nwg) {
-      const int rs = row >> 2, p = (row >> 1) & 1, kvr = row & 1;
-      if (row != wg) xq = (p ? a.v_new : a.k_new)[((int64_t)rs * 2 + kvr) * 256 + tid];
-      const DecodeSeg &rg = a.seg[rs];
-      uint8_t *dst = (p ? rg.v : rg.k) + rg.t_new * a.rs_t + kvr * a.rs_h;
-      float deq;
-      q4k_quantize_superblock_lanes(xq, dst, &sm.run.t.quant.scr, tid, &deq, bar);
-      bar.target += 12;  // the three barriers of that call
-      a.dq[(int64_t)row * 256 + tid] = deq;
-    }
-    __builtin_amdgcn_s_setprio(0);
-  }
-  build_q();
-
-  WaveState S;
-#pragma unroll
-  for (int T2 = 0; T2 < 16; ++T2) S.acc[T2] = f4{0.f, 0.f, 0.f, 0.f};
-  S.accm = f4{0.f, 0.f, 0.f, 0.f};
-  S.m_run = -INFINITY;
-  S.lsum = 0.0f;
-  WaveTab &T = sm.run.t.tab[wave];
-  if (nmine > 0) {
-    const Masks MK = {vconst(0x000F000Fu), vconst(0x00F000F0u), vconst(0x64006400u)};
-    const KScaleSel ks = make_kscale_sel(g);
-    const float clamp_raw = kClampL2 / a.sl2, lazy_raw = kLazy / a.sl2;
-    const VScaleSel vs = make_vscale_sel(lane);
-    for (int i = 0; i < nmine; ++i) {
-      const int si = i & 1;  // block i uses stage i % 2
-      // The two waves of a SIMD are issued oldest-first at equal priority, which lets
-      // the older one run ahead and leaves the younger to finish alone. Lowering the
-      // priority with each block done keeps the one behind first in line.
-      if (i == 0)
-        __builtin_amdgcn_s_setprio(2);
-      else if (i == 1)
-        __builtin_amdgcn_s_setprio(1);
-      else if (i == 2)
-        __builtin_amdgcn_s_setprio(0);
-      if (i + 1 < nmine) {  // block i+1 streams in while block i is processed
-        issue_stage_at(st_lds0 + (uint32_t)(1 - si) * (uint32_t)sizeof(Stage), P,
-                       rsrc_advance(rk, boff + bstep), rsrc_advance(rv, boff + bstep));
-        asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-      } else {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      }
-      const Stage &st = sm.run.st[wave][si];
-      BlockWords W;
-      load_block_words(st, lane, W);
-      __builtin_amdgcn_sched_barrier(0);  // keep the K reads ahead of their phases
-      QKOut qo;
-      float pv[8];
-      phase_q(W, qb, q2, MK, ks, qo);
-      phase_s(W, qo, S, (int)(seq_k - (int64_t)(first + 4 * i) * kBlk), a.sl2, clamp_raw,
-              lazy_raw, lane, pv);
-      phase_p(st, W, S, T, pv, MK, vs, lane);
-      // every LDS read of this stage has completed before it is refilled
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      boff += bstep;
-    }
-    __builtin_amdgcn_s_setprio(0);
-  }
-  // ---- epilogue: per-wave reductions, then the four waves of each KV head merged into
-  // this workgroup's partial
-  S.lsum += __shfl_xor(S.lsum, 16);
-  S.lsum += __shfl_xor(S.lsum, 32);
-  // Row halves: the hi rows 0-7 sit in lanes g < 2 and the lo rows 8-15 of the same
-  // heads 32 lanes up. One v_permlane32_swap sums them for two tiles at once: afterwards
-  // lanes 0-31 hold tile T2 and lanes 32-63 tile T2 + 8, both for rows (heads)
-  // 4 (g & 1) + i.
-  const int gr = g & 1, gh = g >> 1;
-  f4 hs[8];
-#pragma unroll
-  for (int T2 = 0; T2 < 8; ++T2)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) hs[T2][i] = pair_sum32(S.acc[T2][i], S.acc[T2 + 8][i]);
-  // min term, paired alike: cm0 is row 4 (g & 1) + g / 2, cm1 row 4 (g & 1) + 2 + g / 2
-  // (column j = n)
-  const float cm0 = pair_sum32(S.accm[0], S.accm[1]), cm1 = pair_sum32(S.accm[2], S.accm[3]);
-  // Exchange through this wave's own table area: ml = {m of heads 0-7 (log2 units), l,
-  // f * l}, read by the other waves after the barrier; then cmin[head][j] * f.
-  float(*cmin)[8] = reinterpret_cast<float(*)[8]>(&T.kd[0]);
-  float *ml = T.vmd;
-  if (g == 0 && n < 8) {
-    ml[n] = S.m_run * a.sl2;
-    ml[8 + n] = S.lsum;
-  }
-  __syncthreads();  // every wave has left the loop: the stage buffers become the merge area
-  // weights f = 2^(m - M) of this wave's rows against the four waves of its KV head
-  auto weight = [&](int h) {
-    float M = -INFINITY;
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) M = fmaxf(M, sm.run.t.tab[2 * s4 + kv].vmd[h]);
-    const float mine = ml[h];
-    return (mine == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mine - M);
-  };
-  float fr[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) fr[i] = weight(4 * gr + i);
-  // cmin * f, written and read back by this wave only (its LDS operations stay in order)
-  if (n < 8) {
-    cmin[4 * gr + gh][n] = cm0 * (gh ? fr[1] : fr[0]);
-    cmin[4 * gr + 2 + gh][n] = cm1 * (gh ? fr[3] : fr[2]);
-  }
-  // scaled output rows: acc * f - cmin[row][e / 32] * f, one float4 per tile
-#pragma unroll
-  for (int T2 = 0; T2 < 8; ++T2) {
-    const int Tt = T2 + 8 * gh;
-    const int j = tile_e(Tt, n) >> 5;
-    float4 v;
-    v.x = fmaf(hs[T2][0], fr[0], -cmin[4 * gr + 0][j]);
-    v.y = fmaf(hs[T2][1], fr[1], -cmin[4 * gr + 1][j]);
-    v.z = fmaf(hs[T2][2], fr[2], -cmin[4 * gr + 2][j]);
-    v.w = fmaf(hs[T2][3], fr[3], -cmin[4 * gr + 3][j]);
-    sm.merge.o[wave][Tt][gr][n] = v;
-  }
-  if (g == 0 && n < 8) ml[16 + n] = weight(n) * ml[8 + n];
-  __syncthreads();
-  // ---- merge: item (kv, T2, g2, n) sums rows 4 g2 .. 4 g2 + 3 of KV head kv over its four
-  // waves and stores them at tile-order entry 16 T2 + n of heads 8 kv + 4 g2 + i
-  float *dst = a.part + (int64_t)wg * 16 * kPartRow;
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int item = tid + kThreads * it;
-    const int n2 = item & 15, g2 = (item >> 4) & 1, T2 = (item >> 5) & 15, kv2 = item >> 9;
-    float4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      const float4 v = sm.merge.o[2 * s4 + kv2][T2][g2][n2];
-      acc.x += v.x;
-      acc.y += v.y;
-      acc.z += v.z;
-      acc.w += v.w;
-    }
-    float *d0 = dst + (8 * kv2 + 4 * g2) * kPartRow + 16 * T2 + n2;
-    __builtin_nontemporal_store(acc.x, d0);
-    __builtin_nontemporal_store(acc.y, d0 + kPartRow);
-    __builtin_nontemporal_store(acc.z, d0 + 2 * kPartRow);
-    __builtin_nontemporal_store(acc.w, d0 + 3 * kPartRow);
-  }
-  if (tid < 16) {
-    const int kv2 = tid >> 3, h = tid & 7;
-    float M = -INFINITY, L = 0.0f;
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      M = fmaxf(M, sm.run.t.tab[2 * s4 + kv2].vmd[h]);
-      L += sm.run.t.tab[2 * s4 + kv2].vmd[16 + h];
-    }
-    __builtin_nontemporal_store(M, dst + tid * kPartRow + 256);
-    __builtin_nontemporal_store(L, dst + tid * kPartRow + 257);
-  }
-}
-
-}  // namespace
-
-// Plan and launch the decode and combine kernels over n <= kMaxSegs segments.
-static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
-                                  const float *k_new, const float *v_new, float *out,
-                                  int64_t rs_t, int64_t rs_h, float scale, Workspace &ws,
-                                  hipStream_t s) {
-  DecodeArgs d;
-  const bool fused = k_new != nullptr;
-  for (int i = 0; i < n; ++i) {
-    d.seg[i].k = in[i].k;
-    d.seg[i].v = in[i].v;
-    d.seg[i].seq_k = fused ? in[i].seq_k - 1 : in[i].seq_k;  // the new key joins in the combine
-    d.seg[i].t_new = in[i].seq_k - 1;
-    d.seg[i].nblk = (int)((d.seg[i].seq_k + kBlk - 1) / kBlk);
-  }
-  // Blocks per workgroup, a multiple of 4 (one or more per wave pair). One segment:
-  // spread over at most kMainWGs workgroups, one per CU. Several: the multiple that
-  // minimises the estimated makespan, ceil(workgroups / 256) rounds of (bpw / 4 blocks
-  // per wave + a per-workgroup overhead of about 1.3 blocks).
-  int bpw;
-  if (n == 1) {
-    int nwg = (d.seg[0].nblk + 3) / 4;
-    if (nwg > kMainWGs) nwg = kMainWGs;
-    if (nwg < 1) nwg = 1;
-    bpw = (d.seg[0].nblk + nwg - 1) / nwg;
-    bpw = (bpw + 3) / 4 * 4;
-    if (bpw < 4) bpw = 4;
-  } else {
-    bpw = 4;
-    double best = 1e30;
-    for (int cand = 4; cand <= 64; cand += 4) {
-      int64_t w = 0;
-      for (int i = 0; i < n; ++i) w += d.seg[i].nblk > 0 ? (d.seg[i].nblk + cand - 1) / cand : 1;
-      const double cost = (double)((w + kMainWGs - 1) / kMainWGs) * (cand / 4.0 + 1.3);
-      if (cost < best) {
-        best = cost;
-        bpw = cand;
-      }
-    }
-  }
-  CombineArgs c;
-  int wg = 0;
-  for (int i = 0; i < n; ++i) {
-    d.seg[i].wg0 = wg;
-    c.wg0[i] = wg;
-    const int w = d.seg[i].nblk > 0 ? (d.seg[i].nblk + bpw - 1) / bpw : 1;
-    wg += w;
-  }
-  c.wg0[n] = wg;
-  d.nseg = n;
-  d.nwg = wg;
-  d.bpw = bpw;
-  d.rs_t = rs_t;
-  d.rs_h = rs_h;
-  d.sl2 = scale * kLog2e;
-  d.q = q;
-  d.k_new = k_new;
-  d.v_new = v_new;
-  const size_t part_floats = (size_t)wg * 16 * kPartRow;
-  const size_t need = (part_floats + (size_t)n * 4 * 256) * sizeof(float);
-  int rc = ws.reserve(need);
-  if (rc) return rc;
-  d.part = static_cast<float *>(ws.ptr);
-  d.dq = d.part + part_floats;
-  hipLaunchKernelGGL(q4k_decode_kernel, dim3((unsigned)wg), dim3(kThreads), 0, s, d);
-  PKV_HIP(hipGetLastError());
-  c.part = d.part;
-  c.q = q;
-  c.dq = fused ? d.dq : nullptr;
-  c.out = out;
-  c.sl2 = d.sl2;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(16 * 8, (unsigned)n), dim3(256), 0, s, c);
-  PKV_HIP(hipGetLastError());
-  return PKV_OK;
-}
 
 int launch_attend_mfma(const AttnArgs &a, const float *k_new, const float *v_new, uint8_t *kc,
                        uint8_t *vc, int64_t t_new, Workspace &ws, hipStream_t s) {
@@ -801,7 +24,7 @@ int launch_attend_mfma(const AttnArgs &a, const float *k_new, const float *v_new
       in[i].seq_k = a.seq_k;
     }
     const int64_t qo = (int64_t)b0 * 16 * 256, ko = (int64_t)b0 * 2 * 256;
-    const int rc = launch_decode_segments(in, nb, a.q + qo, fused ? k_new + ko : nullptr,
+    const int rc = launch_decode_segments<false>(in, nb, a.q + qo, fused ? k_new + ko : nullptr,
                                           fused ? v_new + ko : nullptr, a.out + qo, a.rs.t,
                                           a.rs.h, a.scale, ws, s);
     if (rc) return rc;
@@ -827,7 +50,7 @@ int launch_append_attend_batched_mfma(int quant, const SeqDesc *seqs, int n, con
       in[i].seq_k = seqs[b0 + i].len;
     }
     const int64_t qo = (int64_t)b0 * 16 * 256, ko = (int64_t)b0 * 2 * 256;
-    const int rc = launch_decode_segments(in, nb, q + qo, k + ko, v + ko, out + qo, rs_t, rs_h,
+    const int rc = launch_decode_segments<false>(in, nb, q + qo, k + ko, v + ko, out + qo, rs_t, rs_h,
                                           scale, ws, s);
     if (rc) return rc;
   }

@@ -108,6 +108,14 @@ struct PrepArgs {
 };
 int launch_prep_append(const PrepArgs &a, hipStream_t s);
 
+// q/k preparation of a fused decode step (the Q4K MFMA decode kernel applies it itself).
+struct DecodePrep {
+  const float *q_alpha, *k_alpha;   // [256]
+  const float *cos_tab, *sin_tab;   // [max_pos][n_rot / 2]
+  float eps;
+  int n_rot;
+};
+
 // ---- launchers (pkv_attn.hip) ----
 struct AttnArgs {
   int quant;
@@ -127,6 +135,13 @@ int launch_attend(const AttnArgs &a, Workspace &ws, hipStream_t s);
 int launch_append_attend(const AttnArgs &a, const float *k_new, const float *v_new,
                          uint8_t *kc, uint8_t *vc, int64_t t_new, Workspace &ws,
                          hipStream_t s);
+
+// Decode step from projection outputs: prepare q and the new k (see DecodePrep), quantize
+// the new row into t_new and attend over keys [0, t_new], all inside the decode and combine
+// kernels. PKV_ERR_UNSUPPORTED when the shape has no such kernel.
+int launch_append_attend_prep_mfma(const AttnArgs &a, const float *k_new, const float *v_new,
+                                   uint8_t *kc, uint8_t *vc, int64_t t_new,
+                                   const DecodePrep &prep, Workspace &ws, hipStream_t s);
 
 struct SeqDesc {
   uint8_t *k, *v;

@@ -12,6 +12,9 @@ NUM_HEADS = 16
 NUM_KV_HEADS = 2
 HEAD_DIM = 256
 SCALE = 1.0 / 16.0
+N_ROT = 64                                   # rope.dimension_count (25% of head_dim)
+ROPE_THETA = 1.0e7                           # rope.freq_base
+RMS_EPS = 1e-6                               # attention.layer_norm_rms_epsilon
 N_LAYERS = 48
 FULL_INTERVAL = 4
 N_FULL = N_LAYERS // FULL_INTERVAL          # 12

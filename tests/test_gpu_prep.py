@@ -119,14 +119,17 @@ def test_prep_append_bitexact(pk, orc, quant, B, Hkv, D, n_rot):
     same_bytes(g, c)
 
 
-@pytest.mark.parametrize("quant", [Q4K, Q8_0, F16])
-def test_append_attend_prep_decode(pk, orc, quant):
+@pytest.mark.parametrize("quant,B,n_rot", [(Q4K, 1, 64), (Q4K, 2, 64), (Q4K, 1, 128),
+                                           (Q4K, 1, 256), (Q8_0, 1, 64),
+                                           (F16, 1, 64)])
+def test_append_attend_prep_decode(pk, orc, quant, B, n_rot):
     """Prefill from projections (l = 300), then decode steps; every step's output against
-    the oracle's attention over its own cache."""
-    say(f"prep decode quant={quant}")
-    rng = np.random.default_rng(400 + quant)
-    B, Hkv, H, D = 1, 2, 16, 256
-    L = Layer(pk, orc, D, 64, 1024, 11)
+    the oracle's attention over its own cache. Q4K with n_rot <= 128 runs the preparation
+    inside the decode kernel, the rest through the prep-append kernel."""
+    say(f"prep decode quant={quant} B={B} n_rot={n_rot}")
+    rng = np.random.default_rng(400 + quant + B + n_rot)
+    Hkv, H, D = 2, 16, 256
+    L = Layer(pk, orc, D, n_rot, 1024, 11)
     g = pk.PreallocatedQuantizedKvCache(B, Hkv, 512, D, pk.KvCacheQuantization(quant))
     c = orc.Cache(quant, B, Hkv, D, 512)
     q = rows(rng, (B, 300, H, D))
