@@ -143,26 +143,27 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs c) {
   }
   const float d = wave_sum(prod);
   if ((tid & 63) == 0) dotp[tid >> 6] = d;
-  accs[ps][g4] = acc;
-  if (g4 == 0) {
-    mx[ps] = m_loc;
-    ls[ps] = lacc;
-  }
+  if (g4 == 0) mx[ps] = m_loc;
+  __syncthreads();
+  // every thread: the new key's score and the overall max M; each slice then rescales
+  // its own sums to M, so that the final sum over slices is plain adds
+  const float s_new = dq != nullptr
+                          ? fminf(fmaxf((dotp[0] + dotp[1] + dotp[2] + dotp[3]) * sl2, -kSplitClampL2), kSplitClampL2)
+                          : -INFINITY;
+  float M = s_new;
+#pragma unroll
+  for (int x = 0; x < kCombSlices; ++x) M = fmaxf(M, mx[x]);
+  const float f = (m_loc == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_loc - M);
+  accs[ps][g4] = float4{acc.x * f, acc.y * f, acc.z * f, acc.w * f};
+  if (g4 == 0) ls[ps] = lacc * f;
   __syncthreads();
   if (tid < 32) {
-    const float s_new = dq != nullptr
-                            ? fminf(fmaxf((dotp[0] + dotp[1] + dotp[2] + dotp[3]) * sl2, -kSplitClampL2), kSplitClampL2)
-                            : -INFINITY;
-    float M = s_new;
-#pragma unroll
-    for (int x = 0; x < kCombSlices; ++x) M = fmaxf(M, mx[x]);
     float sum = 0.0f, L = 0.0f;
     const float *accf = reinterpret_cast<const float *>(&accs[0][0]);
 #pragma unroll
     for (int x = 0; x < kCombSlices; ++x) {
-      const float f = (mx[x] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mx[x] - M);
-      sum += f * accf[32 * x + tid];
-      L += f * ls[x];
+      sum += accf[32 * x + tid];
+      L += ls[x];
     }
     const int e = tile_e((i0 + tid) >> 4, (i0 + tid) & 15);
     const float f_new = (s_new == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_new - M);
