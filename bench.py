@@ -551,12 +551,90 @@ def run_config5(args):
                                      "traffic_per_layer": traffic(5)}})
 
 
+# ------------------------------------------------------------------ config 6
+def run_config6(args):
+    """The other 36 layers of the decode step: one Gated-DeltaNet autoregressive step per
+    linear-attention layer (pkv_deltanet_step; qwen3_next.rs:3392-3470), Qwen3-Next shape
+    (32 value heads, 128 x 128 f32 state), batch --dn-batch. Not a BASELINE config: the
+    row after the KV-cache path (the recurrent state that PrefixCache also restores)."""
+    import torch
+    import paramecia_amd as pk
+    from paramecia_amd import workloads as W
+
+    B, L, H, D = args.dn_batch, W.N_LINEAR, W.DN_HEADS, W.DN_DK
+    layers = []
+    for l in range(L):
+        lin = pk.LinearAttentionState(scale=D ** -0.5, eps=W.RMS_EPS)
+        ssm = torch.empty((B, H, D, D), device="cuda")
+        pk.fill_normal(ssm, W.SEED, W.stream_id(6, W.T_SSM, l), 0.02)
+        conv = torch.zeros((B, W.DN_CONV_DIM, W.DN_CONV_K - 1), device="cuda")
+        lin.recurrent_state = pk.RecurrentState(ssm, conv, torch.zeros((B, H), device="cuda"))
+        layers.append(lin)
+    ins = []
+    for l in range(L):
+        t = {}
+        for name, code, shape in (("q", W.T_DN_Q, (B, 1, H, D)), ("k", W.T_DN_K, (B, 1, H, D)),
+                                  ("v", W.T_DN_V, (B, 1, H, D)), ("g", W.T_DN_GATE, (B, 1, H)),
+                                  ("b", W.T_DN_BETA, (B, 1, H))):
+            t[name] = torch.empty(shape, device="cuda")
+            pk.fill_normal(t[name], W.SEED, W.stream_id(6, code, l))
+        t["g"] = -t["g"].abs() * 0.1  # log decay < 0
+        ins.append(t)
+    outs = [None] * L
+
+    def step():
+        for l in range(L):
+            t = ins[l]
+            outs[l] = layers[l].delta_net_autoregressive(t["q"], t["k"], t["v"], t["g"], t["b"])
+
+    ms_eager = event_time(torch, step, args.steps, args.warmup)
+    ms = graph_time(torch, step, args.steps, args.warmup)
+    # the kernel's share of the graph step: every layer has its own state, so the 36
+    # launches stream 36 distinct states (one layer relaunched alone would find its
+    # state in the 256 MB last-level cache)
+    per_layer = B * H * (2 * D * D * 4 + 3 * D * 4 + 2 * 4 + 4 + D * 4)  # state r+w, q k v, g b, offset, out
+    gbs = per_layer * L / (ms * 1e-3) / 1e9
+    gbs_one, ms_one = gbs, ms / L
+    r = base_result(6, "Gated-DeltaNet decode step µs (36 linear-attention layers, one token)",
+                    round(ms * 1000, 2), "us/step", False, ms, args,
+                    f"config6: 36 Gated-DeltaNet layers, batch {B}, 32 value heads, 128 x 128 "
+                    "f32 state updated in place per layer (l2norm q/k, decay, delta rule, "
+                    "output)",
+                    {"eager_us_per_step": round(ms_eager * 1000, 2),
+                     "step_hbm_gbs": round(gbs, 1),
+                     "roofline": {"kernel": "deltanet_step_kernel (one layer, its share of "
+                                            "the graph-replayed step)", "bound": "hbm",
+                                  "achieved": round(gbs_one, 1), "peak": HBM_PEAK_GBS,
+                                  "unit": "GB/s", "frac": round(gbs_one / HBM_PEAK_GBS, 4),
+                                  "bytes_per_launch": per_layer,
+                                  "avg_launch_us": round(ms_one * 1000, 3), "traffic": None}})
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import numpy as np
+        import oracle as orc
+        t = ins[0]
+        npy = lambda x: np.ascontiguousarray(x.cpu().numpy()[:, 0])  # drop the token axis
+        S = layers[0].recurrent_state.ssm_state.cpu().numpy().copy()
+        go = layers[0].recurrent_state.gate_cumsum_offset.cpu().numpy().copy()
+        args_np = [npy(t[n]) for n in ("q", "k", "v", "g", "b")]
+        t0 = time.perf_counter()
+        orc.deltanet_step(*args_np, S, go, D ** -0.5, W.RMS_EPS)
+        dt = time.perf_counter() - t0
+        r["cpu_baseline"] = {"value": round(dt * L * 1e6, 1), "unit": "us/step", "cores": 1,
+                             "kind": "port",
+                             "sample": f"config 6: 1 of {L} layers, one step timed once and "
+                                       f"multiplied by {L}; scalar oracle on {cpu_model()}"}
+    return r
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="3", help="1, 2, 3 (headline, default), 4, 5 or all")
+    ap.add_argument("--config", default="3",
+                    help="1, 2, 3 (headline, default), 4, 5, 6 (Gated-DeltaNet step) or all")
+    ap.add_argument("--dn-batch", type=int, default=1, help="config 6: sequences per step")
     ap.add_argument("--cached", type=int, default=131072, help="config 3: cached tokens")
     ap.add_argument("--layers", type=int, default=12, help="config 3: layers")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -580,7 +658,7 @@ def main() -> int:
     import torch
     torch.cuda.set_device(torch.device("cuda:0"))
     runners = {"1": run_config1, "2": run_config2, "3": run_config3, "4": run_config4,
-               "5": run_config5}
+               "5": run_config5, "6": run_config6}
     which = list(runners) if args.config == "all" else [args.config]
     for cfg in which:
         if cfg not in runners:

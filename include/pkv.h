@@ -212,6 +212,22 @@ typedef struct {
 int pkv_prefix_restore(const pkv_prefix *p, const pkv_layer_target *targets, int n_layers,
                        int mode, size_t *n_tokens_out, pkv_stream stream);
 
+/* ---- Gated-DeltaNet recurrent state (the linear-attention layers) ---- */
+/* delta_net_autoregressive_step (ops.rs:391-403) as delta_net_autoregressive calls it
+ * (qwen3_next.rs:3392-3470): one token, in place. q, k, v: [batch, heads, head_dim]
+ * (q, k already repeated to the value heads); gate (log decay) and beta (pre-sigmoid):
+ * [batch, heads]; state: [batch, heads, head_dim (value i), head_dim (key j)], the
+ * ssm_state of RecurrentState (qn:683-700); gate_offset: [batch, heads] or NULL, the
+ * gate_cumsum_offset += gate update (qn:3444-3451); out: [batch, heads, head_dim].
+ * qn = q*scale/sqrt(|q|^2+eps), kn = k/sqrt(|k|^2+eps); S *= exp(gate);
+ * S_i += (v_i - S_i.kn) sigmoid(beta) kn; out_i = S_i.qn. head_dim 64, 128 or 256
+ * (else PKV_ERR_UNSUPPORTED); q, k, state 16-byte aligned. A zero state stands for the
+ * reference's missing state (qn:3424-3431). */
+int pkv_deltanet_step(const float *q, const float *k, const float *v, const float *gate,
+                      const float *beta, float *state, float *gate_offset, float *out,
+                      int batch, int heads, int head_dim, float scale, float eps,
+                      pkv_stream stream);
+
 /* ---- utilities ---- */
 /* Seeded synthetic data: dst[i] = normal(seed, stream_id, i) * scale, bit-identical
  * to the CPU oracle's generator (Philox4x32-10, Irwin-Hall of eight 22-bit draws). */

@@ -94,6 +94,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_rms_norm.argtypes = [_fp, _fp, ctypes.c_float, sz, ctypes.c_int, _fp]
     L.orc_rms_norm.restype = None
     L.orc_rope_rows.argtypes = [_fp, sz, ctypes.c_int, ctypes.c_int, _i64p, _fp, _fp]
+    L.orc_deltanet_step.argtypes = [_fp] * 8 + [ctypes.c_int] * 3 + [ctypes.c_float] * 2
     L.orc_qk_prep.argtypes = [_fp, _fp] + [ctypes.c_int] * 5 + [_fp, _fp, ctypes.c_float,
                                                                  ctypes.c_int, _fp, _fp, i64,
                                                                  _fp, _fp]
@@ -335,3 +336,18 @@ class Cache:
         if rc != OK:
             raise ValueError(f"oracle attend failed ({rc})")
         return out
+
+
+def deltanet_step(q, k, v, gate, beta, state, gate_offset, scale: float, eps: float):
+    """orc_deltanet_step on numpy arrays: q, k, v [b, h, d]; gate, beta [b, h]; state
+    [b, h, d, d] (v index, k index) and gate_offset [b, h] (or None) updated in place.
+    Returns out [b, h, d]."""
+    b, h, d = q.shape
+    for a in (q, k, v, gate, beta, state) + ((gate_offset,) if gate_offset is not None else ()):
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+    assert state.shape == (b, h, d, d) and gate.shape == (b, h) and beta.shape == (b, h)
+    out = np.empty_like(v)
+    lib().orc_deltanet_step(_f(q), _f(k), _f(v), _f(gate), _f(beta), _f(state),
+                            _f(gate_offset) if gate_offset is not None else None, _f(out),
+                            b, h, d, scale, eps)
+    return out

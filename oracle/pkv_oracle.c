@@ -775,3 +775,50 @@ int orc_qk_prep(const float *q, const float *k, int batch, int l, int n_heads, i
                      offset, k_out);
   return ORC_OK;
 }
+
+/* ------------------------------------------------------------------ */
+/* Gated-DeltaNet autoregressive step (ops.rs:391-403, qwen3_next.rs:3392-3470) */
+/* ------------------------------------------------------------------ */
+
+void orc_deltanet_step(const float *q, const float *k, const float *v, const float *gate,
+                       const float *beta, float *state, float *gate_offset, float *out,
+                       int batch, int heads, int d, float scale, float eps) {
+  float *qn = (float *)malloc(sizeof(float) * (size_t)d);
+  float *kn = (float *)malloc(sizeof(float) * (size_t)d);
+  for (int b = 0; b < batch; ++b)
+    for (int h = 0; h < heads; ++h) {
+      const size_t hb = (size_t)b * heads + h;
+      const float *qh = q + hb * d, *kh = k + hb * d, *vh = v + hb * d;
+      float *S = state + hb * (size_t)d * d;
+      float sq = 0.0f, sk = 0.0f;
+      for (int j = 0; j < d; ++j) {
+        sq += qh[j] * qh[j];
+        sk += kh[j] * kh[j];
+      }
+      const float iq = 1.0f / sqrtf(sq + eps), ik = 1.0f / sqrtf(sk + eps);
+      for (int j = 0; j < d; ++j) {
+        qn[j] = qh[j] * iq * scale;
+        kn[j] = kh[j] * ik;
+      }
+      const float alpha = expf(gate[hb]);
+      const float bsig = 1.0f / (1.0f + expf(-beta[hb]));
+      for (int i = 0; i < d; ++i) {
+        float *row = S + (size_t)i * d;
+        float u = 0.0f;
+        for (int j = 0; j < d; ++j) {
+          row[j] = row[j] * alpha;
+          u += row[j] * kn[j];
+        }
+        const float di = (vh[i] - u) * bsig;
+        float o = 0.0f;
+        for (int j = 0; j < d; ++j) {
+          row[j] = row[j] + kn[j] * di;
+          o += row[j] * qn[j];
+        }
+        out[hb * d + i] = o;
+      }
+      if (gate_offset) gate_offset[hb] = gate_offset[hb] + gate[hb];
+    }
+  free(qn);
+  free(kn);
+}

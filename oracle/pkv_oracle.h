@@ -55,6 +55,14 @@
  *   The last ulp of these three follows candle's CPU kernels (rms_norm,
  *   rotary_emb::rope) and the host libm's powf/sinf/cosf, restated; the candle fork
  *   is absent, so bit-level agreement with it is UNPINNED (tolerance-level pinned).
+ *   Gated-DeltaNet step ....... pinned: transformers' torch_recurrent_gated_delta_rule
+ *                               (FLA convention, state transposed), a float64
+ *                               restatement, and closed forms (beta -> 0 is pure
+ *                               decay; zero state gives sigmoid(b) v (k.q); a one-hot
+ *                               key with beta = 1 writes v into that state column).
+ *                               The fused CUDA kernel behind ops.rs:391-403 lives in
+ *                               the absent candle fork, so its rounding is UNPINNED
+ *                               (tolerance-level pinned).
  */
 #ifndef PKV_ORACLE_H
 #define PKV_ORACLE_H
@@ -154,6 +162,21 @@ int orc_qk_prep(const float *q, const float *k, int batch, int l, int n_heads, i
                 int d, const float *q_alpha, const float *k_alpha, float eps, int n_rot,
                 const float *cos_tab, const float *sin_tab, int64_t offset, float *q_out,
                 float *k_out);
+
+/* Gated-DeltaNet autoregressive step: candle::deltanet_ops::delta_net_autoregressive_step
+ * (ops.rs:391-403) as the linear-attention layer calls it (qwen3_next.rs:3392-3470).
+ * q, k: [batch, heads, d]; v: [batch, heads, d]; gate (log decay), beta (pre-sigmoid):
+ * [batch, heads]; state: [batch, heads, d (v index i), d (k index j)], updated in place
+ * (qwen3_next.rs:3634-3640 fixes the index roles: v_prime[i] = sum_j k[j] state[i][j]).
+ * Per (b, h), in this order, f32:
+ *   qn = q * scale / sqrtf(sum q*q + eps), kn = k / sqrtf(sum k*k + eps)
+ *   S = S * exp(gate); u_i = sum_j S_ij kn_j; d_i = (v_i - u_i) * sigmoid(beta)
+ *   S_ij = S_ij + kn_j d_i; out_i = sum_j S_ij qn_j
+ * and gate_offset[b, h] += gate (the gate_cumsum_offset update, qwen3_next.rs:3444-3451;
+ * gate_offset may be NULL). Sums run in index order. */
+void orc_deltanet_step(const float *q, const float *k, const float *v, const float *gate,
+                       const float *beta, float *state, float *gate_offset, float *out,
+                       int batch, int heads, int d, float scale, float eps);
 
 #ifdef __cplusplus
 }

@@ -31,6 +31,7 @@ SOURCES = {
     "pkv_prefill_mfma.hip": [],
     "pkv_q8_decode.hip": [],
     "pkv_util.hip": [],
+    "pkv_deltanet.hip": [],
     "pkv_prep.hip": ["-ffp-contract=off"],
     "pkv_api.cpp": ["-x", "hip"],
 }

@@ -750,6 +750,18 @@ int pkv_prefix_restore(const pkv_prefix *p, const pkv_layer_target *targets, int
   return PKV_OK;
 }
 
+int pkv_deltanet_step(const float *q, const float *k, const float *v, const float *gate,
+                      const float *beta, float *state, float *gate_offset, float *out,
+                      int batch, int heads, int head_dim, float scale, float eps,
+                      pkv_stream stream) {
+  if (!q || !k || !v || !gate || !beta || !state || !out)
+    return set_error(PKV_ERR_ARG, "null argument");
+  if (batch <= 0 || heads <= 0 || head_dim <= 0)
+    return set_error(PKV_ERR_ARG, "batch, heads and head_dim must be > 0");
+  return launch_deltanet_step(q, k, v, gate, beta, state, gate_offset, out, batch, heads,
+                              head_dim, scale, eps, static_cast<hipStream_t>(stream));
+}
+
 int pkv_fill_normal(float *dst, size_t n, uint64_t seed, uint64_t stream_id, float scale,
                     pkv_stream stream) {
   if (!dst && n) return set_error(PKV_ERR_ARG, "null destination");

@@ -159,5 +159,9 @@ int launch_scale_channels(float *x, size_t rows, int dim, const int *ch, int n_c
                           float factor, hipStream_t s);
 int launch_copy_segments(void *const *dst, const void *const *src, const size_t *bytes, int n,
                          Workspace &ws, hipStream_t s);
+int launch_deltanet_step(const float *q, const float *k, const float *v, const float *gate,
+                         const float *beta, float *state, float *gate_offset, float *out,
+                         int batch, int heads, int head_dim, float scale, float eps,
+                         hipStream_t s);
 
 }  // namespace pkv

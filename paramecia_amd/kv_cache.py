@@ -422,11 +422,51 @@ class RecurrentState:
 
 
 class LinearAttentionState:
-    def __init__(self):
+    """Recurrent state of one Gated-DeltaNet layer and its per-token step
+    (GatedDeltaNet::delta_net_autoregressive, qwen3_next.rs:3392-3470). scale is
+    1/sqrt(head_v_dim) (qn:3012-3013), eps the layer's rms_norm_eps; conv_dim and
+    conv_kernel size the conv_state created with a first state (qn:3455-3460)."""
+
+    def __init__(self, scale: float = 128 ** -0.5, eps: float = 1e-6, conv_dim: int = 8192,
+                 conv_kernel: int = 4):
         self.recurrent_state: Optional[RecurrentState] = None
+        self.scale, self.eps = scale, eps
+        self.conv_dim, self.conv_kernel = conv_dim, conv_kernel
 
     def clear_state(self) -> None:
         self.recurrent_state = None
+
+    def delta_net_autoregressive(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                                 gate: torch.Tensor, beta: torch.Tensor) -> torch.Tensor:
+        """One token. q, k: [b, 1, heads, dk] (repeated to the value heads), v: [b, 1,
+        heads, dv], gate (log decay) and beta (pre-sigmoid): [b, 1, heads]. Returns
+        [b, 1, heads, dv]. The state [b, heads, dv, dk] is updated in place on the device
+        (pkv_deltanet_step); a missing state starts at zero, and gate_cumsum_offset
+        accumulates gate (qn:3444-3466)."""
+        b, l, H, dk = q.shape
+        dv = v.shape[-1]
+        if l != 1 or k.shape != q.shape or v.shape[:3] != (b, 1, H):
+            raise KvCacheError("delta_net_autoregressive expects one token: q, k [b,1,h,d], v [b,1,h,dv]")
+        if dk != dv:
+            raise KvCacheError(f"delta_net_autoregressive expects matching head dims ({dk} vs {dv})")
+        qq, kk, vv = _f32(q, "q"), _f32(k, "k"), _f32(v, "v")
+        g, bt = _f32(gate, "gate"), _f32(beta, "beta")
+        rs = self.recurrent_state
+        if rs is None:
+            rs = RecurrentState(torch.zeros((b, H, dv, dv), dtype=torch.float32, device=q.device),
+                                torch.zeros((b, self.conv_dim, self.conv_kernel - 1),
+                                            dtype=torch.float32, device=q.device))
+            self.recurrent_state = rs
+        if rs.gate_cumsum_offset is None:
+            rs.gate_cumsum_offset = torch.zeros((b, H), dtype=torch.float32, device=q.device)
+        if tuple(rs.ssm_state.shape) != (b, H, dv, dv) or not rs.ssm_state.is_contiguous():
+            raise KvCacheError("ssm_state must be a contiguous [b, heads, dv, dk] tensor")
+        out = torch.empty_like(vv)
+        _call(lib().pkv_deltanet_step(_ptr(qq), _ptr(kk), _ptr(vv), _ptr(g), _ptr(bt),
+                                      _ptr(rs.ssm_state), _ptr(rs.gate_cumsum_offset), _ptr(out),
+                                      b, H, dv, self.scale, self.eps,
+                                      torch.cuda.current_stream().cuda_stream))
+        return out
 
 
 # ------------------------------------------------------------------ PrefixCache

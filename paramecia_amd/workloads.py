@@ -27,6 +27,7 @@ SEED = 0x5EED_2026
 T_PREFILL_K, T_PREFILL_V, T_Q, T_NEW_K, T_NEW_V = 0, 1, 2, 3, 4
 T_SSM, T_CONV, T_GATE, T_SUFFIX_K, T_SUFFIX_V = 5, 6, 7, 8, 9
 T_CHUNK_K, T_CHUNK_V, T_CHUNK_Q, T_LENGTHS, T_CHANNELS = 10, 11, 12, 13, 14
+T_DN_Q, T_DN_K, T_DN_V, T_DN_GATE, T_DN_BETA = 15, 16, 17, 18, 19
 
 
 def stream_id(config: int, tensor: int, layer: int = 0, seq: int = 0) -> int:
