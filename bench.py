@@ -41,6 +41,7 @@ MEASURED_TRAFFIC = {
     1: (11_460_000, "profiles/q8_decode_config1.md: decode + combine"),
     2: (170_260_000, "profiles/q4k_prefill_config2.md: prefill kernel + split merge"),
     5: (418_800_000, "profiles/q4k_batched_decode_config5.md: decode + combine per layer"),
+    6: (73_730_000, "profiles/deltanet_step_config6.md: per launch at batch 16"),
 }
 
 
@@ -607,7 +608,8 @@ def run_config6(args):
                                   "achieved": round(gbs_one, 1), "peak": HBM_PEAK_GBS,
                                   "unit": "GB/s", "frac": round(gbs_one / HBM_PEAK_GBS, 4),
                                   "bytes_per_launch": per_layer,
-                                  "avg_launch_us": round(ms_one * 1000, 3), "traffic": None}})
+                                  "avg_launch_us": round(ms_one * 1000, 3),
+                                  "traffic": traffic(6) if B == 16 else None}})
     if not args.no_cpu_baseline:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import numpy as np

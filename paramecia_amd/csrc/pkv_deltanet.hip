@@ -8,7 +8,8 @@
 //   S = S * exp(gate); u_i = S_i . kn; d_i = (v_i - u_i) * sigmoid(beta)
 //   S_i = S_i + d_i kn; out_i = S_i . qn; gate_offset += gate
 //
-// HBM-bound: every state element is read once and written once, in place. A group of
+// HBM-bound: every state element is read once and written once, in place, with
+// nontemporal accesses (the state comes back only after the other 47 layers). A group of
 // 16 lanes owns one row S_i (d / 16 consecutive floats per lane, float4 accesses), so a
 // row's two dot products are 16-lane DPP reductions and the update needs no exchange
 // beyond them. Each group also normalises its head's q and k from the raw vectors (d
@@ -20,6 +21,7 @@
 namespace pkv {
 namespace {
 
+typedef float v4f __attribute__((ext_vector_type(4)));
 struct DeltaNetArgs {
   const float *q, *k, *v, *gate, *beta;
   float *state, *gate_offset, *out;
@@ -54,7 +56,7 @@ __global__ __launch_bounds__(256) void deltanet_step_kernel(DeltaNetArgs a) {
   float qv[kEpl], kv[kEpl], sv[kEpl];
 #pragma unroll
   for (int c = 0; c < kV4; ++c) {
-    const float4 x = q4[c], y = k4[c], z = s4[c];
+    const float4 x = q4[c], y = k4[c], z = __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const v4f *>(s4) + c));
     qv[4 * c] = x.x; qv[4 * c + 1] = x.y; qv[4 * c + 2] = x.z; qv[4 * c + 3] = x.w;
     kv[4 * c] = y.x; kv[4 * c + 1] = y.y; kv[4 * c + 2] = y.z; kv[4 * c + 3] = y.w;
     sv[4 * c] = z.x; sv[4 * c + 1] = z.y; sv[4 * c + 2] = z.z; sv[4 * c + 3] = z.w;
@@ -87,7 +89,7 @@ __global__ __launch_bounds__(256) void deltanet_step_kernel(DeltaNetArgs a) {
   }
 #pragma unroll
   for (int c = 0; c < kV4; ++c)
-    s4[c] = float4{sv[4 * c], sv[4 * c + 1], sv[4 * c + 2], sv[4 * c + 3]};
+    __builtin_nontemporal_store(v4f{sv[4 * c], sv[4 * c + 1], sv[4 * c + 2], sv[4 * c + 3]}, reinterpret_cast<v4f *>(s4) + c);
   o = row16_sum(o);
   if (lane == 0) a.out[hb * kD + row] = o;
   if (a.gate_offset != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
