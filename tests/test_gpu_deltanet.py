@@ -131,3 +131,48 @@ def test_rejects_bad_arguments(pk):
     with pytest.raises(Exception):
         pk.LinearAttentionState().delta_net_autoregressive(t(1, 2, 2, 128), t(1, 2, 2, 128),
                                                            t(1, 2, 2, 128), t(1, 2, 2), t(1, 2, 2))
+
+
+def test_prefix_snapshot_survives_later_steps(pk):
+    """PrefixCache save, two more tokens through every layer (DeltaNet states updated in
+    place, K/V appended), restore: the linear layers get the saved states back bit for
+    bit (the in-place updates never touched the snapshot), the full layers their saved
+    length, and replaying the first post-snapshot token gives the same outputs."""
+    say("deltanet: prefix snapshot across in-place steps")
+    m = pk.ModelKvState(8, 4, 16, 2, 256, 64)
+    lin = [l for l in m.layers if isinstance(l, pk.LinearAttentionState)]
+    full = m.full_layers()
+    H, D = 32, 128
+
+    def token(seed):
+        r = np.random.default_rng(seed)
+        kv = [dev(r.standard_normal((1, 2, 1, 256)).astype(np.float32)) for _ in range(2)]
+        dn = [tuple(dev(x) for x in (r.standard_normal((1, 1, H, D)).astype(np.float32),
+                                     r.standard_normal((1, 1, H, D)).astype(np.float32),
+                                     r.standard_normal((1, 1, H, D)).astype(np.float32),
+                                     -np.abs(r.standard_normal((1, 1, H))).astype(np.float32),
+                                     r.standard_normal((1, 1, H)).astype(np.float32)))
+              for _ in lin]
+        return kv, dn
+
+    def step(tok):
+        kv, dn = tok
+        for l in full:
+            l._ensure(1).append_quantized(kv[0], kv[1])
+        return [host(l.delta_net_autoregressive(*x)) for l, x in zip(lin, dn)]
+
+    for t in range(3):
+        step(token(t))
+    prefix = m.save_prefix_cache([11, 12, 13])
+    saved = [(host(l.recurrent_state.ssm_state), host(l.recurrent_state.gate_cumsum_offset)) for l in lin]
+    first = step(token(100))
+    step(token(101))
+    assert not np.array_equal(host(lin[0].recurrent_state.ssm_state), saved[0][0])
+    assert m.restore_prefix_cache(prefix) == 3
+    assert m.cache_seq_len() == 3
+    for l, (s, g) in zip(lin, saved):
+        np.testing.assert_array_equal(host(l.recurrent_state.ssm_state), s)
+        np.testing.assert_array_equal(host(l.recurrent_state.gate_cumsum_offset), g)
+    again = step(token(100))
+    for a, b in zip(first, again):
+        np.testing.assert_array_equal(a, b)
