@@ -629,14 +629,82 @@ def run_config6(args):
     return r
 
 
+# ------------------------------------------------------------------ config 7
+def run_config7(args):
+    """The step after the attention in the 12 full-attention layers: sigmoid gate and the
+    Q4K wo projection (pkv_gated_oproj_q4k; qwen3_next.rs:2657-2680), 4096 -> 2048 (the
+    Qwen3-Next-80B hidden size), batch --op-batch tokens. Not a BASELINE config."""
+    import torch
+    import paramecia_amd as pk
+    from paramecia_amd import workloads as W
+
+    B, L = args.op_batch, W.N_FULL
+    IN, OUT = W.NUM_HEADS * W.HEAD_DIM, W.HIDDEN
+    nsb = IN // 256
+    ws, xs, gs = [], [], []
+    for l in range(L):
+        # the layer's wo, drawn N(0, 0.02) and quantized to GGUF Q4K rows by the library's
+        # own quantize-on-append kernel (one 256-element superblock per cache row)
+        w = torch.empty((1, 1, OUT * nsb, 256), device="cuda")
+        pk.fill_normal(w, W.SEED, W.stream_id(7, W.T_WO, l), 0.02)
+        c = pk.PreallocatedQuantizedKvCache(1, 1, OUT * nsb, 256, pk.KvCacheQuantization.Q4K)
+        c.append_quantized(w, w)
+        kb, _ = c.raw_bytes()
+        ws.append(kb.clone())
+        del c, w, kb
+        x = torch.empty((B, 1, IN), device="cuda")
+        g = torch.empty((B, 1, IN), device="cuda")
+        pk.fill_normal(x, W.SEED, W.stream_id(7, W.T_Q, l))
+        pk.fill_normal(g, W.SEED, W.stream_id(7, W.T_GATE, l))
+        xs.append(x)
+        gs.append(g)
+    outs = [None] * L
+
+    def step():
+        for l in range(L):
+            outs[l] = pk.gated_o_proj(xs[l], gs[l], ws[l], OUT)
+
+    ms_eager = event_time(torch, step, args.steps, args.warmup)
+    ms = graph_time(torch, step, args.steps, args.warmup)
+    per_layer = OUT * nsb * 144 + B * (2 * IN * 4 + OUT * 4)  # weights, attn + gate in, out
+    gbs = per_layer * L / (ms * 1e-3) / 1e9
+    r = base_result(7, "gated o_proj µs/step (12 full-attention layers, Q4K wo 4096 -> 2048)",
+                    round(ms * 1000, 2), "us/step", False, ms, args,
+                    f"config7: sigmoid(gate) * attention output, then the Q4K wo projection "
+                    f"(4096 -> 2048), 12 layers, {B} token(s)",
+                    {"eager_us_per_step": round(ms_eager * 1000, 2),
+                     "roofline": {"kernel": "oproj_q4k_kernel (one layer, its share of the "
+                                            "graph-replayed step)", "bound": "hbm",
+                                  "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": per_layer,
+                                  "avg_launch_us": round(ms * 1000 / L, 3), "traffic": None}})
+    if not args.no_cpu_baseline:
+        import numpy as np
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as orc
+        x0, g0 = xs[0][:, 0].cpu().numpy().copy(), gs[0][:, 0].cpu().numpy().copy()
+        w0 = ws[0].cpu().numpy()
+        t0 = time.perf_counter()
+        orc.gated_oproj_q4k(x0, g0, w0, OUT)
+        dt = time.perf_counter() - t0
+        r["cpu_baseline"] = {"value": round(dt * L * 1e6, 1), "unit": "us/step", "cores": 1,
+                             "kind": "port",
+                             "sample": f"config 7: 1 of {L} layers (dequantize every wo row, "
+                                       f"then the dot products) timed once and multiplied by "
+                                       f"{L}; scalar oracle on {cpu_model()}"}
+    return r
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="3",
-                    help="1, 2, 3 (headline, default), 4, 5, 6 (Gated-DeltaNet step) or all")
+                    help="1, 2, 3 (headline, default), 4, 5, 6 (Gated-DeltaNet step), "
+                         "7 (gated o_proj) or all")
     ap.add_argument("--dn-batch", type=int, default=1, help="config 6: sequences per step")
+    ap.add_argument("--op-batch", type=int, default=1, help="config 7: tokens per step")
     ap.add_argument("--cached", type=int, default=131072, help="config 3: cached tokens")
     ap.add_argument("--layers", type=int, default=12, help="config 3: layers")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -660,7 +728,7 @@ def main() -> int:
     import torch
     torch.cuda.set_device(torch.device("cuda:0"))
     runners = {"1": run_config1, "2": run_config2, "3": run_config3, "4": run_config4,
-               "5": run_config5, "6": run_config6}
+               "5": run_config5, "6": run_config6, "7": run_config7}
     which = list(runners) if args.config == "all" else [args.config]
     for cfg in which:
         if cfg not in runners:

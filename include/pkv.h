@@ -228,6 +228,16 @@ int pkv_deltanet_step(const float *q, const float *k, const float *v, const floa
                       int batch, int heads, int head_dim, float scale, float eps,
                       pkv_stream stream);
 
+/* ---- the step after the attention ---- */
+/* Gated output projection (qn:2657-2680): out[b][o] = sum_i W[o][i] * attn[b][i] *
+ * sigmoid(gate[b][i]), W the layer's GGUF Q4K attn_output weight (self.wo, a QMatMul,
+ * models/with_tracing.rs:253-300 without custom scales or LoRA): out_dim rows of
+ * in_dim / 256 superblocks of 144 B. attn, gate: [batch, in_dim] f32 (gate may be NULL:
+ * no gating); out: [batch, out_dim]. in_dim 4096 or 8192 (else PKV_ERR_UNSUPPORTED);
+ * attn, gate and W 16-byte aligned. */
+int pkv_gated_oproj_q4k(const float *attn, const float *gate, const void *w_q4k, float *out,
+                        int batch, int in_dim, int out_dim, pkv_stream stream);
+
 /* ---- utilities ---- */
 /* Seeded synthetic data: dst[i] = normal(seed, stream_id, i) * scale, bit-identical
  * to the CPU oracle's generator (Philox4x32-10, Irwin-Hall of eight 22-bit draws). */

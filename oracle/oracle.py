@@ -95,6 +95,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_rms_norm.restype = None
     L.orc_rope_rows.argtypes = [_fp, sz, ctypes.c_int, ctypes.c_int, _i64p, _fp, _fp]
     L.orc_deltanet_step.argtypes = [_fp] * 8 + [ctypes.c_int] * 3 + [ctypes.c_float] * 2
+    L.orc_gated_oproj_q4k.argtypes = [_fp, _fp, _u8p, _fp] + [ctypes.c_int] * 3
     L.orc_qk_prep.argtypes = [_fp, _fp] + [ctypes.c_int] * 5 + [_fp, _fp, ctypes.c_float,
                                                                  ctypes.c_int, _fp, _fp, i64,
                                                                  _fp, _fp]
@@ -350,4 +351,15 @@ def deltanet_step(q, k, v, gate, beta, state, gate_offset, scale: float, eps: fl
     lib().orc_deltanet_step(_f(q), _f(k), _f(v), _f(gate), _f(beta), _f(state),
                             _f(gate_offset) if gate_offset is not None else None, _f(out),
                             b, h, d, scale, eps)
+    return out
+
+
+def gated_oproj_q4k(attn, gate, w_bytes, out_dim: int):
+    """orc_gated_oproj_q4k: attn, gate [b, in_dim] f32 (gate None: no gating), w_bytes the
+    uint8 Q4K rows [out_dim * in_dim / 256 * 144]. Returns [b, out_dim]."""
+    b, in_dim = attn.shape
+    assert w_bytes.size == out_dim * (in_dim // 256) * 144
+    out = np.empty((b, out_dim), np.float32)
+    lib().orc_gated_oproj_q4k(_f(attn), _f(gate) if gate is not None else None, _u8(w_bytes),
+                              _f(out), b, in_dim, out_dim)
     return out

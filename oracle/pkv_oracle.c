@@ -822,3 +822,27 @@ void orc_deltanet_step(const float *q, const float *k, const float *v, const flo
   free(qn);
   free(kn);
 }
+
+/* ------------------------------------------------------------------ */
+/* Gated output projection with Q4K weights (qwen3_next.rs:2657-2680)  */
+/* ------------------------------------------------------------------ */
+
+void orc_gated_oproj_q4k(const float *attn, const float *gate, const uint8_t *w, float *out,
+                         int batch, int in_dim, int out_dim) {
+  float *y = (float *)malloc(sizeof(float) * (size_t)in_dim);
+  float *row = (float *)malloc(sizeof(float) * (size_t)in_dim);
+  const size_t row_bytes = (size_t)(in_dim / 256) * 144;
+  for (int b = 0; b < batch; ++b) {
+    const float *x = attn + (size_t)b * in_dim;
+    for (int i = 0; i < in_dim; ++i)
+      y[i] = gate ? x[i] * (1.0f / (1.0f + expf(-gate[(size_t)b * in_dim + i]))) : x[i];
+    for (int o = 0; o < out_dim; ++o) {
+      orc_q4k_dequantize(w + (size_t)o * row_bytes, row, (size_t)in_dim);
+      float acc = 0.0f;
+      for (int i = 0; i < in_dim; ++i) acc += row[i] * y[i];
+      out[(size_t)b * out_dim + o] = acc;
+    }
+  }
+  free(y);
+  free(row);
+}

@@ -63,6 +63,11 @@
  *                               The fused CUDA kernel behind ops.rs:391-403 lives in
  *                               the absent candle fork, so its rounding is UNPINNED
  *                               (tolerance-level pinned).
+ *   gated o_proj (Q4K wo) ..... pinned: float64 numpy restatement of W_deq @ (x * sigmoid
+ *                               (g)) with W_deq from the pinned Q4K dequantizer, and closed
+ *                               forms (gate -> +inf passes x, -inf gives 0, 0 halves it).
+ *                               The reference's QMatMul (candle fork, absent) may quantize x
+ *                               before its dot products; that rounding is UNPINNED.
  */
 #ifndef PKV_ORACLE_H
 #define PKV_ORACLE_H
@@ -177,6 +182,13 @@ int orc_qk_prep(const float *q, const float *k, int batch, int l, int n_heads, i
 void orc_deltanet_step(const float *q, const float *k, const float *v, const float *gate,
                        const float *beta, float *state, float *gate_offset, float *out,
                        int batch, int heads, int d, float scale, float eps);
+
+/* Gated output projection (qwen3_next.rs:2657-2680): y = x * sigmoid(g) (f32:
+ * 1 / (1 + expf(-g)), gate may be NULL), then out[b][o] = sum_i Wdq[o][i] y[i] with Wdq the
+ * Q4K rows of w (out_dim rows of in_dim / 256 superblocks) dequantized by
+ * orc_q4k_dequantize, summed in index order in f32. */
+void orc_gated_oproj_q4k(const float *attn, const float *gate, const uint8_t *w, float *out,
+                         int batch, int in_dim, int out_dim);
 
 #ifdef __cplusplus
 }

@@ -8,5 +8,5 @@ from .kv_cache import (  # noqa: F401
     EmptyCacheError, FullAttentionKv, KvCacheError, KvCacheOffsetMismatch, KvCacheOverflow,
     KvCacheQuantization, LinearAttentionState, ModelKvState, PreallocatedQuantizedKvCache,
     PrefixCache, PrefixCacheEntry, PrefixLayerMismatch, QkPrep, RecurrentState, RotaryEmbedding,
-    append_attend_batched, fill_normal, flash_attn, scale_channels,
+    append_attend_batched, fill_normal, flash_attn, gated_o_proj, scale_channels,
 )

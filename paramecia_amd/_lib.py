@@ -30,6 +30,7 @@ SYMBOLS = (
     "pkv_prefix_restore", "pkv_fill_normal", "pkv_scale_channels", "pkv_copy_segments",
     "pkv_rope_tables_host", "pkv_rope_create", "pkv_rope_destroy", "pkv_rope_geometry",
     "pkv_append_prep", "pkv_append_attend_prep", "pkv_deltanet_step",
+    "pkv_gated_oproj_q4k",
 )
 
 
@@ -123,6 +124,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "pkv_append_prep": ([vp, P(QkPrep), vp, c_int, vp, vp, vp, c_i64, c_i64], c_int),
         "pkv_append_attend_prep": ([vp, P(QkPrep), vp, vp, vp, c_int, fl, c_i64, vp], c_int),
         "pkv_deltanet_step": ([vp] * 8 + [c_int] * 3 + [fl, fl, vp], c_int),
+        "pkv_gated_oproj_q4k": ([vp] * 4 + [c_int] * 3 + [vp], c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

@@ -32,6 +32,7 @@ SOURCES = {
     "pkv_q8_decode.hip": [],
     "pkv_util.hip": [],
     "pkv_deltanet.hip": [],
+    "pkv_oproj.hip": [],
     "pkv_prep.hip": ["-ffp-contract=off"],
     "pkv_api.cpp": ["-x", "hip"],
 }

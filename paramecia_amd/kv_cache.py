@@ -281,6 +281,25 @@ def append_attend_batched(caches: Sequence[PreallocatedQuantizedKvCache], k: tor
     return out
 
 
+def gated_o_proj(attn_output: torch.Tensor, gate: Optional[torch.Tensor], wo_q4k: torch.Tensor,
+                 out_dim: int) -> torch.Tensor:
+    """The attention's gated output projection with a Q4K wo (qwen3_next.rs:2657-2680):
+    attn_output, gate [b, l, in_dim] f32 (gate None: no gating), wo_q4k the uint8 GGUF
+    bytes [out_dim, in_dim / 256, 144]. Returns [b, l, out_dim] (pkv_gated_oproj_q4k)."""
+    x = _f32(attn_output, "attn_output")
+    g = _f32(gate, "gate") if gate is not None else None
+    if g is not None and g.shape != x.shape:
+        raise KvCacheError("gate must have the attention output's shape")
+    in_dim = x.shape[-1]
+    rows = x.numel() // in_dim
+    if wo_q4k.dtype != torch.uint8 or wo_q4k.numel() != out_dim * (in_dim // 256) * 144:
+        raise KvCacheError("wo_q4k must hold out_dim x in_dim / 256 Q4K superblocks (144 B)")
+    out = torch.empty(x.shape[:-1] + (out_dim,), dtype=torch.float32, device=x.device)
+    _call(lib().pkv_gated_oproj_q4k(_ptr(x), _ptr(g), _ptr(wo_q4k.contiguous()), _ptr(out), rows,
+                                    in_dim, out_dim, torch.cuda.current_stream().cuda_stream))
+    return out
+
+
 def fill_normal(t: torch.Tensor, seed: int, stream_id: int, scale: float = 1.0) -> torch.Tensor:
     """Seeded synthetic data identical to the CPU oracle's generator."""
     t = _f32(t, "t")

@@ -15,6 +15,7 @@ SCALE = 1.0 / 16.0
 N_ROT = 64                                   # rope.dimension_count (25% of head_dim)
 ROPE_THETA = 1.0e7                           # rope.freq_base
 RMS_EPS = 1e-6                               # attention.layer_norm_rms_epsilon
+HIDDEN = 2048                                # embedding_length (wo: 4096 -> 2048)
 N_LAYERS = 48
 FULL_INTERVAL = 4
 N_FULL = N_LAYERS // FULL_INTERVAL          # 12
@@ -28,6 +29,7 @@ T_PREFILL_K, T_PREFILL_V, T_Q, T_NEW_K, T_NEW_V = 0, 1, 2, 3, 4
 T_SSM, T_CONV, T_GATE, T_SUFFIX_K, T_SUFFIX_V = 5, 6, 7, 8, 9
 T_CHUNK_K, T_CHUNK_V, T_CHUNK_Q, T_LENGTHS, T_CHANNELS = 10, 11, 12, 13, 14
 T_DN_Q, T_DN_K, T_DN_V, T_DN_GATE, T_DN_BETA = 15, 16, 17, 18, 19
+T_WO = 20
 
 
 def stream_id(config: int, tensor: int, layer: int = 0, seq: int = 0) -> int:

@@ -1,0 +1,64 @@
+"""GPU parity of the gated output projection with a Q4K wo (pkv_gated_oproj_q4k; the step
+after the attention, qwen3_next.rs:2657-2680) against the CPU oracle's f32
+dequantize-then-dot on the same seeded inputs, within 2e-3 absolute + 1e-3 relative.
+The reference's QMatMul lives in the absent candle fork, so its own rounding (it may
+quantize the activations first) is not the bar; the GGUF Q4K weight bytes are shared."""
+import sys
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-3
+Q4K = 4
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def pk():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import paramecia_amd
+    paramecia_amd.lib()
+    return paramecia_amd
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+@pytest.mark.parametrize("b,in_dim,out_dim,gated", [(1, 4096, 2048, True), (3, 4096, 100, True),
+                                                    (2, 8192, 64, True), (2, 4096, 40, False)])
+def test_matches_oracle(pk, orc, b, in_dim, out_dim, gated):
+    say(f"oproj b={b} in={in_dim} out={out_dim} gated={gated}")
+    rng = np.random.default_rng(in_dim + out_dim + b)
+    w = (rng.standard_normal((out_dim, in_dim)) * 0.05).astype(np.float32)
+    wb = orc.quantize(w.reshape(-1), Q4K)
+    x = rng.standard_normal((b, in_dim)).astype(np.float32)
+    g = rng.standard_normal((b, in_dim)).astype(np.float32) if gated else None
+    out = pk.gated_o_proj(dev(x[:, None]), dev(g[:, None]) if gated else None, dev(wb), out_dim)
+    assert tuple(out.shape) == (b, 1, out_dim)
+    ref = orc.gated_oproj_q4k(x, g, wb, out_dim)
+    np.testing.assert_allclose(host(out)[:, 0], ref, atol=ATOL, rtol=RTOL)
+
+
+def test_rejects_unsupported_width(pk):
+    from paramecia_amd._lib import lib, ERR_UNSUPPORTED
+    say("oproj: argument checks")
+    x = torch.zeros((1, 1024), device="cuda")
+    w = torch.zeros(8 * 4 * 144, dtype=torch.uint8, device="cuda")
+    out = torch.zeros((1, 8), device="cuda")
+    assert lib().pkv_gated_oproj_q4k(x.data_ptr(), None, w.data_ptr(), out.data_ptr(), 1, 1024, 8,
+                                     torch.cuda.current_stream().cuda_stream) == ERR_UNSUPPORTED
