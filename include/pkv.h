@@ -238,6 +238,17 @@ int pkv_deltanet_step(const float *q, const float *k, const float *v, const floa
 int pkv_gated_oproj_q4k(const float *attn, const float *gate, const void *w_q4k, float *out,
                         int batch, int in_dim, int out_dim, pkv_stream stream);
 
+/* ---- PrefixCache host spill (the survey's next row after the path: the reference keeps
+ * prefixes in device memory only, qn:856-864; LocalBackend, paramecia-llm, is the caller
+ * that would evict them). A blob is a self-describing host byte image of a prefix:
+ * header, tokens, one descriptor per layer, then the packed K/V rows and DeltaNet states
+ * exactly as saved. serialize copies device -> host on `stream` and waits for it;
+ * deserialize checks every length and bound of the blob before it allocates, then
+ * copies host -> device and waits. A bad or truncated blob -> PKV_ERR_ARG. */
+size_t pkv_prefix_serialized_size(const pkv_prefix *p);
+int pkv_prefix_serialize(const pkv_prefix *p, void *host_dst, size_t capacity, pkv_stream stream);
+int pkv_prefix_deserialize(const void *host_src, size_t n, pkv_prefix **out, pkv_stream stream);
+
 /* ---- utilities ---- */
 /* Seeded synthetic data: dst[i] = normal(seed, stream_id, i) * scale, bit-identical
  * to the CPU oracle's generator (Philox4x32-10, Irwin-Hall of eight 22-bit draws). */

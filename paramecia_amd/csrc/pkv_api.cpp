@@ -5,6 +5,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <cstring>
 #include <string>
 #include <vector>
 
@@ -664,6 +665,176 @@ int pkv_prefix_save_linear(pkv_prefix *p, int layer, const float *ssm, size_t n_
   e.n_ssm = n_ssm;
   e.n_conv = n_conv;
   e.n_gate = n_gate;
+  return PKV_OK;
+}
+
+// ---------------------------------------------------------------- host spill
+// Blob layout (little-endian): BlobHeader, n_tokens u32 tokens, n_layers BlobEntry, then
+// each entry's payload in layer order (FULL: K rows then V rows, len*batch*heads*bpr
+// bytes each; LINEAR: ssm, conv, gate as f32). Everything is 8-byte aligned.
+namespace {
+constexpr uint32_t kBlobMagic = 0x50564B50u;  // "PKVP"
+constexpr uint32_t kBlobVersion = 1;
+struct BlobHeader {
+  uint32_t magic, version;
+  uint64_t n_tokens, n_layers, total;
+};
+struct BlobEntry {
+  int32_t kind, quant, batch, heads, head_dim, pad;
+  uint64_t bpr, len, n_ssm, n_conv, n_gate;
+};
+inline size_t align8(size_t x) { return (x + 7) & ~(size_t)7; }
+inline size_t entry_payload(const BlobEntry &e) {
+  if (e.kind == PKV_ENTRY_FULL) return 2 * align8((size_t)(e.len * (uint64_t)e.batch * e.heads * e.bpr));
+  if (e.kind == PKV_ENTRY_LINEAR) return align8(e.n_ssm * 4) + align8(e.n_conv * 4) + align8(e.n_gate * 4);
+  return 0;
+}
+BlobEntry describe(const Entry &e) {
+  BlobEntry d{};
+  d.kind = e.kind;
+  d.quant = e.quant;
+  d.batch = e.batch;
+  d.heads = e.heads;
+  d.head_dim = e.head_dim;
+  d.bpr = e.bpr;
+  d.len = (uint64_t)e.len;
+  d.n_ssm = e.n_ssm;
+  d.n_conv = e.n_conv;
+  d.n_gate = e.n_gate;
+  return d;
+}
+size_t blob_size(const pkv_prefix *p) {
+  size_t n = sizeof(BlobHeader) + align8(p->tokens.size() * 4) + p->entries.size() * sizeof(BlobEntry);
+  for (const Entry &e : p->entries) n += entry_payload(describe(e));
+  return n;
+}
+}  // namespace
+
+size_t pkv_prefix_serialized_size(const pkv_prefix *p) { return p ? blob_size(p) : 0; }
+
+int pkv_prefix_serialize(const pkv_prefix *p, void *host_dst, size_t capacity, pkv_stream stream) {
+  if (!p || !host_dst) return set_error(PKV_ERR_ARG, "null argument");
+  const size_t total = blob_size(p);
+  if (capacity < total)
+    return set_error(PKV_ERR_ARG, "host buffer too small: " + std::to_string(capacity) + " < " +
+                                       std::to_string(total));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint8_t *o = static_cast<uint8_t *>(host_dst);
+  BlobHeader hd{kBlobMagic, kBlobVersion, p->tokens.size(), p->entries.size(), total};
+  std::memcpy(o, &hd, sizeof hd);
+  size_t at = sizeof hd;
+  std::memcpy(o + at, p->tokens.data(), p->tokens.size() * 4);
+  at += align8(p->tokens.size() * 4);
+  for (const Entry &e : p->entries) {
+    const BlobEntry d = describe(e);
+    std::memcpy(o + at, &d, sizeof d);
+    at += sizeof d;
+  }
+  for (const Entry &e : p->entries) {
+    const BlobEntry d = describe(e);
+    if (e.kind == PKV_ENTRY_FULL) {
+      const size_t bytes = (size_t)(d.len * (uint64_t)d.batch * d.heads * d.bpr);
+      PKV_HIP(hipMemcpyAsync(o + at, e.k, bytes, hipMemcpyDeviceToHost, s));
+      at += align8(bytes);
+      PKV_HIP(hipMemcpyAsync(o + at, e.v, bytes, hipMemcpyDeviceToHost, s));
+      at += align8(bytes);
+    } else if (e.kind == PKV_ENTRY_LINEAR) {
+      PKV_HIP(hipMemcpyAsync(o + at, e.ssm, e.n_ssm * 4, hipMemcpyDeviceToHost, s));
+      at += align8(e.n_ssm * 4);
+      PKV_HIP(hipMemcpyAsync(o + at, e.conv, e.n_conv * 4, hipMemcpyDeviceToHost, s));
+      at += align8(e.n_conv * 4);
+      PKV_HIP(hipMemcpyAsync(o + at, e.gate, e.n_gate * 4, hipMemcpyDeviceToHost, s));
+      at += align8(e.n_gate * 4);
+    }
+  }
+  PKV_HIP(hipStreamSynchronize(s));
+  return PKV_OK;
+}
+
+int pkv_prefix_deserialize(const void *host_src, size_t n, pkv_prefix **out, pkv_stream stream) {
+  if (!host_src || !out) return set_error(PKV_ERR_ARG, "null argument");
+  const uint8_t *in = static_cast<const uint8_t *>(host_src);
+  BlobHeader hd;
+  if (n < sizeof hd) return set_error(PKV_ERR_ARG, "prefix blob truncated (header)");
+  std::memcpy(&hd, in, sizeof hd);
+  if (hd.magic != kBlobMagic || hd.version != kBlobVersion)
+    return set_error(PKV_ERR_ARG, "not a prefix blob of this version");
+  if (hd.total != n || hd.n_tokens > n / 4 || hd.n_layers > n / sizeof(BlobEntry))
+    return set_error(PKV_ERR_ARG, "prefix blob size mismatch");
+  size_t at = sizeof hd + align8(hd.n_tokens * 4);
+  const size_t table = at;
+  if (at + hd.n_layers * sizeof(BlobEntry) > n) return set_error(PKV_ERR_ARG, "prefix blob truncated");
+  std::vector<BlobEntry> ds(hd.n_layers);
+  size_t payload = 0;
+  for (size_t i = 0; i < hd.n_layers; ++i) {
+    std::memcpy(&ds[i], in + table + i * sizeof(BlobEntry), sizeof(BlobEntry));
+    const BlobEntry &d = ds[i];
+    if (d.kind == PKV_ENTRY_FULL) {
+      // every factor bounded before the product: len * batch * heads * bpr <= n
+      if (d.batch <= 0 || d.heads <= 0 || d.head_dim <= 0 || d.bpr == 0 || d.bpr > (1u << 20) ||
+          (uint64_t)d.batch * d.heads > (1ull << 20) || d.bpr != row_bytes(d.quant, d.head_dim) ||
+          d.len > n / ((uint64_t)d.batch * d.heads * d.bpr))
+        return set_error(PKV_ERR_ARG, "prefix blob: bad full-attention entry " + std::to_string(i));
+    } else if (d.kind == PKV_ENTRY_LINEAR) {
+      if (d.n_ssm > n || d.n_conv > n || d.n_gate > n)
+        return set_error(PKV_ERR_ARG, "prefix blob: bad linear entry " + std::to_string(i));
+    } else if (d.kind != PKV_ENTRY_EMPTY) {
+      return set_error(PKV_ERR_ARG, "prefix blob: unknown entry kind");
+    }
+    payload += entry_payload(d);
+    if (payload > n) return set_error(PKV_ERR_ARG, "prefix blob truncated (payload)");
+  }
+  at += hd.n_layers * sizeof(BlobEntry);
+  if (at + payload != n) return set_error(PKV_ERR_ARG, "prefix blob size mismatch (payload)");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  pkv_prefix *p = new pkv_prefix();
+  p->tokens.resize(hd.n_tokens);
+  std::memcpy(p->tokens.data(), in + sizeof hd, hd.n_tokens * 4);
+  p->entries.resize(hd.n_layers);
+  auto fail = [&](hipError_t er) {
+    (void)hipStreamSynchronize(s);
+    for (auto &e : p->entries) e.release();
+    delete p;
+    return hip_error(er, "pkv_prefix_deserialize");
+  };
+  for (size_t i = 0; i < hd.n_layers; ++i) {
+    const BlobEntry &d = ds[i];
+    Entry &e = p->entries[i];
+    hipError_t er = hipSuccess;
+    if (d.kind == PKV_ENTRY_FULL) {
+      const size_t bytes = (size_t)(d.len * (uint64_t)d.batch * d.heads * d.bpr);
+      er = hipMalloc(&e.k, bytes ? bytes : 1);
+      if (er == hipSuccess) er = hipMalloc(&e.v, bytes ? bytes : 1);
+      if (er == hipSuccess) er = hipMemcpyAsync(e.k, in + at, bytes, hipMemcpyHostToDevice, s);
+      at += align8(bytes);
+      if (er == hipSuccess) er = hipMemcpyAsync(e.v, in + at, bytes, hipMemcpyHostToDevice, s);
+      at += align8(bytes);
+      e.quant = d.quant;
+      e.batch = d.batch;
+      e.heads = d.heads;
+      e.head_dim = d.head_dim;
+      e.bpr = d.bpr;
+      e.len = (int64_t)d.len;
+    } else if (d.kind == PKV_ENTRY_LINEAR) {
+      er = hipMalloc(&e.ssm, (d.n_ssm ? d.n_ssm : 1) * 4);
+      if (er == hipSuccess) er = hipMalloc(&e.conv, (d.n_conv ? d.n_conv : 1) * 4);
+      if (er == hipSuccess) er = hipMalloc(&e.gate, (d.n_gate ? d.n_gate : 1) * 4);
+      if (er == hipSuccess) er = hipMemcpyAsync(e.ssm, in + at, d.n_ssm * 4, hipMemcpyHostToDevice, s);
+      at += align8(d.n_ssm * 4);
+      if (er == hipSuccess) er = hipMemcpyAsync(e.conv, in + at, d.n_conv * 4, hipMemcpyHostToDevice, s);
+      at += align8(d.n_conv * 4);
+      if (er == hipSuccess) er = hipMemcpyAsync(e.gate, in + at, d.n_gate * 4, hipMemcpyHostToDevice, s);
+      at += align8(d.n_gate * 4);
+      e.n_ssm = d.n_ssm;
+      e.n_conv = d.n_conv;
+      e.n_gate = d.n_gate;
+    }
+    e.kind = d.kind;
+    if (er != hipSuccess) return fail(er);
+  }
+  const hipError_t er = hipStreamSynchronize(s);
+  if (er != hipSuccess) return fail(er);
+  *out = p;
   return PKV_OK;
 }
 

@@ -10,6 +10,8 @@ torch provides memory and streams only, every kernel is libpkv's.
 from __future__ import annotations
 
 import ctypes
+import json
+import struct
 import enum
 from dataclasses import dataclass, field
 from typing import List, Optional, Sequence
@@ -509,6 +511,40 @@ class PrefixCache:
         if self._native is not None and self._native.value:
             self._free(self._native)
             self._native = None
+
+    def to_bytes(self) -> bytes:
+        """Host spill: the native blob (pkv_prefix_serialize: tokens, per-layer descriptors,
+        packed K/V rows and DeltaNet states as saved), then a JSON trailer with the
+        Python-side state shapes and its u64 length."""
+        n = lib().pkv_prefix_serialized_size(self._native)
+        host = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+        _call(lib().pkv_prefix_serialize(self._native, ctypes.c_void_p(host.data_ptr()), n,
+                                         ctypes.c_void_p(_stream())))
+        meta = json.dumps([[e.kind, e.seq_len, e.shapes] for e in self.layer_caches]).encode()
+        return host.numpy().tobytes() + meta + struct.pack("<Q", len(meta))
+
+    @classmethod
+    def from_bytes(cls, blob: bytes) -> "PrefixCache":
+        """Reload a to_bytes() image into device memory (pkv_prefix_deserialize checks the
+        blob's lengths before it allocates)."""
+        if len(blob) < 8:
+            raise KvCacheError("prefix blob truncated")
+        (m,) = struct.unpack("<Q", blob[-8:])
+        if m > len(blob) - 8:
+            raise KvCacheError("prefix blob truncated")
+        native, meta = blob[:len(blob) - 8 - m], json.loads(blob[len(blob) - 8 - m:-8].decode())
+        host = torch.frombuffer(bytearray(native), dtype=torch.uint8).pin_memory()
+        p = ctypes.c_void_p()
+        _call(lib().pkv_prefix_deserialize(ctypes.c_void_p(host.data_ptr()), len(native),
+                                           ctypes.byref(p), ctypes.c_void_p(_stream())))
+        toks = ctypes.POINTER(ctypes.c_uint32)()
+        nt = ctypes.c_size_t()
+        _call(lib().pkv_prefix_tokens(p, ctypes.byref(toks), ctypes.byref(nt)))
+        entries = [PrefixCacheEntry(k, n_, tuple(tuple(x) for x in sh) if sh else None)
+                   for k, n_, sh in meta]
+        pc = cls([toks[i] for i in range(nt.value)], entries, p)
+        pc._free = lib().pkv_prefix_free
+        return pc
 
 
 class ModelKvState:
