@@ -7,8 +7,9 @@
 //
 // W is out_dim rows of in_dim / 256 Q4K superblocks (144 B each: f16 d, f16 dmin, 12 B
 // of 6-bit scale / min codes, 128 B of nibbles), the GGUF layout. Weight streaming is
-// the cost (HBM; latency at batch 1): a workgroup of 4 waves owns 8 output rows (2 per
-// wave). Its threads first write the gated input row into LDS (each input is gated once
+// the cost (HBM; latency at batch 1): a workgroup of 4 waves owns 4 output rows (one per
+// wave: more workgroups in flight, for one or two tokens) or 8 (two per wave: the gated
+// input staged once for more rows, from four tokens on). Its threads first write the gated input row into LDS (each input is gated once
 // per workgroup); lane l of a wave then takes 64-element chunk l % 4 of superblock l / 4
 // (and further chunks in steps of 64 for wider inputs): the chunk's 32 nibble bytes, its
 // two sub-block scales and mins, and a wave reduction give the row's dot product. Each
@@ -22,7 +23,6 @@
 namespace pkv {
 namespace {
 
-constexpr int kOprojRowsPerWave = 2;
 constexpr int kOprojWaves = 4;
 constexpr int kOprojMaxIn = 8192;  // LDS: one gated input row
 // The gated row sits in LDS as 64-float chunks padded to 68 floats: lane l reads chunk l,
@@ -85,7 +85,8 @@ __device__ __forceinline__ void bytes_to_f32(uint32_t w, float *f) {
   for (int i = 0; i < 4; ++i) f[i] = (float)((w >> (8 * i)) & 0xFFu);
 }
 
-template <int kChunks>  // 64-element chunks per lane: in_dim / 4096
+// kChunks 64-element chunks per lane (in_dim / 4096), kOprojRowsPerWave output rows per wave
+template <int kChunks, int kOprojRowsPerWave>
 __global__ __launch_bounds__(256) void oproj_q4k_kernel(OprojArgs a) {
   __shared__ __attribute__((aligned(16))) float xs[kOprojMaxIn / 64 * kChunkPad];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -203,12 +204,15 @@ int launch_oproj_q4k(const float *attn, const float *gate, const uint8_t *w, flo
       return set_error(PKV_ERR_ARG, "attn, gate and the weights must be 16-byte aligned");
   if (batch > 65535) return set_error(PKV_ERR_ARG, "batch must be <= 65535");
   OprojArgs a{attn, gate, w, out, batch, in_dim, out_dim};
-  const int rows_per_wg = kOprojWaves * kOprojRowsPerWave;
+  const int rows_per_wave = batch < 4 ? 1 : 2;
+  const int rows_per_wg = kOprojWaves * rows_per_wave;
   const dim3 grid((unsigned)((out_dim + rows_per_wg - 1) / rows_per_wg), (unsigned)batch);
-  if (in_dim == 4096)
-    hipLaunchKernelGGL(oproj_q4k_kernel<1>, grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL(oproj_q4k_kernel<2>, grid, dim3(256), 0, s, a);
+  switch ((in_dim / 4096) * 4 + rows_per_wave) {
+    case 5: hipLaunchKernelGGL((oproj_q4k_kernel<1, 1>), grid, dim3(256), 0, s, a); break;
+    case 6: hipLaunchKernelGGL((oproj_q4k_kernel<1, 2>), grid, dim3(256), 0, s, a); break;
+    case 9: hipLaunchKernelGGL((oproj_q4k_kernel<2, 1>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((oproj_q4k_kernel<2, 2>), grid, dim3(256), 0, s, a); break;
+  }
   PKV_HIP(hipGetLastError());
   return PKV_OK;
 }

@@ -39,8 +39,10 @@ def host(t):
     return t.cpu().numpy()
 
 
+# batches below 4 take one output row per wave, from 4 on two (both kernel forms)
 @pytest.mark.parametrize("b,in_dim,out_dim,gated", [(1, 4096, 2048, True), (3, 4096, 100, True),
-                                                    (2, 8192, 64, True), (2, 4096, 40, False)])
+                                                    (2, 8192, 64, True), (2, 4096, 40, False),
+                                                    (5, 4096, 72, True), (4, 8192, 20, True)])
 def test_matches_oracle(pk, orc, b, in_dim, out_dim, gated):
     say(f"oproj b={b} in={in_dim} out={out_dim} gated={gated}")
     rng = np.random.default_rng(in_dim + out_dim + b)
