@@ -242,7 +242,8 @@ int pkv_gated_oproj_q4k(const float *attn, const float *gate, const void *w_q4k,
  * prefixes in device memory only, qn:856-864; LocalBackend, paramecia-llm, is the caller
  * that would evict them). A blob is a self-describing host byte image of a prefix:
  * header, tokens, one descriptor per layer, then the packed K/V rows and DeltaNet states
- * exactly as saved. serialize copies device -> host on `stream` and waits for it;
+ * exactly as saved. serialize first waits for the device (the snapshot copies ran on the
+ * caches' streams), then copies device -> host on `stream` and waits for it;
  * deserialize checks every length and bound of the blob before it allocates, then
  * copies host -> device and waits. A bad or truncated blob -> PKV_ERR_ARG. */
 size_t pkv_prefix_serialized_size(const pkv_prefix *p);

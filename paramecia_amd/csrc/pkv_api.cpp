@@ -719,6 +719,9 @@ int pkv_prefix_serialize(const pkv_prefix *p, void *host_dst, size_t capacity, p
     return set_error(PKV_ERR_ARG, "host buffer too small: " + std::to_string(capacity) + " < " +
                                        std::to_string(total));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // the snapshot copies were issued on the caches' streams (pkv_prefix_save_full /
+  // _save_linear), which need not be `stream`: a spill is rare, so wait for the device
+  PKV_HIP(hipDeviceSynchronize());
   uint8_t *o = static_cast<uint8_t *>(host_dst);
   BlobHeader hd{kBlobMagic, kBlobVersion, p->tokens.size(), p->entries.size(), total};
   std::memcpy(o, &hd, sizeof hd);
