@@ -83,6 +83,10 @@ int64_t pkv_capacity(const pkv_cache *h);       /* max_seq_len */
 int pkv_geometry(const pkv_cache *h, int *quant, int *batch, int *n_kv_heads, int *head_dim,
                  size_t *bytes_per_row);
 int pkv_truncate(pkv_cache *h, int64_t new_len); /* truncate(): min(new_len, len) */
+/* LayerWeights::restore_cache (qn:4326-4337) assigns seq_len directly: len may exceed the
+ * current length (the rows past it are whatever the buffers hold), not the capacity
+ * (PKV_ERR_OVERFLOW). */
+int pkv_set_len(pkv_cache *h, int64_t len);
 int pkv_clear(pkv_cache *h);                     /* clear() */
 int pkv_resize_batch(pkv_cache *h, int batch);   /* resize_batch(): realloc + reset if changed */
 
@@ -194,21 +198,27 @@ int pkv_prefix_linear_sizes(const pkv_prefix *p, int layer, size_t *n_ssm, size_
 int64_t pkv_prefix_full_len(const pkv_prefix *p, int layer);
 
 /* Restore targets for one layer: exactly one of `cache` (full attention) or the three
- * state pointers (linear attention) is set. `*state_valid` is written 1 if the state
- * was restored, 0 if it was cleared (Empty or wrong entry kind, qn:4121-4130). */
+ * state pointers (linear attention) is set. The state pointers come with their capacities
+ * in f32 elements; a LINEAR entry whose saved counts exceed them -> PKV_ERR_LAYOUT before
+ * anything is written. `*state_valid` is written 1 if the state was restored, 0 if it was
+ * cleared (Empty or wrong entry kind, qn:4121-4130). */
 typedef struct {
   pkv_cache *cache;
   float *ssm;
   float *conv;
   float *gate_offset;
   int *state_valid;
+  size_t ssm_cap, conv_cap, gate_cap;
 } pkv_layer_target;
 
 /* restore_prefix_cache (qn:5726-5740): layer count must match (PKV_ERR_LAYERS);
  * every layer is validated before anything is written; all copies go out as ONE
  * batched gather/copy launch on `stream`. FULL entries restore into the cache
  * (len = saved len), Empty/wrong-kind clear it (qn:2874-2882). Writes the prefix
- * token count to *n_tokens_out. mode: PKV_RESTORE_BYTES or PKV_RESTORE_REQUANTIZE. */
+ * token count to *n_tokens_out. mode: PKV_RESTORE_BYTES or PKV_RESTORE_REQUANTIZE.
+ * Ordering: the launch waits for the snapshot's own copies (issued on the stream of
+ * the save call) and for work already queued on each target cache's stream, and each
+ * target cache's stream waits for the launch before its next work. */
 int pkv_prefix_restore(const pkv_prefix *p, const pkv_layer_target *targets, int n_layers,
                        int mode, size_t *n_tokens_out, pkv_stream stream);
 

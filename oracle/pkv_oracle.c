@@ -161,8 +161,95 @@ void orc_q8_0_dequantize(const uint8_t *in, float *y, size_t n) {
 /* Q4K: { f16 d; f16 dmin; u8 scales[12]; u8 qs[128]; } = 144 bytes    */
 /* ------------------------------------------------------------------ */
 
+/* ORC_MUTANT plants one mistake in make_qkx1_quants, for tests/test_oracle_mutants.py
+ * only (the normal build leaves it 0): 1 one pass fewer, 2 one pass more, 3 no early
+ * exit, 4 ties rounded to even, 5 pairwise (tree) sums instead of sequential ones,
+ * 6 GGML's make_qkx2_quants in its place, 7 no `min > 0 -> 0` clamp inside the loop. */
+#ifndef ORC_MUTANT
+#define ORC_MUTANT 0
+#endif
+#if ORC_MUTANT == 5
+static float tree_sum(float *t, int n) {
+  for (int w = 1; w < n; w *= 2)
+    for (int i = 0; i + w < n; i += 2 * w) t[i] = t[i] + t[i + w];
+  return n > 0 ? t[0] : 0.0f;
+}
+#endif
+#if ORC_MUTANT == 6
+/* GGML make_qkx2_quants as quantize_row_q4_K_ref calls it: weights av_x + |x|,
+ * rmin -1, rdelta 0.1, nstep 20, squared error. */
+static void qkx2_mutant(const float *x, int n, int nmax, float *scale_out, float *neg_min_out) {
+  float w[256], sum_x2 = 0.0f;
+  for (int i = 0; i < n; ++i) sum_x2 += x[i] * x[i];
+  const float av_x = sqrtf(sum_x2 / n);
+  for (int i = 0; i < n; ++i) w[i] = av_x + fabsf(x[i]);
+  float mn = x[0], mx = x[0], sum_w = w[0], sum_x = w[0] * x[0];
+  for (int i = 1; i < n; ++i) {
+    if (x[i] < mn) mn = x[i];
+    if (x[i] > mx) mx = x[i];
+    sum_w += w[i];
+    sum_x += w[i] * x[i];
+  }
+  if (mn > 0) mn = 0;
+  if (mx == mn) {
+    *scale_out = 0.0f;
+    *neg_min_out = -mn;
+    return;
+  }
+  float iscale = nmax / (mx - mn), scale = 1.0f / iscale, best = 0.0f;
+  for (int i = 0; i < n; ++i) {
+    int l = nearest_int(iscale * (x[i] - mn));
+    l = l < 0 ? 0 : (l > nmax ? nmax : l);
+    const float d = scale * l + mn - x[i];
+    best += w[i] * d * d;
+  }
+  for (int is = 0; is <= 20; ++is) {
+    iscale = (-1.0f + 0.1f * is + nmax) / (mx - mn);
+    float sl = 0, sl2 = 0, sxl = 0;
+    uint8_t La[256];
+    for (int i = 0; i < n; ++i) {
+      int l = nearest_int(iscale * (x[i] - mn));
+      l = l < 0 ? 0 : (l > nmax ? nmax : l);
+      La[i] = (uint8_t)l;
+      sl += w[i] * l;
+      sl2 += w[i] * l * l;
+      sxl += w[i] * l * x[i];
+    }
+    const float D = sum_w * sl2 - sl * sl;
+    if (D > 0) {
+      float ts = (sum_w * sxl - sum_x * sl) / D, tm = (sl2 * sum_x - sl * sxl) / D;
+      if (tm > 0) {
+        tm = 0;
+        ts = sxl / sl2;
+      }
+      float mad = 0;
+      for (int i = 0; i < n; ++i) {
+        const float d = ts * La[i] + tm - x[i];
+        mad += w[i] * d * d;
+      }
+      if (mad < best) {
+        best = mad;
+        scale = ts;
+        mn = tm;
+      }
+    }
+  }
+  *scale_out = scale;
+  *neg_min_out = -mn;
+}
+#endif
+
 void orc_make_qkx1_quants(const float *x, int n, int nmax, int ntry, float *scale_out,
                           float *neg_min_out) {
+#if ORC_MUTANT == 6
+  qkx2_mutant(x, n, nmax, scale_out, neg_min_out);
+  return;
+#endif
+#if ORC_MUTANT == 1
+  ntry -= 1;
+#elif ORC_MUTANT == 2
+  ntry += 1;
+#endif
   uint8_t L[256];
   memset(L, 0, sizeof(L));
   float mn = x[0], mx = x[0];
@@ -182,24 +269,47 @@ void orc_make_qkx1_quants(const float *x, int n, int nmax, int ntry, float *scal
     float sumlx = 0.0f;
     int32_t suml2 = 0;
     int did_change = 0;
+#if ORC_MUTANT == 5
+    float terms[256];
+#endif
     for (int i = 0; i < n; ++i) {
+#if ORC_MUTANT == 4
+      int32_t li = rust_f32_as_i32(rintf(iscale * (x[i] - min)));
+#else
       int32_t li = nearest_int(iscale * (x[i] - min));
+#endif
       if (li < 0) li = 0;
       if (li > nmax) li = nmax;
       if ((uint8_t)li != L[i]) {
         L[i] = (uint8_t)li;
         did_change = 1;
       }
+#if ORC_MUTANT == 5
+      terms[i] = (x[i] - min) * (float)li;
+#else
       sumlx += (x[i] - min) * (float)li;
+#endif
       suml2 += li * li;
     }
+#if ORC_MUTANT == 5
+    sumlx = tree_sum(terms, n);
+#endif
     scale = sumlx / (float)suml2;
     float sum = -0.0f;
+#if ORC_MUTANT == 5
+    for (int i = 0; i < n; ++i) terms[i] = x[i] - scale * (float)L[i];
+    sum = tree_sum(terms, n);
+#else
     for (int i = 0; i < n; ++i) sum += x[i] - scale * (float)L[i];
+#endif
     min = sum / (float)n;
+#if ORC_MUTANT != 7
     if (min > 0.0f) min = 0.0f;
+#endif
     iscale = 1.0f / scale;
+#if ORC_MUTANT != 3
     if (!did_change) break;
+#endif
   }
   *scale_out = scale;
   *neg_min_out = -min;

@@ -30,11 +30,18 @@
  *                               away from zero), idempotence of Q(DQ(.)).
  *   Q4K dequantize ............ pinned: GGML block layout closed form (hand-built
  *                               blocks with known scales/mins/nibbles).
- *   Q4K quantize .............. partially pinned: hand-derived known-answer blocks,
- *                               format invariants (6-bit codes, nibbles <= 15),
- *                               per-sub-block reconstruction error bound, constant
- *                               sub-block -> zero. Byte parity against the candle
- *                               fork itself is UNPINNED (the fork is absent).
+ *   Q4K quantize .............. pinned against the published algorithm: hand-derived
+ *                               known answers of make_qkx1_quants that take 3 to 5
+ *                               passes, hit rounding ties and show the summation order
+ *                               (tests/q4k_known_answers.py), a whole block built from
+ *                               them, exact-grid blocks, format invariants and the
+ *                               reconstruction error bound; each of seven planted
+ *                               mistakes (pass count +-1, no early exit, ties to even,
+ *                               pairwise sums, make_qkx2_quants, no min clamp; the
+ *                               ORC_MUTANT builds) fails at least one known answer
+ *                               (tests/test_oracle_mutants.py). The candle fork's own
+ *                               bytes are absent; a divergence of the fork from upstream
+ *                               candle would not show.
  *   cache layout/offsets ...... pinned: closed-form row addressing and the
  *                               overflow / offset-mismatch rules.
  *   attention ................. pinned: float64 restatement compared with an

@@ -6,7 +6,7 @@ host-side mirror of the reference's Rust API used by tests and the benchmark.
 from ._lib import PkvError, lib  # noqa: F401
 from .kv_cache import (  # noqa: F401
     EmptyCacheError, FullAttentionKv, KvCacheError, KvCacheOffsetMismatch, KvCacheOverflow,
-    KvCacheQuantization, LinearAttentionState, ModelKvState, PreallocatedQuantizedKvCache,
+    KvCacheQuantization, LayerCheckpoint, LinearAttentionState, ModelKvState, PreallocatedQuantizedKvCache,
     PrefixCache, PrefixCacheEntry, PrefixLayerMismatch, QkPrep, RecurrentState, RotaryEmbedding,
     append_attend_batched, fill_normal, flash_attn, gated_o_proj, scale_channels,
 )

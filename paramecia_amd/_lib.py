@@ -22,7 +22,7 @@ SYMBOLS = (
     "pkv_last_error", "pkv_version", "pkv_quant_parse", "pkv_quant_default",
     "pkv_quant_block_size", "pkv_quant_is_ggml", "pkv_bytes_per_row", "pkv_create",
     "pkv_destroy", "pkv_set_stream", "pkv_len", "pkv_capacity", "pkv_geometry",
-    "pkv_truncate", "pkv_clear", "pkv_resize_batch", "pkv_append", "pkv_attend",
+    "pkv_truncate", "pkv_set_len", "pkv_clear", "pkv_resize_batch", "pkv_append", "pkv_attend",
     "pkv_append_attend", "pkv_get_kv", "pkv_kv_storage", "pkv_flash_attn",
     "pkv_append_attend_batched", "pkv_prefix_create", "pkv_prefix_free", "pkv_prefix_tokens",
     "pkv_prefix_num_layers", "pkv_prefix_entry_kind", "pkv_prefix_save_full",
@@ -48,6 +48,9 @@ class LayerTarget(ctypes.Structure):
         ("conv", ctypes.c_void_p),
         ("gate_offset", ctypes.c_void_p),
         ("state_valid", ctypes.POINTER(ctypes.c_int)),
+        ("ssm_cap", ctypes.c_size_t),
+        ("conv_cap", ctypes.c_size_t),
+        ("gate_cap", ctypes.c_size_t),
     ]
 
 
@@ -95,6 +98,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "pkv_capacity": ([vp], c_i64),
         "pkv_geometry": ([vp, P(c_int), P(c_int), P(c_int), P(c_int), P(c_sz)], c_int),
         "pkv_truncate": ([vp, c_i64], c_int),
+        "pkv_set_len": ([vp, c_i64], c_int),
         "pkv_clear": ([vp], c_int),
         "pkv_resize_batch": ([vp, c_int], c_int),
         "pkv_append": ([vp, vp, vp, c_i64, c_i64], c_int),

@@ -94,12 +94,21 @@ struct Entry {
   // LINEAR: Gated-DeltaNet state copies.
   float *ssm = nullptr, *conv = nullptr, *gate = nullptr;
   size_t n_ssm = 0, n_conv = 0, n_gate = 0;
+  // recorded on the save call's stream after the snapshot copies; a restore waits on it
+  hipEvent_t ready = nullptr;
+  int mark_ready(hipStream_t s) {
+    if (!ready) PKV_HIP(hipEventCreateWithFlags(&ready, hipEventDisableTiming));
+    PKV_HIP(hipEventRecord(ready, s));
+    return PKV_OK;
+  }
   void release() {
+    if (ready) (void)hipEventSynchronize(ready);
     if (k) (void)hipFree(k);
     if (v) (void)hipFree(v);
     if (ssm) (void)hipFree(ssm);
     if (conv) (void)hipFree(conv);
     if (gate) (void)hipFree(gate);
+    if (ready) (void)hipEventDestroy(ready);
     *this = Entry();
   }
 };
@@ -157,12 +166,14 @@ int pkv_create(int quant, int batch, int n_kv_heads, int head_dim, int64_t max_s
   h->bpr = row_bytes(quant, head_dim);
   h->stream = static_cast<hipStream_t>(stream);
   h->k = h->v = nullptr;
+  h->order_ev = nullptr;
   const size_t total = (size_t)batch * n_kv_heads * (size_t)max_seq_len * h->bpr;
   const size_t alloc = total ? total : 256;
   hipError_t e = hipMalloc(&h->k, alloc);
   if (e == hipSuccess) e = hipMalloc(&h->v, alloc);
   if (e == hipSuccess) e = hipMemsetAsync(h->k, 0, alloc, h->stream);  // vec![0u8; total]
   if (e == hipSuccess) e = hipMemsetAsync(h->v, 0, alloc, h->stream);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&h->order_ev, hipEventDisableTiming);
   if (e != hipSuccess) {
     if (h->k) (void)hipFree(h->k);
     if (h->v) (void)hipFree(h->v);
@@ -178,6 +189,7 @@ int pkv_destroy(pkv_cache *h) {
   (void)hipStreamSynchronize(h->stream);
   (void)hipFree(h->k);
   (void)hipFree(h->v);
+  if (h->order_ev) (void)hipEventDestroy(h->order_ev);
   delete h;
   return PKV_OK;
 }
@@ -206,6 +218,17 @@ int pkv_truncate(pkv_cache *h, int64_t new_len) {
   if (!h) return set_error(PKV_ERR_ARG, "null handle");
   if (new_len < 0) new_len = 0;
   if (new_len < h->seq_len) h->seq_len = new_len;
+  return PKV_OK;
+}
+
+int pkv_set_len(pkv_cache *h, int64_t len) {
+  if (!h) return set_error(PKV_ERR_ARG, "null handle");
+  if (len < 0) return set_error(PKV_ERR_ARG, "len must be >= 0");
+  if (len > h->max_seq_len)
+    return set_error(PKV_ERR_OVERFLOW, "Quantized KV cache overflow: trying to store " +
+                                           std::to_string(len) + " tokens but max is " +
+                                           std::to_string(h->max_seq_len));
+  h->seq_len = len;
   return PKV_OK;
 }
 
@@ -628,6 +651,11 @@ int pkv_prefix_save_full(pkv_prefix *p, int layer, const pkv_cache *h) {
   }
   PKV_HIP(hipMemcpyAsync(e.k, h->k, bytes, hipMemcpyDeviceToDevice, h->stream));
   PKV_HIP(hipMemcpyAsync(e.v, h->v, bytes, hipMemcpyDeviceToDevice, h->stream));
+  const int rc = e.mark_ready(h->stream);
+  if (rc) {
+    e.release();
+    return rc;
+  }
   e.kind = PKV_ENTRY_FULL;
   e.quant = h->quant;
   e.batch = h->batch;
@@ -660,6 +688,11 @@ int pkv_prefix_save_linear(pkv_prefix *p, int layer, const float *ssm, size_t n_
   if (er != hipSuccess) {
     e.release();
     return hip_error(er, "pkv_prefix_save_linear");
+  }
+  const int rc = e.mark_ready(s);
+  if (rc) {
+    e.release();
+    return rc;
   }
   e.kind = PKV_ENTRY_LINEAR;
   e.n_ssm = n_ssm;
@@ -868,8 +901,28 @@ int pkv_prefix_restore(const pkv_prefix *p, const pkv_layer_target *targets, int
                                                std::to_string(e.len) + " tokens but max is " +
                                                std::to_string(c->max_seq_len));
     }
-    if (!t.cache && e.kind == PKV_ENTRY_LINEAR && (!t.ssm || !t.conv || !t.gate_offset))
-      return set_error(PKV_ERR_ARG, "layer " + std::to_string(i) + ": missing state targets");
+    if (!t.cache && e.kind == PKV_ENTRY_LINEAR) {
+      if (!t.ssm || !t.conv || !t.gate_offset)
+        return set_error(PKV_ERR_ARG, "layer " + std::to_string(i) + ": missing state targets");
+      if (e.n_ssm > t.ssm_cap || e.n_conv > t.conv_cap || e.n_gate > t.gate_cap)
+        return set_error(PKV_ERR_LAYOUT, "layer " + std::to_string(i) +
+                                             ": saved state (" + std::to_string(e.n_ssm) + ", " +
+                                             std::to_string(e.n_conv) + ", " +
+                                             std::to_string(e.n_gate) +
+                                             " floats) exceeds the restore targets");
+    }
+  }
+  // Order the launch after the snapshot copies and after work already queued on the
+  // target caches' streams (an attention still reading rows about to be overwritten).
+  for (int i = 0; i < n_layers; ++i) {
+    const Entry &e = p->entries[(size_t)i];
+    const pkv_layer_target &t = targets[i];
+    const bool used = t.cache ? e.kind == PKV_ENTRY_FULL : e.kind == PKV_ENTRY_LINEAR;
+    if (used && e.ready) PKV_HIP(hipStreamWaitEvent(s, e.ready, 0));
+    if (t.cache && t.cache->stream != s) {
+      PKV_HIP(hipEventRecord(t.cache->order_ev, t.cache->stream));
+      PKV_HIP(hipStreamWaitEvent(s, t.cache->order_ev, 0));
+    }
   }
   std::vector<void *> dst;
   std::vector<const void *> src;
@@ -894,6 +947,17 @@ int pkv_prefix_restore(const pkv_prefix *p, const pkv_layer_target *targets, int
   int rc = launch_copy_segments(dst.data(), src.data(), bytes.data(), (int)dst.size(),
                                 util_workspace(), s);
   if (rc) return rc;
+  int rc_order = PKV_OK;  // the caches' streams wait for everything below
+  auto order_caches = [&]() {
+    for (int i = 0; i < n_layers && !rc_order; ++i) {
+      pkv_cache *c = targets[i].cache;
+      if (!c || c->stream == s) continue;
+      hipError_t er = hipEventRecord(c->order_ev, s);
+      if (er == hipSuccess) er = hipStreamWaitEvent(c->stream, c->order_ev, 0);
+      if (er != hipSuccess) rc_order = hip_error(er, "pkv_prefix_restore (stream order)");
+    }
+    return rc_order;
+  };
   for (int i = 0; i < n_layers; ++i) {
     const Entry &e = p->entries[(size_t)i];
     const pkv_layer_target &t = targets[i];
@@ -913,13 +977,17 @@ int pkv_prefix_restore(const pkv_prefix *p, const pkv_layer_target *targets, int
         if (!rc)
           rc = launch_append(c->quant, kf, vf, c->k, c->v, c->batch, c->n_kv_heads,
                              c->head_dim, e.len, 0, s);
-        if (rc) return rc;
+        if (rc) {
+          order_caches();
+          return rc;
+        }
       }
       c->seq_len = e.len;
     } else if (t.state_valid) {
       *t.state_valid = e.kind == PKV_ENTRY_LINEAR ? 1 : 0;
     }
   }
+  if (order_caches()) return rc_order;
   if (n_tokens_out) *n_tokens_out = p->tokens.size();
   return PKV_OK;
 }

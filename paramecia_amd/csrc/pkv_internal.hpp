@@ -73,6 +73,7 @@ struct pkv_cache {
   size_t bpr;
   uint8_t *k, *v;
   hipStream_t stream;
+  hipEvent_t order_ev;  // orders a prefix restore (on another stream) with this stream
   pkv::Workspace ws;
   pkv::Workspace qws;  // prepared q of a decode step with q/k preparation
   pkv::RowStrides strides() const {

@@ -51,6 +51,13 @@ _ERRORS = {
 }
 
 
+def np_prod(shape) -> int:
+    n = 1
+    for d in shape:
+        n *= int(d)
+    return n
+
+
 def _call(rc: int) -> None:
     if rc != _lib.OK:
         msg = lib().pkv_last_error().decode()
@@ -252,6 +259,10 @@ class PreallocatedQuantizedKvCache:
     def truncate(self, new_len: int) -> None:
         check(lib().pkv_truncate(self._h, new_len))
 
+    def set_len(self, seq_len: int) -> None:
+        """Assign seq_len directly, as LayerWeights::restore_cache does (qn:4326-4337)."""
+        _call(lib().pkv_set_len(self._h, seq_len))
+
     def resize_batch(self, batch_size: int) -> None:
         self._follow_stream()
         _call(lib().pkv_resize_batch(self._h, batch_size))
@@ -433,13 +444,90 @@ class FullAttentionKv:
         if self.quantized_cache is not None:
             self.quantized_cache.truncate(new_len)
 
+    def _is_float_cache(self) -> bool:
+        c = self.quantized_cache
+        return c is not None and c.quant in (KvCacheQuantization.F16, KvCacheQuantization.BF16)
+
+    def checkpoint(self) -> "LayerCheckpoint":
+        """LayerWeights::checkpoint_cache for a full-attention layer (qn:4311-4322): the
+        reference records preallocated_cache.seq_len, and that field holds only the F16 /
+        BF16 cache; a Q8_0 / Q4K cache lives in quantized_cache, so its checkpoint records 0."""
+        return LayerCheckpoint("FullAttention", self.quantized_cache.seq_len if self._is_float_cache() else 0)
+
+    def restore(self, seq_len: int) -> None:
+        """LayerWeights::restore_cache (qn:4326-4337): assigns seq_len to the F16 / BF16 cache;
+        a quantized cache is left as it is (the reference's preallocated_cache is None then)."""
+        if self._is_float_cache():
+            self.quantized_cache.set_len(seq_len)
+
+
+@dataclass
+class LayerCheckpoint:
+    """LayerCheckpoint (qwen3_next.rs:827-832): FullAttention { seq_len } or the
+    LinearAttention marker (the state sits in the layer's backup buffers)."""
+    kind: str
+    seq_len: int = 0
+
+
+def _copy_segments(pairs) -> None:
+    """Device copies dst <- src of equal-sized tensors, all in one libpkv launch."""
+    n = len(pairs)
+    if n == 0:
+        return
+    dst = (ctypes.c_void_p * n)(*[d.data_ptr() for d, _ in pairs])
+    src = (ctypes.c_void_p * n)(*[x.data_ptr() for _, x in pairs])
+    nb = (ctypes.c_size_t * n)(*[x.numel() * x.element_size() for _, x in pairs])
+    _call(lib().pkv_copy_segments(dst, src, nb, n, ctypes.c_void_p(_stream())))
+
+
+def _reuse(spare: Optional[torch.Tensor], like: torch.Tensor) -> torch.Tensor:
+    if spare is not None and spare.shape == like.shape and spare.dtype == like.dtype:
+        return spare
+    return torch.empty_like(like, memory_format=torch.contiguous_format)
+
 
 @dataclass
 class RecurrentState:
-    """Gated-DeltaNet state of one linear-attention layer (qwen3_next.rs:683-700)."""
+    """Gated-DeltaNet state of one linear-attention layer (qwen3_next.rs:683-700), with the
+    checkpoint / restore backups of speculative decoding (:733-757)."""
     ssm_state: torch.Tensor             # [b, heads, dk, dv] f32
     conv_state: torch.Tensor            # [b, conv_dim, kernel-1] f32
     gate_cumsum_offset: Optional[torch.Tensor] = None  # [b, heads] f32
+    backup_ssm: Optional[torch.Tensor] = None
+    backup_conv: Optional[torch.Tensor] = None
+    backup_gate_offset: Optional[torch.Tensor] = None
+    _spare: list = field(default_factory=lambda: [None, None, None], repr=False)
+
+    def checkpoint(self) -> None:
+        """RecurrentState::checkpoint (qn:733-744). The reference keeps shallow clones
+        because its steps replace the state tensors; pkv_deltanet_step updates them in
+        place, so the backups are copies, made in one launch into buffers kept from the
+        previous restore (no allocation once they exist)."""
+        pairs = []
+        keep = [self.backup_ssm, self.backup_conv, self.backup_gate_offset]
+        spare = [k if k is not None else s for k, s in zip(keep, self._spare)]
+        self.backup_ssm = _reuse(spare[0], self.ssm_state)
+        self.backup_conv = _reuse(spare[1], self.conv_state)
+        pairs += [(self.backup_ssm, self.ssm_state.contiguous()),
+                  (self.backup_conv, self.conv_state.contiguous())]
+        if self.gate_cumsum_offset is not None:
+            self.backup_gate_offset = _reuse(spare[2], self.gate_cumsum_offset)
+            pairs.append((self.backup_gate_offset, self.gate_cumsum_offset.contiguous()))
+        else:
+            self.backup_gate_offset = None
+        self._spare = [None, None, None]
+        _copy_segments(pairs)
+
+    def restore(self) -> None:
+        """RecurrentState::restore (qn:746-757): the backups become the state (O(1)) and are
+        taken; gate_cumsum_offset takes the backup's value, None included. The replaced
+        tensors are kept for the next checkpoint."""
+        if self.backup_ssm is not None:
+            self._spare[0], self.ssm_state, self.backup_ssm = self.ssm_state, self.backup_ssm, None
+        if self.backup_conv is not None:
+            self._spare[1], self.conv_state, self.backup_conv = self.conv_state, self.backup_conv, None
+        self._spare[2] = self.gate_cumsum_offset
+        self.gate_cumsum_offset, self.backup_gate_offset = self.backup_gate_offset, None
 
 
 class LinearAttentionState:
@@ -456,6 +544,22 @@ class LinearAttentionState:
 
     def clear_state(self) -> None:
         self.recurrent_state = None
+
+    def checkpoint_state(self) -> None:
+        """GatedDeltaNet::checkpoint_state (qn:4011-4019): no state, nothing to save."""
+        if self.recurrent_state is not None:
+            self.recurrent_state.checkpoint()
+
+    def restore_state(self) -> None:
+        """GatedDeltaNet::restore_state (qn:4021-4030)."""
+        if self.recurrent_state is not None:
+            self.recurrent_state.restore()
+
+    def restore_to_intermediate_state(self, index: int) -> bool:
+        """GatedDeltaNet::restore_to_intermediate_state (qn:4046-4054). The per-position
+        states come from the chunked verification forward, which is not part of this
+        library, so none are held: False, as the reference returns without them."""
+        return False
 
     def delta_net_autoregressive(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                  gate: torch.Tensor, beta: torch.Tensor) -> torch.Tensor:
@@ -537,14 +641,52 @@ class PrefixCache:
         p = ctypes.c_void_p()
         _call(lib().pkv_prefix_deserialize(ctypes.c_void_p(host.data_ptr()), len(native),
                                            ctypes.byref(p), ctypes.c_void_p(_stream())))
+        try:
+            entries = cls._check_trailer(p, meta)
+        except Exception:
+            lib().pkv_prefix_free(p)
+            raise
         toks = ctypes.POINTER(ctypes.c_uint32)()
         nt = ctypes.c_size_t()
         _call(lib().pkv_prefix_tokens(p, ctypes.byref(toks), ctypes.byref(nt)))
-        entries = [PrefixCacheEntry(k, n_, tuple(tuple(x) for x in sh) if sh else None)
-                   for k, n_, sh in meta]
         pc = cls([toks[i] for i in range(nt.value)], entries, p)
         pc._free = lib().pkv_prefix_free
         return pc
+
+    @staticmethod
+    def _check_trailer(p, meta) -> List["PrefixCacheEntry"]:
+        """The JSON trailer must describe the native blob exactly: same layer count, kinds,
+        FullAttention lengths and LinearAttention element counts (restore sizes its state
+        tensors from these shapes)."""
+        kinds = {"Empty": _lib.ENTRY_EMPTY, "FullAttention": _lib.ENTRY_FULL,
+                 "LinearAttention": _lib.ENTRY_LINEAR}
+        if not isinstance(meta, list) or len(meta) != lib().pkv_prefix_num_layers(p):
+            raise KvCacheError("prefix blob: trailer layer count differs from the blob")
+        entries = []
+        for i, item in enumerate(meta):
+            if not isinstance(item, list) or len(item) != 3 or item[0] not in kinds:
+                raise KvCacheError(f"prefix blob: bad trailer entry {i}")
+            kind, n_, sh = item
+            if lib().pkv_prefix_entry_kind(p, i) != kinds[kind]:
+                raise KvCacheError(f"prefix blob: trailer kind of layer {i} differs from the blob")
+            shapes = None
+            if kind == "FullAttention":
+                if not isinstance(n_, int) or n_ != lib().pkv_prefix_full_len(p, i):
+                    raise KvCacheError(f"prefix blob: trailer length of layer {i} differs")
+            elif kind == "LinearAttention":
+                ns, nc, ng = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+                _call(lib().pkv_prefix_linear_sizes(p, i, ctypes.byref(ns), ctypes.byref(nc),
+                                                    ctypes.byref(ng)))
+                try:
+                    shapes = tuple(tuple(int(d) for d in x) for x in sh)
+                    ok = len(shapes) == 3 and all(d >= 0 for x in shapes for d in x) and \
+                        [int(np_prod(x)) for x in shapes] == [ns.value, nc.value, ng.value]
+                except (TypeError, ValueError):
+                    ok = False
+                if not ok:
+                    raise KvCacheError(f"prefix blob: trailer state shapes of layer {i} differ")
+            entries.append(PrefixCacheEntry(kind, n_ if kind == "FullAttention" else 0, shapes))
+        return entries
 
 
 class ModelKvState:
@@ -586,6 +728,35 @@ class ModelKvState:
             if isinstance(l, FullAttentionKv):
                 return l.cache_seq_len()
         return 0
+
+    def checkpoint_cache(self) -> List[LayerCheckpoint]:
+        """ModelWeights::checkpoint_cache (qn:5479-5488, per layer :4311-4322)."""
+        out = []
+        for l in self.layers:
+            if isinstance(l, FullAttentionKv):
+                out.append(l.checkpoint())
+            else:
+                l.checkpoint_state()
+                out.append(LayerCheckpoint("LinearAttention"))
+        return out
+
+    def restore_cache(self, checkpoints: Sequence[LayerCheckpoint]) -> None:
+        """ModelWeights::restore_cache (qn:5490-5501, per layer :4326-4341); a checkpoint of
+        the other layer kind is ignored, as the reference's match does."""
+        for l, cp in zip(self.layers, checkpoints):
+            if isinstance(l, FullAttentionKv) and cp.kind == "FullAttention":
+                l.restore(cp.seq_len)
+            elif isinstance(l, LinearAttentionState) and cp.kind == "LinearAttention":
+                l.restore_state()
+
+    def restore_to_intermediate_state(self, index: int, offset: int) -> None:
+        """ModelWeights::restore_to_intermediate_state (qn:5377-5381, per layer :4365-4375):
+        full layers truncate to offset + index + 1."""
+        for l in self.layers:
+            if isinstance(l, FullAttentionKv):
+                l.truncate_kv_cache(offset + index + 1)
+            else:
+                l.restore_to_intermediate_state(index)
 
     def save_prefix_cache(self, prefix_tokens: Sequence[int]) -> PrefixCache:
         toks = (ctypes.c_uint32 * max(len(prefix_tokens), 1))(*prefix_tokens)
@@ -642,6 +813,7 @@ class ModelKvState:
                 t = tuple(torch.empty(sh, dtype=torch.float32, device="cuda") for sh in (ss, cs, gs))
                 restored[i] = t
                 targets[i].ssm, targets[i].conv, targets[i].gate_offset = (x.data_ptr() for x in t)
+                targets[i].ssm_cap, targets[i].conv_cap, targets[i].gate_cap = (x.numel() for x in t)
             targets[i].state_valid = ctypes.cast(ctypes.addressof(valid) + 4 * i,
                                                  ctypes.POINTER(ctypes.c_int))
         ntok = ctypes.c_size_t()

@@ -121,3 +121,73 @@ def test_refuses_bad_blobs(pk):
     assert load(bad) == ERR_ARG
     with pytest.raises(Exception):
         pk.PrefixCache.from_bytes(blob[:20])
+
+
+def _retrailer(blob, fn):
+    """The blob with its JSON trailer rewritten by fn (the native part unchanged)."""
+    import json
+    (m,) = struct.unpack("<Q", blob[-8:])
+    native, meta = blob[:len(blob) - 8 - m], json.loads(blob[len(blob) - 8 - m:-8].decode())
+    meta = fn(meta)
+    t = json.dumps(meta).encode()
+    return native + t + struct.pack("<Q", len(t))
+
+
+def test_refuses_trailer_that_disagrees_with_blob(pk):
+    """The Python trailer sizes the restored state tensors, so it must match the native
+    blob: smaller state shapes, a wrong kind, a wrong length or a missing layer are
+    refused before any restore."""
+    say("prefix spill: trailer checks")
+    m = model_with_state(pk, pk.KvCacheQuantization.Q4K)
+    blob = m.save_prefix_cache([7, 8]).to_bytes()
+    pk.PrefixCache.from_bytes(blob)  # unaltered: accepted
+
+    def smaller_state(meta):
+        meta[0][2][0] = [1, 32, 64, 128]       # layer 0 (linear): half the ssm rows
+        return meta
+
+    def wrong_kind(meta):
+        meta[3] = ["Empty", 0, None]            # layer 3 is full attention in the blob
+        return meta
+
+    def wrong_len(meta):
+        meta[3][1] = 19
+        return meta
+
+    def linear_as_empty(meta):
+        meta[1] = ["Empty", 0, None]
+        return meta
+
+    for fn in (smaller_state, wrong_kind, wrong_len, linear_as_empty, lambda m_: m_[:-1]):
+        with pytest.raises(pk.KvCacheError):
+            pk.PrefixCache.from_bytes(_retrailer(blob, fn))
+
+
+def test_restore_refuses_small_state_targets(pk):
+    """pkv_prefix_restore checks each state target's capacity against the saved counts
+    (PKV_ERR_LAYOUT) before it writes anything."""
+    from paramecia_amd._lib import lib, LayerTarget, ERR_LAYOUT
+    say("prefix restore: state target capacities")
+    m = model_with_state(pk, pk.KvCacheQuantization.Q4K)
+    pc = m.save_prefix_cache([1])
+    n = len(m.layers)
+    targets = (LayerTarget * n)()
+    keep = []
+    for i, l in enumerate(m.layers):
+        if isinstance(l, pk.FullAttentionKv):
+            targets[i].cache = l.quantized_cache.handle.value
+        else:
+            rs = l.recurrent_state
+            t = (torch.empty_like(rs.ssm_state), torch.empty_like(rs.conv_state),
+                 torch.empty_like(rs.gate_cumsum_offset))
+            keep.append(t)
+            targets[i].ssm, targets[i].conv, targets[i].gate_offset = (x.data_ptr() for x in t)
+            targets[i].ssm_cap, targets[i].conv_cap, targets[i].gate_cap = (x.numel() for x in t)
+    targets[2].conv_cap -= 1
+    lens = [l.quantized_cache.seq_len for l in m.full_layers()]
+    rc = lib().pkv_prefix_restore(pc._native, targets, n, 0, None, None)
+    assert rc == ERR_LAYOUT, lib().pkv_last_error()
+    assert [l.quantized_cache.seq_len for l in m.full_layers()] == lens
+    targets[2].conv_cap += 1
+    assert lib().pkv_prefix_restore(pc._native, targets, n, 0, None, None) == 0
+    torch.cuda.synchronize()

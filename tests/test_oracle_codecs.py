@@ -192,3 +192,26 @@ def test_q4k_subblocks_independent_given_header(orc):
     y1 = orc.dequantize(b1, Q4K, 256)
     assert np.array_equal(y0[96:128][perm], y1[96:128])
     assert np.array_equal(np.delete(y0, np.s_[96:128]), np.delete(y1, np.s_[96:128]))
+
+
+# ---------------------------------------------------------------- Q4K fit, several passes
+def _bits(v):
+    return int(np.array([v], dtype=np.float32).view(np.uint32)[0])
+
+
+@pytest.mark.parametrize("name", ["A", "B", "P", "Q"])
+def test_make_qkx1_quants_multipass_known_answers(orc, name):
+    """Inputs whose fit needs 3 to 5 passes, with rounding ties (A, P), a pass limit that
+    decides the result (B, Q) and sums whose order shows in the last bit (A); the per-pass
+    derivation is in q4k_known_answers.py."""
+    from q4k_known_answers import FITS
+    x, scale_bits, neg_min_bits = FITS[name]
+    s, m = orc.make_qkx1_quants(np.array(x, dtype=np.float32))
+    assert (_bits(s), _bits(m)) == (scale_bits, neg_min_bits)
+
+
+def test_q4k_block_from_multipass_subblocks(orc):
+    from q4k_known_answers import BLOCK_PQ_X, BLOCK_PQ_HEADER, BLOCK_PQ_QS
+    b = orc.quantize(np.array(BLOCK_PQ_X, dtype=np.float32), Q4K)
+    assert list(b[:16]) == BLOCK_PQ_HEADER
+    assert list(b[16:]) == BLOCK_PQ_QS
