@@ -664,10 +664,13 @@ int orc_attend_f64(const orc_cache *c, const float *q, int l, int num_heads, dou
   const int masked = causal;
   float *K = (float *)malloc((size_t)B * Hkv * (size_t)S * D * sizeof(float) + 4);
   float *V = (float *)malloc((size_t)B * Hkv * (size_t)S * D * sizeof(float) + 4);
-  double *s = (double *)malloc((size_t)S * sizeof(double) + 8);
   orc_cache_get_kv(c, K, V);
+#ifdef _OPENMP
+#pragma omp parallel for collapse(2) schedule(dynamic)
+#endif
   for (int b = 0; b < B; ++b)
     for (int h = 0; h < num_heads; ++h) {
+      double *s = (double *)malloc((size_t)S * sizeof(double) + 8);
       const float *Kh = K + ((size_t)b * Hkv + h / G) * (size_t)S * D;
       const float *Vh = V + ((size_t)b * Hkv + h / G) * (size_t)S * D;
       for (int i = 0; i < l; ++i) {
@@ -689,11 +692,13 @@ int orc_attend_f64(const orc_cache *c, const float *q, int l, int num_heads, dou
         }
         double *o = out + (((size_t)b * l + i) * num_heads + h) * D;
         for (int e = 0; e < D; ++e) o[e] = 0.0;
-        for (int64_t j = 0; j < S; ++j)
-          for (int e = 0; e < D; ++e) o[e] += s[j] / sum * (double)Vh[(size_t)j * D + e];
+        for (int64_t j = 0; j < S; ++j) {
+          const double p = s[j] / sum;
+          for (int e = 0; e < D; ++e) o[e] += p * (double)Vh[(size_t)j * D + e];
+        }
       }
+      free(s);
     }
-  free(s);
   free(K);
   free(V);
   return ORC_OK;

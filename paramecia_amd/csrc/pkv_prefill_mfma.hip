@@ -17,10 +17,15 @@
 //   QK: A[key][e] = nibble * scale code (an integer <= 945, exact in fp16),
 //       B[e][row] = q as fp16 hi and lo parts (two MFMAs into one accumulator),
 //       score = d * S1 - dmin * S2 with S2 = sum_j m_j * qsum_j.
-//   PV: B[key][e] = nibble * scale code * 2^e_d (exact fp16), A[row][key] =
+//   PV: B[key][e] = (nibble - 8) * scale code * 2^e_d (exact fp16), A[row][key] =
 //       p * mantissa(d) as fp16 hi and lo parts; the min term uses A' = p *
-//       mantissa(dmin) (hi and lo) against B'[key][j] = m_j * 2^e_dmin and is
-//       subtracted per (row, sub-block) at the end.
+//       mantissa(dmin) (hi and lo) against B'[key][j] = m_j * 2^e_dmin, minus A against
+//       B''[key][j] = 8 * scale code * 2^e_d, and is subtracted per (row, sub-block) at
+//       the end. Centring the nibbles keeps the running PV sums near the size of the
+//       output: with nibble * scale alone every value carries its sub-block's offset
+//       dmin * m (about 2.5 for N(0,1) rows against outputs near 0.01 at 16k keys), and
+//       the f32 rounding of a sum that long then grew with the keys of a split (row
+//       errors of 1e-4 of the row at 4k keys per split; about 5e-6 centred).
 #include "pkv_mfma_common.hpp"
 
 namespace pkv {
@@ -53,9 +58,10 @@ struct DqBlock {
   h4 ka2[2][64];    // S2 A: m codes of sub-blocks 2g, 2g+1
   h8 vb[16][64];    // PV B: [tile T2 = 8h + 2 byte + hl][lane]
   h8 vbm[64];       // min-term B: m_j * 2^e_dmin for columns j < 8
+  h8 vbc[64];       // centring B: -8 * sc_j * 2^e_d for columns j < 8
   float kd[kBlk], kdm[kBlk];    // K: d * sl2, dmin * sl2
   float vmd[kBlk], vmdm[kBlk];  // V: mantissas of d and dmin
-  _Float16 vsc[8][kBlk], vc[8][kBlk], vm[8][kBlk];  // V constants [j][key]
+  _Float16 vsc[8][kBlk], vc[8][kBlk], vm[8][kBlk], vcc[8][kBlk];  // V constants [j][key]
 };
 
 struct PfSmem {
@@ -127,9 +133,11 @@ __device__ __forceinline__ void dq_values(const Stage &st, DqBlock &D, const Mas
       const int j = 4 * h + 2 * jp + jj;
       uint32_t sc, m;
       scale_min(vh.y, vh.z, vh.w, j, sc, m);
+      // both nibble forms enter as fp16 1024 + 16 n: (1024 + 16 n) * scp / 16 - 72 scp
+      // = (n - 8) scp, exact (72 sc = 8 * 9 sc has at most 10 significant bits)
       const float scp = __builtin_ldexpf((float)sc, ed);
-      D.vsc[j][kk] = (_Float16)(jj ? scp * 0.0625f : scp);
-      D.vc[j][kk] = (_Float16)(jj ? -64.0f * scp : -1024.0f * scp);
+      D.vsc[j][kk] = (_Float16)(scp * 0.0625f);
+      D.vc[j][kk] = (_Float16)(-72.0f * scp);
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -158,7 +166,7 @@ __device__ __forceinline__ void dq_values(const Stage &st, DqBlock &D, const Mas
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
       const uint32_t x = __builtin_amdgcn_perm(vq[2 * pp + 1], vq[2 * pp], sel);
-      const h2 lo = pk_fma(as_h2(and_or(x, MK.lo, MK.magic)), h2{SL[2 * pp], SL[2 * pp + 1]},
+      const h2 lo = pk_fma(as_h2(and_or(x << 4, MK.hi, MK.magic)), h2{SL[2 * pp], SL[2 * pp + 1]},
                            h2{CL[2 * pp], CL[2 * pp + 1]});
       const h2 hi = pk_fma(as_h2(and_or(x, MK.hi, MK.magic)), h2{SH[2 * pp], SH[2 * pp + 1]},
                            h2{CH[2 * pp], CH[2 * pp + 1]});
@@ -188,6 +196,7 @@ __device__ __forceinline__ void dq_value_mins(const Stage &st, DqBlock &D, int l
       uint32_t sc, m;
       scale_min(vh.y, vh.z, vh.w, j, sc, m);
       D.vm[j][kk] = (_Float16)__builtin_ldexpf((float)m, em);
+      D.vcc[j][kk] = (_Float16)__builtin_ldexpf(-8.0f * (float)sc, ed);  // exact: |8 sc| <= 504
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -196,7 +205,9 @@ __device__ __forceinline__ void dq_value_mins(const Stage &st, DqBlock &D, int l
   const int n = lane & 15, g = lane >> 4;
   const h8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
   const h8 bm = *reinterpret_cast<const h8 *>(&D.vm[n & 7][8 * g]);
+  const h8 bc = *reinterpret_cast<const h8 *>(&D.vcc[n & 7][8 * g]);
   D.vbm[lane] = n < 8 ? bm : zero8;
+  D.vbc[lane] = n < 8 ? bc : zero8;
 }
 
 // The 6 loads of one tensor of one block: issued by one wave, so that its vmcnt counts
@@ -437,9 +448,11 @@ __global__ __launch_bounds__(kPfThreads) void q4k_prefill_kernel(PrefillArgs a) 
       acc[T2] = mfma32(A, B, acc[T2]);
       acc[T2] = mfma32(Al, B, acc[T2]);
     }
-    const h8 Bm = D.vbm[lane];
+    const h8 Bm = D.vbm[lane], Bc = D.vbc[lane];
     accm = mfma32(Am, Bm, accm);
     accm = mfma32(Aml, Bm, accm);
+    accm = mfma32(A, Bc, accm);
+    accm = mfma32(Al, Bc, accm);
   }
 
   // ---- epilogue: row sums, min-term subtraction, then output or partial

@@ -6,6 +6,8 @@ import sys
 import numpy as np
 import pytest
 
+from attn_checks import assert_attn_close
+
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
@@ -58,9 +60,9 @@ def run_decode(pk, orc, S, B=1, fused=True, seed=0, k_scale=None, chans=None):
     else:
         out = g.attend(dev(q), 1 / 16, S - 1, True)
         seq = S
-    ref = c.attend(q, 1 / 16, seq - 1, True, mode="f32")
+    ref = c.attend(q, 1 / 16, seq - 1, True, mode="f64")
     got = host(out)
-    np.testing.assert_allclose(got, ref, atol=ATOL, rtol=RTOL)
+    assert_attn_close(got, ref)
     gk, gv = g.raw_bytes()
     ok, ov = c.valid_bytes()
     assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
@@ -125,10 +127,10 @@ def test_decode_full_size_layer(pk, orc):
     ok, ov = c.valid_bytes()
     assert np.array_equal(gk, ok), "K bytes differ"
     assert np.array_equal(gv, ov), "V bytes differ"
-    ref = c.attend(qnp, W.SCALE, S, True, mode="f32")
+    ref = c.attend(qnp, W.SCALE, S, True, mode="f64")
     err = np.abs(out - ref)
     say(f"full-size layer: max|diff| = {err.max():.3e}")
-    np.testing.assert_allclose(out, ref, atol=ATOL, rtol=RTOL)
+    assert_attn_close(out, ref)
 
 
 def run_batched(pk, orc, lens, seed, chans=None):
@@ -160,8 +162,8 @@ def run_batched(pk, orc, lens, seed, chans=None):
     worst = 0.0
     for i, (g, c, S) in enumerate(zip(caches, oracles, lens)):
         assert c.append(kn[i][None, :, None], vn[i][None, :, None]) == 0
-        ref = c.attend(q[i][None, None], 1 / 16, S, True, mode="f32")[0, 0]
-        np.testing.assert_allclose(out[i], ref, atol=ATOL, rtol=RTOL)
+        ref = c.attend(q[i][None, None], 1 / 16, S, True, mode="f64")[0, 0]
+        assert_attn_close(out[i], ref)
         worst = max(worst, float(np.abs(out[i] - ref).max()))
         assert g.seq_len == S + 1
         gk, gv = g.raw_bytes()
@@ -219,9 +221,9 @@ def run_decode_q8(pk, orc, S, B=1, fused=True, seed=0, chans=None):
     else:
         out = g.attend(dev(q), 1 / 16, S - 1, True)
         seq = S
-    ref = c.attend(q, 1 / 16, seq - 1, True, mode="f32")
+    ref = c.attend(q, 1 / 16, seq - 1, True, mode="f64")
     got = host(out)
-    np.testing.assert_allclose(got, ref, atol=ATOL, rtol=RTOL)
+    assert_attn_close(got, ref)
     gk, gv = g.raw_bytes()
     ok, ov = c.valid_bytes()
     assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
@@ -268,8 +270,8 @@ def test_q8_batched_varlen(pk, orc):
     out = host(pk.append_attend_batched(caches, dev(kn), dev(vn), dev(q), 1 / 16))
     for i, (g, c, S) in enumerate(zip(caches, oracles, lens)):
         assert c.append(kn[i][None, :, None], vn[i][None, :, None]) == 0
-        ref = c.attend(q[i][None, None], 1 / 16, S, True, mode="f32")[0, 0]
-        np.testing.assert_allclose(out[i], ref, atol=ATOL, rtol=RTOL)
+        ref = c.attend(q[i][None, None], 1 / 16, S, True, mode="f64")[0, 0]
+        assert_attn_close(out[i], ref)
         gk, gv = g.raw_bytes()
         ok, ov = c.valid_bytes()
         assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)

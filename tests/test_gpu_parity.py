@@ -6,6 +6,8 @@ import sys
 import numpy as np
 import pytest
 
+from attn_checks import assert_attn_close
+
 torch = pytest.importorskip("torch")
 
 pytestmark = pytest.mark.gpu
@@ -144,14 +146,14 @@ def _attend_case(pk, orc, quant, B, H, Hkv, D, S, L, causal, seed, amp=1.0, fuse
         vn = rng.standard_normal((B, Hkv, 1, D)).astype(np.float32)
         out = g.append_attend(dev(kn), dev(vn), dev(q), scale)
         assert c.append(kn, vn) == 0
-        ref = c.attend(q, scale, S, True, mode="f32")
+        ref = c.attend(q, scale, S, True, mode="f64")
         gk, _ = g.raw_bytes()
         assert np.array_equal(host(gk), c.valid_bytes()[0])
     else:
         out = g.attend(dev(q), scale, S - L, causal)
-        ref = c.attend(q, scale, S - L, causal, mode="f32")
+        ref = c.attend(q, scale, S - L, causal, mode="f64")
     got = host(out)
-    np.testing.assert_allclose(got, ref, atol=ATOL, rtol=RTOL)
+    assert_attn_close(got, ref)
     return got, ref
 
 
@@ -308,7 +310,7 @@ def test_batched_decode_matches_per_sequence(pk, orc):
     out = host(pk.append_attend_batched(caches, dev(kn), dev(vn), dev(q), 1 / 16))
     for i, (g, c) in enumerate(zip(caches, oracles)):
         c.append(kn[i][None, :, None], vn[i][None, :, None])
-        ref = c.attend(q[i][None, None], 1 / 16, lens[i], True, mode="f32")[0, 0]
-        np.testing.assert_allclose(out[i], ref, atol=ATOL, rtol=RTOL)
+        ref = c.attend(q[i][None, None], 1 / 16, lens[i], True, mode="f64")[0, 0]
+        assert_attn_close(out[i], ref)
         assert g.seq_len == lens[i] + 1
         assert np.array_equal(host(g.raw_bytes()[0]), c.valid_bytes()[0])

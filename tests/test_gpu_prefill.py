@@ -9,6 +9,8 @@ import sys
 import numpy as np
 import pytest
 
+from attn_checks import assert_attn_close
+
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
@@ -56,9 +58,9 @@ def run_prefill(pk, orc, S, L, B=1, causal=True, seed=0, chans=None):
     g.append_quantized(dev(k[:, :, S:]), dev(v[:, :, S:]), offset=S)
     assert c.append(k, v) == 0
     out = g.attend(dev(q), 1 / 16, S, causal)
-    ref = c.attend(q, 1 / 16, S, causal, mode="f32")
+    ref = c.attend(q, 1 / 16, S, causal, mode="f64")
     got = host(out)
-    np.testing.assert_allclose(got, ref, atol=ATOL, rtol=RTOL)
+    assert_attn_close(got, ref)
     gk, gv = g.raw_bytes()
     ok, ov = c.valid_bytes()
     assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
@@ -131,7 +133,7 @@ def test_prefill_full_chunk(pk, orc):
     ok, ov = c.valid_bytes()
     assert np.array_equal(gk, ok), "K bytes differ"
     assert np.array_equal(gv, ov), "V bytes differ"
-    ref = c.attend(qcn, W.SCALE, S, True, mode="f32")
+    ref = c.attend(qcn, W.SCALE, S, True, mode="f64")
     err = np.abs(out - ref)
     say(f"full prefill chunk: max|diff| = {err.max():.3e}")
-    np.testing.assert_allclose(out, ref, atol=ATOL, rtol=RTOL)
+    assert_attn_close(out, ref)
