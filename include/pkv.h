@@ -128,6 +128,21 @@ int pkv_flash_attn(int quant, const float *q, const void *k_bytes, const void *v
                    int num_kv_heads, int head_dim, int seq_q, int64_t seq_k,
                    int64_t q_offset, int causal, float *out, pkv_stream stream);
 
+/* pkv_flash_attn for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). It has no counterpart
+ * in the reference. Same arguments, kernels and results as pkv_flash_attn, but the
+ * split-K partials go to a library-owned static device array of
+ * PKV_NOALLOC_SCRATCH_BYTES on the current device (each GPU holds its own copy until the
+ * process ends) instead of an allocated workspace: the call allocates nothing, and a
+ * call whose work plan needs more scratch returns PKV_ERR_ARG before it enqueues
+ * anything. `stream` must belong to the current device. Every call on one GPU shares that
+ * GPU's array: calls that overlap in time on one GPU (other streams, other threads) race. */
+#define PKV_NOALLOC_SCRATCH_BYTES (16u << 20)
+int pkv_flash_attn_noalloc(int quant, const float *q, const void *k_bytes, const void *v_bytes,
+                           const int64_t kv_strides[3], float scale, int batch, int num_heads,
+                           int num_kv_heads, int head_dim, int seq_q, int64_t seq_k,
+                           int64_t q_offset, int causal, float *out, pkv_stream stream);
+
 /* Batched decode over independent sequences (serving loop): caches[i] is a batch-1
  * cache; appends one token to each (k, v: [n, n_kv_heads, head_dim]) then attends
  * (q, out: [n, num_heads, head_dim]). All caches share geometry. For the Qwen3-Next

@@ -23,7 +23,7 @@ SYMBOLS = (
     "pkv_quant_block_size", "pkv_quant_is_ggml", "pkv_bytes_per_row", "pkv_create",
     "pkv_destroy", "pkv_set_stream", "pkv_len", "pkv_capacity", "pkv_geometry",
     "pkv_truncate", "pkv_set_len", "pkv_clear", "pkv_resize_batch", "pkv_append", "pkv_attend",
-    "pkv_append_attend", "pkv_get_kv", "pkv_kv_storage", "pkv_flash_attn",
+    "pkv_append_attend", "pkv_get_kv", "pkv_kv_storage", "pkv_flash_attn", "pkv_flash_attn_noalloc",
     "pkv_append_attend_batched", "pkv_prefix_create", "pkv_prefix_free", "pkv_prefix_tokens",
     "pkv_prefix_num_layers", "pkv_prefix_entry_kind", "pkv_prefix_save_full",
     "pkv_prefix_save_linear", "pkv_prefix_linear_sizes", "pkv_prefix_full_len",
@@ -108,6 +108,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "pkv_kv_storage": ([vp, P(vp), P(vp), P(c_sz), P(c_i64)], c_int),
         "pkv_flash_attn": ([c_int, vp, vp, vp, P(c_i64), fl, c_int, c_int, c_int, c_int, c_int,
                             c_i64, c_i64, c_int, vp, vp], c_int),
+        "pkv_flash_attn_noalloc": ([c_int, vp, vp, vp, P(c_i64), fl, c_int, c_int, c_int, c_int,
+                                    c_int, c_i64, c_i64, c_int, vp, vp], c_int),
         "pkv_append_attend_batched": ([P(vp), c_int, vp, vp, vp, c_int, fl, vp, vp], c_int),
         "pkv_prefix_create": ([P(ctypes.c_uint32), c_sz, c_int, P(vp)], c_int),
         "pkv_prefix_free": ([vp], c_int),

@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -27,6 +28,10 @@ int hip_error(hipError_t e, const char *what) {
 
 int Workspace::reserve(size_t need) {
   if (need <= bytes) return PKV_OK;
+  if (fixed)
+    return set_error(PKV_ERR_ARG, "the call needs " + std::to_string(need) +
+                                      " bytes of scratch; the no-alloc scratch holds " +
+                                      std::to_string(bytes));
   size_t grow = need + need / 4 + 4096;
   if (ptr) {
     // A kernel may still read the old buffer; growth is rare, so wait for the device.
@@ -41,6 +46,7 @@ int Workspace::reserve(size_t need) {
 }
 
 int Workspace::reserve_host(size_t need) {
+  if (fixed) return set_error(PKV_ERR_ARG, "no host staging in a no-alloc call");
   if (host_pending) {
     PKV_HIP(hipEventSynchronize(host_ev));
     host_pending = false;
@@ -62,6 +68,7 @@ int Workspace::mark_host_used(hipStream_t s) {
 }
 
 Workspace::~Workspace() {
+  if (fixed) return;
   if (host_pending) (void)hipEventSynchronize(host_ev);
   if (ptr) {
     (void)hipDeviceSynchronize();
@@ -77,6 +84,31 @@ static Workspace &util_workspace() {
 }
 
 static int norm_quant(int q) { return q == PKV_QUANT_NONE ? PKV_QUANT_F16 : q; }
+
+// ---- scratch of the no-alloc entry point (pkv_flash_attn_noalloc). Each GPU the library
+// runs on holds its own copy of this array until the process ends. In host code its name
+// only stands for the symbol: kernels get the device address that hipGetSymbolAddress
+// returns for the current device, looked up once per device and kept.
+static __device__ __align__(256) unsigned char scratch[PKV_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+static void *g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+static int noalloc_scratch(void **out) {
+  int dev = -1;
+  PKV_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(PKV_ERR_ARG, "device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_error(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return set_error(PKV_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PKV_OK;
+}
 
 }  // namespace pkv
 
@@ -367,10 +399,11 @@ int pkv_kv_storage(const pkv_cache *h, const void **k_bytes, const void **v_byte
   return PKV_OK;
 }
 
-int pkv_flash_attn(int quant, const float *q, const void *k_bytes, const void *v_bytes,
-                   const int64_t kv_strides[3], float scale, int batch, int num_heads,
-                   int num_kv_heads, int head_dim, int seq_q, int64_t seq_k, int64_t q_offset,
-                   int causal, float *out, pkv_stream stream) {
+static int flash_attn_ws(int quant, const float *q, const void *k_bytes, const void *v_bytes,
+                         const int64_t kv_strides[3], float scale, int batch, int num_heads,
+                         int num_kv_heads, int head_dim, int seq_q, int64_t seq_k,
+                         int64_t q_offset, int causal, float *out, pkv_stream stream,
+                         Workspace *ws) {
   quant = norm_quant(quant);
   if (!q || !k_bytes || !v_bytes || !kv_strides || !out)
     return set_error(PKV_ERR_ARG, "null argument");
@@ -392,7 +425,29 @@ int pkv_flash_attn(int quant, const float *q, const void *k_bytes, const void *v
   a.q_offset = q_offset;
   a.causal = causal;
   a.out = out;
-  return launch_attend(a, util_workspace(), static_cast<hipStream_t>(stream));
+  return launch_attend(a, ws ? *ws : util_workspace(), static_cast<hipStream_t>(stream));
+}
+
+int pkv_flash_attn(int quant, const float *q, const void *k_bytes, const void *v_bytes,
+                   const int64_t kv_strides[3], float scale, int batch, int num_heads,
+                   int num_kv_heads, int head_dim, int seq_q, int64_t seq_k, int64_t q_offset,
+                   int causal, float *out, pkv_stream stream) {
+  return flash_attn_ws(quant, q, k_bytes, v_bytes, kv_strides, scale, batch, num_heads,
+                       num_kv_heads, head_dim, seq_q, seq_k, q_offset, causal, out, stream,
+                       nullptr);
+}
+
+int pkv_flash_attn_noalloc(int quant, const float *q, const void *k_bytes, const void *v_bytes,
+                           const int64_t kv_strides[3], float scale, int batch, int num_heads,
+                           int num_kv_heads, int head_dim, int seq_q, int64_t seq_k,
+                           int64_t q_offset, int causal, float *out, pkv_stream stream) {
+  Workspace ws;
+  ws.fixed = true;
+  int rc = noalloc_scratch(&ws.ptr);
+  if (rc) return rc;
+  ws.bytes = PKV_NOALLOC_SCRATCH_BYTES;
+  return flash_attn_ws(quant, q, k_bytes, v_bytes, kv_strides, scale, batch, num_heads,
+                       num_kv_heads, head_dim, seq_q, seq_k, q_offset, causal, out, stream, &ws);
 }
 
 // ---- q/k preparation (FullAttention::forward, qwen3_next.rs:2369-2399) ----

@@ -46,9 +46,12 @@ struct RowStrides {
 // Split-K scratch owned by a cache handle or by a stateless call.
 // Device scratch grows (hipMalloc) on demand, never inside a kernel. The pinned host
 // buffer stages small descriptor tables; an event guards its reuse.
+// A fixed workspace (fixed = true) wraps caller-provided device memory: reserve() never
+// allocates and refuses a need beyond `bytes` (PKV_ERR_ARG); nothing is freed.
 struct Workspace {
   void *ptr = nullptr;
   size_t bytes = 0;
+  bool fixed = false;
   void *host = nullptr;
   size_t host_bytes = 0;
   hipEvent_t host_ev = nullptr;
