@@ -64,6 +64,11 @@ enum { PKV_RESTORE_BYTES = 0, PKV_RESTORE_REQUANTIZE = 1 };
 
 const char *pkv_last_error(void);
 const char *pkv_version(void);
+/* Waits for the current device, then reports and clears the errors its kernels flagged
+ * instead of hanging: PKV_ERR_HIP if a fused decode step's bounded barrier gave up (the
+ * step's appended row and output are then invalid), PKV_OK otherwise. No reference
+ * counterpart (the reference's CPU path cannot hang a barrier). */
+int pkv_device_status(void);
 
 /* ---- KvCacheQuantization helpers (qn:107-166) ---- */
 /* from_str: f16|fp16, bf16|bfloat16, q8|q8_0, q4|q4k|q4_k, none (case-insensitive). */

@@ -19,7 +19,7 @@ RESTORE_BYTES, RESTORE_REQUANTIZE = 0, 1
 
 # Every exported symbol of include/pkv.h (checked by tests/test_abi.py).
 SYMBOLS = (
-    "pkv_last_error", "pkv_version", "pkv_quant_parse", "pkv_quant_default",
+    "pkv_last_error", "pkv_version", "pkv_device_status", "pkv_quant_parse", "pkv_quant_default",
     "pkv_quant_block_size", "pkv_quant_is_ggml", "pkv_bytes_per_row", "pkv_create",
     "pkv_destroy", "pkv_set_stream", "pkv_len", "pkv_capacity", "pkv_geometry",
     "pkv_truncate", "pkv_set_len", "pkv_clear", "pkv_resize_batch", "pkv_append", "pkv_attend",
@@ -86,6 +86,7 @@ def _declare(L: ctypes.CDLL) -> None:
     sig = {
         "pkv_last_error": ([], ctypes.c_char_p),
         "pkv_version": ([], ctypes.c_char_p),
+        "pkv_device_status": ([], c_int),
         "pkv_quant_parse": ([ctypes.c_char_p, P(c_int)], c_int),
         "pkv_quant_default": ([], c_int),
         "pkv_quant_block_size": ([c_int], c_int),

@@ -110,6 +110,24 @@ static int noalloc_scratch(void **out) {
   return PKV_OK;
 }
 
+static __device__ __align__(256) unsigned status_word;
+static unsigned *g_status_ptr[kMaxDevices];
+
+int device_status_word(unsigned **out) {
+  int dev = -1;
+  PKV_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(PKV_ERR_ARG, "device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_status_ptr[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(status_word));
+    if (e != hipSuccess) return hip_error(e, "hipGetSymbolAddress(status_word)");
+    g_status_ptr[dev] = static_cast<unsigned *>(p);
+  }
+  *out = g_status_ptr[dev];
+  return PKV_OK;
+}
+
 }  // namespace pkv
 
 using namespace pkv;
@@ -154,6 +172,22 @@ struct pkv_prefix {
 extern "C" {
 
 const char *pkv_last_error(void) { return g_error.c_str(); }
+
+int pkv_device_status(void) {
+  unsigned *w = nullptr;
+  int rc = device_status_word(&w);
+  if (rc) return rc;
+  PKV_HIP(hipDeviceSynchronize());
+  unsigned v = 0;
+  PKV_HIP(hipMemcpy(&v, w, sizeof v, hipMemcpyDeviceToHost));
+  if (v == 0) return PKV_OK;
+  const unsigned zero = 0;
+  PKV_HIP(hipMemcpy(w, &zero, sizeof zero, hipMemcpyHostToDevice));
+  return set_error(PKV_ERR_HIP, (v & kStatusBarrierTimeout)
+                                    ? "a fused decode step's quantizer barrier timed out: its "
+                                      "appended row and attention output are not valid"
+                                    : "device status " + std::to_string(v));
+}
 const char *pkv_version(void) { return "paramecia_amd pkv 0.1 (gfx950)"; }
 
 int pkv_quant_parse(const char *s, int *quant_out) {

@@ -38,6 +38,12 @@ inline size_t row_bytes(int quant, int head_dim) {
   }
 }
 
+// Device status word of the current device (a static __device__ word, one per GPU): kernels
+// that give up a bounded wait set a bit with an atomic OR; pkv_device_status() reads and
+// clears it.
+constexpr unsigned kStatusBarrierTimeout = 1u;  // the fused quantizer's barrier of waves 0-3
+int device_status_word(unsigned **out);
+
 // Byte addressing of packed rows: row(b, t, h) = base + b*sb + t*st + h*sh.
 struct RowStrides {
   int64_t b, t, h;

@@ -40,18 +40,23 @@ __device__ __forceinline__ float ror8(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x128,
                                                             0xF, 0xF, false));
 }
-// fp16(a - c) into the low (mix_sub_lo) or high (mix_sub_hi, low half of d kept) half
-// of a dword: v_fma_mix computes a * 1.0 - c in f32 (exact for c = fp16(a) or 0) and
-// rounds once to fp16; c is the low / high fp16 half of cw.
-__device__ __forceinline__ uint32_t mix_sub_lo(float a, uint32_t cw) {
+// {fp16(a0 - c0), fp16(a1 - c1)} with c0, c1 the fp16 halves of cw: v_fma_mix computes
+// a * 1.0 - c in f32 (exact for c = fp16(a) or 0) and rounds once to fp16. The words feed
+// MFMA operands. The compiler inserts the wait states between a VALU write and an MFMA read
+// only for instructions it can see, so the asm ends with its own (s_nop 4: five wait
+// states, more than a VALU write needs before an MFMA reads the register); its inputs are
+// VALU results, never MFMA results. Written in C instead, the compiler fused the caller's
+// product into a v_fma_mix with two f32 multiplicands, which lost about ten bits of the
+// hi + lo pair; and an inline-asm v_fma_mix that read an MFMA result three instructions
+// after the MFMA returned the previous partial sum, which is why asm here takes no MFMA
+// results.
+__device__ __forceinline__ uint32_t fp16_sub2(float a0, float a1, uint32_t cw) {
   uint32_t d;
-  asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]" : "=v"(d) : "v"(a), "v"(cw));
-  return d;
-}
-__device__ __forceinline__ uint32_t mix_sub_hi(uint32_t d, float a, uint32_t cw) {
-  asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
-      : "+v"(d)
-      : "v"(a), "v"(cw));
+  asm("v_fma_mixlo_f16 %0, %1, 1.0, -%3 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %0, %2, 1.0, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "s_nop 4"
+      : "=&v"(d)
+      : "v"(a0), "v"(a1), "v"(cw));
   return d;
 }
 __device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) {
@@ -153,6 +158,7 @@ __device__ __forceinline__ void issue_stage(Stage *st, const LoadPlan &P, u4s rk
                  o3 = P.nib[3] + boff, h0 = P.hdr[0] + boff, h1 = P.hdr[1] + boff;
   uint32_t saved;
   asm volatile(
+      "s_nop 4\n\t"  // VALU-written SGPRs (v_readfirstlane) read by VMEM: 5 wait states
       "s_mov_b32 %[sv], m0\n\t"
       "s_mov_b32 m0, %[kn]\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o0], %[rk], 0 offen lds\n\t"
@@ -207,6 +213,7 @@ __device__ __forceinline__ void issue_stage_at(uint32_t base, const LoadPlan &P,
   static_assert(sizeof(TensorStage) == 0x1200 && sizeof(Stage) == 0x2400, "stage layout");
   uint32_t saved;
   asm volatile(
+      "s_nop 4\n\t"  // VALU-written SGPRs (v_readfirstlane) read by VMEM: 5 wait states
       "s_mov_b32 %[sv], m0\n\t"
       "s_mov_b32 m0, %[b]\n\ts_nop 0\n\t"
       "buffer_load_dword %[h0], %[rk], 0 offen lds\n\t"

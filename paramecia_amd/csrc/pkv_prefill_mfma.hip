@@ -218,6 +218,7 @@ __device__ __forceinline__ void issue_tensor(TensorStage *ts, const LoadPlan &P,
   const uint32_t h0 = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)&ts->hdr[0]));
   uint32_t saved;
   asm volatile(
+      "s_nop 4\n\t"  // VALU-written SGPRs (v_readfirstlane) read by VMEM: 5 wait states
       "s_mov_b32 %[sv], m0\n\t"
       "s_mov_b32 m0, %[n0]\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o0], %[rs], 0 offen lds\n\t"
@@ -434,9 +435,9 @@ __global__ __launch_bounds__(kPfThreads) void q4k_prefill_kernel(PrefillArgs a) 
       const float y0 = p[2 * k2] * D.vmdm[8 * g + 2 * k2];
       const float y1 = p[2 * k2 + 1] * D.vmdm[8 * g + 2 * k2 + 1];
       wa[k2] = as_u(h2{(_Float16)x0, (_Float16)x1});
-      wl[k2] = mix_sub_hi(mix_sub_lo(x0, wa[k2]), x1, wa[k2]);
+      wl[k2] = fp16_sub2(x0, x1, wa[k2]);
       wm[k2] = as_u(h2{(_Float16)y0, (_Float16)y1});
-      wml[k2] = mix_sub_hi(mix_sub_lo(y0, wm[k2]), y1, wm[k2]);
+      wml[k2] = fp16_sub2(y0, y1, wm[k2]);
     }
     const h8 A = __builtin_bit_cast(h8, u4{wa[0], wa[1], wa[2], wa[3]});
     const h8 Al = __builtin_bit_cast(h8, u4{wl[0], wl[1], wl[2], wl[3]});

@@ -57,6 +57,7 @@ struct DecodeArgs {
   // each segment's new position); used by the kPrep instantiation only
   DecodePrep prep;
   float *q_out;  // [nseg][16][256] prepared q, for the combine
+  unsigned *status;  // the device status word (pkv_device_status)
 };
 
 // Per-wave tables rebuilt for every 32-key block.
@@ -111,6 +112,7 @@ __device__ __forceinline__ void issue_q(void *dst_lds, u4s rq, uint32_t lane16) 
   const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)dst_lds));
   uint32_t saved;
   asm volatile(
+      "s_nop 4\n\t"  // VALU-written SGPRs (v_readfirstlane) read by VMEM: 5 wait states
       "s_mov_b32 %[sv], m0\n\t"
       "s_mov_b32 m0, %[d]\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o0], %[rq], 0 offen lds\n\t"
@@ -184,14 +186,16 @@ __device__ __forceinline__ uint32_t kcode_pair(uint32_t sx, uint32_t s2, uint32_
   return and_or(P >> sh, ks.lo, and_or(P >> 10, ks.up, magic));
 }
 
-// K words of a staged block, read together at the start of the block so that their
-// latencies overlap instead of each one stalling its phase. The V words are read later,
-// in phase P: the stage's V rows are its last loads, and LDS reads issued right after
-// the vmcnt wait have been seen to return stale bytes for them, while reads a phase
-// later have not.
+// Header and K words of a staged block, read together right after the stage's vmcnt
+// wait so that their LDS latencies overlap instead of each one stalling its phase. The
+// wait covers every word of the stage: on gfx950 a buffer_load ... lds counts in vmcnt
+// until its data is in LDS, and the only vector-memory instructions between a stage's
+// issue and its wait are the next stage's 12 loads (checked word by word against
+// global memory in both the immediate and the pipelined pattern).
 struct BlockWords {
   u4 khd[2], kq0[2], kq1[2];  // phase Q: header and nibble pieces of key kk(r) per tile
   uint32_t hx[8];             // phase S: {d, dmin} of keys 8g..8g+7
+  u4 vhd;                     // phase P: V header of key lane % 32
 };
 __device__ __forceinline__ void load_block_words(const Stage &st, int lane, BlockWords &W) {
   const int r = lane & 15, g = lane >> 4;
@@ -206,6 +210,7 @@ __device__ __forceinline__ void load_block_words(const Stage &st, int lane, Bloc
   const uint32_t *hdr32 = reinterpret_cast<const uint32_t *>(st.k.hdr);
 #pragma unroll
   for (int k = 0; k < 8; ++k) W.hx[k] = hdr32[4 * (8 * g + k)];
+  W.vhd = st.v.hdr[lane & 31];
 }
 
 // Phase Q: K rows of a staged block -> raw QK sums.
@@ -254,14 +259,14 @@ __device__ __forceinline__ void phase_q(const BlockWords &W, const h8 *qb, h4 q2
   }
 }
 
-// d * s1 - dmin * s2 with the fp16 pair {d, dmin} of a header dword: two v_fma_mix
+// d * s1 - dmin * s2 with the fp16 pair {d, dmin} of a header dword (one rounded product,
+// then one fma). s1 and s2 are MFMA results: written in C, so that the compiler places the
+// wait states an MFMA result needs before a VALU reads it (it cannot for inline asm).
 __device__ __forceinline__ float hdr_dot(uint32_t hx, float s1, float s2) {
-  float t, r;
-  asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(t) : "v"(hx), "v"(s1));
-  asm("v_fma_mix_f32 %0, -%1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-      : "=v"(r)
-      : "v"(hx), "v"(s2), "v"(t));
-  return r;
+#pragma clang fp contract(off)
+  const h2 dd = as_h2(hx);
+  const float t = (float)dd[0] * s1;
+  return __builtin_fmaf(-(float)dd[1], s2, t);
 }
 
 // Phase S: scores (log2 units) and the online softmax; p[k] for key 8g + k, head n % 8.
@@ -341,7 +346,7 @@ __device__ __forceinline__ void phase_p(const Stage &st, const BlockWords &W, Wa
   // e_d in [-20, 0]; the offsets are -1024 times those.
   {
     const int kk = lane & 31, u = lane >> 5;
-    const u4 vh = st.v.hdr[kk];
+    const u4 vh = W.vhd;
     int ed, em;
     float md, mm;
     split_scale(h2f(vh.x & 0xFFFF), ed, md);
@@ -402,8 +407,8 @@ __device__ __forceinline__ void phase_p(const Stage &st, const BlockWords &W, Wa
     const float y0 = p[2 * kp] * T.vmdm[8 * g + 2 * kp], y1 = p[2 * kp + 1] * T.vmdm[8 * g + 2 * kp + 1];
     const uint32_t cx = as_u(h2{(_Float16)x0, (_Float16)x1}) & lo_mask;
     const uint32_t cy = as_u(h2{(_Float16)y0, (_Float16)y1}) & lo_mask;
-    aw[kp] = mix_sub_hi(mix_sub_lo(x0, cx), x1, cx);
-    amw[kp] = mix_sub_hi(mix_sub_lo(y0, cy), y1, cy);
+    aw[kp] = fp16_sub2(x0, x1, cx);
+    amw[kp] = fp16_sub2(y0, y1, cy);
   }
   const h8 A = __builtin_bit_cast(h8, u4{aw[0], aw[1], aw[2], aw[3]});
   const h8 Am = __builtin_bit_cast(h8, u4{amw[0], amw[1], amw[2], amw[3]});
@@ -442,20 +447,28 @@ __device__ __forceinline__ void phase_p(const Stage &st, const BlockWords &W, Wa
 
 // Barrier of waves 0-3 only (the quantizing waves), through an LDS arrival counter, so
 // that waves 4-7 need not wait for the quantization. Every waiting wave is in this
-// workgroup, hence resident; the bound on the wait is only a safeguard.
+// workgroup, hence resident, and reaches each barrier; the bound on the wait (about
+// 0.1 s) only keeps a fault from hanging the GPU: a wave that gives up sets
+// kStatusBarrierTimeout in the device status word, which pkv_device_status() reports.
 struct QuantWavesBarrier {
   uint32_t *arrivals;
   uint32_t target;
+  unsigned *status;
   __device__ __forceinline__ void operator()() {
     target += 4;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if ((threadIdx.x & 63) == 0)
       __hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    bool done = false;
     for (int spin = 0; spin < (1 << 22); ++spin) {
-      if (__hip_atomic_load(arrivals, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target)
+      if (__hip_atomic_load(arrivals, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) {
+        done = true;
         break;
+      }
       __builtin_amdgcn_s_sleep(1);
     }
+    if (!done && (threadIdx.x & 63) == 0)
+      __hip_atomic_fetch_or(status, kStatusBarrierTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   }
 };
@@ -471,6 +484,7 @@ __device__ __forceinline__ void issue_prep_consts(void *alpha_lds, void *tail_ld
   const uint32_t dt = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)((PKV_LDS void *)tail_lds));
   uint32_t saved;
   asm volatile(
+      "s_nop 4\n\t"  // VALU-written SGPRs (v_readfirstlane) read by VMEM: 5 wait states
       "s_mov_b32 %[sv], m0\n\t"
       "s_mov_b32 m0, %[da]\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %[o16], %[ra], 0 offen lds\n\t"
@@ -613,7 +627,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
         const float a0 = v8[perm[2 * pp]], a1 = v8[perm[2 * pp + 1]];
         const h2 h = {(_Float16)a0, (_Float16)a1};
         const uint32_t c = as_u(h) & lo_mask;
-        w[pp] = mix_sub_hi(mix_sub_lo(a0, c), a1, c);
+        w[pp] = fp16_sub2(a0, a1, c);
       }
       qb[st] = __builtin_bit_cast(h8, u4{w[0], w[1], w[2], w[3]});
     };
@@ -706,7 +720,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
     // the quantization delays this workgroup's blocks: it outranks the block loops of
     // the waves sharing its SIMDs
     __builtin_amdgcn_s_setprio(3);
-    QuantWavesBarrier bar{&sm.run.t.quant.arrivals, 0u};
+    QuantWavesBarrier bar{&sm.run.t.quant.arrivals, 0u, a.status};
     for (int row = wg; row < 4 * a.nseg; row += a.nwg) {
       const int rs = row >> 2, p = (row >> 1) & 1, kvr = row & 1;
       if (row != wg) xq = (p ? a.v_new : a.k_new)[((int64_t)rs * 2 + kvr) * 256 + tid];
@@ -939,6 +953,8 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
   d.dq = d.part + part_floats;
   d.q_out = d.dq + (size_t)n * 4 * 256;
   d.prep = kPrep ? *prep : DecodePrep{};
+  rc = device_status_word(&d.status);
+  if (rc) return rc;
   hipLaunchKernelGGL(q4k_decode_kernel<kPrep>, dim3((unsigned)wg), dim3(kThreads), 0, s, d);
   PKV_HIP(hipGetLastError());
   c.part = d.part;

@@ -66,6 +66,7 @@ def run_decode(pk, orc, S, B=1, fused=True, seed=0, k_scale=None, chans=None):
     gk, gv = g.raw_bytes()
     ok, ov = c.valid_bytes()
     assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
+    assert pk.lib().pkv_device_status() == 0, pk.lib().pkv_last_error()
     return np.abs(got - ref).max()
 
 
@@ -169,6 +170,7 @@ def run_batched(pk, orc, lens, seed, chans=None):
         gk, gv = g.raw_bytes()
         ok, ov = c.valid_bytes()
         assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
+    assert pk.lib().pkv_device_status() == 0, pk.lib().pkv_last_error()
     return worst
 
 
