@@ -3,10 +3,10 @@
 // segment and adds the appended key of a fused decode step. Include-only; every
 // symbol has internal linkage.
 //
-// Partial layout: part[wg][16 heads][kPartRow]: entries 0-255 the un-normalised output in
-// tile order (entry 16 T + n holds element tile_e(T, n)), then the running max m (log2
-// units) and the sum l of 2^(score - m). Rows are padded to 288 floats (1152 bytes, a
-// multiple of 128) so that the combine's 32-entry slices each fill one 128-byte line.
+// Partial layout: part[wg][16 heads][256]: the un-normalised output in tile order (entry
+// 16 T + n holds element tile_e(T, n)); ml[wg][16 heads]: the running max m (log2 units)
+// and the sum l of 2^(score - m). A row is 1 KB, so the combine's 32-entry slices each
+// fill one 128-byte line, and a head's (m, l) pairs of all partials are contiguous.
 #pragma once
 #include <type_traits>
 
@@ -16,7 +16,7 @@ namespace pkv {
 namespace {
 
 constexpr float kSplitClampL2 = 100.0f * 1.4426950408889634f;  // +-100 nats in log2 units
-constexpr int kPartRow = 288;  // floats per partial row: 256 entries, m, l, pad
+constexpr int kPartRow = 256;  // floats per partial row
 
 // e (0..255) of tile-order entry 16 T + n
 __device__ __forceinline__ int tile_e(int T, int n) {
@@ -46,13 +46,6 @@ struct DecodeSegIn {
   uint8_t *k, *v;
   int64_t seq_k;  // keys after the append (fused) or in the cache
 };
-// out[b][h][e] = (sum_w o_w 2^(m_w - M) + [new key]) / (sum_w l_w 2^(m_w - M) + [new key]).
-// One workgroup per (head, 32-entry slice of the tile-order row, batch): thread (ps, g4)
-// reads a float4 of entries and the (m, l) pair of every partial in slice ps of the
-// partials, all loads of a round issued before any is used. Slices keep their own
-// running max and merge through LDS. For a fused decode step the appended key enters
-// here, from its exactly dequantized K and V rows: score = clamp(q . k_new * scale),
-// weight 2^(score - M).
 // Sum over the 64 lanes of a wave, every lane getting it: DPP moves within rows of 16,
 // then v_permlane16_swap and v_permlane32_swap across them (no LDS round trips).
 __device__ __forceinline__ float wave_sum(float x) {
@@ -81,10 +74,19 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// out[b][h][e] = (sum_w o_w 2^(m_w - M) + [new key]) / (sum_w l_w 2^(m_w - M) + [new key]).
+// One workgroup per (head, 32-entry slice of the tile-order row, batch): thread (ps, g4)
+// reads a float4 of entries and the (m, l) pair of every partial in slice ps of the
+// partials. Every load of the first round goes out before the new key's q and dq and
+// before any is used, so the kernel waits for memory once. Slices keep their own running
+// max and merge through LDS. For a fused decode step the appended key enters here, from
+// its exactly dequantized K and V rows: score = clamp(q . k_new * scale), weight
+// 2^(score - M).
 constexpr int kCombSlices = 32;  // partial slices (8 threads each)
 constexpr int kCombChunk = 8;    // partials per slice per round
 struct CombineArgs {
   const float *part;      // [wg][16][kPartRow]
+  const float2 *ml;       // [wg][16] (m, l)
   const float *q, *dq;    // [nseg][16][256], [nseg][4][256] or null
   float *out;             // [nseg][16][256]
   float sl2;
@@ -96,29 +98,35 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs c) {
   __shared__ float4 accs[kCombSlices][8];
   const int h = blockIdx.x >> 3, i0 = 32 * (blockIdx.x & 7), b = blockIdx.y;
   const int tid = threadIdx.x, ps = tid >> 3, g4 = tid & 7;
-  const float *q = c.q, *dq = c.dq;
+  const float *dq = c.dq;
   const float sl2 = c.sl2;
-  float *out = c.out;
-  const int nwg = c.wg0[b + 1] - c.wg0[b];
-  const float *P = c.part + (int64_t)c.wg0[b] * 16 * kPartRow + h * kPartRow;
-  // new key: q . k_new products (reduced below, after the partial loads are issued)
-  const float prod = dq != nullptr ? q[((int64_t)b * 16 + h) * 256 + tid] *
-                                         dq[((int64_t)b * 4 + (h >> 3)) * 256 + tid]
-                                   : 0.0f;
+  const int wbeg = c.wg0[b], nwg = c.wg0[b + 1] - wbeg;
+  const float *P = c.part + ((int64_t)wbeg * 16 + h) * kPartRow + i0 + 4 * g4;
+  const float2 *ML = c.ml + (int64_t)wbeg * 16 + h;
   const int per = (nwg + kCombSlices - 1) / kCombSlices;
   const int w0 = ps * per, w1 = w0 + per < nwg ? w0 + per : nwg;
-  float m_loc = -INFINITY, lacc = 0.0f;
-  float4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int w = w0; w < w1; w += kCombChunk) {
-    float2 mlv[kCombChunk];
-    float4 ov[kCombChunk];
+  float2 mlv[kCombChunk];
+  float4 ov[kCombChunk];
+  auto load_round = [&](int w) {
 #pragma unroll
     for (int x = 0; x < kCombChunk; ++x) {
       const bool ok = w + x < w1;
-      const float *pw = P + (int64_t)(w + x) * 16 * kPartRow;
-      mlv[x] = ok ? *reinterpret_cast<const float2 *>(pw + 256) : float2{-INFINITY, 0.0f};
-      ov[x] = ok ? *reinterpret_cast<const float4 *>(pw + i0 + 4 * g4) : float4{0.f, 0.f, 0.f, 0.f};
+      mlv[x] = ok ? ML[(int64_t)(w + x) * 16] : float2{-INFINITY, 0.0f};
+      ov[x] = ok ? *reinterpret_cast<const float4 *>(P + (int64_t)(w + x) * 16 * kPartRow)
+                 : float4{0.f, 0.f, 0.f, 0.f};
     }
+  };
+  load_round(w0);
+  // the new key's q . k_new products, loaded after the partials (reduced further down)
+  float qv = 0.0f, kv = 0.0f;
+  if (dq != nullptr) {
+    qv = c.q[((int64_t)b * 16 + h) * 256 + tid];
+    kv = dq[((int64_t)b * 4 + (h >> 3)) * 256 + tid];
+  }
+  float m_loc = -INFINITY, lacc = 0.0f;
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int w = w0; w < w1; w += kCombChunk) {
+    if (w != w0) load_round(w);
     float mc = m_loc;
 #pragma unroll
     for (int x = 0; x < kCombChunk; ++x) mc = fmaxf(mc, mlv[x].x);
@@ -141,7 +149,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs c) {
       m_loc = mc;
     }
   }
-  const float d = wave_sum(prod);
+  const float d = wave_sum(qv * kv);
   if ((tid & 63) == 0) dotp[tid >> 6] = d;
   if (g4 == 0) mx[ps] = m_loc;
   __syncthreads();
@@ -169,10 +177,9 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs c) {
     const float f_new = (s_new == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_new - M);
     L += f_new;
     if (dq != nullptr) sum += f_new * dq[((int64_t)b * 4 + 2 + (h >> 3)) * 256 + e];
-    out[((int64_t)b * 16 + h) * 256 + e] = L > 0.0f ? sum / L : 0.0f;
+    c.out[((int64_t)b * 16 + h) * 256 + e] = L > 0.0f ? sum / L : 0.0f;
   }
 }
-
 
 }  // namespace
 

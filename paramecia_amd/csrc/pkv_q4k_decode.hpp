@@ -44,20 +44,28 @@ constexpr int kThreads = 64 * kWaves;  // two waves per SIMD
 constexpr int kMainWGs = 256;
 constexpr float kLazy = 8.0f;  // log2 headroom of the running max before a rescale
 
-struct DecodeArgs {
-  DecodeSeg seg[kMaxSegs];
+// Kernel arguments: the fields shared by every launch, then the segment table sized at
+// compile time (one segment for a single cache of batch 1, kMaxSegs otherwise), so that the
+// common launch carries about 200 bytes of arguments instead of the 1.5 KB of the full
+// table.
+struct DecodeArgsBase {
   int nseg, nwg, bpw;
   int64_t rs_t, rs_h;
   float sl2;                   // scale * log2(e)
   const float *q;              // [nseg][16][256]
   const float *k_new, *v_new;  // [nseg][2][256] or null (fused decode step)
   float *part;                 // [nwg][16][kPartRow]
+  float2 *ml;                  // [nwg][16] running max and sum
   float *dq;  // [nseg][4][256] dequantized new rows (K kv0, K kv1, V kv0, V kv1)
   // q/k preparation of a decode step from projection outputs (q_norm, k_norm, rope at
   // each segment's new position); used by the kPrep instantiation only
   DecodePrep prep;
   float *q_out;  // [nseg][16][256] prepared q, for the combine
   unsigned *status;  // the device status word (pkv_device_status)
+};
+template <int kSegs>
+struct DecodeArgsT : DecodeArgsBase {
+  DecodeSeg seg[kSegs];
 };
 
 // Per-wave tables rebuilt for every 32-key block.
@@ -499,15 +507,17 @@ __device__ __forceinline__ void issue_prep_consts(void *alpha_lds, void *tail_ld
       : "memory", "scc");
 }
 
-template <bool kPrep>
-__global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
+template <bool kPrep, int kSegs>
+__global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs> a) {
   __shared__ Smem sm;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kv = wave & 1, wsub = wave >> 1;
   const int wg = blockIdx.x;
   const int n = lane & 15, g = lane >> 4;
   int b = 0;  // segment of this workgroup
-  while (b + 1 < a.nseg && wg >= a.seg[b + 1].wg0) ++b;
+  if constexpr (kSegs > 1) {
+    while (b + 1 < a.nseg && wg >= a.seg[b + 1].wg0) ++b;
+  }
   const DecodeSeg &sg = a.seg[b];
 
   // ---- blocks of this wave: b0 + wsub, b0 + wsub + 4, ... below b1
@@ -876,8 +886,9 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgs a) {
       M = fmaxf(M, sm.run.t.tab[2 * s4 + kv2].vmd[h]);
       L += sm.run.t.tab[2 * s4 + kv2].vmd[16 + h];
     }
-    __builtin_nontemporal_store(M, dst + tid * kPartRow + 256);
-    __builtin_nontemporal_store(L, dst + tid * kPartRow + 257);
+    float *mlo = reinterpret_cast<float *>(a.ml + (int64_t)wg * 16 + tid);
+    __builtin_nontemporal_store(M, mlo);
+    __builtin_nontemporal_store(L, mlo + 1);
   }
 }
 
@@ -892,7 +903,7 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
                                   const float *k_new, const float *v_new, float *out,
                                   int64_t rs_t, int64_t rs_h, float scale, Workspace &ws,
                                   hipStream_t s, const DecodePrep *prep = nullptr) {
-  DecodeArgs d;
+  DecodeArgsT<kMaxSegs> d;
   const bool fused = k_new != nullptr;
   for (int i = 0; i < n; ++i) {
     d.seg[i].k = in[i].k;
@@ -944,20 +955,31 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
   d.q = q;
   d.k_new = k_new;
   d.v_new = v_new;
-  const size_t part_floats = (size_t)wg * 16 * kPartRow;
-  const size_t need =
-      (part_floats + (size_t)n * 4 * 256 + (kPrep ? (size_t)n * 16 * 256 : 0)) * sizeof(float);
+  const size_t part_floats = (size_t)wg * 16 * kPartRow, ml_floats = (size_t)wg * 16 * 2;
+  const size_t need = (part_floats + ml_floats + (size_t)n * 4 * 256 +
+                       (kPrep ? (size_t)n * 16 * 256 : 0)) *
+                      sizeof(float);
   int rc = ws.reserve(need);
   if (rc) return rc;
   d.part = static_cast<float *>(ws.ptr);
-  d.dq = d.part + part_floats;
+  d.ml = reinterpret_cast<float2 *>(d.part + part_floats);
+  d.dq = d.part + part_floats + ml_floats;
   d.q_out = d.dq + (size_t)n * 4 * 256;
   d.prep = kPrep ? *prep : DecodePrep{};
   rc = device_status_word(&d.status);
   if (rc) return rc;
-  hipLaunchKernelGGL(q4k_decode_kernel<kPrep>, dim3((unsigned)wg), dim3(kThreads), 0, s, d);
+  if (n == 1) {
+    DecodeArgsT<1> d1;
+    static_cast<DecodeArgsBase &>(d1) = d;
+    d1.seg[0] = d.seg[0];
+    hipLaunchKernelGGL((q4k_decode_kernel<kPrep, 1>), dim3((unsigned)wg), dim3(kThreads), 0, s, d1);
+  } else {
+    hipLaunchKernelGGL((q4k_decode_kernel<kPrep, kMaxSegs>), dim3((unsigned)wg), dim3(kThreads), 0, s,
+                       d);
+  }
   PKV_HIP(hipGetLastError());
   c.part = d.part;
+  c.ml = d.ml;
   c.q = kPrep ? d.q_out : q;
   c.dq = fused ? d.dq : nullptr;
   c.out = out;

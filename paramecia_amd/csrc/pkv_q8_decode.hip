@@ -38,6 +38,7 @@ struct Q8Args {
   const float *q;              // [nseg][16][256]
   const float *k_new, *v_new;  // [nseg][2][256] or null
   float *part;                 // [nwg][16][kPartRow]
+  float2 *ml;                  // [nwg][16] running max and sum
   float *dq;                   // [nseg][4][256]
 };
 
@@ -210,10 +211,7 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
   const int idx = tile_index(t);
 #pragma unroll
   for (int h = 0; h < 8; ++h) P[(8 * half + h) * kPartRow + idx] = acc[h];
-  if (kk == 0) {
-    P[(8 * half + hh) * kPartRow + 256] = m_run;
-    P[(8 * half + hh) * kPartRow + 257] = l_run;
-  }
+  if (kk == 0) a.ml[(int64_t)wg * 16 + 8 * half + hh] = float2{m_run, l_run};
 }
 
 }  // namespace
@@ -256,15 +254,17 @@ static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, cons
   d.q = q;
   d.k_new = k_new;
   d.v_new = v_new;
-  const size_t part_floats = (size_t)wg * 16 * kPartRow;
-  const size_t need = (part_floats + (size_t)n * 4 * 256) * sizeof(float);
+  const size_t part_floats = (size_t)wg * 16 * kPartRow, ml_floats = (size_t)wg * 16 * 2;
+  const size_t need = (part_floats + ml_floats + (size_t)n * 4 * 256) * sizeof(float);
   int rc = ws.reserve(need);
   if (rc) return rc;
   d.part = static_cast<float *>(ws.ptr);
-  d.dq = d.part + part_floats;
+  d.ml = reinterpret_cast<float2 *>(d.part + part_floats);
+  d.dq = d.part + part_floats + ml_floats;
   hipLaunchKernelGGL(q8_decode_kernel, dim3((unsigned)wg), dim3(kQ8Threads), 0, s, d);
   PKV_HIP(hipGetLastError());
   c.part = d.part;
+  c.ml = d.ml;
   c.q = q;
   c.dq = fused ? d.dq : nullptr;
   c.out = out;
