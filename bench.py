@@ -40,6 +40,8 @@ MEASURED_TRAFFIC = {
     3: (88_890_000, "profiles/q4k_decode_config3.md: decode + combine per layer"),
     1: (11_460_000, "profiles/q8_decode_config1.md: decode + combine"),
     2: (170_260_000, "profiles/q4k_prefill_config2.md: prefill kernel + split merge"),
+    4: (1_064_255_795, "profiles/prefix_restore_config4.md: copy_segments_kernel read + "
+                       "written"),
     5: (418_800_000, "profiles/q4k_batched_decode_config5.md: decode + combine per layer"),
     6: (73_730_000, "profiles/deltanet_step_config6.md: per launch at batch 16"),
 }
@@ -78,13 +80,18 @@ def event_time(torch, fn, steps, warmup):
     return a.elapsed_time(b) / steps
 
 
+NO_GRAPH = False  # --no-graph: every "graph" time is an eager one (profiler passes)
+
+
 def graph_time(torch, fn, steps, warmup, reps=1):
     """Milliseconds per call of fn, run from a HIP graph: fn is captured `reps` times in a
     row into one graph (after an eager warm-up on the capture stream, which sizes every
     workspace), the graph is replayed, and the time of a replay is divided by `reps`.
     With reps > 1 the graph launch is shared by several steps, as it is in a serving
     loop whose graph holds the whole forward pass; every captured step does all of its
-    work."""
+    work. With --no-graph the calls are timed eagerly instead."""
+    if NO_GRAPH:
+        return event_time(torch, fn, steps, warmup)
     graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -229,17 +236,10 @@ def run_config3(args):
     if args.prep:
         result["unprepared_us_per_step"] = round(
             graph_time(torch, step_plain, args.steps, args.warmup, reps) * 1000.0, 2)
-    if args.calib_copy_mib > 0:
-        n = args.calib_copy_mib * (1 << 20) // 4
-        src = torch.ones(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            torch.neg(src, out=dst)
-        torch.cuda.synchronize()
-        del src, dst
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_decode(
-            caches[0], kn[0], vn[0], q[0], S, args.cpu_threads, 3, 4, W.N_FULL)
+            caches[0], kn[0], vn[0], q[0], S, args.cpu_threads, 3, 4, W.N_FULL,
+            single_keys=min(S, 16384))
     return result
 
 
@@ -257,31 +257,165 @@ def make_preps(torch, pk, W, layers, max_pos):
     return preps
 
 
-def cpu_baseline_decode(cache, kn, vn, q, S, threads, config, quant, layers):
-    """The oracle's faithful restatement of the reference CPU path (CPU quantize of the new
-    token, dequantize the whole cache, permute, repeat_kv, transposed-K copy, matmul,
-    clamp, softmax, matmul) on one layer, extrapolated to `layers` layers."""
+CPU_RUNS = 5  # timed runs per CPU-baseline leg; the median is reported
+
+
+def cpu_threads(threads: int) -> int:
+    """Host threads of the multi-threaded CPU leg: --cpu-threads, else every core the
+    process sees, capped at the 16 cores a one-GPU box grants a job."""
+    return threads if threads > 0 else min(os.cpu_count() or 1, 16)
+
+
+def median(xs):
+    ys = sorted(xs)
+    return ys[len(ys) // 2] if len(ys) % 2 else 0.5 * (ys[len(ys) // 2 - 1] + ys[len(ys) // 2])
+
+
+def oracle_cache_from(cache, quant, S, rows):
+    """An oracle cache (capacity rows + 1) holding the first `rows` rows of a GPU cache's
+    packed bytes."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
     from paramecia_amd import workloads as W
 
-    nthreads = threads if threads > 0 else min(os.cpu_count() or 1, 16)
-    c = orc.Cache(quant, 1, W.NUM_KV_HEADS, W.HEAD_DIM, S + 1)
+    c = orc.Cache(quant, 1, W.NUM_KV_HEADS, W.HEAD_DIM, rows + 1)
+    cache.truncate(S)
+    kb, vb = cache.raw_bytes()
+    c.load_bytes(kb.cpu().numpy(), vb.cpu().numpy(), rows)
+    return c
+
+
+def cpu_baseline_decode(cache, kn, vn, q, S, threads, config, quant, layers, single_keys=None):
+    """The oracle's faithful restatement of the reference CPU path (CPU quantize of the new
+    token, dequantize the whole cache, permute, repeat_kv, transposed-K copy, matmul,
+    clamp, softmax, matmul) for one layer's decode step, extrapolated to `layers` layers.
+    Two legs, each the median of CPU_RUNS timed runs: all cores (cpu_threads) over the
+    full cache, and one thread over the first `single_keys` cached keys (the whole cache
+    when None), scaled by the key count (every step of the path is linear in it)."""
+    from paramecia_amd import workloads as W
+
+    nthreads = cpu_threads(threads)
+    knp, vnp, qnp = kn.cpu().numpy(), vn.cpu().numpy(), q.cpu().numpy()
+
+    def once(c, rows, th):
+        t0 = time.perf_counter()
+        assert c.append_at(knp, vnp, rows) == 0
+        c.attend(qnp, W.SCALE, rows, True, mode="faithful", threads=th)
+        return time.perf_counter() - t0
+
+    c = oracle_cache_from(cache, quant, S, S)
+    multi = [once(c, S, nthreads) for _ in range(CPU_RUNS)]
+    rows1 = S if single_keys is None else min(S, single_keys)
+    c1 = c if rows1 == S else oracle_cache_from(cache, quant, S, rows1)
+    single = [once(c1, rows1, 1) for _ in range(CPU_RUNS)]
+    scale1 = (S + 1) / (rows1 + 1)
+    del c, c1
+    return {
+        "value": round(median(multi) * layers * 1e6, 1), "unit": "us/step", "cores": nthreads,
+        "kind": "port",
+        "sample": f"config {config}: one decode step (append 1 token + attend {S + 1} keys) of "
+                  f"1 of {layers} layers, median of {CPU_RUNS} runs, times {layers}; "
+                  f"{nthreads} OpenMP threads (the cores this process sees, at most 16) on "
+                  f"{cpu_model()}",
+        "runs_s": [round(x, 4) for x in multi],
+        "single_thread": {
+            "value": round(median(single) * scale1 * layers * 1e6, 1), "unit": "us/step",
+            "cores": 1,
+            "sample": f"one thread, one decode step over the first {rows1 + 1} keys, median of "
+                      f"{CPU_RUNS} runs, times {scale1:.4g} (key count) and {layers} (layers)",
+            "runs_s": [round(x, 4) for x in single]},
+    }
+
+
+def cpu_baseline_prefill(cache, kc, vc, qc, k1, v1, q1, S, C, threads):
+    """Config 2's step on the oracle's faithful CPU path: quantize-append the C-token chunk,
+    causal attention of its C queries over S + C keys, then one decode step (append 1
+    token, attend S + C + 1 keys). The chunk attention is timed on two samples of its last
+    query rows and extrapolated linearly in the keys the rows see (t = a + b * keys: the
+    per-call dequantize and copies are a, the products b); the append and the decode step
+    are timed whole. Legs: all cores (cpu_threads) and one thread, medians of CPU_RUNS."""
+    from paramecia_amd import workloads as W
+
+    nthreads = cpu_threads(threads)
+    kcn, vcn, qcn = kc.cpu().numpy(), vc.cpu().numpy(), qc.cpu().numpy()
+    k1n, v1n, q1n = k1.cpu().numpy(), v1.cpu().numpy(), q1.cpu().numpy()
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    c = orc.Cache(4, 1, W.NUM_KV_HEADS, W.HEAD_DIM, S + C + 1)
     cache.truncate(S)
     kb, vb = cache.raw_bytes()
     c.load_bytes(kb.cpu().numpy(), vb.cpu().numpy(), S)
-    knp, vnp, qnp = kn.cpu().numpy(), vn.cpu().numpy(), q.cpu().numpy()
-    t0 = time.perf_counter()
-    assert c.append_at(knp, vnp, S) == 0
-    c.attend(qnp, W.SCALE, S, True, mode="faithful", threads=nthreads)
-    dt = time.perf_counter() - t0
-    return {
-        "value": round(dt * layers * 1e6, 1), "unit": "us/step", "cores": nthreads,
-        "kind": "port",
-        "sample": f"config {config}: 1 of {layers} layers, one decode step (append 1 token + "
-                  f"attend {S + 1} keys) timed once and multiplied by {layers}; {nthreads} "
-                  f"OpenMP threads on {cpu_model()}",
-    }
+    keys = lambda i0, i1: sum(S + i + 1 for i in range(i0, i1))  # keys seen by rows [i0, i1)
+
+    def leg(th, na, nb):
+        ta, tb, tr = [], [], []
+        for _ in range(CPU_RUNS):
+            t0 = time.perf_counter()
+            assert c.append_at(kcn, vcn, S) == 0
+            t1 = time.perf_counter()
+            assert c.append_at(k1n, v1n, S + C) == 0
+            c.attend(q1n, W.SCALE, S + C, True, mode="faithful", threads=th)
+            t2 = time.perf_counter()
+            tr.append((t1 - t0) + (t2 - t1))
+            for n, out in ((na, ta), (nb, tb)):
+                t0 = time.perf_counter()
+                c.attend(qcn[:, C - n:], W.SCALE, S + C - n, True, mode="faithful", threads=th)
+                out.append(time.perf_counter() - t0)
+        a_t, b_t = median(ta), median(tb)
+        slope = (b_t - a_t) / (keys(C - nb, C) - keys(C - na, C))
+        attn = a_t + slope * (keys(0, C) - keys(C - na, C))
+        return median(tr) + attn, (na, nb, a_t, b_t)
+
+    multi, sm = leg(nthreads, 8, 64)
+    single, s1 = leg(1, 2, 8)
+    desc = lambda th, s_: (f"{th} thread(s): append {C} tokens and one decode step timed whole; "
+                           f"chunk attention timed on its last {s_[0]} and {s_[1]} query rows "
+                           f"({s_[2]:.3f} s, {s_[3]:.3f} s) and extrapolated linearly in keys "
+                           f"seen to all {C}; medians of {CPU_RUNS} runs")
+    return {"value": round(multi * 1e6, 1), "unit": "us/step", "cores": nthreads, "kind": "port",
+            "sample": f"config 2 on {cpu_model()}: " + desc(nthreads, sm),
+            "single_thread": {"value": round(single * 1e6, 1), "unit": "us/step", "cores": 1,
+                              "sample": desc(1, s1)}}
+
+
+def copy_ceiling(torch, mib=1024, steps=10):
+    """Measured device-to-device copy rate on this GPU: torch copy_ between two 1 GiB
+    buffers (a runtime blit), read + written bytes over the HIP-event time. The practical
+    ceiling an HBM-bound kernel is compared with, beside the 8 TB/s data-sheet peak."""
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    ms = event_time(torch, lambda: dst.copy_(src), steps, 3)
+    del src, dst
+    torch.cuda.empty_cache()
+    gbs = 2 * n / (ms * 1e-3) / 1e9
+    return {"gbs": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_copy": 2 * n,
+            "method": f"torch copy_ of {mib} MiB device to device, {steps} copies after 3, "
+                      "(read + write bytes) / HIP-event time"}
+
+
+def calib_copy(torch, mib):
+    """torch.neg of `mib` MiB into a second buffer, 3 times: a plain copy (read N, write
+    N bytes) whose rocprofv3 FETCH_SIZE / WRITE_SIZE readings scale the counters to bytes."""
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+
+
+def add_copy_ceiling(torch, r):
+    """Attach the copy ceiling to a result line, and the roofline's fraction of it."""
+    cc = copy_ceiling(torch)
+    r["copy_ceiling"] = cc
+    rf = r.get("roofline")
+    if rf and rf.get("unit") == "GB/s":
+        rf["frac_of_copy_ceiling"] = round(rf["achieved"] / cc["gbs"], 4)
+    return r
 
 
 def base_result(config, metric, value, unit, hib, ms, args, workload, extra):
@@ -410,6 +544,9 @@ def run_config2(args):
         extra["append_chunk_us"] = round(graph_time(
             torch, lambda: c.append_quantized(kc, vc, offset=S), args.steps, args.warmup,
             reps) * 1000, 2)
+    if not args.no_cpu_baseline:
+        extra["cpu_baseline"] = cpu_baseline_prefill(c, kc, vc, qc, k1, v1, q1, S, C,
+                                                     args.cpu_threads)
     return base_result(2, "Q4K prefill chunk + decode µs (512-token append, 512 x 16896 causal "
                        "attention, 1-token decode over 16897 keys)",
                        round(ms * 1000, 2), "us/step", False, ms, args, workload,
@@ -491,7 +628,8 @@ def run_config4(args):
                         "roofline": {"kernel": "copy_segments (restore)", "bound": "hbm",
                                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                                     "bytes_per_launch": moved, "traffic": None}})
+                                     "bytes_per_launch": moved, "traffic": traffic(4),
+                                     "traffic_source": MEASURED_TRAFFIC[4][1]}})
 
 
 # ------------------------------------------------------------------ config 5
@@ -715,10 +853,17 @@ def main() -> int:
                     help="configs 2 and 3: start from the q/k/v projection outputs, so q_norm, "
                          "k_norm and rope run inside the step (the fused preparation)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
-                    help="config 3: after the timed runs, launch a plain elementwise copy of "
-                         "this many MiB (read N, write N) 3 times: the reference kernel that "
-                         "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes")
+                    help="after the timed runs, launch a plain elementwise copy of this many "
+                         "MiB (read N, write N) 3 times: the reference kernel that scales "
+                         "rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="time every step eagerly, capturing no HIP graph (for rocprofv3 "
+                         "counter passes, which do not support graph capture here)")
+    ap.add_argument("--no-copy-ceiling", action="store_true",
+                    help="skip the device-to-device copy ceiling measured after each config")
     args = ap.parse_args()
+    global NO_GRAPH
+    NO_GRAPH = args.no_graph
     if args.gpus != 1:
         print("bench.py measures the single-GPU path only: every GPU box in this build has "
               "one MI355X, and the KV-cache path needs no collectives (see DESIGN.md for how "
@@ -734,8 +879,13 @@ def main() -> int:
         if cfg not in runners:
             print(f"unknown config {cfg}", file=sys.stderr)
             return 2
-        print(json.dumps(runners[cfg](args)), flush=True)
+        r = runners[cfg](args)
         torch.cuda.empty_cache()
+        if args.calib_copy_mib > 0:
+            calib_copy(torch, args.calib_copy_mib)
+        if not args.no_copy_ceiling:
+            add_copy_ceiling(torch, r)
+        print(json.dumps(r), flush=True)
     return 0
 
 

@@ -196,6 +196,41 @@ def test_flash_attn_stateless_matches_cache(pk):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("quant,bpr,L", [(Q8_0, 272, 1), (Q4K, 144, 1), (Q4K, 144, 4),
+                                         (Q8_0, 272, 6)])
+def test_kv_storage_strides_and_flash_attn_batch2(pk, orc, quant, bpr, L):
+    """get_kv_storage at batch 2, where stride_b (one sequence's rows of a token) and
+    stride_seq (one token's rows of every sequence) differ: rows addressed through the
+    returned strides are the oracle's rows, and flash_attn over those pointers and strides
+    matches the oracle's attention (qwen3_next.rs:582-617, ops.rs:756)."""
+    say(f"kv_storage + flash_attn batch 2 quant={quant} L={L}")
+    B, Hkv, H, D, S = 2, 2, 16, 256, 700
+    rng = np.random.default_rng(31 + L)
+    g = pk.PreallocatedQuantizedKvCache(B, Hkv, 1024, D, pk.KvCacheQuantization(quant))
+    c = orc.Cache(quant, B, Hkv, D, 1024)
+    k = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    g.append_quantized(dev(k), dev(v))
+    assert c.append(k, v) == 0
+    kp, vp, n, st = g.get_kv_storage()
+    assert st == (Hkv * bpr, B * Hkv * bpr, bpr, 1) and st[0] != st[1]
+    assert n == S * B * Hkv * bpr
+    kb, vb = g.raw_bytes()
+    hk, hv = host(kb), host(vb)
+    ck, cv = c.valid_bytes()
+    for t, b, h in [(0, 0, 0), (0, 1, 0), (1, 0, 1), (351, 1, 1), (S - 1, 1, 0), (S - 1, 0, 1)]:
+        off = t * st[1] + b * st[0] + h * st[2]
+        row = ((t * B + b) * Hkv + h) * bpr  # the reference's seq-major row index
+        assert np.array_equal(hk[off:off + bpr], ck[row:row + bpr])
+        assert np.array_equal(hv[off:off + bpr], cv[row:row + bpr])
+    q = rng.standard_normal((B, L, H, D)).astype(np.float32)
+    out = pk.flash_attn(pk.KvCacheQuantization(quant), dev(q), kp, vp, st, 1 / 16, Hkv, S,
+                        S - L, True)
+    ref = c.attend(q, 1 / 16, S - L, True, mode="f64")
+    assert_attn_close(host(out), ref)
+    assert torch.equal(out, g.attend(dev(q), 1 / 16, S - L, True))
+
+
 def test_prefix_restore_bytes_and_requantize(pk, orc):
     say("prefix restore")
     from paramecia_amd import workloads as W
