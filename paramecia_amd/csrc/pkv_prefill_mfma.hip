@@ -509,25 +509,51 @@ __global__ __launch_bounds__(kPfThreads) void q4k_prefill_kernel(PrefillArgs a) 
 }
 
 // Merge the key splits: out[b][pos][8 kvg + hh][e] = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
-// One workgroup of 256 threads per (row, batch); thread = tile-order index.
+// One workgroup of 256 threads per 8 rows and batch: 32 threads per row, each taking 8
+// consecutive tile-order entries; every split's (m, l) and entries are loaded before any
+// is used (nsplit <= kMaxMergeSplits).
+constexpr int kMaxMergeSplits = 16;
 __global__ __launch_bounds__(256) void q4k_prefill_merge_kernel(const float *part, int nsplit,
                                                                 int l, float *out) {
-  const int row = blockIdx.x, b = blockIdx.y;  // row = kvg * l * 8 + pos * 8 + hh
+  const int r8 = threadIdx.x >> 5, j = threadIdx.x & 31;
+  const int row = blockIdx.x * 8 + r8, b = blockIdx.y;  // row = kvg * l * 8 + pos * 8 + hh
+  if (row >= 2 * l * 8) return;
   const int kvg = row / (l * 8), rr = row % (l * 8), pos = rr >> 3, hh = rr & 7;
-  const int idx = threadIdx.x;
-  float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s)
-    M = fmaxf(M, part[(((int64_t)(b * nsplit + s) * 2 + kvg) * l * 8 + rr) * 258 + 256]);
-  float acc = 0.0f, L = 0.0f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float *pr = part + (((int64_t)(b * nsplit + s) * 2 + kvg) * l * 8 + rr) * 258;
-    const float ms = pr[256];
-    const float f = (ms == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
-    acc += f * pr[idx];
-    L += f * pr[257];
+  const int64_t split_stride = (int64_t)2 * l * 8 * 258;
+  const float *base = part + (((int64_t)(b * nsplit) * 2 + kvg) * l * 8 + rr) * 258;
+  float2 ml[kMaxMergeSplits], v[kMaxMergeSplits][4];
+#pragma unroll
+  for (int s = 0; s < kMaxMergeSplits; ++s) {
+    if (s < nsplit) {
+      const float *pr = base + s * split_stride;
+      ml[s] = *reinterpret_cast<const float2 *>(pr + 256);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[s][k] = *reinterpret_cast<const float2 *>(pr + 8 * j + 2 * k);
+    }
   }
-  const int e = tile_e(idx >> 4, idx & 15);
-  out[(((int64_t)b * l + pos) * 16 + 8 * kvg + hh) * 256 + e] = L > 0.0f ? acc / L : 0.0f;
+  float M = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kMaxMergeSplits; ++s)
+    if (s < nsplit) M = fmaxf(M, ml[s].x);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, L = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kMaxMergeSplits; ++s) {
+    if (s < nsplit) {
+      const float f = (ml[s].x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ml[s].x - M);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc[2 * k] += f * v[s][k].x;
+        acc[2 * k + 1] += f * v[s][k].y;
+      }
+      L += f * ml[s].y;
+    }
+  }
+  float *orow = out + (((int64_t)b * l + pos) * 16 + 8 * kvg + hh) * 256;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int idx = 8 * j + k;
+    orow[tile_e(idx >> 4, idx & 15)] = L > 0.0f ? acc[k] / L : 0.0f;
+  }
 }
 
 }  // namespace
@@ -555,7 +581,7 @@ int launch_prefill_mfma(const AttnArgs &a, Workspace &ws, hipStream_t s) {
   const int nblk = (int)((a.seq_k + kBlk - 1) / kBlk);
   const int base = d.ntiles * 2 * a.batch;
   int nsplit = (kPfTargetWGs + base - 1) / base;
-  if (nsplit > 16) nsplit = 16;
+  if (nsplit > kMaxMergeSplits) nsplit = kMaxMergeSplits;
   if (nsplit > nblk) nsplit = nblk > 0 ? nblk : 1;
   if (nsplit < 1) nsplit = 1;
   d.bps = (nblk + nsplit - 1) / nsplit;
@@ -573,7 +599,7 @@ int launch_prefill_mfma(const AttnArgs &a, Workspace &ws, hipStream_t s) {
                      dim3(kPfThreads), 0, s, d);
   PKV_HIP(hipGetLastError());
   if (nsplit > 1) {
-    hipLaunchKernelGGL(q4k_prefill_merge_kernel, dim3((unsigned)(2 * a.l * 8), (unsigned)a.batch),
+    hipLaunchKernelGGL(q4k_prefill_merge_kernel, dim3((unsigned)((2 * a.l * 8 + 7) / 8), (unsigned)a.batch),
                        dim3(256), 0, s, d.part, nsplit, a.l, a.out);
     PKV_HIP(hipGetLastError());
   }
