@@ -1003,7 +1003,14 @@ int pkv_prefix_restore(const pkv_prefix *p, const pkv_layer_target *targets, int
   }
   // Order the launch after the snapshot copies and after work already queued on the
   // target caches' streams (an attention still reading rows about to be overwritten).
-  for (int i = 0; i < n_layers; ++i) {
+  // Under stream capture there is no cross-stream ordering to add: an event recorded
+  // outside the capture cannot be waited on inside it, and a cache stream made to wait on
+  // the capturing stream would join the capture unjoined. The graph's own order applies
+  // when it is replayed.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  PKV_HIP(hipStreamIsCapturing(s, &cap));
+  const bool capturing = cap != hipStreamCaptureStatusNone;
+  for (int i = 0; i < n_layers && !capturing; ++i) {
     const Entry &e = p->entries[(size_t)i];
     const pkv_layer_target &t = targets[i];
     const bool used = t.cache ? e.kind == PKV_ENTRY_FULL : e.kind == PKV_ENTRY_LINEAR;
@@ -1038,7 +1045,7 @@ int pkv_prefix_restore(const pkv_prefix *p, const pkv_layer_target *targets, int
   if (rc) return rc;
   int rc_order = PKV_OK;  // the caches' streams wait for everything below
   auto order_caches = [&]() {
-    for (int i = 0; i < n_layers && !rc_order; ++i) {
+    for (int i = 0; i < n_layers && !rc_order && !capturing; ++i) {
       pkv_cache *c = targets[i].cache;
       if (!c || c->stream == s) continue;
       hipError_t er = hipEventRecord(c->order_ev, s);

@@ -37,7 +37,22 @@ __device__ __forceinline__ int64_t dst_row(const AppendArgs &a, int64_t t, int b
   return ((a.t0 + t) * a.batch + b) * a.heads + h;
 }
 
+// clamp(nearest_int(v), 0, 15) as a float: nearest_int is candle's v.round() as i32
+// (half away from zero, NaN -> 0). rint rounds half to even; a tie it rounded down
+// (v - r == 0.5, exact: |v - r| <= 0.5 and r is v's nearest integer) goes up instead. A
+// tie below zero, a negative value, -0 and NaN all give +0 after the clamp, as the
+// integer path does.
+__device__ __forceinline__ float q4_level(float v) {
+  float r = __builtin_rintf(v);
+  r = (v - r == 0.5f) ? r + 1.0f : r;
+  r = (r > 0.0f) ? r : 0.0f;
+  return (r < 15.0f) ? r : 15.0f;
+}
+
 // candle make_qkx1_quants(nmax = 15, ntry = 5) over the 32 values of one sub-block.
+// The levels are kept as floats (small integers, exact), suml2 is summed in f32 (an
+// integer below 2^24, exact), and every other sum runs in the reference's order with one
+// rounding per operation.
 __device__ void make_qkx1_quants_32(const float x[32], float &scale_out, float &neg_min_out) {
   float mn = x[0], mx = x[0];
 #pragma unroll
@@ -50,31 +65,28 @@ __device__ void make_qkx1_quants_32(const float x[32], float &scale_out, float &
     neg_min_out = 0.0f;
     return;
   }
-  uint8_t L[32];
+  float L[32];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) L[i] = 0;
+  for (int i = 0; i < 32; ++i) L[i] = 0.0f;
   float min = fmin_rs(mn, 0.0f);
   float iscale = 15.0f / (mx - min);
   float scale = 1.0f / iscale;
   for (int t = 0; t < 5; ++t) {
-    float sumlx = 0.0f;
-    int32_t suml2 = 0;
+    float sumlx = 0.0f, suml2 = 0.0f;
     bool did_change = false;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      int32_t li = nearest_int(iscale * (x[i] - min));
-      li = li < 0 ? 0 : (li > 15 ? 15 : li);
-      if ((uint8_t)li != L[i]) {
-        L[i] = (uint8_t)li;
-        did_change = true;
-      }
-      sumlx += (x[i] - min) * (float)li;
-      suml2 += li * li;
+      const float d = x[i] - min;
+      const float li = q4_level(iscale * d);
+      did_change |= li != L[i];
+      L[i] = li;
+      sumlx += d * li;
+      suml2 = __builtin_fmaf(li, li, suml2);  // exact
     }
-    scale = sumlx / (float)suml2;
+    scale = sumlx / suml2;
     float sum = -0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) sum += x[i] - scale * (float)L[i];
+    for (int i = 0; i < 32; ++i) sum += x[i] - scale * L[i];
     min = sum / 32.0f;
     if (min > 0.0f) min = 0.0f;
     iscale = 1.0f / scale;
@@ -144,15 +156,37 @@ __global__ __launch_bounds__(256) void q4k_append_kernel(AppendArgs a, int64_t u
   const uint16_t mh = f32_to_f16(max_min / 63.0f);
 
   // get_scale_min_k4(j) of the packed codes returns (ls, lm) for this sub-block.
+  // Levels clamp(nearest_int((x + dm) / dd), 0, 15) with a correctly rounded division.
+  // Fast path: q = (x + dm) * rcp(dd) is within about 2 ulp of the rounded quotient
+  // (v_rcp_f32 within 1 ulp), so rint(q) is its nearest integer unless q lies within
+  // 2^-12 of a half-integer (a possible tie); those elements, and every element when
+  // rcp(dd) is not finite, take the IEEE division.
   uint32_t Lw[4] = {0u, 0u, 0u, 0u};
   const float dd = f16_to_f32(dh) * (float)ls;
   if (dd != 0.0f) {
     const float dm = f16_to_f32(mh) * (float)lm;
+    const float rdd = __builtin_amdgcn_rcpf(dd);
+    const bool exact_all = !(__builtin_fabsf(rdd) < 3.0e38f);
+    uint32_t slow = 0u;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      int32_t l = nearest_int((x[i] + dm) / dd);
-      l = l < 0 ? 0 : (l > 15 ? 15 : l);
+      const float q = (x[i] + dm) * rdd;
+      const float r = __builtin_rintf(q);
+      const bool near_tie = __builtin_fabsf(q - r) > 0.5f - 0x1p-12f;
+      slow |= (near_tie || exact_all) ? (1u << i) : 0u;
+      float l = (r > 0.0f) ? r : 0.0f;  // negatives, -0 and NaN -> 0
+      l = (l < 15.0f) ? l : 15.0f;
       Lw[i >> 3] |= (uint32_t)l << (4 * (i & 7));
+    }
+    if (slow != 0u) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        if (slow & (1u << i)) {
+          int32_t l = nearest_int((x[i] + dm) / dd);
+          l = l < 0 ? 0 : (l > 15 ? 15 : l);
+          Lw[i >> 3] = (Lw[i >> 3] & ~(15u << (4 * (i & 7)))) | ((uint32_t)l << (4 * (i & 7)));
+        }
+      }
     }
   }
 

@@ -157,6 +157,31 @@ int launch_copy_segments(void *const *dst, const void *const *src, const size_t 
   if (segs.empty()) return PKV_OK;
   const unsigned grid = (unsigned)(chunks < (uint64_t)kCopyWGs ? chunks : (uint64_t)kCopyWGs);
   const int ns = (int)segs.size();
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  PKV_HIP(hipStreamIsCapturing(s, &cap));
+  if (cap != hipStreamCaptureStatusNone && (ns > kArgSegs || chunks >= (1ull << 32))) {
+    // Under stream capture the table travels in kernel arguments only, kArgSegs segments
+    // per launch: a table copied from the pinned host buffer would be read when the graph
+    // is replayed, after later calls have reused the buffer.
+    for (int i0 = 0; i0 < ns; i0 += kArgSegs) {
+      const int m = ns - i0 < kArgSegs ? ns - i0 : kArgSegs;
+      ArgTable t;
+      uint64_t c = 0;
+      for (int i = 0; i < m; ++i) {
+        const Segment &g = segs[(size_t)(i0 + i)];
+        t.dst[i] = g.dst;
+        t.src[i] = g.src;
+        t.bytes[i] = g.bytes;
+        t.first[i] = (uint32_t)c;
+        c += (g.bytes + kChunk - 1) / kChunk;
+      }
+      if (c >= (1ull << 32)) return set_error(PKV_ERR_UNSUPPORTED, "copy of 2^32 chunks or more");
+      const unsigned gm = (unsigned)(c < (uint64_t)kCopyWGs ? c : (uint64_t)kCopyWGs);
+      hipLaunchKernelGGL(copy_segments_kernel<ArgTable>, dim3(gm), dim3(256), 0, s, t, m, c);
+      PKV_HIP(hipGetLastError());
+    }
+    return PKV_OK;
+  }
   if (ns <= kArgSegs && chunks < (1ull << 32)) {
     ArgTable t;
     for (int i = 0; i < ns; ++i) {

@@ -325,6 +325,68 @@ def test_prefix_restore_many_segments(pk):
         assert np.array_equal(host(st.gate_cumsum_offset), gs)
 
 
+def test_prefix_restore_graph_capture(pk):
+    """A restore captured into a HIP graph on a stream other than the caches' (as a serving
+    loop replays it), with more segments than one kernel-argument table holds: the capture
+    completes, and every replay, after eager work has overwritten the caches and states,
+    restores them byte for byte."""
+    say("prefix restore captured in a graph, 176 segments")
+    m = pk.ModelKvState(64, 4, 16, 2, 256, 256, pk.KvCacheQuantization.Q4K)
+    full = m.full_layers()
+    for l in full:
+        l._ensure(1).append_quantized(torch.randn(1, 2, 37, 256, device="cuda"),
+                                      torch.randn(1, 2, 37, 256, device="cuda"))
+    lin = [l for l in m.layers if isinstance(l, pk.LinearAttentionState)]
+    for l in lin:
+        l.recurrent_state = pk.RecurrentState(torch.randn(1, 3, 5, 7, device="cuda"),
+                                              torch.randn(1, 11, 3, device="cuda"),
+                                              torch.randn(1, 3, device="cuda"))
+    snap = [tuple(host(x).copy() for x in l.quantized_cache.raw_bytes()) for l in full]
+    states = [tuple(host(x).copy() for x in (l.recurrent_state.ssm_state,
+                                             l.recurrent_state.conv_state,
+                                             l.recurrent_state.gate_cumsum_offset)) for l in lin]
+    pc = m.save_prefix_cache(list(range(37)))
+    torch.cuda.synchronize()
+
+    def diverge(i):
+        for l in full:
+            l.quantized_cache.append_quantized(torch.randn(1, 2, 5, 256, device="cuda"),
+                                               torch.randn(1, 2, 5, 256, device="cuda"),
+                                               offset=10 + i)
+        for l in lin:
+            for x in (l.recurrent_state.ssm_state, l.recurrent_state.conv_state,
+                      l.recurrent_state.gate_cumsum_offset):
+                x.fill_(5.0 + i)
+
+    def check(what):
+        for l, (kb, vb) in zip(full, snap):
+            l.quantized_cache.set_len(37)
+            gk, gv = l.quantized_cache.raw_bytes()
+            assert np.array_equal(host(gk), kb) and np.array_equal(host(gv), vb), what
+        for l, (ss, cs, gs) in zip(lin, states):
+            st = l.recurrent_state
+            assert np.array_equal(host(st.ssm_state), ss), what
+            assert np.array_equal(host(st.conv_state), cs), what
+            assert np.array_equal(host(st.gate_cumsum_offset), gs), what
+
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        assert m.restore_prefix_cache(pc) == 37  # eager, sizes every workspace
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            m.restore_prefix_cache(pc)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for i in range(3):
+        diverge(i)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        check(f"replay {i}")
+
+
 def test_batched_decode_matches_per_sequence(pk, orc):
     say("batched decode")
     rng = np.random.default_rng(10)
