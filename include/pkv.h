@@ -268,6 +268,19 @@ int pkv_deltanet_step(const float *q, const float *k, const float *v, const floa
 int pkv_gated_oproj_q4k(const float *attn, const float *gate, const void *w_q4k, float *out,
                         int batch, int in_dim, int out_dim, pkv_stream stream);
 
+/* GGUF weight types of the output projection: GGML's ggml_type numbers, as a GGUF file
+ * stores them per tensor (the reference's GgmlDType of self.wo, qn:1412-1413). */
+enum { PKV_WTYPE_Q8_0 = 8, PKV_WTYPE_Q4K = 12, PKV_WTYPE_Q5K = 13, PKV_WTYPE_Q6K = 14 };
+
+/* The same gated projection for any of the k-quant types a GGUF Qwen3-Next checkpoint
+ * stores attn_output in (Q4K, Q5K, Q6K; Q8_0 checkpoints): W is out_dim rows of in_dim
+ * elements of type w_type (Q4K 144 B, Q5K 176 B, Q6K 210 B per 256 inputs; Q8_0 34 B per
+ * 32), the GGUF tensor bytes as stored. Same shapes and alignment as
+ * pkv_gated_oproj_q4k; another w_type -> PKV_ERR_UNSUPPORTED. w_type Q4K is
+ * pkv_gated_oproj_q4k. */
+int pkv_gated_oproj(const float *attn, const float *gate, const void *w, int w_type, float *out,
+                    int batch, int in_dim, int out_dim, pkv_stream stream);
+
 /* ---- PrefixCache host spill (the survey's next row after the path: the reference keeps
  * prefixes in device memory only, qn:856-864; LocalBackend, paramecia-llm, is the caller
  * that would evict them). A blob is a self-describing host byte image of a prefix:

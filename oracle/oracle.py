@@ -67,7 +67,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_f16_to_f32_n.argtypes = [_u16p, _fp, sz]
     for name in ("orc_q8_0_quantize", "orc_q4k_quantize"):
         getattr(L, name).argtypes = [_fp, _u8p, sz]
-    for name in ("orc_q8_0_dequantize", "orc_q4k_dequantize"):
+    for name in ("orc_q8_0_dequantize", "orc_q4k_dequantize", "orc_q5k_dequantize",
+                 "orc_q6k_dequantize"):
         getattr(L, name).argtypes = [_u8p, _fp, sz]
     L.orc_make_qkx1_quants.argtypes = [_fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _fp, _fp]
     L.orc_philox4x32_10.argtypes = [ctypes.POINTER(ctypes.c_uint32)] * 3
@@ -96,6 +97,9 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_rope_rows.argtypes = [_fp, sz, ctypes.c_int, ctypes.c_int, _i64p, _fp, _fp]
     L.orc_deltanet_step.argtypes = [_fp] * 8 + [ctypes.c_int] * 3 + [ctypes.c_float] * 2
     L.orc_gated_oproj_q4k.argtypes = [_fp, _fp, _u8p, _fp] + [ctypes.c_int] * 3
+    L.orc_gated_oproj.argtypes = [_fp, _fp, _u8p, ctypes.c_int, _fp] + [ctypes.c_int] * 3
+    L.orc_weight_row_bytes.argtypes = [ctypes.c_int, ctypes.c_int]
+    L.orc_weight_row_bytes.restype = sz
     L.orc_qk_prep.argtypes = [_fp, _fp] + [ctypes.c_int] * 5 + [_fp, _fp, ctypes.c_float,
                                                                  ctypes.c_int, _fp, _fp, i64,
                                                                  _fp, _fp]
@@ -351,6 +355,35 @@ def deltanet_step(q, k, v, gate, beta, state, gate_offset, scale: float, eps: fl
     lib().orc_deltanet_step(_f(q), _f(k), _f(v), _f(gate), _f(beta), _f(state),
                             _f(gate_offset) if gate_offset is not None else None, _f(out),
                             b, h, d, scale, eps)
+    return out
+
+
+# GGUF weight types of the output projection (GGML's ggml_type numbers)
+W_Q8_0, W_Q4K, W_Q5K, W_Q6K = 8, 12, 13, 14
+W_BLOCK = {W_Q8_0: 32, W_Q4K: 256, W_Q5K: 256, W_Q6K: 256}
+W_BLOCK_BYTES = {W_Q8_0: 34, W_Q4K: 144, W_Q5K: 176, W_Q6K: 210}
+
+
+def dequantize_weight(b: np.ndarray, w_type: int, n: int) -> np.ndarray:
+    """orc_{q8_0,q4k,q5k,q6k}_dequantize of n elements of GGUF type w_type."""
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    assert b.size >= n // W_BLOCK[w_type] * W_BLOCK_BYTES[w_type]
+    y = np.zeros(n, dtype=np.float32)
+    fn = {W_Q8_0: lib().orc_q8_0_dequantize, W_Q4K: lib().orc_q4k_dequantize,
+          W_Q5K: lib().orc_q5k_dequantize, W_Q6K: lib().orc_q6k_dequantize}[w_type]
+    fn(_u8(b), _f(y), n)
+    return y
+
+
+def gated_oproj(attn, gate, w_bytes, w_type: int, out_dim: int):
+    """orc_gated_oproj: attn, gate [b, in_dim] f32 (gate None: no gating), w_bytes the uint8
+    rows of GGUF type w_type [out_dim * row bytes]. Returns [b, out_dim]."""
+    b, in_dim = attn.shape
+    assert w_bytes.size == out_dim * lib().orc_weight_row_bytes(w_type, in_dim)
+    out = np.empty((b, out_dim), np.float32)
+    rc = lib().orc_gated_oproj(_f(attn), _f(gate) if gate is not None else None, _u8(w_bytes),
+                               w_type, _f(out), b, in_dim, out_dim)
+    assert rc == 0, rc
     return out
 
 

@@ -404,6 +404,68 @@ void orc_q4k_dequantize(const uint8_t *in, float *y, size_t n) {
   }
 }
 
+/* GGUF Q5_K: 176-byte superblocks {f16 d, f16 dmin, 12 B 6-bit scale/min codes (the Q4K
+ * packing), 32 B high bits qh, 128 B low nibbles qs}. Element 64 c + l (c = 0..3, l < 32)
+ * takes the low nibble of qs[32 c + l] plus 16 if bit 2 c of qh[l] is set, scaled by
+ * sub-block 2 c; element 64 c + 32 + l takes the high nibble plus bit 2 c + 1, scaled by
+ * sub-block 2 c + 1. y = (d * sc) * code - dmin * m in f32 (upstream candle k_quants.rs
+ * BlockQ5K::to_float; ggml dequantize_row_q5_K). */
+void orc_q5k_dequantize(const uint8_t *in, float *y, size_t n) {
+  for (size_t b = 0; b < n / 256; ++b) {
+    const uint8_t *blk = in + 176 * b;
+    const float d = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+    const float min = orc_f16_to_f32((uint16_t)(blk[2] | (blk[3] << 8)));
+    const uint8_t *sc = blk + 4, *qh = blk + 16, *qs = blk + 48;
+    float *yb = y + 256 * b;
+    for (int c = 0; c < 4; ++c) {
+      uint8_t s, m;
+      orc_get_scale_min_k4(2 * c, sc, &s, &m);
+      const float d1 = d * (float)s, m1 = min * (float)m;
+      orc_get_scale_min_k4(2 * c + 1, sc, &s, &m);
+      const float d2 = d * (float)s, m2 = min * (float)m;
+      const uint8_t u1 = (uint8_t)(1u << (2 * c)), u2 = (uint8_t)(2u << (2 * c));
+      for (int l = 0; l < 32; ++l) {
+        const float add = (qh[l] & u1) ? 16.0f : 0.0f;
+        yb[64 * c + l] = d1 * ((float)(qs[32 * c + l] & 0xF) + add) - m1;
+      }
+      for (int l = 0; l < 32; ++l) {
+        const float add = (qh[l] & u2) ? 16.0f : 0.0f;
+        yb[64 * c + 32 + l] = d2 * ((float)(qs[32 * c + l] >> 4) + add) - m2;
+      }
+    }
+  }
+}
+
+/* GGUF Q6_K: 210-byte superblocks {128 B low nibbles ql, 64 B high bit pairs qh, 16 int8
+ * scales, f16 d (last)}. In half h (elements 128 h ..) with l < 32: groups g = 0..3 hold
+ * elements 128 h + 32 g + l; the low 4 bits come from ql[64 h + l + 32 (g & 1)] (low
+ * nibble for g < 2, high for g >= 2), bits 4-5 from bits 2 g, 2 g + 1 of qh[32 h + l];
+ * the signed code is that minus 32, scaled by scales[8 h + 2 g + l / 16], which is
+ * scales[e / 16] for element e. y = (d * sc) * q in f32 (upstream candle k_quants.rs
+ * BlockQ6K::to_float; ggml dequantize_row_q6_K). */
+void orc_q6k_dequantize(const uint8_t *in, float *y, size_t n) {
+  for (size_t b = 0; b < n / 256; ++b) {
+    const uint8_t *blk = in + 210 * b;
+    const float d = orc_f16_to_f32((uint16_t)(blk[208] | (blk[209] << 8)));
+    float *yb = y + 256 * b;
+    for (int h = 0; h < 2; ++h) {
+      const uint8_t *ql = blk + 64 * h, *qh = blk + 128 + 32 * h;
+      const int8_t *sc = (const int8_t *)(blk + 192 + 8 * h);
+      for (int l = 0; l < 32; ++l) {
+        const int is = l / 16;
+        const int q1 = (int)((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32;
+        const int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+        const int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+        const int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+        yb[128 * h + l] = d * (float)sc[is] * (float)q1;
+        yb[128 * h + l + 32] = d * (float)sc[is + 2] * (float)q2;
+        yb[128 * h + l + 64] = d * (float)sc[is + 4] * (float)q3;
+        yb[128 * h + l + 96] = d * (float)sc[is + 6] * (float)q4;
+      }
+    }
+  }
+}
+
 /* ------------------------------------------------------------------ */
 /* Seeded synthetic data: Philox4x32-10 + Irwin-Hall(8) normal          */
 /* ------------------------------------------------------------------ */
@@ -942,17 +1004,36 @@ void orc_deltanet_step(const float *q, const float *k, const float *v, const flo
 /* Gated output projection with Q4K weights (qwen3_next.rs:2657-2680)  */
 /* ------------------------------------------------------------------ */
 
-void orc_gated_oproj_q4k(const float *attn, const float *gate, const uint8_t *w, float *out,
-                         int batch, int in_dim, int out_dim) {
+size_t orc_weight_row_bytes(int w_type, int in_dim) {
+  switch (w_type) {
+    case ORC_W_Q8_0: return (size_t)(in_dim / 32) * 34;
+    case ORC_W_Q4K: return (size_t)(in_dim / 256) * 144;
+    case ORC_W_Q5K: return (size_t)(in_dim / 256) * 176;
+    case ORC_W_Q6K: return (size_t)(in_dim / 256) * 210;
+    default: return 0;
+  }
+}
+
+int orc_gated_oproj(const float *attn, const float *gate, const uint8_t *w, int w_type,
+                    float *out, int batch, int in_dim, int out_dim) {
+  const size_t row_bytes = orc_weight_row_bytes(w_type, in_dim);
+  const int blk = w_type == ORC_W_Q8_0 ? 32 : 256;
+  if (row_bytes == 0 || in_dim <= 0 || in_dim % blk != 0 || batch < 0 || out_dim < 0)
+    return ORC_ERR_ARG;
   float *y = (float *)malloc(sizeof(float) * (size_t)in_dim);
   float *row = (float *)malloc(sizeof(float) * (size_t)in_dim);
-  const size_t row_bytes = (size_t)(in_dim / 256) * 144;
   for (int b = 0; b < batch; ++b) {
     const float *x = attn + (size_t)b * in_dim;
     for (int i = 0; i < in_dim; ++i)
       y[i] = gate ? x[i] * (1.0f / (1.0f + expf(-gate[(size_t)b * in_dim + i]))) : x[i];
     for (int o = 0; o < out_dim; ++o) {
-      orc_q4k_dequantize(w + (size_t)o * row_bytes, row, (size_t)in_dim);
+      const uint8_t *wr = w + (size_t)o * row_bytes;
+      switch (w_type) {
+        case ORC_W_Q8_0: orc_q8_0_dequantize(wr, row, (size_t)in_dim); break;
+        case ORC_W_Q4K: orc_q4k_dequantize(wr, row, (size_t)in_dim); break;
+        case ORC_W_Q5K: orc_q5k_dequantize(wr, row, (size_t)in_dim); break;
+        default: orc_q6k_dequantize(wr, row, (size_t)in_dim); break;
+      }
       float acc = 0.0f;
       for (int i = 0; i < in_dim; ++i) acc += row[i] * y[i];
       out[(size_t)b * out_dim + o] = acc;
@@ -960,4 +1041,10 @@ void orc_gated_oproj_q4k(const float *attn, const float *gate, const uint8_t *w,
   }
   free(y);
   free(row);
+  return ORC_OK;
+}
+
+void orc_gated_oproj_q4k(const float *attn, const float *gate, const uint8_t *w, float *out,
+                         int batch, int in_dim, int out_dim) {
+  (void)orc_gated_oproj(attn, gate, w, ORC_W_Q4K, out, batch, in_dim, out_dim);
 }

@@ -70,8 +70,16 @@
  *                               The fused CUDA kernel behind ops.rs:391-403 lives in
  *                               the absent candle fork, so its rounding is UNPINNED
  *                               (tolerance-level pinned).
- *   gated o_proj (Q4K wo) ..... pinned: float64 numpy restatement of W_deq @ (x * sigmoid
- *                               (g)) with W_deq from the pinned Q4K dequantizer, and closed
+ *   Q5K / Q6K dequantize ...... pinned against the published GGML block layouts (the
+ *                               reference holds no Q5K/Q6K vectors): blocks packed element
+ *                               by element decode bit-exactly to the closed form, single-bit
+ *                               perturbations move exactly the element the layout names, a
+ *                               Q5K block without high bits decodes as the Q4K block
+ *                               (tests/test_oracle_kquants.py). The fork's decoders are
+ *                               absent; a divergence of the fork from upstream would not show.
+ *   gated o_proj (Q8_0/Q4K/Q5K/Q6K wo)
+ *                               pinned: float64 numpy restatement of W_deq @ (x * sigmoid
+ *                               (g)) with W_deq from the pinned dequantizers, and closed
  *                               forms (gate -> +inf passes x, -inf gives 0, 0 halves it).
  *                               The reference's QMatMul (candle fork, absent) may quantize x
  *                               before its dot products; that rounding is UNPINNED.
@@ -89,6 +97,8 @@ extern "C" {
 /* Same numbering as include/pkv.h */
 enum { ORC_F16 = 1, ORC_BF16 = 2, ORC_Q8_0 = 3, ORC_Q4K = 4 };
 enum { ORC_OK = 0, ORC_ERR_OVERFLOW = 1, ORC_ERR_OFFSET = 2, ORC_ERR_ARG = 3 };
+/* GGUF weight types of the output projection: GGML's ggml_type numbers */
+enum { ORC_W_Q8_0 = 8, ORC_W_Q4K = 12, ORC_W_Q5K = 13, ORC_W_Q6K = 14 };
 
 /* ---- scalar conversions (half crate semantics) ---- */
 uint16_t orc_f32_to_f16(float x);
@@ -107,6 +117,8 @@ void orc_make_qkx1_quants(const float *x, int n, int nmax, int ntry, float *scal
 void orc_get_scale_min_k4(int j, const uint8_t *scales, uint8_t *sc, uint8_t *m);
 void orc_q4k_quantize(const float *x, uint8_t *out, size_t n);
 void orc_q4k_dequantize(const uint8_t *in, float *y, size_t n);
+void orc_q5k_dequantize(const uint8_t *in, float *y, size_t n); /* 176 B per 256 */
+void orc_q6k_dequantize(const uint8_t *in, float *y, size_t n); /* 210 B per 256 */
 
 /* ---- seeded synthetic data (identical on the GPU side) ---- */
 void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
@@ -192,8 +204,12 @@ void orc_deltanet_step(const float *q, const float *k, const float *v, const flo
 
 /* Gated output projection (qwen3_next.rs:2657-2680): y = x * sigmoid(g) (f32:
  * 1 / (1 + expf(-g)), gate may be NULL), then out[b][o] = sum_i Wdq[o][i] y[i] with Wdq the
- * Q4K rows of w (out_dim rows of in_dim / 256 superblocks) dequantized by
- * orc_q4k_dequantize, summed in index order in f32. */
+ * rows of w (out_dim rows of in_dim elements in GGUF type w_type, ORC_W_*) dequantized by
+ * the matching orc_*_dequantize, summed in index order in f32. ORC_ERR_ARG for an unknown
+ * type or an in_dim that is not a whole number of blocks. */
+size_t orc_weight_row_bytes(int w_type, int in_dim);
+int orc_gated_oproj(const float *attn, const float *gate, const uint8_t *w, int w_type,
+                    float *out, int batch, int in_dim, int out_dim);
 void orc_gated_oproj_q4k(const float *attn, const float *gate, const uint8_t *w, float *out,
                          int batch, int in_dim, int out_dim);
 

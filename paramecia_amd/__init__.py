@@ -9,4 +9,5 @@ from .kv_cache import (  # noqa: F401
     KvCacheQuantization, LayerCheckpoint, LinearAttentionState, ModelKvState, PreallocatedQuantizedKvCache,
     PrefixCache, PrefixCacheEntry, PrefixLayerMismatch, QkPrep, RecurrentState, RotaryEmbedding,
     append_attend_batched, fill_normal, flash_attn, gated_o_proj, scale_channels,
+    WTYPE_Q4K, WTYPE_Q5K, WTYPE_Q6K, WTYPE_Q8_0,
 )

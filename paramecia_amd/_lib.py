@@ -30,7 +30,7 @@ SYMBOLS = (
     "pkv_prefix_restore", "pkv_fill_normal", "pkv_scale_channels", "pkv_copy_segments",
     "pkv_rope_tables_host", "pkv_rope_create", "pkv_rope_destroy", "pkv_rope_geometry",
     "pkv_append_prep", "pkv_append_attend_prep", "pkv_deltanet_step",
-    "pkv_gated_oproj_q4k", "pkv_prefix_serialized_size", "pkv_prefix_serialize",
+    "pkv_gated_oproj_q4k", "pkv_gated_oproj", "pkv_prefix_serialized_size", "pkv_prefix_serialize",
     "pkv_prefix_deserialize",
 )
 
@@ -133,6 +133,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "pkv_append_attend_prep": ([vp, P(QkPrep), vp, vp, vp, c_int, fl, c_i64, vp], c_int),
         "pkv_deltanet_step": ([vp] * 8 + [c_int] * 3 + [fl, fl, vp], c_int),
         "pkv_gated_oproj_q4k": ([vp] * 4 + [c_int] * 3 + [vp], c_int),
+        "pkv_gated_oproj": ([vp] * 3 + [c_int, vp] + [c_int] * 3 + [vp], c_int),
         "pkv_prefix_serialized_size": ([vp], c_sz),
         "pkv_prefix_serialize": ([vp, vp, c_sz, vp], c_int),
         "pkv_prefix_deserialize": ([vp, c_sz, P(vp), vp], c_int),

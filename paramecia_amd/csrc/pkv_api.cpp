@@ -1109,6 +1109,15 @@ int pkv_gated_oproj_q4k(const float *attn, const float *gate, const void *w_q4k,
                           out_dim, static_cast<hipStream_t>(stream));
 }
 
+int pkv_gated_oproj(const float *attn, const float *gate, const void *w, int w_type, float *out,
+                    int batch, int in_dim, int out_dim, pkv_stream stream) {
+  if (!attn || !w || !out) return set_error(PKV_ERR_ARG, "null argument");
+  if (batch <= 0 || in_dim <= 0 || out_dim <= 0)
+    return set_error(PKV_ERR_ARG, "batch, in_dim and out_dim must be > 0");
+  return launch_oproj(attn, gate, static_cast<const uint8_t *>(w), w_type, out, batch, in_dim,
+                      out_dim, static_cast<hipStream_t>(stream));
+}
+
 int pkv_fill_normal(float *dst, size_t n, uint64_t seed, uint64_t stream_id, float scale,
                     pkv_stream stream) {
   if (!dst && n) return set_error(PKV_ERR_ARG, "null destination");

@@ -171,6 +171,8 @@ int launch_copy_segments(void *const *dst, const void *const *src, const size_t 
                          Workspace &ws, hipStream_t s);
 int launch_oproj_q4k(const float *attn, const float *gate, const uint8_t *w, float *out,
                      int batch, int in_dim, int out_dim, hipStream_t s);
+int launch_oproj(const float *attn, const float *gate, const uint8_t *w, int w_type, float *out,
+                 int batch, int in_dim, int out_dim, hipStream_t s);
 int launch_deltanet_step(const float *q, const float *k, const float *v, const float *gate,
                          const float *beta, float *state, float *gate_offset, float *out,
                          int batch, int heads, int head_dim, float scale, float eps,

@@ -294,22 +294,32 @@ def append_attend_batched(caches: Sequence[PreallocatedQuantizedKvCache], k: tor
     return out
 
 
-def gated_o_proj(attn_output: torch.Tensor, gate: Optional[torch.Tensor], wo_q4k: torch.Tensor,
-                 out_dim: int) -> torch.Tensor:
-    """The attention's gated output projection with a Q4K wo (qwen3_next.rs:2657-2680):
-    attn_output, gate [b, l, in_dim] f32 (gate None: no gating), wo_q4k the uint8 GGUF
-    bytes [out_dim, in_dim / 256, 144]. Returns [b, l, out_dim] (pkv_gated_oproj_q4k)."""
+# GGUF weight types of the output projection (GGML's ggml_type numbers)
+WTYPE_Q8_0, WTYPE_Q4K, WTYPE_Q5K, WTYPE_Q6K = 8, 12, 13, 14
+_W_BLOCK = {WTYPE_Q8_0: (32, 34), WTYPE_Q4K: (256, 144), WTYPE_Q5K: (256, 176),
+            WTYPE_Q6K: (256, 210)}
+
+
+def gated_o_proj(attn_output: torch.Tensor, gate: Optional[torch.Tensor], wo: torch.Tensor,
+                 out_dim: int, w_type: int = WTYPE_Q4K) -> torch.Tensor:
+    """The attention's gated output projection (qwen3_next.rs:2657-2680): attn_output, gate
+    [b, l, in_dim] f32 (gate None: no gating), wo the uint8 GGUF bytes of self.wo in GGUF
+    type w_type (Q4K: [out_dim, in_dim / 256, 144]; Q5K 176 B, Q6K 210 B per 256 inputs;
+    Q8_0 34 B per 32). Returns [b, l, out_dim] (pkv_gated_oproj)."""
     x = _f32(attn_output, "attn_output")
     g = _f32(gate, "gate") if gate is not None else None
     if g is not None and g.shape != x.shape:
         raise KvCacheError("gate must have the attention output's shape")
+    if w_type not in _W_BLOCK:
+        raise KvCacheError(f"unsupported weight type {w_type} (Q8_0 8, Q4K 12, Q5K 13, Q6K 14)")
     in_dim = x.shape[-1]
     rows = x.numel() // in_dim
-    if wo_q4k.dtype != torch.uint8 or wo_q4k.numel() != out_dim * (in_dim // 256) * 144:
-        raise KvCacheError("wo_q4k must hold out_dim x in_dim / 256 Q4K superblocks (144 B)")
+    blk, nbytes = _W_BLOCK[w_type]
+    if wo.dtype != torch.uint8 or wo.numel() != out_dim * (in_dim // blk) * nbytes:
+        raise KvCacheError(f"wo must hold out_dim x in_dim / {blk} blocks of {nbytes} B")
     out = torch.empty(x.shape[:-1] + (out_dim,), dtype=torch.float32, device=x.device)
-    _call(lib().pkv_gated_oproj_q4k(_ptr(x), _ptr(g), _ptr(wo_q4k.contiguous()), _ptr(out), rows,
-                                    in_dim, out_dim, torch.cuda.current_stream().cuda_stream))
+    _call(lib().pkv_gated_oproj(_ptr(x), _ptr(g), _ptr(wo.contiguous()), w_type, _ptr(out), rows,
+                                in_dim, out_dim, torch.cuda.current_stream().cuda_stream))
     return out
 
 

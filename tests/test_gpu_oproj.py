@@ -1,8 +1,9 @@
-"""GPU parity of the gated output projection with a Q4K wo (pkv_gated_oproj_q4k; the step
-after the attention, qwen3_next.rs:2657-2680) against the CPU oracle's f32
-dequantize-then-dot on the same seeded inputs, within 2e-3 absolute + 1e-3 relative.
-The reference's QMatMul lives in the absent candle fork, so its own rounding (it may
-quantize the activations first) is not the bar; the GGUF Q4K weight bytes are shared."""
+"""GPU parity of the gated output projection (pkv_gated_oproj_q4k, pkv_gated_oproj; the step
+after the attention, qwen3_next.rs:2657-2680) with a Q4K, Q5K, Q6K or Q8_0 wo against the
+CPU oracle's f32 dequantize-then-dot on the same seeded inputs, within 2e-3 absolute +
+1e-3 relative. The reference's QMatMul lives in the absent candle fork, so its own
+rounding (it may quantize the activations first) is not the bar; the GGUF weight bytes
+are shared. Q5K/Q6K/Q8_0 weights are random valid blocks (tests/kquant_blocks.py)."""
 import sys
 
 import numpy as np
@@ -14,6 +15,7 @@ pytestmark = pytest.mark.gpu
 
 ATOL, RTOL = 2e-3, 1e-3
 Q4K = 4
+W_Q8_0, W_Q4K, W_Q5K, W_Q6K = 8, 12, 13, 14
 
 
 def say(*a):
@@ -64,3 +66,41 @@ def test_rejects_unsupported_width(pk):
     out = torch.zeros((1, 8), device="cuda")
     assert lib().pkv_gated_oproj_q4k(x.data_ptr(), None, w.data_ptr(), out.data_ptr(), 1, 1024, 8,
                                      torch.cuda.current_stream().cuda_stream) == ERR_UNSUPPORTED
+
+
+# every weight type through pkv_gated_oproj: both row forms (batch < 4, >= 4), both input
+# widths, a ragged row tail (out_dim not a multiple of the 4 or 8 rows of a workgroup) and
+# no gate
+SHAPES = [(1, 4096, 2048, True), (3, 4096, 100, True), (2, 8192, 64, True),
+          (2, 4096, 42, False), (5, 4096, 70, True), (4, 8192, 22, True)]
+
+
+@pytest.mark.parametrize("w_type", [W_Q4K, W_Q5K, W_Q6K, W_Q8_0])
+@pytest.mark.parametrize("b,in_dim,out_dim,gated", SHAPES)
+def test_weight_types_match_oracle(pk, orc, w_type, b, in_dim, out_dim, gated):
+    from kquant_blocks import random_weight_bytes
+    say(f"oproj w_type={w_type} b={b} in={in_dim} out={out_dim} gated={gated}")
+    rng = np.random.default_rng(1000 * w_type + in_dim + out_dim + b)
+    wb = random_weight_bytes(rng, w_type, out_dim, in_dim, d_scale=1e-4)
+    x = rng.standard_normal((b, in_dim)).astype(np.float32)
+    g = rng.standard_normal((b, in_dim)).astype(np.float32) if gated else None
+    out = pk.gated_o_proj(dev(x[:, None]), dev(g[:, None]) if gated else None, dev(wb), out_dim,
+                          w_type=w_type)
+    ref = orc.gated_oproj(x, g, wb, w_type, out_dim)
+    assert np.abs(ref).max() > 0.1  # the weights are not degenerate
+    np.testing.assert_allclose(host(out)[:, 0], ref, atol=ATOL, rtol=RTOL)
+
+
+def test_generic_entry_checks(pk):
+    from paramecia_amd._lib import lib, ERR_UNSUPPORTED
+    say("oproj: generic entry argument checks")
+    x = torch.zeros((1, 4096), device="cuda")
+    w = torch.zeros(8 * 16 * 210, dtype=torch.uint8, device="cuda")
+    out = torch.zeros((1, 8), device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    assert lib().pkv_gated_oproj(x.data_ptr(), None, w.data_ptr(), 2, out.data_ptr(), 1, 4096, 8,
+                                 s) == ERR_UNSUPPORTED  # Q4_1: no kernel
+    assert lib().pkv_gated_oproj(x.data_ptr(), None, w.data_ptr(), W_Q6K, out.data_ptr(), 1, 2048,
+                                 8, s) == ERR_UNSUPPORTED
+    with pytest.raises(pk.KvCacheError):
+        pk.gated_o_proj(x[:, None], None, w[:-1], 8, w_type=W_Q6K)
