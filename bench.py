@@ -770,26 +770,34 @@ def run_config6(args):
 # ------------------------------------------------------------------ config 7
 def run_config7(args):
     """The step after the attention in the 12 full-attention layers: sigmoid gate and the
-    Q4K wo projection (pkv_gated_oproj_q4k; qwen3_next.rs:2657-2680), 4096 -> 2048 (the
-    Qwen3-Next-80B hidden size), batch --op-batch tokens. Not a BASELINE config."""
+    wo projection (pkv_gated_oproj; qwen3_next.rs:2657-2680), 4096 -> 2048 (the
+    Qwen3-Next-80B hidden size), batch --op-batch tokens, weight type --op-wtype. From 8
+    tokens on the library runs the batched MFMA form (pkv_oproj_mfma.hip), below it the
+    per-token GEMV. Not a BASELINE config."""
     import torch
     import paramecia_amd as pk
     from paramecia_amd import workloads as W
 
     B, L = args.op_batch, W.N_FULL
     IN, OUT = W.NUM_HEADS * W.HEAD_DIM, W.HIDDEN
+    wt = W.W_TYPES[args.op_wtype]
+    blk, nbytes = W.W_BLOCK[wt]
     nsb = IN // 256
     ws, xs, gs = [], [], []
     for l in range(L):
-        # the layer's wo, drawn N(0, 0.02) and quantized to GGUF Q4K rows by the library's
-        # own quantize-on-append kernel (one 256-element superblock per cache row)
-        w = torch.empty((1, 1, OUT * nsb, 256), device="cuda")
-        pk.fill_normal(w, W.SEED, W.stream_id(7, W.T_WO, l), 0.02)
-        c = pk.PreallocatedQuantizedKvCache(1, 1, OUT * nsb, 256, pk.KvCacheQuantization.Q4K)
-        c.append_quantized(w, w)
-        kb, _ = c.raw_bytes()
-        ws.append(kb.clone())
-        del c, w, kb
+        if wt == 12:
+            # the layer's wo, drawn N(0, 0.02) and quantized to GGUF Q4K rows by the
+            # library's own quantize-on-append kernel (one superblock per cache row)
+            w = torch.empty((1, 1, OUT * nsb, 256), device="cuda")
+            pk.fill_normal(w, W.SEED, W.stream_id(7, W.T_WO, l), 0.02)
+            c = pk.PreallocatedQuantizedKvCache(1, 1, OUT * nsb, 256, pk.KvCacheQuantization.Q4K)
+            c.append_quantized(w, w)
+            kb, _ = c.raw_bytes()
+            ws.append(kb.clone())
+            del c, w, kb
+        else:
+            # random valid blocks of the type (no quantizer for it on the path)
+            ws.append(torch.from_numpy(W.kquant_rows(wt, OUT, IN, W.SEED + 101 * l)).cuda())
         x = torch.empty((B, 1, IN), device="cuda")
         g = torch.empty((B, 1, IN), device="cuda")
         pk.fill_normal(x, W.SEED, W.stream_id(7, W.T_Q, l))
@@ -800,36 +808,53 @@ def run_config7(args):
 
     def step():
         for l in range(L):
-            outs[l] = pk.gated_o_proj(xs[l], gs[l], ws[l], OUT)
+            outs[l] = pk.gated_o_proj(xs[l], gs[l], ws[l], OUT, w_type=wt)
 
+    step()  # grow the library's workspace before any capture
     ms_eager = event_time(torch, step, args.steps, args.warmup)
     ms = graph_time(torch, step, args.steps, args.warmup)
-    per_layer = OUT * nsb * 144 + B * (2 * IN * 4 + OUT * 4)  # weights, attn + gate in, out
+    wbytes = OUT * (IN // blk) * nbytes
+    per_layer = wbytes + B * (2 * IN * 4 + OUT * 4)  # weights, attn + gate in, out
     gbs = per_layer * L / (ms * 1e-3) / 1e9
-    r = base_result(7, "gated o_proj µs/step (12 full-attention layers, Q4K wo 4096 -> 2048)",
+    batched = B >= 8 and wt != 8
+    name = args.op_wtype.upper()
+    extra = {"eager_us_per_step": round(ms_eager * 1000, 2), "w_type": name,
+             "form": "batched MFMA" if batched else "per-token GEMV"}
+    if batched:
+        flops = 2.0 * B * OUT * IN  # algorithmic: one multiply-add per weight and token
+        tfs = flops * L / (ms * 1e-3) / 1e12
+        extra["roofline"] = {"kernel": "oproj_xprep + oproj_mfma (+ reduce) per layer, its share "
+                                       "of the graph-replayed step", "bound": "mfma",
+                             "achieved": round(tfs, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                             "frac": round(tfs / 2500.0, 4), "flops_per_launch": flops,
+                             "avg_launch_us": round(ms * 1000 / L, 3), "traffic": None,
+                             "hbm_bytes_per_launch": per_layer,
+                             "hbm_GBps": round(gbs, 1)}
+    else:
+        extra["roofline"] = {"kernel": f"oproj GEMV ({name}; one layer, its share of the "
+                                       "graph-replayed step)", "bound": "hbm",
+                             "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": per_layer,
+                             "avg_launch_us": round(ms * 1000 / L, 3), "traffic": None}
+    r = base_result(7, f"gated o_proj µs/step (12 full-attention layers, {name} wo 4096 -> 2048)",
                     round(ms * 1000, 2), "us/step", False, ms, args,
-                    f"config7: sigmoid(gate) * attention output, then the Q4K wo projection "
-                    f"(4096 -> 2048), 12 layers, {B} token(s)",
-                    {"eager_us_per_step": round(ms_eager * 1000, 2),
-                     "roofline": {"kernel": "oproj_q4k_kernel (one layer, its share of the "
-                                            "graph-replayed step)", "bound": "hbm",
-                                  "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                  "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": per_layer,
-                                  "avg_launch_us": round(ms * 1000 / L, 3), "traffic": None}})
+                    f"config7: sigmoid(gate) * attention output, then the {name} wo projection "
+                    f"(4096 -> 2048), 12 layers, {B} token(s)", extra)
     if not args.no_cpu_baseline:
-        import numpy as np
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle as orc
-        x0, g0 = xs[0][:, 0].cpu().numpy().copy(), gs[0][:, 0].cpu().numpy().copy()
+        nb = min(B, 4)  # the scalar oracle takes ~0.1 s per token and layer
+        x0, g0 = xs[0][:nb, 0].cpu().numpy().copy(), gs[0][:nb, 0].cpu().numpy().copy()
         w0 = ws[0].cpu().numpy()
         t0 = time.perf_counter()
-        orc.gated_oproj_q4k(x0, g0, w0, OUT)
+        orc.gated_oproj(x0, g0, w0, wt, OUT)
         dt = time.perf_counter() - t0
-        r["cpu_baseline"] = {"value": round(dt * L * 1e6, 1), "unit": "us/step", "cores": 1,
-                             "kind": "port",
-                             "sample": f"config 7: 1 of {L} layers (dequantize every wo row, "
-                                       f"then the dot products) timed once and multiplied by "
-                                       f"{L}; scalar oracle on {cpu_model()}"}
+        r["cpu_baseline"] = {"value": round(dt * L * B / nb * 1e6, 1), "unit": "us/step",
+                             "cores": 1, "kind": "port",
+                             "sample": f"config 7: {nb} of {B} tokens of 1 of {L} layers "
+                                       f"(dequantize every wo row per token, then the dot "
+                                       f"products) timed once and scaled by {B / nb:g} x {L}; "
+                                       f"scalar oracle on {cpu_model()}"}
     return r
 
 
@@ -843,6 +868,8 @@ def main() -> int:
                          "7 (gated o_proj) or all")
     ap.add_argument("--dn-batch", type=int, default=1, help="config 6: sequences per step")
     ap.add_argument("--op-batch", type=int, default=1, help="config 7: tokens per step")
+    ap.add_argument("--op-wtype", default="q4k", choices=["q4k", "q5k", "q6k", "q8_0"],
+                    help="config 7: GGUF type of wo")
     ap.add_argument("--cached", type=int, default=131072, help="config 3: cached tokens")
     ap.add_argument("--layers", type=int, default=12, help="config 3: layers")
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -33,6 +33,7 @@ SOURCES = {
     "pkv_util.hip": [],
     "pkv_deltanet.hip": [],
     "pkv_oproj.hip": [],
+    "pkv_oproj_mfma.hip": [],
     "pkv_prep.hip": ["-ffp-contract=off"],
     "pkv_api.cpp": ["-x", "hip"],
 }

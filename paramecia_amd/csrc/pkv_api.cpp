@@ -1100,22 +1100,27 @@ int pkv_deltanet_step(const float *q, const float *k, const float *v, const floa
                               head_dim, scale, eps, static_cast<hipStream_t>(stream));
 }
 
-int pkv_gated_oproj_q4k(const float *attn, const float *gate, const void *w_q4k, float *out,
-                        int batch, int in_dim, int out_dim, pkv_stream stream) {
-  if (!attn || !w_q4k || !out) return set_error(PKV_ERR_ARG, "null argument");
-  if (batch <= 0 || in_dim <= 0 || out_dim <= 0)
-    return set_error(PKV_ERR_ARG, "batch, in_dim and out_dim must be > 0");
-  return launch_oproj_q4k(attn, gate, static_cast<const uint8_t *>(w_q4k), out, batch, in_dim,
-                          out_dim, static_cast<hipStream_t>(stream));
-}
+// From this many tokens on, the k-quant projection runs as the batched MFMA form (each
+// decoded weight serves 32 tokens); below it, per-token GEMV workgroups.
+constexpr int kOprojMfmaMinBatch = 8;
 
 int pkv_gated_oproj(const float *attn, const float *gate, const void *w, int w_type, float *out,
                     int batch, int in_dim, int out_dim, pkv_stream stream) {
   if (!attn || !w || !out) return set_error(PKV_ERR_ARG, "null argument");
   if (batch <= 0 || in_dim <= 0 || out_dim <= 0)
     return set_error(PKV_ERR_ARG, "batch, in_dim and out_dim must be > 0");
-  return launch_oproj(attn, gate, static_cast<const uint8_t *>(w), w_type, out, batch, in_dim,
-                      out_dim, static_cast<hipStream_t>(stream));
+  const auto *wb = static_cast<const uint8_t *>(w);
+  const auto s = static_cast<hipStream_t>(stream);
+  if (batch >= kOprojMfmaMinBatch &&
+      (w_type == PKV_WTYPE_Q4K || w_type == PKV_WTYPE_Q5K || w_type == PKV_WTYPE_Q6K))
+    return launch_oproj_mfma(attn, gate, wb, w_type, out, batch, in_dim, out_dim,
+                             util_workspace(), s);
+  return launch_oproj(attn, gate, wb, w_type, out, batch, in_dim, out_dim, s);
+}
+
+int pkv_gated_oproj_q4k(const float *attn, const float *gate, const void *w_q4k, float *out,
+                        int batch, int in_dim, int out_dim, pkv_stream stream) {
+  return pkv_gated_oproj(attn, gate, w_q4k, PKV_WTYPE_Q4K, out, batch, in_dim, out_dim, stream);
 }
 
 int pkv_fill_normal(float *dst, size_t n, uint64_t seed, uint64_t stream_id, float scale,

@@ -169,10 +169,12 @@ int launch_scale_channels(float *x, size_t rows, int dim, const int *ch, int n_c
                           float factor, hipStream_t s);
 int launch_copy_segments(void *const *dst, const void *const *src, const size_t *bytes, int n,
                          Workspace &ws, hipStream_t s);
-int launch_oproj_q4k(const float *attn, const float *gate, const uint8_t *w, float *out,
-                     int batch, int in_dim, int out_dim, hipStream_t s);
 int launch_oproj(const float *attn, const float *gate, const uint8_t *w, int w_type, float *out,
                  int batch, int in_dim, int out_dim, hipStream_t s);
+// ---- launcher (pkv_oproj_mfma.hip): the batched form, Q4K/Q5K/Q6K ----
+int launch_oproj_mfma(const float *attn, const float *gate, const uint8_t *w, int w_type,
+                      float *out, int batch, int in_dim, int out_dim, Workspace &ws,
+                      hipStream_t s);
 int launch_deltanet_step(const float *q, const float *k, const float *v, const float *gate,
                          const float *beta, float *state, float *gate_offset, float *out,
                          int batch, int heads, int head_dim, float scale, float eps,

@@ -457,9 +457,4 @@ int launch_oproj(const float *attn, const float *gate, const uint8_t *w, int w_t
   return PKV_OK;
 }
 
-int launch_oproj_q4k(const float *attn, const float *gate, const uint8_t *w, float *out,
-                     int batch, int in_dim, int out_dim, hipStream_t s) {
-  return launch_oproj(attn, gate, w, kWQ4K, out, batch, in_dim, out_dim, s);
-}
-
 }  // namespace pkv

@@ -80,3 +80,28 @@ def c5_channels(seed: int = SEED):
         if c not in chans:
             chans.append(c)
     return sorted(chans)
+
+
+# GGUF weight types of the output projection (GGML numbering) and their block geometry
+W_TYPES = {"q8_0": 8, "q4k": 12, "q5k": 13, "q6k": 14}
+W_BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+
+
+def kquant_rows(w_type: int, out_dim: int, in_dim: int, seed: int, d_scale: float = 1e-4):
+    """Synthetic GGUF weight bytes: out_dim rows of in_dim inputs of type w_type with
+    uniform random codes and scale codes and finite f16 (d, dmin) of about d_scale (so a
+    row dotted with N(0, 1) inputs stays O(1)). numpy, seeded; uint8 [out_dim * row bytes]."""
+    import numpy as np
+    blk, nbytes = W_BLOCK[w_type]
+    nb = out_dim * in_dim // blk
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, (nb, nbytes), dtype=np.uint8)
+    d = (np.abs(rng.standard_normal(nb)) * d_scale + d_scale / 8).astype(np.float16)
+    if w_type == 14:
+        b[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    else:
+        b[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    if w_type in (12, 13):
+        dmin = (np.abs(rng.standard_normal(nb)) * d_scale).astype(np.float16)
+        b[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+    return np.ascontiguousarray(b.reshape(-1))

@@ -104,3 +104,69 @@ def test_generic_entry_checks(pk):
                                  8, s) == ERR_UNSUPPORTED
     with pytest.raises(pk.KvCacheError):
         pk.gated_o_proj(x[:, None], None, w[:-1], 8, w_type=W_Q6K)
+
+
+# ---- the batched MFMA form (from 8 tokens on, Q4K/Q5K/Q6K): fp16 hi/lo activations and
+# exact scaled weight codes. Besides the oracle's tolerance, the error relative to the
+# outputs' RMS must stay below 2e-5: dropping the lo halves (fp16 activations only) gives
+# about 2.4e-4, a wrong scale or code far more.
+def rms_rel_err(got, ref):
+    ref = np.asarray(ref, np.float64)
+    return np.abs(np.asarray(got, np.float64) - ref).max() / np.sqrt((ref ** 2).mean())
+
+
+BATCHED = [(8, 4096, 256, True), (33, 4096, 300, True), (40, 8192, 264, False),
+           (96, 4096, 520, True), (7, 4096, 64, True)]
+
+
+@pytest.mark.parametrize("w_type", [W_Q4K, W_Q5K, W_Q6K])
+@pytest.mark.parametrize("b,in_dim,out_dim,gated", BATCHED)
+def test_batched_form_matches_oracle(pk, orc, w_type, b, in_dim, out_dim, gated):
+    from kquant_blocks import random_weight_bytes
+    say(f"oproj batched w_type={w_type} b={b} in={in_dim} out={out_dim} gated={gated}")
+    rng = np.random.default_rng(3000 * w_type + in_dim + out_dim + b)
+    wb = random_weight_bytes(rng, w_type, out_dim, in_dim, d_scale=1e-4)
+    x = rng.standard_normal((b, in_dim)).astype(np.float32)
+    g = rng.standard_normal((b, in_dim)).astype(np.float32) if gated else None
+    out = host(pk.gated_o_proj(dev(x), dev(g) if gated else None, dev(wb), out_dim,
+                               w_type=w_type))
+    ref = orc.gated_oproj(x, g, wb, w_type, out_dim)
+    np.testing.assert_allclose(out, ref, atol=ATOL, rtol=RTOL)
+    assert rms_rel_err(out, ref) < 2e-5
+
+
+def test_batched_form_token_scales(pk, orc):
+    """Per-token power-of-two scaling: rows of 1e-30, 1e4 and 0 magnitudes beside N(0, 1)
+    rows keep the relative accuracy of each row; the zero row gives exact zeros."""
+    from kquant_blocks import random_weight_bytes
+    say("oproj batched: token scales")
+    rng = np.random.default_rng(77)
+    b, in_dim, out_dim = 12, 4096, 96
+    wb = random_weight_bytes(rng, W_Q4K, out_dim, in_dim, d_scale=1e-4)
+    x = rng.standard_normal((b, in_dim)).astype(np.float32)
+    x[1] *= np.float32(1e-30)
+    x[2] *= np.float32(1e4)
+    x[3] = 0.0
+    out = host(pk.gated_o_proj(dev(x), None, dev(wb), out_dim, w_type=W_Q4K))
+    ref = orc.gated_oproj(x, None, wb, W_Q4K, out_dim)
+    assert np.all(out[3] == 0.0)
+    for r in (0, 1, 2, 4):
+        assert rms_rel_err(out[r], ref[r]) < 2e-5, r
+
+
+@pytest.mark.parametrize("w_type", [W_Q4K, W_Q6K])
+def test_batched_form_prefill_chunk(pk, orc, w_type):
+    """The config-2 prefill chunk at full size: 512 tokens through a 4096 -> 2048 wo, against
+    a float64 product over the oracle's dequantized rows."""
+    from kquant_blocks import random_weight_bytes
+    say(f"oproj batched: 512-token chunk w_type={w_type}")
+    rng = np.random.default_rng(512 + w_type)
+    b, in_dim, out_dim = 512, 4096, 2048
+    wb = random_weight_bytes(rng, w_type, out_dim, in_dim, d_scale=1e-4)
+    x = rng.standard_normal((b, in_dim)).astype(np.float32)
+    g = rng.standard_normal((b, in_dim)).astype(np.float32)
+    out = host(pk.gated_o_proj(dev(x[None]), dev(g[None]), dev(wb), out_dim, w_type=w_type))[0]
+    wdq = orc.dequantize_weight(wb, w_type, out_dim * in_dim).reshape(out_dim, in_dim)
+    y = x.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64)))
+    ref = y @ wdq.astype(np.float64).T
+    assert rms_rel_err(out, ref) < 2e-5
