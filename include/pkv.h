@@ -293,6 +293,54 @@ size_t pkv_prefix_serialized_size(const pkv_prefix *p);
 int pkv_prefix_serialize(const pkv_prefix *p, void *host_dst, size_t capacity, pkv_stream stream);
 int pkv_prefix_deserialize(const void *host_src, size_t n, pkv_prefix **out, pkv_stream stream);
 
+/* ---- Paged KV caches for multi-sequence serving (the survey's next row after the path:
+ * the reference preallocates one PreallocatedQuantizedKvCache per layer and sequence at
+ * max_seq_len, qn:343-380, and its serving caller LocalBackend keeps one sequence with a
+ * deep-copied prefix, paramecia-llm/src/backend/local.rs:743-800). A pool holds n_pages
+ * pages of page_tokens tokens (a power of two in [32, 2^20]) for one layer; a page is the
+ * K and V rows of page_tokens tokens x n_kv_heads in the pool's encoding (PKV_QUANT_*),
+ * laid out as a batch-1 cache of that capacity. A sequence is a list of pages. Work runs
+ * on the pool's stream, in order. Not thread-safe: one host thread per pool. */
+typedef struct pkv_pool pkv_pool;
+typedef struct pkv_seq pkv_seq;
+int pkv_pool_create(int quant, int n_kv_heads, int head_dim, int page_tokens, int n_pages,
+                    pkv_stream stream, pkv_pool **out);
+/* PKV_ERR_ARG while the pool still has sequences. */
+int pkv_pool_destroy(pkv_pool *p);
+int pkv_pool_free_pages(const pkv_pool *p);
+/* The stream later work on the pool's sequences is queued on (the caller orders it after
+ * work on the previous stream). */
+int pkv_pool_set_stream(pkv_pool *p, pkv_stream stream);
+int pkv_seq_create(pkv_pool *p, pkv_seq **out);
+/* Waits for the pool's stream, then returns the sequence's pages. */
+int pkv_seq_destroy(pkv_seq *s);
+int64_t pkv_seq_len(const pkv_seq *s);
+int pkv_seq_pages(const pkv_seq *s);
+/* A new sequence sharing every page of s (no copy; a shared, partly filled last page is
+ * copied when either sequence first appends into it). A prefix cache entry kept as a
+ * sequence is restored by a fork. */
+int pkv_seq_fork(const pkv_seq *s, pkv_seq **out);
+/* Keep tokens [0, new_len) (new_len >= len: no change); whole pages past it return to the
+ * pool. */
+int pkv_seq_truncate(pkv_seq *s, int64_t new_len);
+/* append_quantized (qn:431-509) into the sequence's pages: k, v [1, n_kv_heads, n,
+ * head_dim] f32; offset as pkv_append (-1 appends at the end, a smaller offset rewinds,
+ * a larger one -> PKV_ERR_OFFSET). PKV_ERR_OVERFLOW, with nothing written, when the
+ * pool lacks pages. */
+int pkv_seq_append(pkv_seq *s, const float *k, const float *v, int64_t n, int64_t offset);
+/* Attention over the sequence's keys, as pkv_attend: q [1, l, num_heads, head_dim],
+ * out the same shape. */
+int pkv_seq_attend(pkv_seq *s, const float *q, int l, int num_heads, float scale,
+                   int64_t q_offset, int causal, float *out);
+/* One decode query per sequence (varlen), all sequences in one pool: q, out
+ * [n, num_heads, head_dim]; each sees all its keys. Q4K / Q8_0 pools of the model's shape
+ * (16 query heads, 2 KV heads, head_dim 256) run one decode launch per 32 sequences over
+ * all their pages; other pools attend sequence by sequence. */
+int pkv_seq_decode_batched(pkv_seq *const *seqs, int n, const float *q, int num_heads,
+                           float scale, float *out);
+/* get_kv (qn:520-575): dequantized [1, n_kv_heads, len, head_dim] f32. */
+int pkv_seq_get_kv(const pkv_seq *s, float *k_out, float *v_out);
+
 /* ---- utilities ---- */
 /* Seeded synthetic data: dst[i] = normal(seed, stream_id, i) * scale, bit-identical
  * to the CPU oracle's generator (Philox4x32-10, Irwin-Hall of eight 22-bit draws). */

@@ -31,7 +31,10 @@ SYMBOLS = (
     "pkv_rope_tables_host", "pkv_rope_create", "pkv_rope_destroy", "pkv_rope_geometry",
     "pkv_append_prep", "pkv_append_attend_prep", "pkv_deltanet_step",
     "pkv_gated_oproj_q4k", "pkv_gated_oproj", "pkv_prefix_serialized_size", "pkv_prefix_serialize",
-    "pkv_prefix_deserialize",
+    "pkv_prefix_deserialize", "pkv_pool_create", "pkv_pool_destroy", "pkv_pool_free_pages",
+    "pkv_pool_set_stream", "pkv_seq_create", "pkv_seq_destroy", "pkv_seq_len", "pkv_seq_pages",
+    "pkv_seq_fork", "pkv_seq_truncate", "pkv_seq_append", "pkv_seq_attend",
+    "pkv_seq_decode_batched", "pkv_seq_get_kv",
 )
 
 
@@ -137,6 +140,20 @@ def _declare(L: ctypes.CDLL) -> None:
         "pkv_prefix_serialized_size": ([vp], c_sz),
         "pkv_prefix_serialize": ([vp, vp, c_sz, vp], c_int),
         "pkv_prefix_deserialize": ([vp, c_sz, P(vp), vp], c_int),
+        "pkv_pool_create": ([c_int] * 5 + [vp, P(vp)], c_int),
+        "pkv_pool_destroy": ([vp], c_int),
+        "pkv_pool_free_pages": ([vp], c_int),
+        "pkv_pool_set_stream": ([vp, vp], c_int),
+        "pkv_seq_create": ([vp, P(vp)], c_int),
+        "pkv_seq_destroy": ([vp], c_int),
+        "pkv_seq_len": ([vp], c_i64),
+        "pkv_seq_pages": ([vp], c_int),
+        "pkv_seq_fork": ([vp, P(vp)], c_int),
+        "pkv_seq_truncate": ([vp, c_i64], c_int),
+        "pkv_seq_append": ([vp, vp, vp, c_i64, c_i64], c_int),
+        "pkv_seq_attend": ([vp, vp, c_int, c_int, fl, c_i64, c_int, vp], c_int),
+        "pkv_seq_decode_batched": ([P(vp), c_int, vp, c_int, fl, vp], c_int),
+        "pkv_seq_get_kv": ([vp, vp, vp], c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

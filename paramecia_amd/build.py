@@ -36,6 +36,7 @@ SOURCES = {
     "pkv_oproj_mfma.hip": [],
     "pkv_prep.hip": ["-ffp-contract=off"],
     "pkv_api.cpp": ["-x", "hip"],
+    "pkv_paged.cpp": ["-x", "hip"],
 }
 
 

@@ -1,5 +1,8 @@
 // Q4K MFMA decode launchers (decode kernel without q/k preparation); the kernel, its
 // helpers and the launch plan are in pkv_q4k_decode.hpp.
+#include <cstring>
+#include <vector>
+
 #include "pkv_q4k_decode.hpp"
 
 namespace pkv {
@@ -54,6 +57,106 @@ int launch_append_attend_batched_mfma(int quant, const SeqDesc *seqs, int n, con
                                           scale, ws, s);
     if (rc) return rc;
   }
+  return PKV_OK;
+}
+
+// Paged decode: every page run is a segment with the same number of workgroups (wps), so
+// workgroup w serves segment w / wps; the combine merges all partials of a sequence (its
+// segments are consecutive). Up to kMaxSegs segments travel in the kernel arguments
+// (also under stream capture); more go to a device table staged through the workspace.
+int launch_paged_decode_q4k(const PagedSeg *segs, int nseg, int nseq, int page_tokens,
+                            const float *q, float *out, int64_t rs_t, int64_t rs_h,
+                            float scale, Workspace &ws, hipStream_t s) {
+  if (nseq < 1 || nseq > kMaxPagedSeqs || nseg < nseq || page_tokens % kBlk != 0)
+    return set_error(PKV_ERR_ARG, "paged decode: bad segment plan");
+  if (!decode_rows_fit(page_tokens, rs_t)) return PKV_ERR_UNSUPPORTED;
+  // blocks per workgroup: the multiple of 4 that minimises the estimated makespan
+  // (rounds of 256 workgroups x (bpw / 4 blocks per wave + ~1.3 blocks of set-up))
+  const int pblk = page_tokens / kBlk;
+  int bpw = 4;
+  double best = 1e30;
+  for (int cand = 4; cand <= ((pblk + 3) / 4) * 4 && cand <= 64; cand += 4) {
+    const int64_t w = (int64_t)nseg * ((pblk + cand - 1) / cand);
+    const double cost = (double)((w + kMainWGs - 1) / kMainWGs) * (cand / 4.0 + 1.3);
+    if (cost < best) {
+      best = cost;
+      bpw = cand;
+    }
+  }
+  const int wps = (pblk + bpw - 1) / bpw;
+  const int64_t nwg64 = (int64_t)nseg * wps;
+  if (nwg64 > (1 << 24)) return set_error(PKV_ERR_ARG, "paged decode: too many pages");
+  const int nwg = (int)nwg64;
+  std::vector<DecodeSeg> tab((size_t)nseg);
+  CombineArgs c;
+  int qprev = -1;
+  for (int i = 0; i < nseg; ++i) {
+    DecodeSeg &d = tab[(size_t)i];
+    if (segs[i].qi < qprev || segs[i].qi >= nseq || segs[i].len < 0 || segs[i].len > page_tokens)
+      return set_error(PKV_ERR_ARG, "paged decode: segments out of order");
+    while (qprev < segs[i].qi) c.wg0[++qprev] = i * wps;
+    d.k = segs[i].k;
+    d.v = segs[i].v;
+    d.seq_k = segs[i].len;
+    d.t_new = 0;
+    d.nblk = (int)((segs[i].len + kBlk - 1) / kBlk);
+    d.wg0 = i * wps;
+    d.qi = segs[i].qi;
+  }
+  if (qprev != nseq - 1) return set_error(PKV_ERR_ARG, "paged decode: a sequence has no page");
+  c.wg0[nseq] = nwg;
+  DecodeArgsT<kMaxSegs> d;
+  d.nseg = nseg;
+  d.nwg = nwg;
+  d.bpw = bpw;
+  d.rs_t = rs_t;
+  d.rs_h = rs_h;
+  d.sl2 = scale * kLog2e;
+  d.q = q;
+  d.k_new = d.v_new = nullptr;
+  d.prep = DecodePrep{};
+  d.q_out = nullptr;
+  const size_t part_floats = (size_t)nwg * 16 * kPartRow, ml_floats = (size_t)nwg * 16 * 2;
+  const size_t tab_off = (part_floats + ml_floats) * sizeof(float);
+  const size_t tab_bytes = nseg > kMaxSegs ? (size_t)nseg * sizeof(DecodeSeg) : 0;
+  int rc = ws.reserve(tab_off + tab_bytes);
+  if (rc) return rc;
+  d.part = static_cast<float *>(ws.ptr);
+  d.ml = reinterpret_cast<float2 *>(d.part + part_floats);
+  d.dq = nullptr;
+  rc = device_status_word(&d.status);
+  if (rc) return rc;
+  if (nseg <= kMaxSegs) {
+    for (int i = 0; i < nseg; ++i) d.seg[i] = tab[(size_t)i];
+    d.dseg = nullptr;
+    d.wps = wps;
+  } else {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    PKV_HIP(hipStreamIsCapturing(s, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+      return set_error(PKV_ERR_UNSUPPORTED,
+                       "paged decode over more than 32 pages cannot be captured in a graph");
+    rc = ws.reserve_host(tab_bytes);
+    if (rc) return rc;
+    memcpy(ws.host, tab.data(), tab_bytes);
+    DecodeSeg *dtab = reinterpret_cast<DecodeSeg *>(static_cast<uint8_t *>(ws.ptr) + tab_off);
+    PKV_HIP(hipMemcpyAsync(dtab, ws.host, tab_bytes, hipMemcpyHostToDevice, s));
+    rc = ws.mark_host_used(s);
+    if (rc) return rc;
+    d.dseg = dtab;
+    d.wps = wps;
+  }
+  hipLaunchKernelGGL((q4k_decode_kernel<false, kMaxSegs>), dim3((unsigned)nwg), dim3(kThreads), 0,
+                     s, d);
+  PKV_HIP(hipGetLastError());
+  c.part = d.part;
+  c.ml = d.ml;
+  c.q = q;
+  c.dq = nullptr;
+  c.out = out;
+  c.sl2 = d.sl2;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(16 * 8, (unsigned)nseq), dim3(256), 0, s, c);
+  PKV_HIP(hipGetLastError());
   return PKV_OK;
 }
 

@@ -41,6 +41,8 @@ struct DecodeSeg {
   int64_t seq_k;   // keys held in the cache before this step's append (all attended)
   int64_t t_new;   // row the fused step writes
   int nblk, wg0;
+  int qi;          // query / output row of the segment (several segments may share one:
+                   // the pages of a paged sequence, merged by the combine)
 };
 struct DecodeSegIn {
   uint8_t *k, *v;

@@ -98,6 +98,12 @@ namespace pkv {
 // starting at token `t0` of the K and V buffers.
 int launch_append(int quant, const float *k, const float *v, uint8_t *kc, uint8_t *vc,
                   int batch, int heads, int head_dim, int64_t n, int64_t t0, hipStream_t s);
+// The same into the pages of a paged sequence: token t's rows sit in page
+// page_tab[t >> page_lg] of the K and V planes (pages page_bytes apart), row t % 2^page_lg.
+int launch_append_paged(int quant, const float *k, const float *v, uint8_t *kpool,
+                        uint8_t *vpool, const int32_t *page_tab, int page_lg,
+                        int64_t page_bytes, int heads, int head_dim, int64_t n, int64_t t0,
+                        hipStream_t s);
 // Dequantize rows [0, S) to f32 [batch, heads, S, head_dim].
 int launch_dequant(int quant, const uint8_t *kc, const uint8_t *vc, float *ko, float *vo,
                    int batch, int heads, int head_dim, int64_t S, hipStream_t s);
@@ -161,6 +167,26 @@ int launch_append_attend_batched(int quant, const SeqDesc *seqs_host, int n, con
                                  const float *v, const float *q, int num_heads,
                                  int num_kv_heads, int head_dim, float scale, float *out,
                                  Workspace &ws, hipStream_t s);
+
+// ---- paged decode (pkv_attn_mfma.hip: Q4K, pkv_q8_decode.hip: Q8_0) ----
+// One page run of one sequence: rows of tokens [0, len) of the page (K and V planes, rows
+// of head 1 at rs_h), for query / output row qi.
+struct PagedSeg {
+  uint8_t *k, *v;
+  int64_t len;
+  int qi;
+};
+// Decode attention of nseq <= kMaxPagedSeqs sequences, one query each (q, out
+// [nseq][16][256]), over their pages: segs lists every page run, sequence by sequence
+// (qi 0, 0, .., 1, ..), each at most page_tokens keys. 16 query heads, 2 KV heads,
+// head_dim 256.
+constexpr int kMaxPagedSeqs = 32;
+int launch_paged_decode_q4k(const PagedSeg *segs, int nseg, int nseq, int page_tokens,
+                            const float *q, float *out, int64_t rs_t, int64_t rs_h,
+                            float scale, Workspace &ws, hipStream_t s);
+int launch_paged_decode_q8(const PagedSeg *segs, int nseg, int nseq, int page_tokens,
+                           const float *q, float *out, int64_t rs_t, int64_t rs_h, float scale,
+                           Workspace &ws, hipStream_t s);
 
 // ---- launchers (pkv_util.hip) ----
 int launch_fill_normal(float *dst, size_t n, uint64_t seed, uint64_t stream_id, float scale,

@@ -62,6 +62,10 @@ struct DecodeArgsBase {
   DecodePrep prep;
   float *q_out;  // [nseg][16][256] prepared q, for the combine
   unsigned *status;  // the device status word (pkv_device_status)
+  // Paged mode (dseg non-null): the segment table lives in device memory, segment s
+  // owning workgroups [s * wps, (s + 1) * wps); the seg array is unused
+  const DecodeSeg *dseg;
+  int wps;
 };
 template <int kSegs>
 struct DecodeArgsT : DecodeArgsBase {
@@ -515,10 +519,17 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
   const int wg = blockIdx.x;
   const int n = lane & 15, g = lane >> 4;
   int b = 0;  // segment of this workgroup
-  if constexpr (kSegs > 1) {
-    while (b + 1 < a.nseg && wg >= a.seg[b + 1].wg0) ++b;
+  DecodeSeg sgv;
+  if (a.dseg != nullptr) {
+    b = wg / a.wps;
+    sgv = a.dseg[b];
+  } else {
+    if constexpr (kSegs > 1) {
+      while (b + 1 < a.nseg && wg >= a.seg[b + 1].wg0) ++b;
+    }
+    sgv = a.seg[b];
   }
-  const DecodeSeg &sg = a.seg[b];
+  const DecodeSeg &sg = sgv;
 
   // ---- blocks of this wave: b0 + wsub, b0 + wsub + 4, ... below b1
   const int b0 = (wg - sg.wg0) * a.bpw;
@@ -593,7 +604,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
                           make_rsrc(a.prep.sin_tab + ro, (uint32_t)half * 4u), (uint32_t)lane);
       }
     }
-    const u4s rq = make_rsrc(a.q + ((int64_t)b * 16 + 8 * kvu) * 256, 8 * 256 * 4);
+    const u4s rq = make_rsrc(a.q + ((int64_t)sg.qi * 16 + 8 * kvu) * 256, 8 * 256 * 4);
     issue_q(&sm.run.st[wave][1], rq, 16u * lane);
   }
   __syncthreads();
@@ -700,7 +711,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
         }
       }
       if (wg == sg.wg0 && wsub == 0 && n < 8) {  // the combine's copy of the prepared q
-        float *qo = a.q_out + ((int64_t)b * 16 + 8 * kvu + n) * 256 + 64 * g;
+        float *qo = a.q_out + ((int64_t)sg.qi * 16 + 8 * kvu + n) * 256 + 64 * g;
 #pragma unroll
         for (int st = 0; st < 8; ++st) {
           *reinterpret_cast<float4 *>(qo + 8 * st) = float4{v[st][0], v[st][1], v[st][2], v[st][3]};
@@ -911,7 +922,10 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
     d.seg[i].seq_k = fused ? in[i].seq_k - 1 : in[i].seq_k;  // the new key joins in the combine
     d.seg[i].t_new = in[i].seq_k - 1;
     d.seg[i].nblk = (int)((d.seg[i].seq_k + kBlk - 1) / kBlk);
+    d.seg[i].qi = i;
   }
+  d.dseg = nullptr;
+  d.wps = 0;
   // Blocks per workgroup, a multiple of 4 (one or more per wave pair). One segment:
   // spread over at most kMainWGs workgroups, one per CU. Several: the multiple that
   // minimises the estimated makespan, ceil(workgroups / 256) rounds of (bpw / 4 blocks

@@ -19,6 +19,9 @@
 //
 // Fused append: workgroups 0 .. 4 * segments - 1 first quantize one new row each
 // (BlockQ8_0::from_float, bit-exact) and publish it dequantized for the combine.
+#include <cstring>
+#include <vector>
+
 #include "pkv_decode_split.hpp"
 #include "pkv_scalar.hpp"
 
@@ -40,6 +43,10 @@ struct Q8Args {
   float *part;                 // [nwg][16][kPartRow]
   float2 *ml;                  // [nwg][16] running max and sum
   float *dq;                   // [nseg][4][256]
+  // Paged mode (dseg non-null): the segment table lives in device memory, segment s
+  // owning workgroups [s * wps, (s + 1) * wps); the seg array is unused
+  const DecodeSeg *dseg;
+  int wps;
 };
 
 struct Q8Smem {
@@ -84,8 +91,15 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
   const int tid = threadIdx.x, half = tid >> 8, t = tid & 255;
   const int wg = blockIdx.x;
   int b = 0;
-  while (b + 1 < a.nseg && wg >= a.seg[b + 1].wg0) ++b;
-  const DecodeSeg &sg = a.seg[b];
+  DecodeSeg sgv;
+  if (a.dseg != nullptr) {
+    b = wg / a.wps;
+    sgv = a.dseg[b];
+  } else {
+    while (b + 1 < a.nseg && wg >= a.seg[b + 1].wg0) ++b;
+    sgv = a.seg[b];
+  }
+  const DecodeSeg &sg = sgv;
   const int64_t k0 = (int64_t)(wg - sg.wg0) * a.kpw;
   const int64_t k1 = k0 + a.kpw < sg.seq_k ? k0 + a.kpw : sg.seq_k;
 
@@ -102,7 +116,7 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
 
   // ---- q of the 16 heads into LDS
   {
-    const float4 *q4 = reinterpret_cast<const float4 *>(a.q + (int64_t)b * 16 * 256);
+    const float4 *q4 = reinterpret_cast<const float4 *>(a.q + (int64_t)sg.qi * 16 * 256);
     float4 *s4 = reinterpret_cast<float4 *>(&sm.q[0][0]);
     s4[tid] = q4[tid];
     s4[tid + 512] = q4[tid + 512];
@@ -229,8 +243,11 @@ static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, cons
     d.seg[i].seq_k = fused ? in[i].seq_k - 1 : in[i].seq_k;
     d.seg[i].t_new = in[i].seq_k - 1;
     d.seg[i].nblk = 0;
+    d.seg[i].qi = i;
     if (d.seg[i].seq_k > longest) longest = d.seg[i].seq_k;
   }
+  d.dseg = nullptr;
+  d.wps = 0;
   // keys per workgroup: one 32-key chunk while that keeps <= 512 partials per
   // segment, more chunks per workgroup for longer caches
   int64_t kpw = (longest + 511) / 512;
@@ -270,6 +287,93 @@ static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, cons
   c.out = out;
   c.sl2 = d.sl2;
   hipLaunchKernelGGL(decode_combine_kernel, dim3(16 * 8, (unsigned)n), dim3(256), 0, s, c);
+  PKV_HIP(hipGetLastError());
+  return PKV_OK;
+}
+
+// Paged decode: every page run is a segment with the same number of workgroups (wps =
+// page_tokens / keys per workgroup), so workgroup w serves segment w / wps; the combine
+// merges all partials of a sequence (its segments are consecutive). Up to kMaxSegs
+// segments travel in the kernel arguments; more go to a device table in the workspace.
+int launch_paged_decode_q8(const PagedSeg *segs, int nseg, int nseq, int page_tokens,
+                           const float *q, float *out, int64_t rs_t, int64_t rs_h, float scale,
+                           Workspace &ws, hipStream_t s) {
+  if (nseq < 1 || nseq > kMaxPagedSeqs || nseg < nseq || page_tokens % kQ8Chunk != 0)
+    return set_error(PKV_ERR_ARG, "paged decode: bad segment plan");
+  if (rs_h != kQ8Row || !decode_rows_fit(page_tokens, rs_t)) return PKV_ERR_UNSUPPORTED;
+  // keys per workgroup: a multiple of 32 dividing the page into equal parts, aiming at
+  // about 768 workgroups over the whole launch
+  int64_t kpw = (int64_t)page_tokens * nseg / 768;
+  kpw = (kpw + kQ8Chunk - 1) / kQ8Chunk * kQ8Chunk;
+  if (kpw < kQ8Chunk) kpw = kQ8Chunk;
+  if (kpw > page_tokens) kpw = page_tokens;
+  const int wps = (int)((page_tokens + kpw - 1) / kpw);
+  const int64_t nwg64 = (int64_t)nseg * wps;
+  if (nwg64 > (1 << 24)) return set_error(PKV_ERR_ARG, "paged decode: too many pages");
+  const int nwg = (int)nwg64;
+  std::vector<DecodeSeg> tab((size_t)nseg);
+  CombineArgs c;
+  int qprev = -1;
+  for (int i = 0; i < nseg; ++i) {
+    DecodeSeg &d = tab[(size_t)i];
+    if (segs[i].qi < qprev || segs[i].qi >= nseq || segs[i].len < 0 || segs[i].len > page_tokens)
+      return set_error(PKV_ERR_ARG, "paged decode: segments out of order");
+    while (qprev < segs[i].qi) c.wg0[++qprev] = i * wps;
+    d.k = segs[i].k;
+    d.v = segs[i].v;
+    d.seq_k = segs[i].len;
+    d.t_new = 0;
+    d.nblk = 0;
+    d.wg0 = i * wps;
+    d.qi = segs[i].qi;
+  }
+  if (qprev != nseq - 1) return set_error(PKV_ERR_ARG, "paged decode: a sequence has no page");
+  c.wg0[nseq] = nwg;
+  Q8Args d;
+  d.nseg = nseg;
+  d.nwg = nwg;
+  d.kpw = (int)kpw;
+  d.rs_t = rs_t;
+  d.rs_h = rs_h;
+  d.sl2 = scale * 1.4426950408889634f;
+  d.q = q;
+  d.k_new = d.v_new = nullptr;
+  const size_t part_floats = (size_t)nwg * 16 * kPartRow, ml_floats = (size_t)nwg * 16 * 2;
+  const size_t tab_off = (part_floats + ml_floats) * sizeof(float);
+  const size_t tab_bytes = nseg > kMaxSegs ? (size_t)nseg * sizeof(DecodeSeg) : 0;
+  int rc = ws.reserve(tab_off + tab_bytes);
+  if (rc) return rc;
+  d.part = static_cast<float *>(ws.ptr);
+  d.ml = reinterpret_cast<float2 *>(d.part + part_floats);
+  d.dq = nullptr;
+  d.wps = wps;
+  if (nseg <= kMaxSegs) {
+    for (int i = 0; i < nseg; ++i) d.seg[i] = tab[(size_t)i];
+    d.dseg = nullptr;
+  } else {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    PKV_HIP(hipStreamIsCapturing(s, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+      return set_error(PKV_ERR_UNSUPPORTED,
+                       "paged decode over more than 32 pages cannot be captured in a graph");
+    rc = ws.reserve_host(tab_bytes);
+    if (rc) return rc;
+    memcpy(ws.host, tab.data(), tab_bytes);
+    DecodeSeg *dtab = reinterpret_cast<DecodeSeg *>(static_cast<uint8_t *>(ws.ptr) + tab_off);
+    PKV_HIP(hipMemcpyAsync(dtab, ws.host, tab_bytes, hipMemcpyHostToDevice, s));
+    rc = ws.mark_host_used(s);
+    if (rc) return rc;
+    d.dseg = dtab;
+  }
+  hipLaunchKernelGGL(q8_decode_kernel, dim3((unsigned)nwg), dim3(kQ8Threads), 0, s, d);
+  PKV_HIP(hipGetLastError());
+  c.part = d.part;
+  c.ml = d.ml;
+  c.q = q;
+  c.dq = nullptr;
+  c.out = out;
+  c.sl2 = d.sl2;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(16 * 8, (unsigned)nseq), dim3(256), 0, s, c);
   PKV_HIP(hipGetLastError());
   return PKV_OK;
 }

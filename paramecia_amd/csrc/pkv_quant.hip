@@ -20,10 +20,15 @@ namespace {
 
 struct AppendArgs {
   const float *src[2];  // k, v: [batch, heads, n, head_dim]
-  uint8_t *dst[2];      // K, V row buffers
+  uint8_t *dst[2];      // K, V row buffers (paged: the pool's K and V page planes)
   int batch, heads, head_dim, padded;
   int64_t n, t0;
   int64_t bpr;
+  // Paged rows (page_tab non-null): token t lives in page page_tab[t >> page_lg], row
+  // t & (2^page_lg - 1) of that page, each page page_bytes long in each plane
+  const int32_t *page_tab;
+  int page_lg;
+  int64_t page_bytes;
 };
 
 // Source element e (< padded) of new row (t, b, h); zero padding past head_dim.
@@ -35,6 +40,15 @@ __device__ __forceinline__ float load_elem(const float *src, const AppendArgs &a
 
 __device__ __forceinline__ int64_t dst_row(const AppendArgs &a, int64_t t, int b, int h) {
   return ((a.t0 + t) * a.batch + b) * a.heads + h;
+}
+// The destination row of new token t (batch row b, head h) in plane p (K 0, V 1).
+__device__ __forceinline__ uint8_t *row_ptr(const AppendArgs &a, int p, int64_t t, int b, int h) {
+  if (a.page_tab != nullptr) {
+    const int64_t tok = a.t0 + t, in_page = tok & ((int64_t(1) << a.page_lg) - 1);
+    const int64_t pg = a.page_tab[tok >> a.page_lg];
+    return a.dst[p] + pg * a.page_bytes + ((in_page * a.batch + b) * a.heads + h) * a.bpr;
+  }
+  return a.dst[p] + dst_row(a, t, b, h) * a.bpr;
 }
 
 // clamp(nearest_int(v), 0, 15) as a float: nearest_int is candle's v.round() as i32
@@ -225,7 +239,7 @@ __global__ __launch_bounds__(256) void q4k_append_kernel(AppendArgs a, int64_t u
     outw[w] = v;
   }
   if (!active) return;
-  uint8_t *blk = a.dst[p] + dst_row(a, t, b, h) * a.bpr + (int64_t)sb * 144;
+  uint8_t *blk = row_ptr(a, p, t, b, h) + (int64_t)sb * 144;
   uint4 q4 = {outw[0], outw[1], outw[2], outw[3]};
   *reinterpret_cast<uint4 *>(blk + 16 + 16 * j) = q4;
   if (j == 0) {
@@ -251,7 +265,7 @@ __global__ __launch_bounds__(256) void q4k_append_small_kernel(AppendArgs a, int
   const int64_t t = u % a.n;
   const int p = (int)(u / a.n);
   const float x = load_elem(a.src[p], a, t, b, h, sb * 256 + (int)threadIdx.x);
-  uint8_t *blk = a.dst[p] + dst_row(a, t, b, h) * a.bpr + (int64_t)sb * 144;
+  uint8_t *blk = row_ptr(a, p, t, b, h) + (int64_t)sb * 144;
   q4k_quantize_superblock_lanes(x, blk, &scr, (int)threadIdx.x);
 }
 
@@ -285,7 +299,7 @@ __global__ __launch_bounds__(256) void q8_0_append_kernel(AppendArgs a, int64_t 
     w[1 + i] = (uint16_t)(q0 | (q1 << 8));
   }
   uint16_t *dst =
-      reinterpret_cast<uint16_t *>(a.dst[p] + dst_row(a, t, b, h) * a.bpr + (int64_t)blk * 34);
+      reinterpret_cast<uint16_t *>(row_ptr(a, p, t, b, h) + (int64_t)blk * 34);
 #pragma unroll
   for (int i = 0; i < 17; ++i) dst[i] = w[i];
 }
@@ -304,7 +318,7 @@ __global__ __launch_bounds__(256) void half_append_kernel(AppendArgs a, int64_t 
   const int b = (int)(u % a.batch);
   const int64_t t = u / a.batch;
   const float x = load_elem(a.src[p], a, t, b, h, e);
-  uint16_t *dst = reinterpret_cast<uint16_t *>(a.dst[p] + dst_row(a, t, b, h) * a.bpr);
+  uint16_t *dst = reinterpret_cast<uint16_t *>(row_ptr(a, p, t, b, h));
   dst[e] = BF ? f32_to_bf16(x) : f32_to_f16(x);
 }
 
@@ -330,6 +344,8 @@ __global__ __launch_bounds__(256) void dequant_kernel(int quant, const uint8_t *
 
 }  // namespace
 
+static int launch_append_args(int quant, AppendArgs &a, hipStream_t s);
+
 int launch_append(int quant, const float *k, const float *v, uint8_t *kc, uint8_t *vc,
                   int batch, int heads, int head_dim, int64_t n, int64_t t0, hipStream_t s) {
   if (n == 0) return PKV_OK;
@@ -345,6 +361,38 @@ int launch_append(int quant, const float *k, const float *v, uint8_t *kc, uint8_
   a.n = n;
   a.t0 = t0;
   a.bpr = (int64_t)row_bytes(quant, head_dim);
+  a.page_tab = nullptr;
+  a.page_lg = 0;
+  a.page_bytes = 0;
+  return launch_append_args(quant, a, s);
+}
+
+int launch_append_paged(int quant, const float *k, const float *v, uint8_t *kpool,
+                        uint8_t *vpool, const int32_t *page_tab, int page_lg,
+                        int64_t page_bytes, int heads, int head_dim, int64_t n, int64_t t0,
+                        hipStream_t s) {
+  if (n == 0) return PKV_OK;
+  AppendArgs a;
+  a.src[0] = k;
+  a.src[1] = v;
+  a.dst[0] = kpool;
+  a.dst[1] = vpool;
+  a.batch = 1;
+  a.heads = heads;
+  a.head_dim = head_dim;
+  a.padded = padded_dim(quant, head_dim);
+  a.n = n;
+  a.t0 = t0;
+  a.bpr = (int64_t)row_bytes(quant, head_dim);
+  a.page_tab = page_tab;
+  a.page_lg = page_lg;
+  a.page_bytes = page_bytes;
+  return launch_append_args(quant, a, s);
+}
+
+static int launch_append_args(int quant, AppendArgs &a, hipStream_t s) {
+  const int batch = a.batch, heads = a.heads;
+  const int64_t n = a.n;
   const int64_t rows = n * batch * heads;
   if (quant == PKV_QUANT_Q4K && rows * (a.padded / 256) * 2 <= 1024) {
     // few superblocks: latency-bound, one workgroup each

@@ -268,6 +268,132 @@ class PreallocatedQuantizedKvCache:
         _call(lib().pkv_resize_batch(self._h, batch_size))
 
 
+# ------------------------------------------------------------------ paged caches
+class PagedKvPool:
+    """Pages of KV rows for one layer, shared by many sequences (pkv_pool_*): the
+    multi-sequence form of PreallocatedQuantizedKvCache (qwen3_next.rs:343-643) for a
+    serving loop, where the reference keeps one preallocated cache per sequence
+    (paramecia-llm/src/backend/local.rs:743-800)."""
+
+    def __init__(self, num_kv_heads: int, head_dim: int, page_tokens: int, n_pages: int,
+                 quant: KvCacheQuantization = KvCacheQuantization.Q4K,
+                 stream: Optional[int] = None):
+        h = ctypes.c_void_p()
+        self._stream = stream if stream is not None else _stream()
+        _call(lib().pkv_pool_create(int(quant), num_kv_heads, head_dim, page_tokens, n_pages,
+                                    ctypes.c_void_p(self._stream), ctypes.byref(h)))
+        self._h = h
+        self._lib = lib()
+        self.quant = KvCacheQuantization(int(quant) or _lib.QUANT_F16)
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.page_tokens = page_tokens
+        self.n_pages = n_pages
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._lib.pkv_pool_destroy(h)
+            self._h = None
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    @property
+    def free_pages(self) -> int:
+        return lib().pkv_pool_free_pages(self._h)
+
+    def _follow_stream(self) -> None:
+        s = _stream()
+        if s != self._stream:
+            check(lib().pkv_pool_set_stream(self._h, ctypes.c_void_p(s)))
+            self._stream = s
+
+    def sequence(self) -> "PagedSequence":
+        return PagedSequence(self)
+
+    def decode_batched(self, seqs: Sequence["PagedSequence"], q: torch.Tensor,
+                       scale: float) -> torch.Tensor:
+        """One decode query per sequence: q [n, num_heads, head_dim] -> out of that shape,
+        each sequence attending over all its keys (pkv_seq_decode_batched)."""
+        self._follow_stream()
+        q = _f32(q, "q")
+        if q.dim() != 3 or q.shape[0] != len(seqs):
+            raise KvCacheError("q must be [n_sequences, num_heads, head_dim]")
+        out = torch.empty_like(q)
+        arr = (ctypes.c_void_p * len(seqs))(*[sq.handle.value for sq in seqs])
+        _call(lib().pkv_seq_decode_batched(arr, len(seqs), _ptr(q), q.shape[1], scale, _ptr(out)))
+        return out
+
+
+class PagedSequence:
+    """One sequence of a PagedKvPool, with the cache API of PreallocatedQuantizedKvCache at
+    batch 1 (append_quantized / attend / get_kv / truncate) plus fork (page sharing)."""
+
+    def __init__(self, pool: PagedKvPool, _handle: Optional[ctypes.c_void_p] = None):
+        self.pool = pool  # keeps the pool alive while the sequence lives
+        self._lib = lib()
+        if _handle is None:
+            _handle = ctypes.c_void_p()
+            _call(lib().pkv_seq_create(pool.handle, ctypes.byref(_handle)))
+        self._h = _handle
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._lib.pkv_seq_destroy(h)
+            self._h = None
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    @property
+    def seq_len(self) -> int:
+        return lib().pkv_seq_len(self._h)
+
+    @property
+    def pages(self) -> int:
+        return lib().pkv_seq_pages(self._h)
+
+    def fork(self) -> "PagedSequence":
+        h = ctypes.c_void_p()
+        _call(lib().pkv_seq_fork(self._h, ctypes.byref(h)))
+        return PagedSequence(self.pool, h)
+
+    def append_quantized(self, new_k: torch.Tensor, new_v: torch.Tensor,
+                         offset: int = -1) -> None:
+        """new_k, new_v: [1, num_kv_heads, n, head_dim] f32."""
+        self.pool._follow_stream()
+        k, v = _f32(new_k, "new_k"), _f32(new_v, "new_v")
+        if k.shape != v.shape or k.dim() != 4 or k.shape[0] != 1:
+            raise KvCacheError("new_k/new_v must both be [1, heads, n, head_dim]")
+        _call(lib().pkv_seq_append(self._h, _ptr(k), _ptr(v), k.shape[2], offset))
+
+    def get_kv(self):
+        """Dequantized [1, heads, seq_len, head_dim] f32 tensors."""
+        self.pool._follow_stream()
+        shape = (1, self.pool.num_kv_heads, self.seq_len, self.pool.head_dim)
+        k = torch.empty(shape, dtype=torch.float32, device="cuda")
+        v = torch.empty(shape, dtype=torch.float32, device="cuda")
+        _call(lib().pkv_seq_get_kv(self._h, _ptr(k), _ptr(v)))
+        return k, v
+
+    def attend(self, q: torch.Tensor, scale: float, q_offset: int,
+               causal: bool = True) -> torch.Tensor:
+        """q: [1, l, num_heads, head_dim] f32 -> out of the same shape."""
+        self.pool._follow_stream()
+        q = _f32(q, "q")
+        out = torch.empty_like(q)
+        _call(lib().pkv_seq_attend(self._h, _ptr(q), q.shape[1], q.shape[2], scale, q_offset,
+                                   int(causal), _ptr(out)))
+        return out
+
+    def truncate(self, new_len: int) -> None:
+        _call(lib().pkv_seq_truncate(self._h, new_len))
+
+
 def flash_attn(quant: KvCacheQuantization, q: torch.Tensor, k_ptr: int, v_ptr: int,
                strides: Sequence[int], scale: float, num_kv_heads: int, seq_k: int,
                q_offset: int, causal: bool) -> torch.Tensor:

@@ -1,0 +1,221 @@
+"""GPU parity of the paged KV caches (pkv_pool_* / pkv_seq_*): a pool of pages shared by
+many sequences, against the CPU oracle's contiguous PreallocatedQuantizedKvCache
+(qwen3_next.rs:343-643) on the same appended rows.
+
+- Bytes: a sequence filled in chunks that cross page boundaries holds exactly the rows
+  the oracle's cache holds (get_kv bit-exact), for every encoding.
+- Decode (the model's shape, Q4K / Q8_0: one segment per page in the split-K decode
+  kernels, kernel-argument and device segment tables) and prefill chunks / other shapes
+  (rows gathered first) attend like the oracle (attn_checks' two gates); a batched varlen
+  decode over several sequences matches each sequence alone.
+- Sharing: a fork shares pages; appending into a shared, partly filled page copies it
+  first, so neither sequence sees the other's rows; pages return to the pool.
+- Rules: the cache offset rule (rewind / PKV_ERR_OFFSET), and pool exhaustion as
+  PKV_ERR_OVERFLOW with nothing written."""
+import sys
+
+import numpy as np
+import pytest
+
+from attn_checks import assert_attn_close
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+F16, BF16, Q8_0, Q4K = 1, 2, 3, 4
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def pk():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import paramecia_amd
+    paramecia_amd.lib()
+    return paramecia_amd
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def fill(pk, orc, seq, cache, rng, chunks, H, D):
+    for n in chunks:
+        k = rng.standard_normal((1, H, n, D)).astype(np.float32)
+        v = rng.standard_normal((1, H, n, D)).astype(np.float32)
+        seq.append_quantized(dev(k), dev(v))
+        assert cache.append(k, v) == 0
+
+
+@pytest.mark.parametrize("quant,H,D,page", [(Q4K, 2, 256, 64), (Q8_0, 2, 256, 32),
+                                            (F16, 4, 64, 128), (BF16, 1, 128, 32),
+                                            (Q4K, 3, 200, 256)])
+def test_bytes_match_oracle(pk, orc, quant, H, D, page):
+    say(f"paged bytes quant={quant} H={H} D={D} page={page}")
+    rng = np.random.default_rng(quant * 100 + page)
+    pool = pk.PagedKvPool(H, D, page, 16, pk.KvCacheQuantization(quant))
+    seq = pool.sequence()
+    chunks = [37, page, 1, 90, 2 * page - 5]
+    c = orc.Cache(quant, 1, H, D, sum(chunks))
+    fill(pk, orc, seq, c, rng, chunks, H, D)
+    assert seq.seq_len == sum(chunks) and seq.pages == -(-sum(chunks) // page)
+    k, v = seq.get_kv()
+    rk, rv = c.get_kv()
+    assert np.array_equal(host(k), rk) and np.array_equal(host(v), rv)
+
+
+def _attend(pk, orc, quant, H, Hkv, D, page, chunks, L, causal, seed, pool_pages=64):
+    rng = np.random.default_rng(seed)
+    pool = pk.PagedKvPool(Hkv, D, page, pool_pages, pk.KvCacheQuantization(quant))
+    seq = pool.sequence()
+    S = sum(chunks)
+    c = orc.Cache(quant, 1, Hkv, D, S)
+    fill(pk, orc, seq, c, rng, chunks, Hkv, D)
+    q = rng.standard_normal((1, L, H, D)).astype(np.float32)
+    scale = float(1 / np.sqrt(D))
+    out = host(seq.attend(dev(q), scale, S - L, causal))
+    ref = c.attend(q, scale, S - L, causal, mode="f64")
+    assert_attn_close(out, ref, what=f"quant={quant} page={page} S={S} L={L}")
+    return pool, seq
+
+
+@pytest.mark.parametrize("quant,page,chunks", [
+    (Q4K, 256, [1000]),              # 4 pages, last one partial: kernel-argument table
+    (Q8_0, 256, [700, 300, 1]),
+    (Q4K, 32, [2000, 21]),           # 64 pages: device segment table
+    (Q8_0, 32, [1500]),              # 47 pages: device segment table
+    (Q4K, 1024, [5000]),
+    (Q4K, 64, [64]),                 # one full page
+    (Q8_0, 128, [1]),                # one key
+])
+def test_decode_matches_oracle(pk, orc, quant, page, chunks):
+    say(f"paged decode quant={quant} page={page} chunks={chunks}")
+    _attend(pk, orc, quant, 16, 2, 256, page, chunks, 1, True, seed=sum(chunks) + page)
+
+
+@pytest.mark.parametrize("quant,H,Hkv,D,page,chunks,L,causal", [
+    (Q4K, 16, 2, 256, 256, [600, 64], 64, True),   # prefill chunk (gathered rows)
+    (Q8_0, 16, 2, 256, 64, [300], 40, True),
+    (F16, 4, 2, 64, 32, [257], 2, True),           # other shapes and encodings
+    (Q8_0, 8, 8, 128, 64, [300], 3, False),
+    (Q4K, 16, 2, 256, 128, [500], 1, False),        # decode without causality
+])
+def test_other_attends_match_oracle(pk, orc, quant, H, Hkv, D, page, chunks, L, causal):
+    say(f"paged attend quant={quant} H={H}/{Hkv} D={D} page={page} L={L}")
+    _attend(pk, orc, quant, H, Hkv, D, page, chunks, L, causal, seed=L + page)
+
+
+@pytest.mark.parametrize("quant,page", [(Q4K, 256), (Q8_0, 128), (Q4K, 32)])
+def test_batched_varlen_decode(pk, orc, quant, page):
+    say(f"paged batched decode quant={quant} page={page}")
+    rng = np.random.default_rng(7 + page)
+    lens = [1, 31, 257, 1000, 70, 513, 32, 900]
+    pool = pk.PagedKvPool(2, 256, page, sum(-(-n // page) for n in lens) + 2,
+                          pk.KvCacheQuantization(quant))
+    seqs, caches = [], []
+    for n in lens:
+        s = pool.sequence()
+        c = orc.Cache(quant, 1, 2, 256, n)
+        fill(pk, orc, s, c, rng, [n], 2, 256)
+        seqs.append(s)
+        caches.append(c)
+    q = rng.standard_normal((len(lens), 16, 256)).astype(np.float32)
+    out = host(pool.decode_batched(seqs, dev(q), 1 / 16))
+    for i, (s, c) in enumerate(zip(seqs, caches)):
+        ref = c.attend(q[i][None, None], 1 / 16, lens[i] - 1, True, mode="f64")[0, 0]
+        assert_attn_close(out[i], ref, what=f"sequence {i} ({lens[i]} keys)")
+        alone = host(s.attend(dev(q[i][None, None]), 1 / 16, lens[i] - 1))[0, 0]
+        np.testing.assert_allclose(out[i], alone, rtol=1e-5, atol=1e-6)
+
+
+def test_many_sequences_batched(pk, orc):
+    """40 sequences: two launches of at most 32."""
+    say("paged batched decode, 40 sequences")
+    rng = np.random.default_rng(40)
+    lens = [int(x) for x in rng.integers(1, 300, 40)]
+    pool = pk.PagedKvPool(2, 256, 64, sum(-(-n // 64) for n in lens), pk.KvCacheQuantization.Q8_0)
+    seqs, caches = [], []
+    for n in lens:
+        s = pool.sequence()
+        c = orc.Cache(Q8_0, 1, 2, 256, n)
+        fill(pk, orc, s, c, rng, [n], 2, 256)
+        seqs.append(s)
+        caches.append(c)
+    assert pool.free_pages == 0
+    q = rng.standard_normal((40, 16, 256)).astype(np.float32)
+    out = host(pool.decode_batched(seqs, dev(q), 1 / 16))
+    for i in (0, 17, 31, 32, 39):
+        ref = caches[i].attend(q[i][None, None], 1 / 16, lens[i] - 1, True, mode="f64")[0, 0]
+        assert_attn_close(out[i], ref, what=f"sequence {i}")
+
+
+@pytest.mark.parametrize("quant", [Q4K, Q8_0])
+def test_fork_copy_on_write(pk, orc, quant):
+    say(f"paged fork / copy on write quant={quant}")
+    rng = np.random.default_rng(99)
+    pool = pk.PagedKvPool(2, 256, 64, 8, pk.KvCacheQuantization(quant))
+    a = pool.sequence()
+    ca = orc.Cache(quant, 1, 2, 256, 400)
+    fill(pk, orc, a, ca, rng, [100], 2, 256)         # pages: one full, one with 36 rows
+    assert pool.free_pages == 6
+    b = a.fork()
+    assert pool.free_pages == 6 and b.seq_len == 100 and b.pages == 2
+    cb = orc.Cache(quant, 1, 2, 256, 400)
+    cb.load_bytes(*ca.valid_bytes(), 100)
+    fill(pk, orc, b, cb, rng, [10], 2, 256)           # copies the shared partial page
+    assert pool.free_pages == 5
+    fill(pk, orc, a, ca, rng, [50], 2, 256)           # a's page is its own again: no copy
+    assert pool.free_pages == 4
+    for s, c in ((a, ca), (b, cb)):
+        k, v = s.get_kv()
+        rk, rv = c.get_kv()
+        assert np.array_equal(host(k), rk) and np.array_equal(host(v), rv)
+    q = rng.standard_normal((1, 1, 16, 256)).astype(np.float32)
+    for s, c in ((a, ca), (b, cb)):
+        out = host(s.attend(dev(q), 1 / 16, s.seq_len - 1))
+        assert_attn_close(out, c.attend(q, 1 / 16, s.seq_len - 1, True, mode="f64"))
+    del s, b  # (the loop variable held b too)
+    assert pool.free_pages == 5                       # b's own page back; page 0 still a's
+
+
+def test_rules_offset_overflow_truncate_reuse(pk, orc):
+    say("paged rules")
+    rng = np.random.default_rng(5)
+    pool = pk.PagedKvPool(2, 256, 32, 4, pk.KvCacheQuantization.Q4K)
+    s = pool.sequence()
+    c = orc.Cache(Q4K, 1, 2, 256, 128)
+    fill(pk, orc, s, c, rng, [70], 2, 256)
+    assert pool.free_pages == 1
+    k = dev(rng.standard_normal((1, 2, 80, 256)).astype(np.float32))
+    with pytest.raises(pk.KvCacheOverflow):
+        s.append_quantized(k, k)                      # 150 tokens need 5 pages
+    assert s.seq_len == 70 and pool.free_pages == 1  # nothing written
+    with pytest.raises(pk.KvCacheOffsetMismatch):
+        s.append_quantized(k[:, :, :1], k[:, :, :1], offset=71)
+    # a smaller offset rewinds (the cache offset rule), then appends
+    k2 = rng.standard_normal((1, 2, 5, 256)).astype(np.float32)
+    s.append_quantized(dev(k2), dev(k2), offset=40)
+    c.truncate(40)
+    assert c.append(k2, k2) == 0
+    assert s.seq_len == 45 and s.pages == 2 and pool.free_pages == 2
+    got = host(s.get_kv()[0])
+    assert np.array_equal(got, c.get_kv()[0])
+    s.truncate(10)
+    assert s.pages == 1 and pool.free_pages == 3
+    del s                                             # every page back
+    assert pool.free_pages == 4
+    t = pool.sequence()                               # reused pages hold the new rows
+    c2 = orc.Cache(Q4K, 1, 2, 256, 128)
+    fill(pk, orc, t, c2, rng, [128], 2, 256)
+    assert pool.free_pages == 0
+    assert np.array_equal(host(t.get_kv()[1]), c2.get_kv()[1])
