@@ -644,6 +644,8 @@ def run_config5(args):
     lens = W.c5_lengths()
     chans = W.c5_channels()
     L, N = W.N_FULL, W.C5_SEQS
+    if args.paged:
+        return run_config5_paged(args, lens, chans)
     caches = [[None] * N for _ in range(L)]
     for l in range(L):
         for i, S in enumerate(lens):
@@ -688,6 +690,70 @@ def run_config5(args):
                                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                                      "bytes_per_step": nbytes,
                                      "traffic_per_layer": traffic(5)}})
+
+
+def run_config5_paged(args, lens, chans):
+    """Config 5's workload on paged caches: per layer one page pool (--paged tokens per
+    page) holding the 16 sequences; a step appends one token to every sequence in one
+    launch (pkv_seq_append_batched) and runs one batched decode over all their pages
+    (pkv_seq_decode_batched). Timed eagerly: with more than 32 pages per launch the
+    segment table is staged through host memory, which a HIP graph cannot replay."""
+    import torch
+    import paramecia_amd as pk
+    from paramecia_amd import workloads as W
+
+    L, N, P = W.N_FULL, W.C5_SEQS, args.paged
+    pools, seqs = [], []
+    for l in range(L):
+        pool = pk.PagedKvPool(2, 256, P, sum(-(-(S + 1) // P) for S in lens) + N,
+                              pk.KvCacheQuantization.Q4K)
+        row = []
+        for i, S in enumerate(lens):
+            sq = pool.sequence()
+            kb = torch.empty((1, 2, S, 256), device="cuda")
+            vb = torch.empty_like(kb)
+            pk.fill_normal(kb, W.SEED, W.stream_id(5, W.T_PREFILL_K, l, i))
+            pk.fill_normal(vb, W.SEED, W.stream_id(5, W.T_PREFILL_V, l, i))
+            pk.scale_channels(kb, chans, W.C5_OUTLIER_SCALE)
+            pk.scale_channels(vb, chans, W.C5_OUTLIER_SCALE)
+            sq.append_quantized(kb, vb)
+            row.append(sq)
+            del kb, vb
+        pools.append(pool)
+        seqs.append(row)
+    q = torch.empty((L, N, 16, 256), device="cuda")
+    kn = torch.empty((L, N, 2, 1, 256), device="cuda")
+    vn = torch.empty_like(kn)
+    for l in range(L):
+        pk.fill_normal(q[l], W.SEED, W.stream_id(5, W.T_Q, l))
+        pk.fill_normal(kn[l], W.SEED, W.stream_id(5, W.T_NEW_K, l))
+        pk.fill_normal(vn[l], W.SEED, W.stream_id(5, W.T_NEW_V, l))
+        pk.scale_channels(kn[l], chans, W.C5_OUTLIER_SCALE)
+        pk.scale_channels(vn[l], chans, W.C5_OUTLIER_SCALE)
+    outs = [None] * L
+
+    def step():
+        for l in range(L):
+            for i, S in enumerate(lens):
+                seqs[l][i].truncate(S)  # rewind the previous step's token
+            pools[l].append_batched(seqs[l], kn[l], vn[l])
+            outs[l] = pools[l].decode_batched(seqs[l], q[l], W.SCALE)
+
+    ms = event_time(torch, step, args.steps, args.warmup)
+    nbytes = L * sum(layer_bytes(S + 1) for S in lens)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    pages = sum(-(-(S + 1) // P) for S in lens)
+    return base_result(5, "batched decode µs/step (16 sequences, 12 layers, Q4K, paged caches)",
+                       round(ms * 1000, 2), "us/step", False, ms, args,
+                       f"config5 on paged caches: one pool per layer, {P}-token pages "
+                       f"({pages} pages per layer), the 16 sequences of config 5; step = one "
+                       "batched append + one batched decode per layer (eager)",
+                       {"sequence_lengths": lens, "page_tokens": P, "pages_per_layer": pages,
+                        "roofline": {"kernel": "pkv_seq_append_batched + pkv_seq_decode_batched",
+                                     "bound": "hbm", "achieved": round(gbs, 1),
+                                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                     "bytes_per_step": nbytes, "traffic": None}})
 
 
 # ------------------------------------------------------------------ config 6
@@ -871,6 +937,9 @@ def main() -> int:
     ap.add_argument("--op-wtype", default="q4k", choices=["q4k", "q5k", "q6k", "q8_0"],
                     help="config 7: GGUF type of wo")
     ap.add_argument("--cached", type=int, default=131072, help="config 3: cached tokens")
+    ap.add_argument("--paged", type=int, default=0,
+                    help="config 5: run the workload on paged caches with this many tokens "
+                         "per page (a power of two)")
     ap.add_argument("--layers", type=int, default=12, help="config 3: layers")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph-reps", type=int, default=0,

@@ -328,6 +328,10 @@ int pkv_seq_truncate(pkv_seq *s, int64_t new_len);
  * a larger one -> PKV_ERR_OFFSET). PKV_ERR_OVERFLOW, with nothing written, when the
  * pool lacks pages. */
 int pkv_seq_append(pkv_seq *s, const float *k, const float *v, int64_t n, int64_t offset);
+/* One token appended to each of n sequences of one pool in one launch (the decode step of
+ * a serving batch): k, v [n, n_kv_heads, 1, head_dim] f32. All or nothing: PKV_ERR_OVERFLOW,
+ * with nothing written, when the pool lacks pages for any of them. */
+int pkv_seq_append_batched(pkv_seq *const *seqs, int n, const float *k, const float *v);
 /* Attention over the sequence's keys, as pkv_attend: q [1, l, num_heads, head_dim],
  * out the same shape. */
 int pkv_seq_attend(pkv_seq *s, const float *q, int l, int num_heads, float scale,

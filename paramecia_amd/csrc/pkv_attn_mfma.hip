@@ -66,7 +66,9 @@ int launch_append_attend_batched_mfma(int quant, const SeqDesc *seqs, int n, con
 // (also under stream capture); more go to a device table staged through the workspace.
 int launch_paged_decode_q4k(const PagedSeg *segs, int nseg, int nseq, int page_tokens,
                             const float *q, float *out, int64_t rs_t, int64_t rs_h,
-                            float scale, Workspace &ws, hipStream_t s) {
+                            float scale, void *stage, Workspace &ws, hipStream_t s) {
+  static_assert(sizeof(DecodeSeg) <= kPagedSegBytes, "segment table entry size");
+  static_assert(kPagedArgSegs == kMaxSegs, "kernel-argument segment count");
   if (nseq < 1 || nseq > kMaxPagedSeqs || nseg < nseq || page_tokens % kBlk != 0)
     return set_error(PKV_ERR_ARG, "paged decode: bad segment plan");
   if (!decode_rows_fit(page_tokens, rs_t)) return PKV_ERR_UNSUPPORTED;
@@ -136,13 +138,10 @@ int launch_paged_decode_q4k(const PagedSeg *segs, int nseg, int nseq, int page_t
     if (cap != hipStreamCaptureStatusNone)
       return set_error(PKV_ERR_UNSUPPORTED,
                        "paged decode over more than 32 pages cannot be captured in a graph");
-    rc = ws.reserve_host(tab_bytes);
-    if (rc) return rc;
-    memcpy(ws.host, tab.data(), tab_bytes);
+    if (stage == nullptr) return set_error(PKV_ERR_ARG, "paged decode: no staging buffer");
+    memcpy(stage, tab.data(), tab_bytes);
     DecodeSeg *dtab = reinterpret_cast<DecodeSeg *>(static_cast<uint8_t *>(ws.ptr) + tab_off);
-    PKV_HIP(hipMemcpyAsync(dtab, ws.host, tab_bytes, hipMemcpyHostToDevice, s));
-    rc = ws.mark_host_used(s);
-    if (rc) return rc;
+    PKV_HIP(hipMemcpyAsync(dtab, stage, tab_bytes, hipMemcpyHostToDevice, s));
     d.dseg = dtab;
     d.wps = wps;
   }

@@ -104,6 +104,11 @@ int launch_append_paged(int quant, const float *k, const float *v, uint8_t *kpoo
                         uint8_t *vpool, const int32_t *page_tab, int page_lg,
                         int64_t page_bytes, int heads, int head_dim, int64_t n, int64_t t0,
                         hipStream_t s);
+// One token into each of n <= kAppendSeqs rows sets (k, v [n, heads, 1, head_dim]): row
+// (b, h) at row_off[b] + h * bpr of each pool plane.
+constexpr int kAppendSeqs = 32;
+int launch_append_rows(int quant, const float *k, const float *v, uint8_t *kpool, uint8_t *vpool,
+                       const int64_t *row_off, int n, int heads, int head_dim, hipStream_t s);
 // Dequantize rows [0, S) to f32 [batch, heads, S, head_dim].
 int launch_dequant(int quant, const uint8_t *kc, const uint8_t *vc, float *ko, float *vo,
                    int batch, int heads, int head_dim, int64_t S, hipStream_t s);
@@ -180,13 +185,18 @@ struct PagedSeg {
 // [nseq][16][256]), over their pages: segs lists every page run, sequence by sequence
 // (qi 0, 0, .., 1, ..), each at most page_tokens keys. 16 query heads, 2 KV heads,
 // head_dim 256.
+// More than 32 segments travel in a device table copied from `stage`, a pinned host
+// buffer of at least nseg * kPagedSegBytes bytes that the caller keeps unchanged until the
+// copy has run (it records an event after the call).
 constexpr int kMaxPagedSeqs = 32;
+constexpr int kPagedArgSegs = 32;  // segments carried in the kernel arguments
+constexpr size_t kPagedSegBytes = 64;
 int launch_paged_decode_q4k(const PagedSeg *segs, int nseg, int nseq, int page_tokens,
                             const float *q, float *out, int64_t rs_t, int64_t rs_h,
-                            float scale, Workspace &ws, hipStream_t s);
+                            float scale, void *stage, Workspace &ws, hipStream_t s);
 int launch_paged_decode_q8(const PagedSeg *segs, int nseg, int nseq, int page_tokens,
                            const float *q, float *out, int64_t rs_t, int64_t rs_h, float scale,
-                           Workspace &ws, hipStream_t s);
+                           void *stage, Workspace &ws, hipStream_t s);
 
 // ---- launchers (pkv_util.hip) ----
 int launch_fill_normal(float *dst, size_t n, uint64_t seed, uint64_t stream_id, float scale,

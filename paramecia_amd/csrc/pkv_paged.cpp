@@ -40,6 +40,15 @@ struct pkv_pool {
   int live_seqs;
   pkv::Workspace ws;      // split-K partials, copy tables, pinned staging
   pkv::Workspace gather;  // contiguous rows of one sequence
+  // Pinned staging slots for segment and page tables, used in turn: a slot is reused only
+  // after the copy that read it has run (its event), which for kStages slots is kStages
+  // calls back, so the host rarely waits for the device
+  static constexpr int kStages = 8;
+  void *stage[kStages] = {};
+  size_t stage_bytes[kStages] = {};
+  hipEvent_t stage_ev[kStages] = {};
+  bool stage_pending[kStages] = {};
+  int stage_next = 0;
 };
 
 struct pkv_seq {
@@ -78,16 +87,44 @@ size_t pages_for(const pkv_pool *p, int64_t tokens) {
 uint8_t *page_k(const pkv_pool *p, int32_t id) { return p->k + (size_t)id * p->page_bytes; }
 uint8_t *page_v(const pkv_pool *p, int32_t id) { return p->v + (size_t)id * p->page_bytes; }
 
-// The page table of s into its device copy, staged through the pool's pinned buffer.
+// A free pinned staging slot of at least `bytes` (waits for the copy that last read it).
+int stage_acquire(pkv_pool *p, size_t bytes, int *slot) {
+  const int i = p->stage_next;
+  p->stage_next = (i + 1) % pkv_pool::kStages;
+  if (p->stage_pending[i]) {
+    PKV_HIP(hipEventSynchronize(p->stage_ev[i]));
+    p->stage_pending[i] = false;
+  }
+  if (p->stage_bytes[i] < bytes) {  // (sized at creation for every page of the pool)
+    if (p->stage[i]) PKV_HIP(hipHostFree(p->stage[i]));
+    p->stage[i] = nullptr;
+    p->stage_bytes[i] = 0;
+    const size_t want = bytes < 4096 ? 4096 : bytes + bytes / 2;
+    PKV_HIP(hipHostMalloc(&p->stage[i], want, hipHostMallocDefault));
+    p->stage_bytes[i] = want;
+  }
+  *slot = i;
+  return PKV_OK;
+}
+
+// The slot's copy is queued: mark it in use until the stream passes this point.
+int stage_release(pkv_pool *p, int slot) {
+  PKV_HIP(hipEventRecord(p->stage_ev[slot], p->stream));
+  p->stage_pending[slot] = true;
+  return PKV_OK;
+}
+
+// The page table of s into its device copy, staged through a pinned slot.
 int upload_pages(pkv_seq *s) {
   pkv_pool *p = s->pool;
   const size_t bytes = s->pages.size() * sizeof(int32_t);
   if (bytes == 0) return PKV_OK;
-  int rc = p->ws.reserve_host(bytes);
+  int slot = 0;
+  int rc = stage_acquire(p, bytes, &slot);
   if (rc) return rc;
-  memcpy(p->ws.host, s->pages.data(), bytes);
-  PKV_HIP(hipMemcpyAsync(s->d_pages, p->ws.host, bytes, hipMemcpyHostToDevice, p->stream));
-  return p->ws.mark_host_used(p->stream);
+  memcpy(p->stage[slot], s->pages.data(), bytes);
+  PKV_HIP(hipMemcpyAsync(s->d_pages, p->stage[slot], bytes, hipMemcpyHostToDevice, p->stream));
+  return stage_release(p, slot);
 }
 
 // The rows of tokens [0, len) of s, contiguous ([token][head] rows) in p->gather: K at
@@ -118,6 +155,38 @@ int gather_rows(const pkv_seq *s, uint8_t **kc, uint8_t **vc) {
                               p->stream);
 }
 
+// Pages for n more tokens of s: a shared, partly filled last page is first copied into a
+// page of s's own, then fresh pages follow. PKV_ERR_OVERFLOW, with nothing changed, when
+// the pool lacks them (`reserved`: pages already promised to other sequences of the call).
+int make_room(pkv_seq *s, int64_t n, size_t *reserved) {
+  pkv_pool *p = s->pool;
+  const size_t have = s->pages.size(), need = pages_for(p, s->len + n);
+  const bool cow = (s->len & (p->page_tokens - 1)) != 0 && p->refs[(size_t)s->pages.back()] > 1;
+  const size_t fresh = need - have + (cow ? 1 : 0);
+  const size_t avail = p->free_list.size() - (reserved ? *reserved : 0);
+  if (fresh > avail)
+    return set_error(PKV_ERR_OVERFLOW, "Paged KV pool overflow: " + std::to_string(fresh) +
+                                           " more pages needed, " + std::to_string(avail) +
+                                           " free");
+  if (reserved) {  // a dry run: count only
+    *reserved += fresh;
+    return PKV_OK;
+  }
+  if (cow) {
+    // the shared, partly filled last page: its rows into a page of this sequence's own
+    const int32_t old = s->pages.back(), mine = take_page(p);
+    const size_t bytes = (size_t)(s->len & (p->page_tokens - 1)) * p->n_kv_heads * p->bpr;
+    PKV_HIP(hipMemcpyAsync(page_k(p, mine), page_k(p, old), bytes, hipMemcpyDeviceToDevice,
+                           p->stream));
+    PKV_HIP(hipMemcpyAsync(page_v(p, mine), page_v(p, old), bytes, hipMemcpyDeviceToDevice,
+                           p->stream));
+    release_page(p, old);
+    s->pages.back() = mine;
+  }
+  while (s->pages.size() < need) s->pages.push_back(take_page(p));
+  return PKV_OK;
+}
+
 bool fast_decode_shape(const pkv_pool *p, int num_heads) {
   return (p->quant == PKV_QUANT_Q4K || p->quant == PKV_QUANT_Q8_0) && p->head_dim == 256 &&
          p->n_kv_heads == 2 && num_heads == 16;
@@ -137,11 +206,24 @@ int paged_decode(pkv_pool *p, pkv_seq *const *seqs, int n, const float *q, float
     }
   }
   const int64_t rs_t = (int64_t)p->n_kv_heads * (int64_t)p->bpr, rs_h = (int64_t)p->bpr;
-  if (p->quant == PKV_QUANT_Q4K)
-    return launch_paged_decode_q4k(segs.data(), (int)segs.size(), n, p->page_tokens, q, out,
-                                   rs_t, rs_h, scale, p->ws, p->stream);
-  return launch_paged_decode_q8(segs.data(), (int)segs.size(), n, p->page_tokens, q, out, rs_t,
-                                rs_h, scale, p->ws, p->stream);
+  int slot = -1;
+  void *stage = nullptr;
+  if (segs.size() > (size_t)kPagedArgSegs) {  // a device table, staged through a pinned slot
+    const int rc = stage_acquire(p, segs.size() * kPagedSegBytes, &slot);
+    if (rc) return rc;
+    stage = p->stage[slot];
+  }
+  const int rc =
+      p->quant == PKV_QUANT_Q4K
+          ? launch_paged_decode_q4k(segs.data(), (int)segs.size(), n, p->page_tokens, q, out,
+                                    rs_t, rs_h, scale, stage, p->ws, p->stream)
+          : launch_paged_decode_q8(segs.data(), (int)segs.size(), n, p->page_tokens, q, out,
+                                   rs_t, rs_h, scale, stage, p->ws, p->stream);
+  if (slot >= 0) {
+    const int rs = stage_release(p, slot);
+    if (!rc && rs) return rs;
+  }
+  return rc;
 }
 
 }  // namespace
@@ -184,6 +266,24 @@ int pkv_pool_create(int quant, int n_kv_heads, int head_dim, int page_tokens, in
     delete p;
     return set_error(PKV_ERR_HIP, std::string("pool allocation: ") + hipGetErrorString(e));
   }
+  // the staging slots up front (pinned allocations can wait for the device): each holds a
+  // segment table of every page of the pool, or a page table
+  const size_t stage_bytes = (size_t)n_pages * kPagedSegBytes + 4096;
+  for (int i = 0; i < pkv_pool::kStages && e == hipSuccess; ++i) {
+    e = hipHostMalloc(&p->stage[i], stage_bytes, hipHostMallocDefault);
+    if (e == hipSuccess) p->stage_bytes[i] = stage_bytes;
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&p->stage_ev[i], hipEventDisableTiming);
+  }
+  if (e != hipSuccess) {
+    for (int i = 0; i < pkv_pool::kStages; ++i) {
+      if (p->stage[i]) (void)hipHostFree(p->stage[i]);
+      if (p->stage_ev[i]) (void)hipEventDestroy(p->stage_ev[i]);
+    }
+    (void)hipFree(p->k);
+    (void)hipFree(p->v);
+    delete p;
+    return set_error(PKV_ERR_HIP, std::string("pool staging allocation: ") + hipGetErrorString(e));
+  }
   p->refs.assign((size_t)n_pages, 0);
   p->free_list.reserve((size_t)n_pages);
   for (int i = n_pages - 1; i >= 0; --i) p->free_list.push_back(i);  // page 0 first
@@ -199,6 +299,10 @@ int pkv_pool_destroy(pkv_pool *p) {
   PKV_HIP(hipStreamSynchronize(p->stream));
   (void)hipFree(p->k);
   (void)hipFree(p->v);
+  for (int i = 0; i < pkv_pool::kStages; ++i) {
+    if (p->stage[i]) (void)hipHostFree(p->stage[i]);
+    if (p->stage_ev[i]) (void)hipEventDestroy(p->stage_ev[i]);
+  }
   delete p;
   return PKV_OK;
 }
@@ -278,32 +382,50 @@ int pkv_seq_append(pkv_seq *s, const float *k, const float *v, int64_t n, int64_
     pkv_seq_truncate(s, offset);
   }
   if (n == 0) return PKV_OK;
-  const size_t have = s->pages.size(), need = pages_for(p, s->len + n);
-  const bool cow = (s->len & (p->page_tokens - 1)) != 0 && p->refs[(size_t)s->pages.back()] > 1;
-  const size_t fresh = need - have + (cow ? 1 : 0);
-  if (fresh > p->free_list.size())
-    return set_error(PKV_ERR_OVERFLOW, "Paged KV pool overflow: " + std::to_string(fresh) +
-                                           " more pages needed, " +
-                                           std::to_string(p->free_list.size()) + " free");
-  if (cow) {
-    // the shared, partly filled last page: its rows into a page of this sequence's own
-    const int32_t old = s->pages.back(), mine = take_page(p);
-    const size_t bytes = (size_t)(s->len & (p->page_tokens - 1)) * p->n_kv_heads * p->bpr;
-    PKV_HIP(hipMemcpyAsync(page_k(p, mine), page_k(p, old), bytes, hipMemcpyDeviceToDevice,
-                           p->stream));
-    PKV_HIP(hipMemcpyAsync(page_v(p, mine), page_v(p, old), bytes, hipMemcpyDeviceToDevice,
-                           p->stream));
-    release_page(p, old);
-    s->pages.back() = mine;
-  }
-  while (s->pages.size() < need) s->pages.push_back(take_page(p));
-  int rc = upload_pages(s);
+  int rc = make_room(s, n, nullptr);
+  if (rc) return rc;
+  rc = upload_pages(s);
   if (rc) return rc;
   rc = launch_append_paged(p->quant, k, v, p->k, p->v, s->d_pages, p->page_lg,
                            (int64_t)p->page_bytes, p->n_kv_heads, p->head_dim, n, s->len,
                            p->stream);
   if (rc) return rc;
   s->len += n;
+  return PKV_OK;
+}
+
+int pkv_seq_append_batched(pkv_seq *const *seqs, int n, const float *k, const float *v) {
+  if (!seqs || n <= 0 || !k || !v) return set_error(PKV_ERR_ARG, "null argument or n <= 0");
+  pkv_pool *p = seqs[0] ? seqs[0]->pool : nullptr;
+  for (int i = 0; i < n; ++i) {
+    if (!seqs[i] || seqs[i]->pool != p)
+      return set_error(PKV_ERR_ARG, "every sequence must belong to the same pool");
+    for (int j = 0; j < i; ++j)
+      if (seqs[j] == seqs[i]) return set_error(PKV_ERR_ARG, "a sequence appears twice");
+  }
+  // all or nothing: count the pages first
+  size_t reserved = 0;
+  for (int i = 0; i < n; ++i) {
+    const int rc = make_room(seqs[i], 1, &reserved);
+    if (rc) return rc;
+  }
+  const size_t per = (size_t)p->n_kv_heads * p->head_dim;
+  for (int i0 = 0; i0 < n; i0 += kAppendSeqs) {
+    const int m = n - i0 < kAppendSeqs ? n - i0 : kAppendSeqs;
+    int64_t off[kAppendSeqs];
+    for (int i = 0; i < m; ++i) {
+      pkv_seq *s = seqs[i0 + i];
+      const int rc = make_room(s, 1, nullptr);
+      if (rc) return rc;
+      const int64_t t = s->len;
+      off[i] = (int64_t)s->pages[(size_t)(t >> p->page_lg)] * (int64_t)p->page_bytes +
+               (t & (p->page_tokens - 1)) * (int64_t)p->n_kv_heads * (int64_t)p->bpr;
+    }
+    const int rc = launch_append_rows(p->quant, k + i0 * per, v + i0 * per, p->k, p->v, off, m,
+                                      p->n_kv_heads, p->head_dim, p->stream);
+    if (rc) return rc;
+    for (int i = 0; i < m; ++i) ++seqs[i0 + i]->len;
+  }
   return PKV_OK;
 }
 

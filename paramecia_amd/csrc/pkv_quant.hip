@@ -29,6 +29,10 @@ struct AppendArgs {
   const int32_t *page_tab;
   int page_lg;
   int64_t page_bytes;
+  // One token into each of `batch` paged sequences (row_mode): row (b, h) at byte
+  // row_off[b] + h * bpr of each plane
+  int row_mode;
+  int64_t row_off[kAppendSeqs];
 };
 
 // Source element e (< padded) of new row (t, b, h); zero padding past head_dim.
@@ -43,6 +47,7 @@ __device__ __forceinline__ int64_t dst_row(const AppendArgs &a, int64_t t, int b
 }
 // The destination row of new token t (batch row b, head h) in plane p (K 0, V 1).
 __device__ __forceinline__ uint8_t *row_ptr(const AppendArgs &a, int p, int64_t t, int b, int h) {
+  if (a.row_mode) return a.dst[p] + a.row_off[b] + (int64_t)h * a.bpr;
   if (a.page_tab != nullptr) {
     const int64_t tok = a.t0 + t, in_page = tok & ((int64_t(1) << a.page_lg) - 1);
     const int64_t pg = a.page_tab[tok >> a.page_lg];
@@ -364,6 +369,7 @@ int launch_append(int quant, const float *k, const float *v, uint8_t *kc, uint8_
   a.page_tab = nullptr;
   a.page_lg = 0;
   a.page_bytes = 0;
+  a.row_mode = 0;
   return launch_append_args(quant, a, s);
 }
 
@@ -387,6 +393,31 @@ int launch_append_paged(int quant, const float *k, const float *v, uint8_t *kpoo
   a.page_tab = page_tab;
   a.page_lg = page_lg;
   a.page_bytes = page_bytes;
+  a.row_mode = 0;
+  return launch_append_args(quant, a, s);
+}
+
+int launch_append_rows(int quant, const float *k, const float *v, uint8_t *kpool, uint8_t *vpool,
+                       const int64_t *row_off, int n, int heads, int head_dim, hipStream_t s) {
+  if (n <= 0) return PKV_OK;
+  if (n > kAppendSeqs) return set_error(PKV_ERR_ARG, "too many rows for one append launch");
+  AppendArgs a;
+  a.src[0] = k;
+  a.src[1] = v;
+  a.dst[0] = kpool;
+  a.dst[1] = vpool;
+  a.batch = n;
+  a.heads = heads;
+  a.head_dim = head_dim;
+  a.padded = padded_dim(quant, head_dim);
+  a.n = 1;
+  a.t0 = 0;
+  a.bpr = (int64_t)row_bytes(quant, head_dim);
+  a.page_tab = nullptr;
+  a.page_lg = 0;
+  a.page_bytes = 0;
+  a.row_mode = 1;
+  for (int i = 0; i < n; ++i) a.row_off[i] = row_off[i];
   return launch_append_args(quant, a, s);
 }
 

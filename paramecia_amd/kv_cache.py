@@ -313,6 +313,17 @@ class PagedKvPool:
     def sequence(self) -> "PagedSequence":
         return PagedSequence(self)
 
+    def append_batched(self, seqs: Sequence["PagedSequence"], new_k: torch.Tensor,
+                       new_v: torch.Tensor) -> None:
+        """One token per sequence: new_k, new_v [n, num_kv_heads, 1, head_dim] f32
+        (pkv_seq_append_batched)."""
+        self._follow_stream()
+        k, v = _f32(new_k, "new_k"), _f32(new_v, "new_v")
+        if k.shape != v.shape or k.dim() != 4 or k.shape[0] != len(seqs) or k.shape[2] != 1:
+            raise KvCacheError("new_k/new_v must both be [n_sequences, heads, 1, head_dim]")
+        arr = (ctypes.c_void_p * len(seqs))(*[sq.handle.value for sq in seqs])
+        _call(lib().pkv_seq_append_batched(arr, len(seqs), _ptr(k), _ptr(v)))
+
     def decode_batched(self, seqs: Sequence["PagedSequence"], q: torch.Tensor,
                        scale: float) -> torch.Tensor:
         """One decode query per sequence: q [n, num_heads, head_dim] -> out of that shape,

@@ -219,3 +219,37 @@ def test_rules_offset_overflow_truncate_reuse(pk, orc):
     fill(pk, orc, t, c2, rng, [128], 2, 256)
     assert pool.free_pages == 0
     assert np.array_equal(host(t.get_kv()[1]), c2.get_kv()[1])
+
+
+@pytest.mark.parametrize("quant", [Q4K, Q8_0, F16])
+def test_append_batched_matches_single(pk, orc, quant):
+    """One token into each of 5 sequences in one launch: a sequence at a page boundary, a
+    forked pair sharing a partly filled page (each copies it first), an empty one."""
+    say(f"paged batched append quant={quant}")
+    rng = np.random.default_rng(123 + quant)
+    pool = pk.PagedKvPool(2, 256, 32, 32, pk.KvCacheQuantization(quant))
+    lens = [32, 40, 0, 5]
+    seqs, caches = [], []
+    for n in lens:
+        s = pool.sequence()
+        c = orc.Cache(quant, 1, 2, 256, 64)
+        if n:
+            fill(pk, orc, s, c, rng, [n], 2, 256)
+        seqs.append(s)
+        caches.append(c)
+    fork = seqs[1].fork()  # shares seqs[1]'s page with 8 rows
+    cf = orc.Cache(quant, 1, 2, 256, 64)
+    cf.load_bytes(*caches[1].valid_bytes(), 40)
+    seqs.append(fork)
+    caches.append(cf)
+    kn = rng.standard_normal((5, 2, 1, 256)).astype(np.float32)
+    vn = rng.standard_normal((5, 2, 1, 256)).astype(np.float32)
+    pool.append_batched(seqs, dev(kn), dev(vn))
+    for i, (s, c) in enumerate(zip(seqs, caches)):
+        assert c.append(kn[i:i + 1], vn[i:i + 1]) == 0
+        assert s.seq_len == c.seq_len
+        k, v = s.get_kv()
+        rk, rv = c.get_kv()
+        assert np.array_equal(host(k), rk) and np.array_equal(host(v), rv), i
+    with pytest.raises(pk.KvCacheError):
+        pool.append_batched([seqs[0], seqs[0]], dev(kn[:2]), dev(vn[:2]))
