@@ -12,10 +12,15 @@ better); `roofline` prices the dominant kernel against MI355X's 8 TB/s HBM peak;
 `cpu_baseline` times the CPU oracle's faithful restatement of the reference path
 (dequantize-all + repeat_kv + SDPA, qwen3_next.rs:2470-2605) on the host cores.
 
-`--config N` measures another workload of the path instead (one JSON line each;
-`--config all` prints all five): 1 Q8_0 decode over 4097 keys, 2 a 512-token Q4K
-prefill chunk over 16896 keys, 4 PrefixCache restore of 12 full + 36 linear layers plus
-a 1024-token suffix, 5 a 16-sequence batched decode step over 12 layers.
+The default run also measures the other BASELINE configs after the headline, in the
+same process, and attaches them to the headline line as `other_configs` (value, unit,
+roofline; their CPU baselines are left to their own `--config N` runs):
+1 Q8_0 decode over 4097 keys, 2 a 512-token Q4K prefill chunk over 16896 keys, 4
+PrefixCache restore of 12 full + 36 linear layers plus a 1024-token suffix, 5 a
+16-sequence batched decode step over 12 layers. `--headline-only` skips them.
+
+`--config N` measures one workload instead (one JSON line each; `--config all` prints
+every config's line, 6 and 7 included).
 """
 from __future__ import annotations
 
@@ -175,8 +180,11 @@ def run_config3(args):
     ms = graph_time(torch, step, args.steps, args.warmup, reps)
     ms_1 = graph_time(torch, step, args.steps, args.warmup, 1)
 
-    # per-launch duration of the layer's kernels: the GPU is kept busy by a sleep kernel
-    # while the host enqueues, so each event pair brackets device time only
+    # Per-launch duration of a layer's kernels (decode + combine): the layer's share of
+    # the graph-timed step, ms / L, which also holds the gaps between launches and agrees
+    # with rocprofv3's kernel durations. Also reported: each layer bracketed by its own
+    # event pair while a sleep kernel keeps the GPU busy as the host enqueues (the event
+    # records then add about 3 us per layer).
     ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(L)] for _ in range(args.steps)]
     sleep = getattr(torch.cuda, "_sleep", None)
@@ -185,7 +193,8 @@ def run_config3(args):
             sleep(20_000_000)
         step(ev[s_])
     torch.cuda.synchronize()
-    per_launch_ms = sum(a.elapsed_time(b) for row in ev for a, b in row) / (args.steps * L)
+    bracketed_ms = sum(a.elapsed_time(b) for row in ev for a, b in row) / (args.steps * L)
+    per_launch_ms = ms / L
 
     keys = S + 1
     step_bytes = L * layer_bytes(keys)
@@ -228,6 +237,8 @@ def run_config3(args):
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
             "bytes_per_launch": layer_bytes(keys),
             "avg_launch_us": round(per_launch_ms * 1000.0, 2),
+            "avg_launch_source": "graph-timed step / layers (HIP events around the replays)",
+            "event_bracketed_launch_us": round(bracketed_ms * 1000.0, 2),
             "traffic": traffic(3),
             "traffic_source": MEASURED_TRAFFIC[3][1],
         },
@@ -924,11 +935,39 @@ def run_config7(args):
     return r
 
 
+COMPANIONS = ("1", "2", "4", "5")  # BASELINE configs measured beside the headline
+
+
+def companion_configs(torch, args, runners):
+    """Configs 1, 2, 4 and 5 measured after the headline in the same run (no CPU
+    baselines), summarised for the headline line. A config that fails records its error
+    instead, so that the headline line is still printed."""
+    sub = argparse.Namespace(**vars(args))
+    sub.no_cpu_baseline = True
+    sub.paged = 0
+    out = {}
+    for cfg in COMPANIONS:
+        try:
+            r = runners[cfg](sub)
+            c = {k: r[k] for k in ("metric", "value", "unit", "ms_per_step", "steps")}
+            c["workload"] = r["config"]["workload"]
+            rf = r.get("roofline")
+            if rf:
+                c["roofline"] = {k: rf[k] for k in ("kernel", "bound", "achieved", "peak",
+                                                     "unit", "frac") if k in rf}
+            out[cfg] = c
+        except Exception as e:  # reported in the line, not raised
+            out[cfg] = {"error": f"{type(e).__name__}: {e}"}
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="3",
                     help="1, 2, 3 (headline, default), 4, 5, 6 (Gated-DeltaNet step), "
                          "7 (gated o_proj) or all")
@@ -957,6 +996,8 @@ def main() -> int:
                          "counter passes, which do not support graph capture here)")
     ap.add_argument("--no-copy-ceiling", action="store_true",
                     help="skip the device-to-device copy ceiling measured after each config")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="default run: measure config 3 only, without configs 1, 2, 4 and 5")
     args = ap.parse_args()
     global NO_GRAPH
     NO_GRAPH = args.no_graph
@@ -981,6 +1022,8 @@ def main() -> int:
             calib_copy(torch, args.calib_copy_mib)
         if not args.no_copy_ceiling:
             add_copy_ceiling(torch, r)
+        if cfg == "3" and args.config == "3" and not args.headline_only:
+            r["other_configs"] = companion_configs(torch, args, runners)
         print(json.dumps(r), flush=True)
     return 0
 
