@@ -47,7 +47,7 @@ MEASURED_TRAFFIC = {
     2: (170_260_000, "profiles/q4k_prefill_config2.md: prefill kernel + split merge"),
     4: (1_064_255_795, "profiles/prefix_restore_config4.md: copy_segments_kernel read + "
                        "written"),
-    5: (418_800_000, "profiles/q4k_batched_decode_config5.md: decode + combine per layer"),
+    5: (415_070_000, "profiles/q4k_batched_decode_config5.md: decode + combine per layer"),
     6: (73_730_000, "profiles/deltanet_step_config6.md: per launch at batch 16"),
 }
 

@@ -97,6 +97,7 @@ int launch_paged_decode_q4k(const PagedSeg *segs, int nseg, int nseq, int page_t
     if (segs[i].qi < qprev || segs[i].qi >= nseq || segs[i].len < 0 || segs[i].len > page_tokens)
       return set_error(PKV_ERR_ARG, "paged decode: segments out of order");
     while (qprev < segs[i].qi) c.wg0[++qprev] = i * wps;
+    c.wg1[qprev] = (i + 1) * wps;
     d.k = segs[i].k;
     d.v = segs[i].v;
     d.seq_k = segs[i].len;
@@ -104,13 +105,15 @@ int launch_paged_decode_q4k(const PagedSeg *segs, int nseg, int nseq, int page_t
     d.nblk = (int)((segs[i].len + kBlk - 1) / kBlk);
     d.wg0 = i * wps;
     d.qi = segs[i].qi;
+    d.voff = 0;
   }
   if (qprev != nseq - 1) return set_error(PKV_ERR_ARG, "paged decode: a sequence has no page");
-  c.wg0[nseq] = nwg;
   DecodeArgsT<kMaxSegs> d;
   d.nseg = nseg;
   d.nwg = nwg;
   d.bpw = bpw;
+  d.wps = wps;
+  d.vq = d.vr = 0;
   d.rs_t = rs_t;
   d.rs_h = rs_h;
   d.sl2 = scale * kLog2e;
@@ -131,7 +134,6 @@ int launch_paged_decode_q4k(const PagedSeg *segs, int nseg, int nseq, int page_t
   if (nseg <= kMaxSegs) {
     for (int i = 0; i < nseg; ++i) d.seg[i] = tab[(size_t)i];
     d.dseg = nullptr;
-    d.wps = wps;
   } else {
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     PKV_HIP(hipStreamIsCapturing(s, &cap));
@@ -143,7 +145,6 @@ int launch_paged_decode_q4k(const PagedSeg *segs, int nseg, int nseq, int page_t
     DecodeSeg *dtab = reinterpret_cast<DecodeSeg *>(static_cast<uint8_t *>(ws.ptr) + tab_off);
     PKV_HIP(hipMemcpyAsync(dtab, stage, tab_bytes, hipMemcpyHostToDevice, s));
     d.dseg = dtab;
-    d.wps = wps;
   }
   hipLaunchKernelGGL((q4k_decode_kernel<false, kMaxSegs>), dim3((unsigned)nwg), dim3(kThreads), 0,
                      s, d);
@@ -154,8 +155,7 @@ int launch_paged_decode_q4k(const PagedSeg *segs, int nseg, int nseq, int page_t
   c.dq = nullptr;
   c.out = out;
   c.sl2 = d.sl2;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(16 * 8, (unsigned)nseq), dim3(256), 0, s, c);
-  PKV_HIP(hipGetLastError());
+  if (const int rc_ = launch_combine(c, nseq, s)) return rc_;
   return PKV_OK;
 }
 

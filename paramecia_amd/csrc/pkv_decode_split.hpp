@@ -32,17 +32,19 @@ __host__ __device__ __forceinline__ int tile_index(int e) {
 }
 
 // One launch serves up to kMaxSegs segments: the batch rows of one cache, or the
-// sequences of a batched decode step (each with its own cache and length). Segment s
-// owns workgroups [wg0, next wg0); every workgroup writes one split-K partial, indexed
-// by its workgroup id.
+// sequences of a batched decode step (each with its own cache and length), or the pages
+// of paged sequences. Every piece of work (a workgroup's blocks of one segment) writes
+// one split-K partial; the combine merges the partials of each output row.
 constexpr int kMaxSegs = 32;
 struct DecodeSeg {
   uint8_t *k, *v;  // K and V rows of token 0, KV head 0 (rows of head 1 follow at rs_h)
   int64_t seq_k;   // keys held in the cache before this step's append (all attended)
   int64_t t_new;   // row the fused step writes
-  int nblk, wg0;
+  int nblk;
+  int wg0;         // first workgroup with blocks of this segment
   int qi;          // query / output row of the segment (several segments may share one:
                    // the pages of a paged sequence, merged by the combine)
+  int voff;        // stream mode: first block of the segment on the virtual block line
 };
 struct DecodeSegIn {
   uint8_t *k, *v;
@@ -86,15 +88,21 @@ __device__ __forceinline__ float wave_sum(float x) {
 // 2^(score - M).
 constexpr int kCombSlices = 32;  // partial slices (8 threads each)
 constexpr int kCombChunk = 8;    // partials per slice per round
-struct CombineArgs {
+// The output-row table is sized at compile time: one row for a single cache of batch 1
+// (the common launch carries the small argument block), kMaxSegs otherwise.
+template <int kRows>
+struct CombineArgsT {
   const float *part;      // [wg][16][kPartRow]
   const float2 *ml;       // [wg][16] (m, l)
   const float *q, *dq;    // [nseg][16][256], [nseg][4][256] or null
   float *out;             // [nseg][16][256]
   float sl2;
-  int wg0[kMaxSegs + 1];  // segment s owns partials [wg0[s], wg0[s + 1])
+  int wg0[kRows];  // output row b merges partials [wg0[b], wg1[b])
+  int wg1[kRows];
 };
-__global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs c) {
+using CombineArgs = CombineArgsT<kMaxSegs>;
+template <int kRows>
+__global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgsT<kRows> c) {
   __shared__ float dotp[4];
   __shared__ float mx[kCombSlices], ls[kCombSlices];
   __shared__ float4 accs[kCombSlices][8];
@@ -102,7 +110,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs c) {
   const int tid = threadIdx.x, ps = tid >> 3, g4 = tid & 7;
   const float *dq = c.dq;
   const float sl2 = c.sl2;
-  const int wbeg = c.wg0[b], nwg = c.wg0[b + 1] - wbeg;
+  const int wbeg = c.wg0[b], nwg = c.wg1[b] - wbeg;
   const float *P = c.part + ((int64_t)wbeg * 16 + h) * kPartRow + i0 + 4 * g4;
   const float2 *ML = c.ml + (int64_t)wbeg * 16 + h;
   const int per = (nwg + kCombSlices - 1) / kCombSlices;
@@ -181,6 +189,27 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs c) {
     if (dq != nullptr) sum += f_new * dq[((int64_t)b * 4 + 2 + (h >> 3)) * 256 + e];
     c.out[((int64_t)b * 16 + h) * 256 + e] = L > 0.0f ? sum / L : 0.0f;
   }
+}
+
+// Launch the combine over n output rows (grid: 128 (head, slice) workgroups per row).
+static inline int launch_combine(const CombineArgs &c, int n, hipStream_t s) {
+  if (n == 1) {
+    CombineArgsT<1> c1;
+    c1.part = c.part;
+    c1.ml = c.ml;
+    c1.q = c.q;
+    c1.dq = c.dq;
+    c1.out = c.out;
+    c1.sl2 = c.sl2;
+    c1.wg0[0] = c.wg0[0];
+    c1.wg1[0] = c.wg1[0];
+    hipLaunchKernelGGL(decode_combine_kernel<1>, dim3(16 * 8, 1u), dim3(256), 0, s, c1);
+  } else {
+    hipLaunchKernelGGL(decode_combine_kernel<kMaxSegs>, dim3(16 * 8, (unsigned)n), dim3(256), 0,
+                       s, c);
+  }
+  PKV_HIP(hipGetLastError());
+  return PKV_OK;
 }
 
 }  // namespace

@@ -9,8 +9,11 @@
 // SIMD always has a second wave to issue while one waits) owns a contiguous block
 // range; waves 2s and 2s+1 take KV heads 0 and 1 of the same blocks, so the two halves
 // of a token's 288-byte K (and V) rows are read together. Each wave streams its blocks
-// through two LDS stages with buffer_load ... lds. Extra workgroups past the main ones
-// quantize the new token's rows for a fused decode step (bit-exact Q4K).
+// through two LDS stages with buffer_load ... lds. With several segments (the sequences
+// of a batched step) the launch's blocks form one line that the workgroups split evenly
+// (stream-K): a workgroup whose range crosses a segment boundary runs one pass per
+// segment, each with its own partial. Waves 0-3 of the first workgroups also quantize
+// the new token's rows for a fused decode step (bit-exact Q4K).
 //
 // Arithmetic (per KV head, per 16 keys, MFMA f32_16x16x32_f16):
 //   QK: A[key][e] = nibble * sub-block scale code, an integer <= 945 built exactly in
@@ -43,13 +46,17 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;  // two waves per SIMD
 constexpr int kMainWGs = 256;
 constexpr float kLazy = 8.0f;  // log2 headroom of the running max before a rescale
+constexpr int kPieceGap = 6;   // virtual blocks before each segment after the first
 
 // Kernel arguments: the fields shared by every launch, then the segment table sized at
 // compile time (one segment for a single cache of batch 1, kMaxSegs otherwise), so that the
 // common launch carries about 200 bytes of arguments instead of the 1.5 KB of the full
 // table.
 struct DecodeArgsBase {
-  int nseg, nwg, bpw;
+  int nseg, nwg;
+  int bpw, wps;  // fixed mode (wps > 0): blocks per workgroup, workgroups per segment
+  int vq, vr;    // stream mode: workgroup w's range on the virtual block line starts at
+                 // w vq + min(w, vr) and holds vq + (w < vr) blocks
   int64_t rs_t, rs_h;
   float sl2;                   // scale * log2(e)
   const float *q;              // [nseg][16][256]
@@ -62,10 +69,9 @@ struct DecodeArgsBase {
   DecodePrep prep;
   float *q_out;  // [nseg][16][256] prepared q, for the combine
   unsigned *status;  // the device status word (pkv_device_status)
-  // Paged mode (dseg non-null): the segment table lives in device memory, segment s
-  // owning workgroups [s * wps, (s + 1) * wps); the seg array is unused
+  // Fixed mode with dseg non-null: the segment table lives in device memory (the seg
+  // array is unused)
   const DecodeSeg *dseg;
-  int wps;
 };
 template <int kSegs>
 struct DecodeArgsT : DecodeArgsBase {
@@ -518,39 +524,58 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
   const int kv = wave & 1, wsub = wave >> 1;
   const int wg = blockIdx.x;
   const int n = lane & 15, g = lane >> 4;
-  int b = 0;  // segment of this workgroup
-  DecodeSeg sgv;
-  if (a.dseg != nullptr) {
-    b = wg / a.wps;
-    sgv = a.dseg[b];
-  } else {
-    if constexpr (kSegs > 1) {
-      while (b + 1 < a.nseg && wg >= a.seg[b + 1].wg0) ++b;
-    }
-    sgv = a.seg[b];
-  }
-  const DecodeSeg &sg = sgv;
-
-  // ---- blocks of this wave: b0 + wsub, b0 + wsub + 4, ... below b1
-  const int b0 = (wg - sg.wg0) * a.bpw;
-  const int b1 = b0 + a.bpw < sg.nblk ? b0 + a.bpw : sg.nblk;
-  // wave-uniform: loop control and the key mask stay scalar
-  const int first = __builtin_amdgcn_readfirstlane(b0 + wsub);
-  const int nmine = __builtin_amdgcn_readfirstlane(first < b1 ? (b1 - first + 3) / 4 : 0);
   const int kvu = __builtin_amdgcn_readfirstlane(kv);
-  const uint8_t *kbase = sg.k + kvu * a.rs_h;
-  const uint8_t *vbase = sg.v + kvu * a.rs_h;
   const uint32_t rs_t = (uint32_t)a.rs_t;
-  const int64_t seq_k = sg.seq_k;
-  // rows of keys [0, seq_k) of this head; loads past them return zeros (masked keys)
-  const uint32_t span = seq_k > 0 ? (uint32_t)(seq_k - 1) * rs_t + 144u : 0u;
-  const u4s rk = make_rsrc(kbase, span), rv = make_rsrc(vbase, span);
   const LoadPlan P = make_plan(lane, rs_t);
-  const uint32_t bstep = 4u * kBlk * rs_t;  // byte distance between this wave's blocks
-  uint32_t boff = __builtin_amdgcn_readfirstlane((uint32_t)first * kBlk * rs_t);
+  const uint32_t bstep = 4u * kBlk * rs_t;  // byte distance between a wave's blocks
   // LDS byte addresses of this wave's two stages
   const uint32_t st_lds0 = __builtin_amdgcn_readfirstlane(
       (uint32_t)(size_t)((PKV_LDS void *)&sm.run.st[wave][0]));
+
+  // ---- pieces of this workgroup (wave-uniform): segment ps, its blocks [pb0, pb1), the
+  // partial slot. Fixed mode (wps > 0, paged segments): one piece, blocks
+  // [(wg - wg0) bpw, ..) of segment wg / wps, slot wg. Stream mode: the blocks of
+  // [V0, V1) on the launch's virtual block line, one piece per segment met, slot wg + s
+  // (distinct for every piece, consecutive for the pieces of one segment).
+  const int V0 = wg * a.vq + (wg < a.vr ? wg : a.vr);
+  const int V1 = V0 + a.vq + (wg < a.vr ? 1 : 0);
+  int ps = -1, pb0 = 0, pb1 = 0, slot = wg;
+  DecodeSeg sgv = {};  // read only while a piece is held
+  auto next_piece = [&]() -> bool {
+    if constexpr (kSegs == 1) {  // one segment at voff 0: the range is the piece
+      if (ps >= 0) return false;
+      ps = 0;
+      sgv = a.seg[0];
+      pb0 = V0;
+      pb1 = V1 < sgv.nblk ? V1 : sgv.nblk;
+      return V0 < (sgv.nblk > 0 ? sgv.nblk : 1);
+    }
+    if (a.wps > 0) {
+      if (ps >= 0) return false;
+      ps = wg / a.wps;
+      sgv = a.dseg != nullptr ? a.dseg[ps] : a.seg[ps];
+      pb0 = (wg - sgv.wg0) * a.bpw;
+      pb1 = pb0 + a.bpw < sgv.nblk ? pb0 + a.bpw : sgv.nblk;
+      return true;
+    }
+    for (int s = ps + 1; s < a.nseg; ++s) {
+      const int vs = a.seg[s].voff;
+      if (vs >= V1) return false;
+      const int nb = a.seg[s].nblk;
+      const int ve = vs + (nb > 0 ? nb : 1);  // an empty segment holds one virtual block
+      if (ve > V0) {
+        ps = s;
+        sgv = a.seg[s];
+        pb0 = (V0 > vs ? V0 : vs) - vs;
+        const int e = (V1 < ve ? V1 : ve) - vs;
+        pb1 = e < nb ? e : nb;
+        slot = wg + s;
+        return true;
+      }
+    }
+    return false;
+  };
+  bool have = next_piece();
 
   // Fused append: threads 0-255 (waves 0-3) of workgroup r quantize new row r (row
   // 4s + 2p + kv: segment s, K (p = 0) or V (p = 1), KV head kv; further rows go
@@ -580,8 +605,10 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
       if (p == 0) kpe[0] = k_prep_elem(wg >> 2);
       qa4 = reinterpret_cast<const f4 *>(a.prep.q_alpha)[lane];
       const int half = a.prep.n_rot >> 1;
-      rcos = a.prep.cos_tab[sg.t_new * half + (lane & (half - 1))];
-      rsin = a.prep.sin_tab[sg.t_new * half + (lane & (half - 1))];
+      if (have) {  // the first piece's q position (a workgroup without blocks has none)
+        rcos = a.prep.cos_tab[sgv.t_new * half + (lane & (half - 1))];
+        rsin = a.prep.sin_tab[sgv.t_new * half + (lane & (half - 1))];
+      }
       asm volatile("" : "+v"(xq), "+v"(kpe[0].alpha), "+v"(kpe[0].c), "+v"(kpe[0].s),
                    "+v"(rcos), "+v"(rsin), "+v"(qa4));
     } else {
@@ -589,155 +616,8 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
     }
   }
   if (tid == 0) sm.run.t.quant.arrivals = 0u;
-
-  // ---- this wave's q rows, then its first block, into LDS. Every wave's q loads go out
-  // before any stage load (one barrier), so q returns ahead of the block data.
-  {
-    if constexpr (kPrep) {
-      if (!quant) {
-        const int half = a.prep.n_rot >> 1;
-        const int64_t ro = sg.t_new * half;
-        issue_prep_consts(&sm.run.t.tab[wave],
-                          reinterpret_cast<uint8_t *>(&sm.run.st[wave][1]) + 8 * kQRow,
-                          make_rsrc(a.prep.q_alpha, 1024u),
-                          make_rsrc(a.prep.cos_tab + ro, (uint32_t)half * 4u),
-                          make_rsrc(a.prep.sin_tab + ro, (uint32_t)half * 4u), (uint32_t)lane);
-      }
-    }
-    const u4s rq = make_rsrc(a.q + ((int64_t)sg.qi * 16 + 8 * kvu) * 256, 8 * 256 * 4);
-    issue_q(&sm.run.st[wave][1], rq, 16u * lane);
-  }
-  __syncthreads();
-  // every issued block has its first key below seq_k, so its offset is inside the range
-  if (nmine > 0) issue_stage_at(st_lds0, P, rsrc_advance(rk, boff), rsrc_advance(rv, boff));
-
-  // QK B operands: lane (n, g) takes q of head n % 8, elements 64g + 32(s/4) + 8(s%4) +
-  // perm[slot], as the fp16 hi part (n < 8) or the lo remainder (n >= 8); S2 B operand:
-  // the sums of sub-blocks 2g and 2g+1 (elements 64g..64g+31, 64g+32..64g+63, in order).
-  // Built from the wave's own copy of q, so no workgroup barrier is needed.
-  h8 qb[8];
-  h4 q2 = {0, 0, 0, 0};
-  auto build_q = [&]() {
-    // q was issued before this wave's stage loads (12): once at most 12 loads are
-    // outstanding, q has landed
-    if (nmine > 0)
-      asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if constexpr (kPrep) {
-      if (quant) {  // after quantizing: the constants into this wave's table area and tail
-        float *tail = reinterpret_cast<float *>(&sm.run.st[wave][1]) + 8 * (kQRow / 4);
-        reinterpret_cast<f4 *>(&sm.run.t.tab[wave])[lane] = qa4;
-        tail[lane] = lane < 32 ? rcos : 0.0f;
-        tail[64 + lane] = lane < 32 ? rsin : 0.0f;
-        __builtin_amdgcn_wave_barrier();
-      }
-    }
-    const float *qrow = reinterpret_cast<const float *>(&sm.run.st[wave][1]) + (n & 7) * (kQRow / 4) + 64 * g;
-    constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-    float qsum[2] = {0.0f, 0.0f};
-    // hi lanes (n < 8) take fp16(q), lo lanes fp16(q - fp16(q)): both are fp16(q - c)
-    // with c = fp16(q) masked to zero on the hi lanes
-    const uint32_t lo_mask = n < 8 ? 0u : 0xFFFFFFFFu;
-    auto convert = [&](int st, const float (&v8)[8]) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) qsum[st >> 2] += v8[k];
-      uint32_t w[4];
-#pragma unroll
-      for (int pp = 0; pp < 4; ++pp) {
-        const float a0 = v8[perm[2 * pp]], a1 = v8[perm[2 * pp + 1]];
-        const h2 h = {(_Float16)a0, (_Float16)a1};
-        const uint32_t c = as_u(h) & lo_mask;
-        w[pp] = fp16_sub2(a0, a1, c);
-      }
-      qb[st] = __builtin_bit_cast(h8, u4{w[0], w[1], w[2], w[3]});
-    };
-    if constexpr (kPrep) {
-      // q_norm and rope in registers: v[st][k] is element 8 st + k of the lane's 64
-      // (64 g ..) of row n % 8; the row's 4 lanes (g = 0..3) pool their sums of squares,
-      // and the g = 0 lanes hold every rope pair (j, j + 32) of n_rot = 64. q feeds the
-      // attention only: sums in any order and x * (1 / m) are within its tolerance.
-      float v[8][8];
-#pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        const float4 r0 = *reinterpret_cast<const float4 *>(qrow + 8 * st);
-        const float4 r1 = *reinterpret_cast<const float4 *>(qrow + 8 * st + 4);
-        v[st][0] = r0.x; v[st][1] = r0.y; v[st][2] = r0.z; v[st][3] = r0.w;
-        v[st][4] = r1.x; v[st][5] = r1.y; v[st][6] = r1.z; v[st][7] = r1.w;
-      }
-      float ss = 0.0f;
-#pragma unroll
-      for (int st = 0; st < 8; ++st)
-#pragma unroll
-        for (int k = 0; k < 8; ++k) ss = fmaf(v[st][k], v[st][k], ss);
-      {
-        const uint32_t u = __builtin_bit_cast(uint32_t, ss);
-        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-        const uint32_t r0 = r[0], r1 = r[1];
-        ss = __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
-      }
-      {
-        const uint32_t u = __builtin_bit_cast(uint32_t, ss);
-        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-        const uint32_t r0 = r[0], r1 = r[1];
-        ss = __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
-      }
-      const float inv = 1.0f / __builtin_sqrtf(ss * (1.0f / 256.0f) + a.prep.eps);
-      const float *al = reinterpret_cast<const float *>(&sm.run.t.tab[wave]) + 64 * g;
-#pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        const float4 a0 = *reinterpret_cast<const float4 *>(al + 8 * st);
-        const float4 a1 = *reinterpret_cast<const float4 *>(al + 8 * st + 4);
-        const float a8[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-#pragma unroll
-        for (int k = 0; k < 8; ++k) v[st][k] = v[st][k] * inv * a8[k];
-      }
-      if (g == 0) {
-        const float *tail = reinterpret_cast<const float *>(&sm.run.st[wave][1]) + 8 * (kQRow / 4);
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          const float4 c0 = *reinterpret_cast<const float4 *>(tail + 8 * st);
-          const float4 c1 = *reinterpret_cast<const float4 *>(tail + 8 * st + 4);
-          const float4 s0 = *reinterpret_cast<const float4 *>(tail + 64 + 8 * st);
-          const float4 s1 = *reinterpret_cast<const float4 *>(tail + 64 + 8 * st + 4);
-          const float c8[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-          const float s8[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            const float x1 = v[st][k], x2 = v[st + 4][k];
-            v[st][k] = x1 * c8[k] - x2 * s8[k];
-            v[st + 4][k] = x1 * s8[k] + x2 * c8[k];
-          }
-        }
-      }
-      if (wg == sg.wg0 && wsub == 0 && n < 8) {  // the combine's copy of the prepared q
-        float *qo = a.q_out + ((int64_t)sg.qi * 16 + 8 * kvu + n) * 256 + 64 * g;
-#pragma unroll
-        for (int st = 0; st < 8; ++st) {
-          *reinterpret_cast<float4 *>(qo + 8 * st) = float4{v[st][0], v[st][1], v[st][2], v[st][3]};
-          *reinterpret_cast<float4 *>(qo + 8 * st + 4) = float4{v[st][4], v[st][5], v[st][6], v[st][7]};
-        }
-      }
-#pragma unroll
-      for (int st = 0; st < 8; ++st) convert(st, v[st]);
-    } else {
-#pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        const float4 r0 = *reinterpret_cast<const float4 *>(qrow + 32 * (st >> 2) + 8 * (st & 3));
-        const float4 r1 = *reinterpret_cast<const float4 *>(qrow + 32 * (st >> 2) + 8 * (st & 3) + 4);
-        const float v8[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-        convert(st, v8);
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const _Float16 hi = (_Float16)qsum[t];
-      q2[t] = (n < 8) ? hi : (_Float16)(qsum[t] - (float)hi);
-    }
-  };
-  static_assert(kLoadsPerStage == 12, "the vmcnt above counts one stage of loads");
-
-  if (quant) {
+  // Fused append (waves 0-3 of the quantizing workgroups, once): the rows, as above.
+  auto quantize_rows = [&]() {
     // the quantization delays this workgroup's blocks: it outranks the block loops of
     // the waves sharing its SIMDs
     __builtin_amdgcn_s_setprio(3);
@@ -762,146 +642,319 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
       a.dq[(int64_t)row * 256 + tid] = deq;
     }
     __builtin_amdgcn_s_setprio(0);
-  }
-  build_q();
-
-  WaveState S;
-#pragma unroll
-  for (int T2 = 0; T2 < 16; ++T2) S.acc[T2] = f4{0.f, 0.f, 0.f, 0.f};
-  S.accm = f4{0.f, 0.f, 0.f, 0.f};
-  S.m_run = -INFINITY;
-  S.lsum = 0.0f;
-  WaveTab &T = sm.run.t.tab[wave];
-  if (nmine > 0) {
-    const Masks MK = {vconst(0x000F000Fu), vconst(0x00F000F0u), vconst(0x64006400u)};
-    const KScaleSel ks = make_kscale_sel(g);
-    const float clamp_raw = kClampL2 / a.sl2, lazy_raw = kLazy / a.sl2;
-    const VScaleSel vs = make_vscale_sel(lane);
-    for (int i = 0; i < nmine; ++i) {
-      const int si = i & 1;  // block i uses stage i % 2
-      // The two waves of a SIMD are issued oldest-first at equal priority, which lets
-      // the older one run ahead and leaves the younger to finish alone. Lowering the
-      // priority with each block done keeps the one behind first in line.
-      if (i == 0)
-        __builtin_amdgcn_s_setprio(2);
-      else if (i == 1)
-        __builtin_amdgcn_s_setprio(1);
-      else if (i == 2)
-        __builtin_amdgcn_s_setprio(0);
-      if (i + 1 < nmine) {  // block i+1 streams in while block i is processed
-        issue_stage_at(st_lds0 + (uint32_t)(1 - si) * (uint32_t)sizeof(Stage), P,
-                       rsrc_advance(rk, boff + bstep), rsrc_advance(rv, boff + bstep));
-        asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-      } else {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      }
-      const Stage &st = sm.run.st[wave][si];
-      BlockWords W;
-      load_block_words(st, lane, W);
-      __builtin_amdgcn_sched_barrier(0);  // keep the K reads ahead of their phases
-      QKOut qo;
-      float pv[8];
-      phase_q(W, qb, q2, MK, ks, qo);
-      phase_s(W, qo, S, (int)(seq_k - (int64_t)(first + 4 * i) * kBlk), a.sl2, clamp_raw,
-              lazy_raw, lane, pv);
-      phase_p(st, W, S, T, pv, MK, vs, lane);
-      // every LDS read of this stage has completed before it is refilled
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      boff += bstep;
-    }
-    __builtin_amdgcn_s_setprio(0);
-  }
-  // ---- epilogue: per-wave reductions, then the four waves of each KV head merged into
-  // this workgroup's partial
-  S.lsum += __shfl_xor(S.lsum, 16);
-  S.lsum += __shfl_xor(S.lsum, 32);
-  // Row halves: the hi rows 0-7 sit in lanes g < 2 and the lo rows 8-15 of the same
-  // heads 32 lanes up. One v_permlane32_swap sums them for two tiles at once: afterwards
-  // lanes 0-31 hold tile T2 and lanes 32-63 tile T2 + 8, both for rows (heads)
-  // 4 (g & 1) + i.
-  const int gr = g & 1, gh = g >> 1;
-  f4 hs[8];
-#pragma unroll
-  for (int T2 = 0; T2 < 8; ++T2)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) hs[T2][i] = pair_sum32(S.acc[T2][i], S.acc[T2 + 8][i]);
-  // min term, paired alike: cm0 is row 4 (g & 1) + g / 2, cm1 row 4 (g & 1) + 2 + g / 2
-  // (column j = n)
-  const float cm0 = pair_sum32(S.accm[0], S.accm[1]), cm1 = pair_sum32(S.accm[2], S.accm[3]);
-  // Exchange through this wave's own table area: ml = {m of heads 0-7 (log2 units), l,
-  // f * l}, read by the other waves after the barrier; then cmin[head][j] * f.
-  float(*cmin)[8] = reinterpret_cast<float(*)[8]>(&T.kd[0]);
-  float *ml = T.vmd;
-  if (g == 0 && n < 8) {
-    ml[n] = S.m_run * a.sl2;
-    ml[8 + n] = S.lsum;
-  }
-  __syncthreads();  // every wave has left the loop: the stage buffers become the merge area
-  // weights f = 2^(m - M) of this wave's rows against the four waves of its KV head
-  auto weight = [&](int h) {
-    float M = -INFINITY;
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) M = fmaxf(M, sm.run.t.tab[2 * s4 + kv].vmd[h]);
-    const float mine = ml[h];
-    return (mine == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mine - M);
   };
-  float fr[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) fr[i] = weight(4 * gr + i);
-  // cmin * f, written and read back by this wave only (its LDS operations stay in order)
-  if (n < 8) {
-    cmin[4 * gr + gh][n] = cm0 * (gh ? fr[1] : fr[0]);
-    cmin[4 * gr + 2 + gh][n] = cm1 * (gh ? fr[3] : fr[2]);
-  }
-  // scaled output rows: acc * f - cmin[row][e / 32] * f, one float4 per tile
-#pragma unroll
-  for (int T2 = 0; T2 < 8; ++T2) {
-    const int Tt = T2 + 8 * gh;
-    const int j = tile_e(Tt, n) >> 5;
-    float4 v;
-    v.x = fmaf(hs[T2][0], fr[0], -cmin[4 * gr + 0][j]);
-    v.y = fmaf(hs[T2][1], fr[1], -cmin[4 * gr + 1][j]);
-    v.z = fmaf(hs[T2][2], fr[2], -cmin[4 * gr + 2][j]);
-    v.w = fmaf(hs[T2][3], fr[3], -cmin[4 * gr + 3][j]);
-    sm.merge.o[wave][Tt][gr][n] = v;
-  }
-  if (g == 0 && n < 8) ml[16 + n] = weight(n) * ml[8 + n];
-  __syncthreads();
-  // ---- merge: item (kv, T2, g2, n) sums rows 4 g2 .. 4 g2 + 3 of KV head kv over its four
-  // waves and stores them at tile-order entry 16 T2 + n of heads 8 kv + 4 g2 + i
-  float *dst = a.part + (int64_t)wg * 16 * kPartRow;
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int item = tid + kThreads * it;
-    const int n2 = item & 15, g2 = (item >> 4) & 1, T2 = (item >> 5) & 15, kv2 = item >> 9;
-    float4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      const float4 v = sm.merge.o[2 * s4 + kv2][T2][g2][n2];
-      acc.x += v.x;
-      acc.y += v.y;
-      acc.z += v.z;
-      acc.w += v.w;
+  // One pass per piece; the fused append runs in the first. A workgroup without blocks
+  // on its part of the line (have false) only quantizes, if it is a quantizing one.
+  for (int pc = 0;; ++pc) {
+    const bool qnow = quant && pc == 0;
+    const DecodeSeg &sg = sgv;
+    // ---- blocks of this wave: pb0 + wsub, pb0 + wsub + 4, ... below pb1
+    // wave-uniform: loop control and the key mask stay scalar
+    const int first = __builtin_amdgcn_readfirstlane(pb0 + wsub);
+    const int nmine =
+        __builtin_amdgcn_readfirstlane(have && first < pb1 ? (pb1 - first + 3) / 4 : 0);
+    const uint8_t *kbase = sg.k + kvu * a.rs_h;
+    const uint8_t *vbase = sg.v + kvu * a.rs_h;
+    const int64_t seq_k = sg.seq_k;
+    // rows of keys [0, seq_k) of this head; loads past them return zeros (masked keys)
+    const uint32_t span = seq_k > 0 ? (uint32_t)(seq_k - 1) * rs_t + 144u : 0u;
+    const u4s rk = make_rsrc(kbase, span), rv = make_rsrc(vbase, span);
+    uint32_t boff = __builtin_amdgcn_readfirstlane((uint32_t)first * kBlk * rs_t);
+
+    // ---- this wave's q rows, then its first block, into LDS. Every wave's q loads go out
+    // before any stage load (one barrier), so q returns ahead of the block data.
+    if (have) {
+      if constexpr (kPrep) {
+        if (!qnow) {
+          const int half = a.prep.n_rot >> 1;
+          const int64_t ro = sg.t_new * half;
+          issue_prep_consts(&sm.run.t.tab[wave],
+                            reinterpret_cast<uint8_t *>(&sm.run.st[wave][1]) + 8 * kQRow,
+                            make_rsrc(a.prep.q_alpha, 1024u),
+                            make_rsrc(a.prep.cos_tab + ro, (uint32_t)half * 4u),
+                            make_rsrc(a.prep.sin_tab + ro, (uint32_t)half * 4u), (uint32_t)lane);
+        }
+      }
+      const u4s rq = make_rsrc(a.q + ((int64_t)sg.qi * 16 + 8 * kvu) * 256, 8 * 256 * 4);
+      issue_q(&sm.run.st[wave][1], rq, 16u * lane);
     }
-    float *d0 = dst + (8 * kv2 + 4 * g2) * kPartRow + 16 * T2 + n2;
-    __builtin_nontemporal_store(acc.x, d0);
-    __builtin_nontemporal_store(acc.y, d0 + kPartRow);
-    __builtin_nontemporal_store(acc.z, d0 + 2 * kPartRow);
-    __builtin_nontemporal_store(acc.w, d0 + 3 * kPartRow);
-  }
-  if (tid < 16) {
-    const int kv2 = tid >> 3, h = tid & 7;
-    float M = -INFINITY, L = 0.0f;
+    __syncthreads();
+    // every issued block has its first key below seq_k, so its offset is inside the range
+    if (nmine > 0) issue_stage_at(st_lds0, P, rsrc_advance(rk, boff), rsrc_advance(rv, boff));
+
+    // QK B operands: lane (n, g) takes q of head n % 8, elements 64g + 32(s/4) + 8(s%4) +
+    // perm[slot], as the fp16 hi part (n < 8) or the lo remainder (n >= 8); S2 B operand:
+    // the sums of sub-blocks 2g and 2g+1 (elements 64g..64g+31, 64g+32..64g+63, in order).
+    // Built from the wave's own copy of q, so no workgroup barrier is needed.
+    h8 qb[8];
+    h4 q2 = {0, 0, 0, 0};
+    auto build_q = [&]() {
+      // q was issued before this wave's stage loads (12): once at most 12 loads are
+      // outstanding, q has landed
+      if (nmine > 0)
+        asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if constexpr (kPrep) {
+        if (qnow) {  // after quantizing: the constants into this wave's table area and tail
+          float *tail = reinterpret_cast<float *>(&sm.run.st[wave][1]) + 8 * (kQRow / 4);
+          reinterpret_cast<f4 *>(&sm.run.t.tab[wave])[lane] = qa4;
+          tail[lane] = lane < 32 ? rcos : 0.0f;
+          tail[64 + lane] = lane < 32 ? rsin : 0.0f;
+          __builtin_amdgcn_wave_barrier();
+        }
+      }
+      const float *qrow = reinterpret_cast<const float *>(&sm.run.st[wave][1]) + (n & 7) * (kQRow / 4) + 64 * g;
+      constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+      float qsum[2] = {0.0f, 0.0f};
+      // hi lanes (n < 8) take fp16(q), lo lanes fp16(q - fp16(q)): both are fp16(q - c)
+      // with c = fp16(q) masked to zero on the hi lanes
+      const uint32_t lo_mask = n < 8 ? 0u : 0xFFFFFFFFu;
+      auto convert = [&](int st, const float (&v8)[8]) {
 #pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      M = fmaxf(M, sm.run.t.tab[2 * s4 + kv2].vmd[h]);
-      L += sm.run.t.tab[2 * s4 + kv2].vmd[16 + h];
+        for (int k = 0; k < 8; ++k) qsum[st >> 2] += v8[k];
+        uint32_t w[4];
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+          const float a0 = v8[perm[2 * pp]], a1 = v8[perm[2 * pp + 1]];
+          const h2 h = {(_Float16)a0, (_Float16)a1};
+          const uint32_t c = as_u(h) & lo_mask;
+          w[pp] = fp16_sub2(a0, a1, c);
+        }
+        qb[st] = __builtin_bit_cast(h8, u4{w[0], w[1], w[2], w[3]});
+      };
+      if constexpr (kPrep) {
+        // q_norm and rope in registers: v[st][k] is element 8 st + k of the lane's 64
+        // (64 g ..) of row n % 8; the row's 4 lanes (g = 0..3) pool their sums of squares,
+        // and the g = 0 lanes hold every rope pair (j, j + 32) of n_rot = 64. q feeds the
+        // attention only: sums in any order and x * (1 / m) are within its tolerance.
+        float v[8][8];
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+          const float4 r0 = *reinterpret_cast<const float4 *>(qrow + 8 * st);
+          const float4 r1 = *reinterpret_cast<const float4 *>(qrow + 8 * st + 4);
+          v[st][0] = r0.x; v[st][1] = r0.y; v[st][2] = r0.z; v[st][3] = r0.w;
+          v[st][4] = r1.x; v[st][5] = r1.y; v[st][6] = r1.z; v[st][7] = r1.w;
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int st = 0; st < 8; ++st)
+#pragma unroll
+          for (int k = 0; k < 8; ++k) ss = fmaf(v[st][k], v[st][k], ss);
+        {
+          const uint32_t u = __builtin_bit_cast(uint32_t, ss);
+          const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+          const uint32_t r0 = r[0], r1 = r[1];
+          ss = __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+        }
+        {
+          const uint32_t u = __builtin_bit_cast(uint32_t, ss);
+          const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+          const uint32_t r0 = r[0], r1 = r[1];
+          ss = __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+        }
+        const float inv = 1.0f / __builtin_sqrtf(ss * (1.0f / 256.0f) + a.prep.eps);
+        const float *al = reinterpret_cast<const float *>(&sm.run.t.tab[wave]) + 64 * g;
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+          const float4 a0 = *reinterpret_cast<const float4 *>(al + 8 * st);
+          const float4 a1 = *reinterpret_cast<const float4 *>(al + 8 * st + 4);
+          const float a8[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+          for (int k = 0; k < 8; ++k) v[st][k] = v[st][k] * inv * a8[k];
+        }
+        if (g == 0) {
+          const float *tail = reinterpret_cast<const float *>(&sm.run.st[wave][1]) + 8 * (kQRow / 4);
+#pragma unroll
+          for (int st = 0; st < 4; ++st) {
+            const float4 c0 = *reinterpret_cast<const float4 *>(tail + 8 * st);
+            const float4 c1 = *reinterpret_cast<const float4 *>(tail + 8 * st + 4);
+            const float4 s0 = *reinterpret_cast<const float4 *>(tail + 64 + 8 * st);
+            const float4 s1 = *reinterpret_cast<const float4 *>(tail + 64 + 8 * st + 4);
+            const float c8[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            const float s8[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              const float x1 = v[st][k], x2 = v[st + 4][k];
+              v[st][k] = x1 * c8[k] - x2 * s8[k];
+              v[st + 4][k] = x1 * s8[k] + x2 * c8[k];
+            }
+          }
+        }
+        if (wg == sg.wg0 && wsub == 0 && n < 8) {  // the combine's copy of the prepared q
+          float *qo = a.q_out + ((int64_t)sg.qi * 16 + 8 * kvu + n) * 256 + 64 * g;
+#pragma unroll
+          for (int st = 0; st < 8; ++st) {
+            *reinterpret_cast<float4 *>(qo + 8 * st) = float4{v[st][0], v[st][1], v[st][2], v[st][3]};
+            *reinterpret_cast<float4 *>(qo + 8 * st + 4) = float4{v[st][4], v[st][5], v[st][6], v[st][7]};
+          }
+        }
+#pragma unroll
+        for (int st = 0; st < 8; ++st) convert(st, v[st]);
+      } else {
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+          const float4 r0 = *reinterpret_cast<const float4 *>(qrow + 32 * (st >> 2) + 8 * (st & 3));
+          const float4 r1 = *reinterpret_cast<const float4 *>(qrow + 32 * (st >> 2) + 8 * (st & 3) + 4);
+          const float v8[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+          convert(st, v8);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const _Float16 hi = (_Float16)qsum[t];
+        q2[t] = (n < 8) ? hi : (_Float16)(qsum[t] - (float)hi);
+      }
+    };
+    static_assert(kLoadsPerStage == 12, "the vmcnt above counts one stage of loads");
+
+    if (qnow) quantize_rows();
+    if (!have) return;
+    build_q();
+
+    WaveState S;
+#pragma unroll
+    for (int T2 = 0; T2 < 16; ++T2) S.acc[T2] = f4{0.f, 0.f, 0.f, 0.f};
+    S.accm = f4{0.f, 0.f, 0.f, 0.f};
+    S.m_run = -INFINITY;
+    S.lsum = 0.0f;
+    WaveTab &T = sm.run.t.tab[wave];
+    if (nmine > 0) {
+      const Masks MK = {vconst(0x000F000Fu), vconst(0x00F000F0u), vconst(0x64006400u)};
+      const KScaleSel ks = make_kscale_sel(g);
+      const float clamp_raw = kClampL2 / a.sl2, lazy_raw = kLazy / a.sl2;
+      const VScaleSel vs = make_vscale_sel(lane);
+      for (int i = 0; i < nmine; ++i) {
+        const int si = i & 1;  // block i uses stage i % 2
+        // The two waves of a SIMD are issued oldest-first at equal priority, which lets
+        // the older one run ahead and leaves the younger to finish alone. Lowering the
+        // priority with each block done keeps the one behind first in line.
+        if (i == 0)
+          __builtin_amdgcn_s_setprio(2);
+        else if (i == 1)
+          __builtin_amdgcn_s_setprio(1);
+        else if (i == 2)
+          __builtin_amdgcn_s_setprio(0);
+        if (i + 1 < nmine) {  // block i+1 streams in while block i is processed
+          issue_stage_at(st_lds0 + (uint32_t)(1 - si) * (uint32_t)sizeof(Stage), P,
+                         rsrc_advance(rk, boff + bstep), rsrc_advance(rv, boff + bstep));
+          asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+        } else {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        const Stage &st = sm.run.st[wave][si];
+        BlockWords W;
+        load_block_words(st, lane, W);
+        __builtin_amdgcn_sched_barrier(0);  // keep the K reads ahead of their phases
+        QKOut qo;
+        float pv[8];
+        phase_q(W, qb, q2, MK, ks, qo);
+        phase_s(W, qo, S, (int)(seq_k - (int64_t)(first + 4 * i) * kBlk), a.sl2, clamp_raw,
+                lazy_raw, lane, pv);
+        phase_p(st, W, S, T, pv, MK, vs, lane);
+        // every LDS read of this stage has completed before it is refilled
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        boff += bstep;
+      }
+      __builtin_amdgcn_s_setprio(0);
     }
-    float *mlo = reinterpret_cast<float *>(a.ml + (int64_t)wg * 16 + tid);
-    __builtin_nontemporal_store(M, mlo);
-    __builtin_nontemporal_store(L, mlo + 1);
+    // ---- epilogue: per-wave reductions, then the four waves of each KV head merged into
+    // this workgroup's partial
+    S.lsum += __shfl_xor(S.lsum, 16);
+    S.lsum += __shfl_xor(S.lsum, 32);
+    // Row halves: the hi rows 0-7 sit in lanes g < 2 and the lo rows 8-15 of the same
+    // heads 32 lanes up. One v_permlane32_swap sums them for two tiles at once: afterwards
+    // lanes 0-31 hold tile T2 and lanes 32-63 tile T2 + 8, both for rows (heads)
+    // 4 (g & 1) + i.
+    const int gr = g & 1, gh = g >> 1;
+    f4 hs[8];
+#pragma unroll
+    for (int T2 = 0; T2 < 8; ++T2)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) hs[T2][i] = pair_sum32(S.acc[T2][i], S.acc[T2 + 8][i]);
+    // min term, paired alike: cm0 is row 4 (g & 1) + g / 2, cm1 row 4 (g & 1) + 2 + g / 2
+    // (column j = n)
+    const float cm0 = pair_sum32(S.accm[0], S.accm[1]), cm1 = pair_sum32(S.accm[2], S.accm[3]);
+    // Exchange through this wave's own table area: ml = {m of heads 0-7 (log2 units), l,
+    // f * l}, read by the other waves after the barrier; then cmin[head][j] * f.
+    float(*cmin)[8] = reinterpret_cast<float(*)[8]>(&T.kd[0]);
+    float *ml = T.vmd;
+    if (g == 0 && n < 8) {
+      ml[n] = S.m_run * a.sl2;
+      ml[8 + n] = S.lsum;
+    }
+    __syncthreads();  // every wave has left the loop: the stage buffers become the merge area
+    // weights f = 2^(m - M) of this wave's rows against the four waves of its KV head
+    auto weight = [&](int h) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) M = fmaxf(M, sm.run.t.tab[2 * s4 + kv].vmd[h]);
+      const float mine = ml[h];
+      return (mine == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mine - M);
+    };
+    float fr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fr[i] = weight(4 * gr + i);
+    // cmin * f, written and read back by this wave only (its LDS operations stay in order)
+    if (n < 8) {
+      cmin[4 * gr + gh][n] = cm0 * (gh ? fr[1] : fr[0]);
+      cmin[4 * gr + 2 + gh][n] = cm1 * (gh ? fr[3] : fr[2]);
+    }
+    // scaled output rows: acc * f - cmin[row][e / 32] * f, one float4 per tile
+#pragma unroll
+    for (int T2 = 0; T2 < 8; ++T2) {
+      const int Tt = T2 + 8 * gh;
+      const int j = tile_e(Tt, n) >> 5;
+      float4 v;
+      v.x = fmaf(hs[T2][0], fr[0], -cmin[4 * gr + 0][j]);
+      v.y = fmaf(hs[T2][1], fr[1], -cmin[4 * gr + 1][j]);
+      v.z = fmaf(hs[T2][2], fr[2], -cmin[4 * gr + 2][j]);
+      v.w = fmaf(hs[T2][3], fr[3], -cmin[4 * gr + 3][j]);
+      sm.merge.o[wave][Tt][gr][n] = v;
+    }
+    if (g == 0 && n < 8) ml[16 + n] = weight(n) * ml[8 + n];
+    __syncthreads();
+    // ---- merge: item (kv, T2, g2, n) sums rows 4 g2 .. 4 g2 + 3 of KV head kv over its four
+    // waves and stores them at tile-order entry 16 T2 + n of heads 8 kv + 4 g2 + i
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int item = tid + kThreads * it;
+      const int n2 = item & 15, g2 = (item >> 4) & 1, T2 = (item >> 5) & 15, kv2 = item >> 9;
+      float4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const float4 v = sm.merge.o[2 * s4 + kv2][T2][g2][n2];
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+      }
+      // one 32-bit index (slot < 2^16), so that no per-lane address outlives the piece
+      float *d0 = a.part + ((slot * 16 + 8 * kv2 + 4 * g2) * kPartRow + 16 * T2 + n2);
+      __builtin_nontemporal_store(acc.x, d0);
+      __builtin_nontemporal_store(acc.y, d0 + kPartRow);
+      __builtin_nontemporal_store(acc.z, d0 + 2 * kPartRow);
+      __builtin_nontemporal_store(acc.w, d0 + 3 * kPartRow);
+    }
+    if (tid < 16) {
+      const int kv2 = tid >> 3, h = tid & 7;
+      float M = -INFINITY, L = 0.0f;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        M = fmaxf(M, sm.run.t.tab[2 * s4 + kv2].vmd[h]);
+        L += sm.run.t.tab[2 * s4 + kv2].vmd[16 + h];
+      }
+      float *mlo = reinterpret_cast<float *>(a.ml + (slot * 16 + tid));
+      __builtin_nontemporal_store(M, mlo);
+      __builtin_nontemporal_store(L, mlo + 1);
+    }
+    if constexpr (kSegs == 1) break;  // one segment: one piece
+    if (!next_piece()) break;
+    // the next piece's q and blocks refill the stage buffers, the merge area until here
+    __syncthreads();
   }
 }
+
 
 }  // namespace
 
@@ -925,44 +978,45 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
     d.seg[i].qi = i;
   }
   d.dseg = nullptr;
-  d.wps = 0;
-  // Blocks per workgroup, a multiple of 4 (one or more per wave pair). One segment:
-  // spread over at most kMainWGs workgroups, one per CU. Several: the multiple that
-  // minimises the estimated makespan, ceil(workgroups / 256) rounds of (bpw / 4 blocks
-  // per wave + a per-workgroup overhead of about 1.3 blocks).
-  int bpw;
-  if (n == 1) {
-    int nwg = (d.seg[0].nblk + 3) / 4;
-    if (nwg > kMainWGs) nwg = kMainWGs;
-    if (nwg < 1) nwg = 1;
-    bpw = (d.seg[0].nblk + nwg - 1) / nwg;
-    bpw = (bpw + 3) / 4 * 4;
-    if (bpw < 4) bpw = 4;
-  } else {
-    bpw = 4;
-    double best = 1e30;
-    for (int cand = 4; cand <= 64; cand += 4) {
-      int64_t w = 0;
-      for (int i = 0; i < n; ++i) w += d.seg[i].nblk > 0 ? (d.seg[i].nblk + cand - 1) / cand : 1;
-      const double cost = (double)((w + kMainWGs - 1) / kMainWGs) * (cand / 4.0 + 1.3);
-      if (cost < best) {
-        best = cost;
-        bpw = cand;
-      }
-    }
-  }
-  CombineArgs c;
-  int wg = 0;
+  // Stream-K plan: the segments' blocks on one virtual line (segment i from voff, an
+  // empty segment as one block), with a gap of kPieceGap blocks before every segment
+  // after the first, the estimated cost of one more pass (epilogue, q staging and the
+  // first block's latency), so that a workgroup whose range crosses a boundary gets
+  // fewer blocks. The nwg workgroups split the V blocks into ranges of vq or vq + 1
+  // (about 4 blocks or more each, one per wave pair; at most one workgroup per CU),
+  // the vr longer ones first. Workgroup w's piece of segment s writes partial slot
+  // w + s; segment s has pieces on the workgroups from the one whose range holds its
+  // first virtual block to the one that holds its last, so its slots are consecutive.
+  int V = 0;
   for (int i = 0; i < n; ++i) {
-    d.seg[i].wg0 = wg;
-    c.wg0[i] = wg;
-    const int w = d.seg[i].nblk > 0 ? (d.seg[i].nblk + bpw - 1) / bpw : 1;
-    wg += w;
+    if (i > 0) V += kPieceGap;
+    d.seg[i].voff = V;
+    V += d.seg[i].nblk > 0 ? d.seg[i].nblk : 1;
   }
-  c.wg0[n] = wg;
+  int nwg = (V + 3) / 4;
+  if (nwg > kMainWGs) nwg = kMainWGs;
+  if (nwg < 1) nwg = 1;
+  CombineArgs c;
+  const int vq = V / nwg, vr = V % nwg;
+  // the workgroup whose range holds virtual block x (ranges of vq + 1, vr times, then vq)
+  auto wg_of = [&](int x) {
+    const int big = vr * (vq + 1);
+    return x < big ? x / (vq + 1) : vr + (x - big) / vq;
+  };
+  for (int i = 0; i < n; ++i) {
+    const int vs = d.seg[i].voff, ve = vs + (d.seg[i].nblk > 0 ? d.seg[i].nblk : 1);
+    const int w0 = wg_of(vs), w1 = wg_of(ve - 1);
+    d.seg[i].wg0 = w0;
+    c.wg0[i] = w0 + i;
+    c.wg1[i] = w1 + i + 1;
+  }
+  const int wg = nwg + n - 1;  // partial slots
   d.nseg = n;
-  d.nwg = wg;
-  d.bpw = bpw;
+  d.nwg = nwg;
+  d.bpw = 0;
+  d.wps = 0;
+  d.vq = vq;
+  d.vr = vr;
   d.rs_t = rs_t;
   d.rs_h = rs_h;
   d.sl2 = scale * kLog2e;
@@ -986,10 +1040,10 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
     DecodeArgsT<1> d1;
     static_cast<DecodeArgsBase &>(d1) = d;
     d1.seg[0] = d.seg[0];
-    hipLaunchKernelGGL((q4k_decode_kernel<kPrep, 1>), dim3((unsigned)wg), dim3(kThreads), 0, s, d1);
+    hipLaunchKernelGGL((q4k_decode_kernel<kPrep, 1>), dim3((unsigned)nwg), dim3(kThreads), 0, s, d1);
   } else {
-    hipLaunchKernelGGL((q4k_decode_kernel<kPrep, kMaxSegs>), dim3((unsigned)wg), dim3(kThreads), 0, s,
-                       d);
+    hipLaunchKernelGGL((q4k_decode_kernel<kPrep, kMaxSegs>), dim3((unsigned)nwg), dim3(kThreads), 0,
+                       s, d);
   }
   PKV_HIP(hipGetLastError());
   c.part = d.part;
@@ -998,8 +1052,7 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
   c.dq = fused ? d.dq : nullptr;
   c.out = out;
   c.sl2 = d.sl2;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(16 * 8, (unsigned)n), dim3(256), 0, s, c);
-  PKV_HIP(hipGetLastError());
+  if (const int rc_ = launch_combine(c, n, s)) return rc_;
   return PKV_OK;
 }
 

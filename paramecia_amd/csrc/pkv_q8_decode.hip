@@ -260,8 +260,8 @@ static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, cons
     c.wg0[i] = wg;
     const int64_t w = d.seg[i].seq_k > 0 ? (d.seg[i].seq_k + kpw - 1) / kpw : 1;
     wg += (int)w;
+    c.wg1[i] = wg;
   }
-  c.wg0[n] = wg;
   d.nseg = n;
   d.nwg = wg;
   d.kpw = (int)kpw;
@@ -286,8 +286,7 @@ static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, cons
   c.dq = fused ? d.dq : nullptr;
   c.out = out;
   c.sl2 = d.sl2;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(16 * 8, (unsigned)n), dim3(256), 0, s, c);
-  PKV_HIP(hipGetLastError());
+  if (const int rc_ = launch_combine(c, n, s)) return rc_;
   return PKV_OK;
 }
 
@@ -321,6 +320,7 @@ int launch_paged_decode_q8(const PagedSeg *segs, int nseg, int nseq, int page_to
     if (segs[i].qi < qprev || segs[i].qi >= nseq || segs[i].len < 0 || segs[i].len > page_tokens)
       return set_error(PKV_ERR_ARG, "paged decode: segments out of order");
     while (qprev < segs[i].qi) c.wg0[++qprev] = i * wps;
+    c.wg1[qprev] = (i + 1) * wps;
     d.k = segs[i].k;
     d.v = segs[i].v;
     d.seq_k = segs[i].len;
@@ -328,9 +328,9 @@ int launch_paged_decode_q8(const PagedSeg *segs, int nseg, int nseq, int page_to
     d.nblk = 0;
     d.wg0 = i * wps;
     d.qi = segs[i].qi;
+    d.voff = 0;
   }
   if (qprev != nseq - 1) return set_error(PKV_ERR_ARG, "paged decode: a sequence has no page");
-  c.wg0[nseq] = nwg;
   Q8Args d;
   d.nseg = nseg;
   d.nwg = nwg;
@@ -372,8 +372,7 @@ int launch_paged_decode_q8(const PagedSeg *segs, int nseg, int nseq, int page_to
   c.dq = nullptr;
   c.out = out;
   c.sl2 = d.sl2;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(16 * 8, (unsigned)nseq), dim3(256), 0, s, c);
-  PKV_HIP(hipGetLastError());
+  if (const int rc_ = launch_combine(c, nseq, s)) return rc_;
   return PKV_OK;
 }
 

@@ -187,6 +187,25 @@ def test_batched_over_segment_limit(pk, orc):
     run_batched(pk, orc, lens, seed=21)
 
 
+def test_batched_stream_tiny_and_empty(pk, orc):
+    """32 sequences of 0-40 keys in one launch: the launch's blocks lie on one line with
+    a gap before every sequence, so most workgroups' ranges cross a boundary or fall in a
+    gap (no blocks at all), and the 128 new rows outnumber the workgroups."""
+    say("batched decode, 32 tiny sequences")
+    lens = [int(x) for x in np.random.default_rng(23).integers(0, 41, size=32)]
+    lens[:6] = [0, 0, 1, 31, 32, 33]
+    run_batched(pk, orc, lens, seed=23)
+
+
+def test_batched_stream_long_and_short(pk, orc):
+    """One long sequence among short ones: the long one spans most workgroups, the short
+    ones share workgroups, so a piece boundary falls inside many workgroups' ranges."""
+    say("batched decode, long and short sequences")
+    rng = np.random.default_rng(24)
+    lens = [20000] + [int(x) for x in rng.integers(1, 300, size=15)] + [4096, 4097, 31, 1, 6000]
+    run_batched(pk, orc, lens, seed=24)
+
+
 def test_batched_outliers_config5_shape(pk, orc):
     """16 sequences of seeded lengths with the config-5 outlier channels (x20), at
     lengths cut to 1/8 of config 5's so the oracle stays fast."""

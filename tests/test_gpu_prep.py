@@ -119,7 +119,7 @@ def test_prep_append_bitexact(pk, orc, quant, B, Hkv, D, n_rot):
     same_bytes(g, c)
 
 
-@pytest.mark.parametrize("quant,B,n_rot", [(Q4K, 1, 64), (Q4K, 2, 64), (Q4K, 1, 128),
+@pytest.mark.parametrize("quant,B,n_rot", [(Q4K, 1, 64), (Q4K, 2, 64), (Q4K, 5, 64), (Q4K, 1, 128),
                                            (Q4K, 1, 256), (Q8_0, 1, 64),
                                            (F16, 1, 64)])
 def test_append_attend_prep_decode(pk, orc, quant, B, n_rot):
