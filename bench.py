@@ -705,9 +705,10 @@ def run_config5(args):
 
 def run_config5_paged(args, lens, chans):
     """Config 5's workload on paged caches: per layer one page pool (--paged tokens per
-    page) holding the 16 sequences; a step appends one token to every sequence in one
-    launch (pkv_seq_append_batched) and runs one batched decode over all their pages
-    (pkv_seq_decode_batched). Timed eagerly: with more than 32 pages per launch the
+    page) holding the 16 sequences; a step is one fused call per layer
+    (pkv_seq_append_decode_batched: one decode launch over all the sequences' pages that
+    also quantizes their new tokens, then the combine). The unfused form (one batched
+    append launch, then pkv_seq_decode_batched) is timed beside it. Timed eagerly: the
     segment table is staged through host memory, which a HIP graph cannot replay."""
     import torch
     import paramecia_amd as pk
@@ -747,10 +748,17 @@ def run_config5_paged(args, lens, chans):
         for l in range(L):
             for i, S in enumerate(lens):
                 seqs[l][i].truncate(S)  # rewind the previous step's token
+            outs[l] = pools[l].append_decode_batched(seqs[l], kn[l], vn[l], q[l], W.SCALE)
+
+    def step_unfused():
+        for l in range(L):
+            for i, S in enumerate(lens):
+                seqs[l][i].truncate(S)
             pools[l].append_batched(seqs[l], kn[l], vn[l])
             outs[l] = pools[l].decode_batched(seqs[l], q[l], W.SCALE)
 
     ms = event_time(torch, step, args.steps, args.warmup)
+    ms_unfused = event_time(torch, step_unfused, args.steps, args.warmup)
     nbytes = L * sum(layer_bytes(S + 1) for S in lens)
     gbs = nbytes / (ms * 1e-3) / 1e9
     pages = sum(-(-(S + 1) // P) for S in lens)
@@ -758,9 +766,10 @@ def run_config5_paged(args, lens, chans):
                        round(ms * 1000, 2), "us/step", False, ms, args,
                        f"config5 on paged caches: one pool per layer, {P}-token pages "
                        f"({pages} pages per layer), the 16 sequences of config 5; step = one "
-                       "batched append + one batched decode per layer (eager)",
+                       "fused append + decode call per layer (eager)",
                        {"sequence_lengths": lens, "page_tokens": P, "pages_per_layer": pages,
-                        "roofline": {"kernel": "pkv_seq_append_batched + pkv_seq_decode_batched",
+                        "unfused_us_per_step": round(ms_unfused * 1000, 2),
+                        "roofline": {"kernel": "pkv_seq_append_decode_batched",
                                      "bound": "hbm", "achieved": round(gbs, 1),
                                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                      "frac": round(gbs / HBM_PEAK_GBS, 4),

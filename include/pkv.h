@@ -342,6 +342,16 @@ int pkv_seq_attend(pkv_seq *s, const float *q, int l, int num_heads, float scale
  * all their pages; other pools attend sequence by sequence. */
 int pkv_seq_decode_batched(pkv_seq *const *seqs, int n, const float *q, int num_heads,
                            float scale, float *out);
+/* The fused decode step of a serving batch (the paged form of pkv_append_attend_batched):
+ * one token appended to each of n sequences of one pool (k, v [n, n_kv_heads, 1,
+ * head_dim] f32), then one decode query per sequence over all its keys, the new one
+ * included (q, out [n, num_heads, head_dim]). Q4K pools of the model's shape run one
+ * decode launch per 32 sequences that also quantizes the new rows (its segment table is
+ * staged through pinned memory, so the call cannot be captured in a HIP graph); other
+ * pools run pkv_seq_append_batched then pkv_seq_decode_batched. All or nothing:
+ * PKV_ERR_OVERFLOW, with nothing written, when the pool lacks pages for any of them. */
+int pkv_seq_append_decode_batched(pkv_seq *const *seqs, int n, const float *k, const float *v,
+                                  const float *q, int num_heads, float scale, float *out);
 /* get_kv (qn:520-575): dequantized [1, n_kv_heads, len, head_dim] f32. */
 int pkv_seq_get_kv(const pkv_seq *s, float *k_out, float *v_out);
 

@@ -35,6 +35,7 @@ SYMBOLS = (
     "pkv_pool_set_stream", "pkv_seq_create", "pkv_seq_destroy", "pkv_seq_len", "pkv_seq_pages",
     "pkv_seq_fork", "pkv_seq_truncate", "pkv_seq_append", "pkv_seq_attend",
     "pkv_seq_decode_batched", "pkv_seq_get_kv", "pkv_seq_append_batched",
+    "pkv_seq_append_decode_batched",
 )
 
 
@@ -155,6 +156,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "pkv_seq_decode_batched": ([P(vp), c_int, vp, c_int, fl, vp], c_int),
         "pkv_seq_get_kv": ([vp, vp, vp], c_int),
         "pkv_seq_append_batched": ([P(vp), c_int, vp, vp], c_int),
+        "pkv_seq_append_decode_batched": ([P(vp), c_int, vp, vp, vp, c_int, fl, vp], c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

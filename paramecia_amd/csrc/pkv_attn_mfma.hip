@@ -60,80 +60,139 @@ int launch_append_attend_batched_mfma(int quant, const SeqDesc *seqs, int n, con
   return PKV_OK;
 }
 
-// Paged decode: every page run is a segment with the same number of workgroups (wps), so
-// workgroup w serves segment w / wps; the combine merges all partials of a sequence (its
-// segments are consecutive). Up to kMaxSegs segments travel in the kernel arguments
-// (also under stream capture); more go to a device table staged through the workspace.
+// Paged decode: every page run is a segment; the combine merges all partials of a
+// sequence (its segments are consecutive). Up to kMaxSegs segments travel in the kernel
+// arguments (also under stream capture), each page with the same number of workgroups
+// (wps, fixed mode: workgroup w serves segment w / wps). More pages go to a device table
+// staged through the workspace and are split stream-K: the pages' blocks on one virtual
+// line with a gap before every page after the first (the cost of one more pass), 256
+// workgroups with equal ranges, one partial per piece, the pieces of a sequence in
+// consecutive slots (the per-workgroup first segment and first slot travel in the
+// table too).
 int launch_paged_decode_q4k(const PagedSeg *segs, int nseg, int nseq, int page_tokens,
                             const float *q, float *out, int64_t rs_t, int64_t rs_h,
-                            float scale, void *stage, Workspace &ws, hipStream_t s) {
+                            float scale, void *stage, Workspace &ws, hipStream_t s,
+                            const float *k_new, const float *v_new, const NewRow *rows) {
+  // the staging buffer holds nseg * kPagedSegBytes + kPagedStageExtra bytes
   static_assert(sizeof(DecodeSeg) <= kPagedSegBytes, "segment table entry size");
+  static_assert(kMainWGs * sizeof(int2) + kMaxPagedSeqs * sizeof(NewRow) <= kPagedStageExtra,
+                "workgroup and new-row table size");
+  const bool fused = k_new != nullptr;
+  if (fused && (v_new == nullptr || rows == nullptr))
+    return set_error(PKV_ERR_ARG, "paged decode: fused step without its new rows");
   static_assert(kPagedArgSegs == kMaxSegs, "kernel-argument segment count");
   if (nseq < 1 || nseq > kMaxPagedSeqs || nseg < nseq || page_tokens % kBlk != 0)
     return set_error(PKV_ERR_ARG, "paged decode: bad segment plan");
   if (!decode_rows_fit(page_tokens, rs_t)) return PKV_ERR_UNSUPPORTED;
-  // blocks per workgroup: the multiple of 4 that minimises the estimated makespan
-  // (rounds of 256 workgroups x (bpw / 4 blocks per wave + ~1.3 blocks of set-up))
-  const int pblk = page_tokens / kBlk;
-  int bpw = 4;
-  double best = 1e30;
-  for (int cand = 4; cand <= ((pblk + 3) / 4) * 4 && cand <= 64; cand += 4) {
-    const int64_t w = (int64_t)nseg * ((pblk + cand - 1) / cand);
-    const double cost = (double)((w + kMainWGs - 1) / kMainWGs) * (cand / 4.0 + 1.3);
-    if (cost < best) {
-      best = cost;
-      bpw = cand;
-    }
-  }
-  const int wps = (pblk + bpw - 1) / bpw;
-  const int64_t nwg64 = (int64_t)nseg * wps;
-  if (nwg64 > (1 << 24)) return set_error(PKV_ERR_ARG, "paged decode: too many pages");
-  const int nwg = (int)nwg64;
+  if (nseg > (1 << 20)) return set_error(PKV_ERR_ARG, "paged decode: too many pages");
+  const bool stream = fused || nseg > kMaxSegs;
   std::vector<DecodeSeg> tab((size_t)nseg);
-  CombineArgs c;
   int qprev = -1;
+  int V = 0;
   for (int i = 0; i < nseg; ++i) {
     DecodeSeg &d = tab[(size_t)i];
     if (segs[i].qi < qprev || segs[i].qi >= nseq || segs[i].len < 0 || segs[i].len > page_tokens)
       return set_error(PKV_ERR_ARG, "paged decode: segments out of order");
-    while (qprev < segs[i].qi) c.wg0[++qprev] = i * wps;
-    c.wg1[qprev] = (i + 1) * wps;
+    if (segs[i].qi > qprev + 1) return set_error(PKV_ERR_ARG, "paged decode: a sequence has no page");
+    qprev = segs[i].qi;
     d.k = segs[i].k;
     d.v = segs[i].v;
     d.seq_k = segs[i].len;
     d.t_new = 0;
     d.nblk = (int)((segs[i].len + kBlk - 1) / kBlk);
-    d.wg0 = i * wps;
     d.qi = segs[i].qi;
-    d.voff = 0;
+    if (i > 0) V += kPieceGap;
+    d.voff = V;
+    V += d.nblk > 0 ? d.nblk : 1;
   }
   if (qprev != nseq - 1) return set_error(PKV_ERR_ARG, "paged decode: a sequence has no page");
   DecodeArgsT<kMaxSegs> d;
+  CombineArgs c;
+  int nwg, nslots;
+  std::vector<int2> wt;
+  if (!stream) {
+    // blocks per workgroup: the multiple of 4 that minimises the estimated makespan
+    // (rounds of 256 workgroups x (bpw / 4 blocks per wave + ~1.3 blocks of set-up))
+    const int pblk = page_tokens / kBlk;
+    int bpw = 4;
+    double best = 1e30;
+    for (int cand = 4; cand <= ((pblk + 3) / 4) * 4 && cand <= 64; cand += 4) {
+      const int64_t w = (int64_t)nseg * ((pblk + cand - 1) / cand);
+      const double cost = (double)((w + kMainWGs - 1) / kMainWGs) * (cand / 4.0 + 1.3);
+      if (cost < best) {
+        best = cost;
+        bpw = cand;
+      }
+    }
+    const int wps = (pblk + bpw - 1) / bpw;
+    nwg = nseg * wps;
+    nslots = nwg;
+    for (int i = 0; i < nseg; ++i) {
+      tab[(size_t)i].wg0 = i * wps;
+      const int qi = tab[(size_t)i].qi;
+      if (i == 0 || tab[(size_t)i - 1].qi != qi) c.wg0[qi] = i * wps;
+      c.wg1[qi] = (i + 1) * wps;
+    }
+    d.bpw = bpw;
+    d.wps = wps;
+    d.vq = d.vr = 0;
+  } else {
+    nwg = (V + 3) / 4;
+    if (nwg > kMainWGs) nwg = kMainWGs;
+    const int vq = V / nwg, vr = V % nwg;
+    wt.resize((size_t)nwg);
+    for (int q2 = 0; q2 < nseq; ++q2) c.wg0[q2] = -1;
+    int slot = 0, sfirst = 0;
+    for (int w = 0; w < nwg; ++w) {
+      const int V0 = w * vq + (w < vr ? w : vr), V1 = V0 + vq + (w < vr ? 1 : 0);
+      auto vend = [&](int i) {
+        return tab[(size_t)i].voff + (tab[(size_t)i].nblk > 0 ? tab[(size_t)i].nblk : 1);
+      };
+      while (sfirst < nseg && vend(sfirst) <= V0) ++sfirst;
+      wt[(size_t)w] = int2{sfirst, slot};
+      for (int i = sfirst; i < nseg && tab[(size_t)i].voff < V1; ++i) {
+        const int qi = tab[(size_t)i].qi;
+        if (c.wg0[qi] < 0) c.wg0[qi] = slot;
+        c.wg1[qi] = ++slot;
+      }
+    }
+    nslots = slot;
+    for (int i = 0; i < nseg; ++i) tab[(size_t)i].wg0 = 0;  // no prepared q on this path
+    d.bpw = 0;
+    d.wps = 0;
+    d.vq = vq;
+    d.vr = vr;
+  }
   d.nseg = nseg;
   d.nwg = nwg;
-  d.bpw = bpw;
-  d.wps = wps;
-  d.vq = d.vr = 0;
   d.rs_t = rs_t;
   d.rs_h = rs_h;
   d.sl2 = scale * kLog2e;
   d.q = q;
-  d.k_new = d.v_new = nullptr;
+  d.k_new = k_new;
+  d.v_new = v_new;
+  d.nnew = fused ? nseq : 0;
   d.prep = DecodePrep{};
   d.q_out = nullptr;
-  const size_t part_floats = (size_t)nwg * 16 * kPartRow, ml_floats = (size_t)nwg * 16 * 2;
-  const size_t tab_off = (part_floats + ml_floats) * sizeof(float);
-  const size_t tab_bytes = nseg > kMaxSegs ? (size_t)nseg * sizeof(DecodeSeg) : 0;
+  const size_t part_floats = (size_t)nslots * 16 * kPartRow, ml_floats = (size_t)nslots * 16 * 2;
+  const size_t dq_floats = fused ? (size_t)nseq * 4 * 256 : 0;
+  const size_t tab_off = (part_floats + ml_floats + dq_floats) * sizeof(float);
+  const size_t seg_bytes = stream ? (size_t)nseg * sizeof(DecodeSeg) : 0;
+  const size_t wt_bytes = stream ? (size_t)nwg * sizeof(int2) : 0;
+  const size_t row_bytes_ = fused ? (size_t)nseq * sizeof(NewRow) : 0;
+  const size_t tab_bytes = seg_bytes + wt_bytes + row_bytes_;
   int rc = ws.reserve(tab_off + tab_bytes);
   if (rc) return rc;
   d.part = static_cast<float *>(ws.ptr);
   d.ml = reinterpret_cast<float2 *>(d.part + part_floats);
-  d.dq = nullptr;
+  d.dq = fused ? d.part + part_floats + ml_floats : nullptr;
   rc = device_status_word(&d.status);
   if (rc) return rc;
-  if (nseg <= kMaxSegs) {
+  d.newrows = nullptr;
+  if (!stream) {
     for (int i = 0; i < nseg; ++i) d.seg[i] = tab[(size_t)i];
     d.dseg = nullptr;
+    d.wtab = nullptr;
   } else {
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     PKV_HIP(hipStreamIsCapturing(s, &cap));
@@ -141,10 +200,14 @@ int launch_paged_decode_q4k(const PagedSeg *segs, int nseg, int nseq, int page_t
       return set_error(PKV_ERR_UNSUPPORTED,
                        "paged decode over more than 32 pages cannot be captured in a graph");
     if (stage == nullptr) return set_error(PKV_ERR_ARG, "paged decode: no staging buffer");
-    memcpy(stage, tab.data(), tab_bytes);
-    DecodeSeg *dtab = reinterpret_cast<DecodeSeg *>(static_cast<uint8_t *>(ws.ptr) + tab_off);
+    memcpy(stage, tab.data(), seg_bytes);
+    memcpy(static_cast<uint8_t *>(stage) + seg_bytes, wt.data(), wt_bytes);
+    if (fused) memcpy(static_cast<uint8_t *>(stage) + seg_bytes + wt_bytes, rows, row_bytes_);
+    uint8_t *dtab = static_cast<uint8_t *>(ws.ptr) + tab_off;
     PKV_HIP(hipMemcpyAsync(dtab, stage, tab_bytes, hipMemcpyHostToDevice, s));
-    d.dseg = dtab;
+    d.dseg = reinterpret_cast<DecodeSeg *>(dtab);
+    d.wtab = reinterpret_cast<const int2 *>(dtab + seg_bytes);
+    if (fused) d.newrows = reinterpret_cast<const NewRow *>(dtab + seg_bytes + wt_bytes);
   }
   hipLaunchKernelGGL((q4k_decode_kernel<false, kMaxSegs>), dim3((unsigned)nwg), dim3(kThreads), 0,
                      s, d);
@@ -152,7 +215,7 @@ int launch_paged_decode_q4k(const PagedSeg *segs, int nseg, int nseq, int page_t
   c.part = d.part;
   c.ml = d.ml;
   c.q = q;
-  c.dq = nullptr;
+  c.dq = d.dq;
   c.out = out;
   c.sl2 = d.sl2;
   if (const int rc_ = launch_combine(c, nseq, s)) return rc_;

@@ -193,30 +193,43 @@ bool fast_decode_shape(const pkv_pool *p, int num_heads) {
 }
 
 // Paged decode of seqs[0..n) (n <= kMaxPagedSeqs, all in pool p, each non-empty), query
-// row i of q for sequence i.
+// row i of q for sequence i. With k non-null (a fused step; Q4K pools): each sequence
+// holds len keys (possibly none) and a page for one more token; the decode launch also
+// quantizes k / v ([n][n_kv_heads][head_dim]) into row len of each sequence and attends
+// to it, so sequence i sees len + 1 keys (the caller then advances len).
 int paged_decode(pkv_pool *p, pkv_seq *const *seqs, int n, const float *q, float scale,
-                 float *out) {
+                 float *out, const float *k = nullptr, const float *v = nullptr) {
   std::vector<PagedSeg> segs;
+  std::vector<NewRow> rows;
+  const int64_t rs_t = (int64_t)p->n_kv_heads * (int64_t)p->bpr, rs_h = (int64_t)p->bpr;
   for (int i = 0; i < n; ++i) {
     const pkv_seq *s = seqs[i];
-    for (size_t j = 0; j < pages_for(p, s->len); ++j) {
+    const size_t np = pages_for(p, s->len);
+    for (size_t j = 0; j < np; ++j) {
       const int64_t t0 = (int64_t)j << p->page_lg;
       const int64_t m = s->len - t0 < p->page_tokens ? s->len - t0 : p->page_tokens;
       segs.push_back(PagedSeg{page_k(p, s->pages[j]), page_v(p, s->pages[j]), m, i});
     }
+    if (k != nullptr) {
+      const int64_t t = s->len;
+      const int32_t pg = s->pages[(size_t)(t >> p->page_lg)];
+      const int64_t off = (t & (p->page_tokens - 1)) * rs_t;
+      if (np == 0) segs.push_back(PagedSeg{page_k(p, pg), page_v(p, pg), 0, i});  // no keys yet
+      rows.push_back(NewRow{page_k(p, pg) + off, page_v(p, pg) + off});
+    }
   }
-  const int64_t rs_t = (int64_t)p->n_kv_heads * (int64_t)p->bpr, rs_h = (int64_t)p->bpr;
   int slot = -1;
   void *stage = nullptr;
-  if (segs.size() > (size_t)kPagedArgSegs) {  // a device table, staged through a pinned slot
-    const int rc = stage_acquire(p, segs.size() * kPagedSegBytes, &slot);
+  if (k != nullptr || segs.size() > (size_t)kPagedArgSegs) {  // a device table, staged through a pinned slot
+    const int rc = stage_acquire(p, segs.size() * kPagedSegBytes + kPagedStageExtra, &slot);
     if (rc) return rc;
     stage = p->stage[slot];
   }
   const int rc =
       p->quant == PKV_QUANT_Q4K
           ? launch_paged_decode_q4k(segs.data(), (int)segs.size(), n, p->page_tokens, q, out,
-                                    rs_t, rs_h, scale, stage, p->ws, p->stream)
+                                    rs_t, rs_h, scale, stage, p->ws, p->stream, k, v,
+                                    k != nullptr ? rows.data() : nullptr)
           : launch_paged_decode_q8(segs.data(), (int)segs.size(), n, p->page_tokens, q, out,
                                    rs_t, rs_h, scale, stage, p->ws, p->stream);
   if (slot >= 0) {
@@ -268,7 +281,7 @@ int pkv_pool_create(int quant, int n_kv_heads, int head_dim, int page_tokens, in
   }
   // the staging slots up front (pinned allocations can wait for the device): each holds a
   // segment table of every page of the pool, or a page table
-  const size_t stage_bytes = (size_t)n_pages * kPagedSegBytes + 4096;
+  const size_t stage_bytes = (size_t)n_pages * kPagedSegBytes + kPagedStageExtra;
   for (int i = 0; i < pkv_pool::kStages && e == hipSuccess; ++i) {
     e = hipHostMalloc(&p->stage[i], stage_bytes, hipHostMallocDefault);
     if (e == hipSuccess) p->stage_bytes[i] = stage_bytes;
@@ -488,6 +501,47 @@ int pkv_seq_decode_batched(pkv_seq *const *seqs, int n, const float *q, int num_
     const int m = n - i0 < kMaxPagedSeqs ? n - i0 : kMaxPagedSeqs;
     const int rc = paged_decode(p, seqs + i0, m, q + i0 * qrow, scale, out + i0 * qrow);
     if (rc) return rc;
+  }
+  return PKV_OK;
+}
+
+int pkv_seq_append_decode_batched(pkv_seq *const *seqs, int n, const float *k, const float *v,
+                                  const float *q, int num_heads, float scale, float *out) {
+  if (!seqs || n <= 0 || !k || !v || !q || !out)
+    return set_error(PKV_ERR_ARG, "null argument or n <= 0");
+  pkv_pool *p = seqs[0] ? seqs[0]->pool : nullptr;
+  for (int i = 0; i < n; ++i) {
+    if (!seqs[i] || seqs[i]->pool != p)
+      return set_error(PKV_ERR_ARG, "every sequence must belong to the same pool");
+    for (int j = 0; j < i; ++j)
+      if (seqs[j] == seqs[i]) return set_error(PKV_ERR_ARG, "a sequence appears twice");
+  }
+  if (num_heads <= 0 || num_heads % p->n_kv_heads)
+    return set_error(PKV_ERR_ARG, "num_heads must be a multiple of num_kv_heads");
+  if (p->quant != PKV_QUANT_Q4K || !fast_decode_shape(p, num_heads)) {
+    const int rc = pkv_seq_append_batched(seqs, n, k, v);
+    if (rc) return rc;
+    return pkv_seq_decode_batched(seqs, n, q, num_heads, scale, out);
+  }
+  // all or nothing: count the pages first
+  size_t reserved = 0;
+  for (int i = 0; i < n; ++i) {
+    const int rc = make_room(seqs[i], 1, &reserved);
+    if (rc) return rc;
+  }
+  const size_t per = (size_t)p->n_kv_heads * p->head_dim, qrow = (size_t)num_heads * p->head_dim;
+  for (int i0 = 0; i0 < n; i0 += kMaxPagedSeqs) {
+    const int m = n - i0 < kMaxPagedSeqs ? n - i0 : kMaxPagedSeqs;
+    int rc = PKV_OK;
+    for (int i = 0; i < m && !rc; ++i) rc = make_room(seqs[i0 + i], 1, nullptr);
+    if (!rc)
+      rc = paged_decode(p, seqs + i0, m, q + i0 * qrow, scale, out + i0 * qrow, k + i0 * per,
+                        v + i0 * per);
+    if (rc) {  // nothing of this chunk was queued: give back the pages taken for it
+      for (int i = 0; i < m; ++i) release_tail(seqs[i0 + i], pages_for(p, seqs[i0 + i]->len));
+      return rc;
+    }
+    for (int i = 0; i < m; ++i) ++seqs[i0 + i]->len;
   }
   return PKV_OK;
 }

@@ -69,9 +69,16 @@ struct DecodeArgsBase {
   DecodePrep prep;
   float *q_out;  // [nseg][16][256] prepared q, for the combine
   unsigned *status;  // the device status word (pkv_device_status)
-  // Fixed mode with dseg non-null: the segment table lives in device memory (the seg
-  // array is unused)
+  // dseg non-null: the segment table lives in device memory (the seg array is unused);
+  // in stream mode wtab then holds, per workgroup, its first segment on the line and the
+  // slot of its first partial (its pieces take consecutive slots)
   const DecodeSeg *dseg;
+  const int2 *wtab;
+  // Fused step: the new rows of nnew output rows (4 nnew rows: K and V of each KV head),
+  // written at newrows[i] (device table; the paged step) or, when null, at row t_new of
+  // segment i (nnew = nseg)
+  int nnew;
+  const NewRow *newrows;
 };
 template <int kSegs>
 struct DecodeArgsT : DecodeArgsBase {
@@ -536,7 +543,8 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
   // partial slot. Fixed mode (wps > 0, paged segments): one piece, blocks
   // [(wg - wg0) bpw, ..) of segment wg / wps, slot wg. Stream mode: the blocks of
   // [V0, V1) on the launch's virtual block line, one piece per segment met, slot wg + s
-  // (distinct for every piece, consecutive for the pieces of one segment).
+  // (distinct for every piece, consecutive for the pieces of one segment), or with a
+  // device table the slots from wtab (consecutive for the pieces of one output row).
   const int V0 = wg * a.vq + (wg < a.vr ? wg : a.vr);
   const int V1 = V0 + a.vq + (wg < a.vr ? 1 : 0);
   int ps = -1, pb0 = 0, pb1 = 0, slot = wg;
@@ -557,6 +565,28 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
       pb0 = (wg - sgv.wg0) * a.bpw;
       pb1 = pb0 + a.bpw < sgv.nblk ? pb0 + a.bpw : sgv.nblk;
       return true;
+    }
+    if (a.dseg != nullptr) {
+      if (ps < 0) {
+        const int2 st = a.wtab[wg];
+        ps = st.x - 1;
+        slot = st.y - 1;
+      }
+      for (int s = ps + 1; s < a.nseg; ++s) {
+        const DecodeSeg e = a.dseg[s];
+        if (e.voff >= V1) return false;
+        const int ve = e.voff + (e.nblk > 0 ? e.nblk : 1);
+        if (ve > V0) {
+          ps = s;
+          sgv = e;
+          pb0 = (V0 > e.voff ? V0 : e.voff) - e.voff;
+          const int x = (V1 < ve ? V1 : ve) - e.voff;
+          pb1 = x < e.nblk ? x : e.nblk;
+          ++slot;
+          return true;
+        }
+      }
+      return false;
     }
     for (int s = ps + 1; s < a.nseg; ++s) {
       const int vs = a.seg[s].voff;
@@ -583,7 +613,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
   // step, which attends to the new key. This runs while the first block streams in.
   // The row is read before any staging load is issued, so the compiler's wait for it
   // does not wait for the stage too.
-  const bool quant = a.k_new != nullptr && wg < 4 * a.nseg && tid < 256;
+  const bool quant = a.k_new != nullptr && wg < 4 * a.nnew && tid < 256;
   float xq = 0.0f;
   PrepElem kpe[1] = {PrepElem{1.0f, 1.0f, 0.0f}};
   auto k_prep_elem = [&](int rs) {
@@ -622,11 +652,17 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
     // the waves sharing its SIMDs
     __builtin_amdgcn_s_setprio(3);
     QuantWavesBarrier bar{&sm.run.t.quant.arrivals, 0u, a.status};
-    for (int row = wg; row < 4 * a.nseg; row += a.nwg) {
+    for (int row = wg; row < 4 * a.nnew; row += a.nwg) {
       const int rs = row >> 2, p = (row >> 1) & 1, kvr = row & 1;
       if (row != wg) xq = (p ? a.v_new : a.k_new)[((int64_t)rs * 2 + kvr) * 256 + tid];
-      const DecodeSeg &rg = a.seg[rs];
-      uint8_t *dst = (p ? rg.v : rg.k) + rg.t_new * a.rs_t + kvr * a.rs_h;
+      uint8_t *dst;
+      if (a.newrows != nullptr) {
+        const NewRow nr = a.newrows[rs];
+        dst = (p ? nr.v : nr.k) + kvr * a.rs_h;
+      } else {
+        const DecodeSeg &rg = a.seg[rs];
+        dst = (p ? rg.v : rg.k) + rg.t_new * a.rs_t + kvr * a.rs_h;
+      }
       if constexpr (kPrep) {
         if (p == 0) {  // k_norm and rope of the new K row (bit-exact), then its quantization
           if (row != wg) kpe[0] = k_prep_elem(rs);
@@ -978,6 +1014,9 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
     d.seg[i].qi = i;
   }
   d.dseg = nullptr;
+  d.wtab = nullptr;
+  d.nnew = n;
+  d.newrows = nullptr;
   // Stream-K plan: the segments' blocks on one virtual line (segment i from voff, an
   // empty segment as one block), with a gap of kPieceGap blocks before every segment
   // after the first, the estimated cost of one more pass (epilogue, q staging and the

@@ -337,6 +337,24 @@ class PagedKvPool:
         _call(lib().pkv_seq_decode_batched(arr, len(seqs), _ptr(q), q.shape[1], scale, _ptr(out)))
         return out
 
+    def append_decode_batched(self, seqs: Sequence["PagedSequence"], new_k: torch.Tensor,
+                              new_v: torch.Tensor, q: torch.Tensor, scale: float) -> torch.Tensor:
+        """The fused decode step: one token appended to each sequence (new_k, new_v [n,
+        num_kv_heads, 1, head_dim]) and one query per sequence over all its keys, the new
+        one included (q [n, num_heads, head_dim] -> out of that shape;
+        pkv_seq_append_decode_batched)."""
+        self._follow_stream()
+        k, v, q = _f32(new_k, "new_k"), _f32(new_v, "new_v"), _f32(q, "q")
+        if k.shape != v.shape or k.dim() != 4 or k.shape[0] != len(seqs) or k.shape[2] != 1:
+            raise KvCacheError("new_k/new_v must both be [n_sequences, heads, 1, head_dim]")
+        if q.dim() != 3 or q.shape[0] != len(seqs):
+            raise KvCacheError("q must be [n_sequences, num_heads, head_dim]")
+        out = torch.empty_like(q)
+        arr = (ctypes.c_void_p * len(seqs))(*[sq.handle.value for sq in seqs])
+        _call(lib().pkv_seq_append_decode_batched(arr, len(seqs), _ptr(k), _ptr(v), _ptr(q),
+                                                  q.shape[1], scale, _ptr(out)))
+        return out
+
 
 class PagedSequence:
     """One sequence of a PagedKvPool, with the cache API of PreallocatedQuantizedKvCache at

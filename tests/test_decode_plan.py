@@ -100,3 +100,81 @@ def test_plan_random():
         else:
             nb = [rng.choice([0, 1, 10, 33, 2048, 4096]) for _ in range(n)]
         check(nb)
+
+
+def paged_plan(nblks, qis):
+    """launch_paged_decode_q4k's stream plan (more than 32 pages): per workgroup its
+    first segment and first slot; slots numbered piece by piece in workgroup order."""
+    n, voff, V = len(nblks), [], 0
+    for i, nb in enumerate(nblks):
+        if i > 0:
+            V += GAP
+        voff.append(V)
+        V += max(nb, 1)
+    nwg = min(max((V + 3) // 4, 1), MAX_WGS)
+    vq, vr = V // nwg, V % nwg
+    wt, slot, sfirst = [], 0, 0
+    nseq = max(qis) + 1
+    wg0, wg1 = [-1] * nseq, [-1] * nseq
+    for w in range(nwg):
+        V0 = w * vq + min(w, vr)
+        V1 = V0 + vq + (1 if w < vr else 0)
+        while sfirst < n and voff[sfirst] + max(nblks[sfirst], 1) <= V0:
+            sfirst += 1
+        wt.append((sfirst, slot))
+        i = sfirst
+        while i < n and voff[i] < V1:
+            if wg0[qis[i]] < 0:
+                wg0[qis[i]] = slot
+            slot += 1
+            wg1[qis[i]] = slot
+            i += 1
+    return voff, nwg, vq, vr, wt, slot, wg0, wg1
+
+
+def paged_pieces(nblks, voff, vq, vr, wt, w):
+    """The kernel's scan over the device table (next_piece, dseg branch)."""
+    V0 = w * vq + min(w, vr)
+    V1 = V0 + vq + (1 if w < vr else 0)
+    ps, slot = wt[w][0] - 1, wt[w][1] - 1
+    out = []
+    while True:
+        for s in range(ps + 1, len(nblks)):
+            if voff[s] >= V1:
+                return out
+            nb = nblks[s]
+            ve = voff[s] + (nb if nb > 0 else 1)
+            if ve > V0:
+                ps, slot = s, slot + 1
+                out.append((s, max(V0, voff[s]) - voff[s], min(min(V1, ve) - voff[s], nb), slot))
+                break
+        else:
+            return out
+
+
+def test_paged_plan_random():
+    rng = random.Random(2)
+    for _ in range(1500):
+        nseq = rng.randint(1, 32)
+        pblk = rng.choice([1, 4, 32, 128, 512])
+        nblks, qis = [], []
+        for q in range(nseq):
+            for p in range(rng.randint(1, 12)):
+                nblks.append(pblk)
+                qis.append(q)
+            nblks[-1] = rng.randint(0, pblk)  # the last page of a sequence is partly full
+        if len(nblks) <= 32:
+            continue
+        voff, nwg, vq, vr, wt, nslots, wg0, wg1 = paged_plan(nblks, qis)
+        cover = [[0] * nb for nb in nblks]
+        seen = []
+        for w in range(nwg):
+            for s, b0, b1, slot in paged_pieces(nblks, voff, vq, vr, wt, w):
+                seen.append((slot, qis[s]))
+                for b in range(b0, b1):
+                    cover[s][b] += 1
+        assert all(c == 1 for row in cover for c in row)
+        slots = [x[0] for x in seen]
+        assert sorted(slots) == list(range(nslots))
+        for q in range(max(qis) + 1):
+            assert {sl for sl, qq in seen if qq == q} == set(range(wg0[q], wg1[q]))

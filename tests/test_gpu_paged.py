@@ -138,16 +138,18 @@ def test_batched_varlen_decode(pk, orc, quant, page):
         np.testing.assert_allclose(out[i], alone, rtol=1e-5, atol=1e-6)
 
 
-def test_many_sequences_batched(pk, orc):
-    """40 sequences: two launches of at most 32."""
-    say("paged batched decode, 40 sequences")
+@pytest.mark.parametrize("quant", [Q4K, Q8_0])
+def test_many_sequences_batched(pk, orc, quant):
+    """40 sequences: two launches of at most 32 (Q4K: each over a device table, split
+    stream-K over the pages)."""
+    say(f"paged batched decode, 40 sequences, quant={quant}")
     rng = np.random.default_rng(40)
     lens = [int(x) for x in rng.integers(1, 300, 40)]
-    pool = pk.PagedKvPool(2, 256, 64, sum(-(-n // 64) for n in lens), pk.KvCacheQuantization.Q8_0)
+    pool = pk.PagedKvPool(2, 256, 64, sum(-(-n // 64) for n in lens), pk.KvCacheQuantization(quant))
     seqs, caches = [], []
     for n in lens:
         s = pool.sequence()
-        c = orc.Cache(Q8_0, 1, 2, 256, n)
+        c = orc.Cache(quant, 1, 2, 256, n)
         fill(pk, orc, s, c, rng, [n], 2, 256)
         seqs.append(s)
         caches.append(c)
@@ -157,6 +159,95 @@ def test_many_sequences_batched(pk, orc):
     for i in (0, 17, 31, 32, 39):
         ref = caches[i].attend(q[i][None, None], 1 / 16, lens[i] - 1, True, mode="f64")[0, 0]
         assert_attn_close(out[i], ref, what=f"sequence {i}")
+
+
+@pytest.mark.parametrize("quant,page,nseq", [(Q4K, 32, 8), (Q4K, 256, 8), (Q8_0, 64, 8),
+                                             (Q4K, 64, 40)])
+def test_append_decode_batched(pk, orc, quant, page, nseq):
+    """The fused step (pkv_seq_append_decode_batched) over empty, page-boundary and forked
+    sequences, two steps in a row: each step's outputs against the oracle's attention over
+    len + 1 keys, then every sequence's rows bit-exact to the oracle's cache. Q4K quantizes
+    the new rows inside the decode launch; 40 sequences take two launches."""
+    say(f"paged fused step quant={quant} page={page} sequences={nseq}")
+    rng = np.random.default_rng(300 + page + nseq)
+    base = [0, 1, page - 1, page, page + 1, 3 * page + 5, 700]
+    lens = (base + [int(x) for x in rng.integers(1, 400, nseq)])[:nseq - 1]
+    pool = pk.PagedKvPool(2, 256, page, sum(-(-(n + 2) // page) for n in lens) + 8 + 2 * nseq,
+                          pk.KvCacheQuantization(quant))
+    seqs, caches = [], []
+    for n in lens:
+        s = pool.sequence()
+        c = orc.Cache(quant, 1, 2, 256, n + 2)
+        if n:
+            fill(pk, orc, s, c, rng, [n], 2, 256)
+        seqs.append(s)
+        caches.append(c)
+    # a fork of the sequence whose last page is partly full: the step copies that page first
+    src = 5 if nseq > 5 else 2
+    f = seqs[src].fork()
+    cf = orc.Cache(quant, 1, 2, 256, lens[src] + 2)
+    cf.load_bytes(*caches[src].valid_bytes(), lens[src])
+    seqs.append(f)
+    caches.append(cf)
+    for step in range(2):
+        kn = rng.standard_normal((nseq, 2, 1, 256)).astype(np.float32)
+        vn = rng.standard_normal((nseq, 2, 1, 256)).astype(np.float32)
+        q = rng.standard_normal((nseq, 16, 256)).astype(np.float32)
+        out = host(pool.append_decode_batched(seqs, dev(kn), dev(vn), dev(q), 1 / 16))
+        for i, (s, c) in enumerate(zip(seqs, caches)):
+            assert c.append(kn[i][None], vn[i][None]) == 0
+            assert s.seq_len == c.seq_len
+            ref = c.attend(q[i][None, None], 1 / 16, c.seq_len - 1, True, mode="f64")[0, 0]
+            assert_attn_close(out[i], ref, what=f"step {step} sequence {i} ({c.seq_len} keys)")
+    for i, (s, c) in enumerate(zip(seqs, caches)):
+        k, v = s.get_kv()
+        rk, rv = c.get_kv()
+        assert np.array_equal(host(k), rk) and np.array_equal(host(v), rv), f"sequence {i}"
+    assert pk.lib().pkv_device_status() == 0, pk.lib().pkv_last_error()
+
+
+def test_append_decode_batched_all_or_nothing(pk, orc):
+    """A pool one page short: PKV_ERR_OVERFLOW, no length or page changes."""
+    say("paged fused step, pool overflow")
+    rng = np.random.default_rng(8)
+    pool = pk.PagedKvPool(2, 256, 32, 3, pk.KvCacheQuantization.Q4K)
+    a, b = pool.sequence(), pool.sequence()
+    ca, cb = orc.Cache(Q4K, 1, 2, 256, 64), orc.Cache(Q4K, 1, 2, 256, 64)
+    fill(pk, orc, a, ca, rng, [32], 2, 256)   # one full page: the step needs a new one
+    fill(pk, orc, b, cb, rng, [64], 2, 256)   # two full pages: so does this one
+    assert pool.free_pages == 0
+    kn = dev(rng.standard_normal((2, 2, 1, 256)).astype(np.float32))
+    q = dev(rng.standard_normal((2, 16, 256)).astype(np.float32))
+    with pytest.raises(pk.KvCacheOverflow):
+        pool.append_decode_batched([a, b], kn, kn, q, 1 / 16)
+    assert (a.seq_len, b.seq_len, a.pages, b.pages, pool.free_pages) == (32, 64, 1, 2, 0)
+
+
+@pytest.mark.parametrize("quant", [Q4K, Q8_0])
+def test_batched_decode_of_forks(pk, orc, quant):
+    """Four sequences forked from one 1000-token prefix, each with its own suffix, decoded
+    in one batched call: the shared pages appear once per sequence, so the launch lists
+    more pages than the pool holds (the staging buffer grows)."""
+    say(f"paged batched decode of forks, quant={quant}")
+    rng = np.random.default_rng(77)
+    pool = pk.PagedKvPool(2, 256, 32, 48, pk.KvCacheQuantization(quant))
+    root = pool.sequence()
+    croot = orc.Cache(quant, 1, 2, 256, 1000)
+    fill(pk, orc, root, croot, rng, [1000], 2, 256)
+    seqs, caches = [root], [croot]
+    for i, extra in enumerate((5, 40, 90)):
+        f = root.fork()
+        c = orc.Cache(quant, 1, 2, 256, 1000 + extra)
+        c.load_bytes(*croot.valid_bytes(), 1000)
+        fill(pk, orc, f, c, rng, [extra], 2, 256)
+        seqs.append(f)
+        caches.append(c)
+    assert sum(s.pages for s in seqs) > 48
+    q = rng.standard_normal((4, 16, 256)).astype(np.float32)
+    out = host(pool.decode_batched(seqs, dev(q), 1 / 16))
+    for i, (s, c) in enumerate(zip(seqs, caches)):
+        ref = c.attend(q[i][None, None], 1 / 16, s.seq_len - 1, True, mode="f64")[0, 0]
+        assert_attn_close(out[i], ref, what=f"sequence {i} ({s.seq_len} keys)")
 
 
 @pytest.mark.parametrize("quant", [Q4K, Q8_0])
