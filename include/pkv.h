@@ -346,10 +346,12 @@ int pkv_seq_decode_batched(pkv_seq *const *seqs, int n, const float *q, int num_
  * one token appended to each of n sequences of one pool (k, v [n, n_kv_heads, 1,
  * head_dim] f32), then one decode query per sequence over all its keys, the new one
  * included (q, out [n, num_heads, head_dim]). Q4K pools of the model's shape run one
- * decode launch per 32 sequences that also quantizes the new rows (its segment table is
- * staged through pinned memory, so the call cannot be captured in a HIP graph); other
- * pools run pkv_seq_append_batched then pkv_seq_decode_batched. All or nothing:
- * PKV_ERR_OVERFLOW, with nothing written, when the pool lacks pages for any of them. */
+ * decode launch per 32 sequences that also quantizes the new rows (kernel arguments and
+ * the sequences' device page lists only: a step in which no sequence's page list changes
+ * can be captured in a HIP graph; one that must copy a changed list returns
+ * PKV_ERR_UNSUPPORTED under capture); other pools run pkv_seq_append_batched then
+ * pkv_seq_decode_batched. All or nothing: PKV_ERR_OVERFLOW, with nothing written, when
+ * the pool lacks pages for any of them. */
 int pkv_seq_append_decode_batched(pkv_seq *const *seqs, int n, const float *k, const float *v,
                                   const float *q, int num_heads, float scale, float *out);
 /* get_kv (qn:520-575): dequantized [1, n_kv_heads, len, head_dim] f32. */

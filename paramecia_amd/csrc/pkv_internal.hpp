@@ -174,38 +174,39 @@ int launch_append_attend_batched(int quant, const SeqDesc *seqs_host, int n, con
                                  Workspace &ws, hipStream_t s);
 
 // ---- paged decode (pkv_attn_mfma.hip: Q4K, pkv_q8_decode.hip: Q8_0) ----
-// One page run of one sequence: rows of tokens [0, len) of the page (K and V planes, rows
-// of head 1 at rs_h), for query / output row qi.
+// Decode attention of nseq <= kMaxPagedSeqs paged sequences, one query each (q, out
+// [nseq][16][256]), 16 query heads, 2 KV heads, head_dim 256, Q4K: sequence i attends to
+// its len keys, held in the pages listed (device memory, in token order) at
+// seqs[i].pages of the pool's K and V planes. Fused step (k_new non-null): the launch
+// also quantizes each sequence's new token (k_new, v_new [nseq][2][256] f32) into row
+// len of page pages[len >> page_lg] (allocated by the caller) and attends to it as well;
+// a sequence may then hold no keys yet.
+struct PagedSeqDesc {
+  const int32_t *pages;
+  int64_t len;
+};
+struct PagedPoolDesc {
+  uint8_t *k, *v;  // planes: page p at p * page_bytes
+  int64_t page_bytes;
+  int page_lg;  // log2 tokens per page
+};
+constexpr int kMaxPagedSeqs = 32;
+int launch_paged_decode_q4k(const PagedSeqDesc *seqs, int nseq, const PagedPoolDesc &pool,
+                            const float *q, float *out, float scale, Workspace &ws,
+                            hipStream_t s, const float *k_new = nullptr,
+                            const float *v_new = nullptr);
+// Q8_0: segs lists every page run, sequence by sequence (qi 0, 0, .., 1, ..), each at most
+// page_tokens keys: rows of tokens [0, len) of the page (K and V planes, rows of head 1 at
+// rs_h), for query / output row qi. More than 32 segments travel in a device table
+// copied from `stage`, a pinned host buffer of at least nseg * kPagedSegBytes bytes that
+// the caller keeps unchanged until the copy has run (it records an event after the call).
 struct PagedSeg {
   uint8_t *k, *v;
   int64_t len;
   int qi;
 };
-// Where a fused paged step writes sequence i's new token: its K and V rows (KV head 0;
-// head h follows at h row strides) in the sequence's last page.
-struct NewRow {
-  uint8_t *k, *v;
-};
-// Decode attention of nseq <= kMaxPagedSeqs sequences, one query each (q, out
-// [nseq][16][256]), over their pages: segs lists every page run, sequence by sequence
-// (qi 0, 0, .., 1, ..), each at most page_tokens keys. 16 query heads, 2 KV heads,
-// head_dim 256.
-// More than 32 segments travel in a device table copied from `stage`, a pinned host
-// buffer of at least nseg * kPagedSegBytes + kPagedStageExtra bytes that the caller keeps
-// unchanged until the copy has run (it records an event after the call).
-// Q4K fused step (k_new non-null): the kernel also quantizes each sequence's new token
-// (k_new, v_new [nseq][2][256] f32) into rows[i] and the combine attends to it; segs
-// then hold the keys before the append (a sequence without keys as one empty segment),
-// and the device table is used whatever the segment count.
-constexpr int kMaxPagedSeqs = 32;
 constexpr int kPagedArgSegs = 32;  // segments carried in the kernel arguments
 constexpr size_t kPagedSegBytes = 64;
-constexpr size_t kPagedStageExtra = 4096;  // room for the per-workgroup and new-row tables
-int launch_paged_decode_q4k(const PagedSeg *segs, int nseg, int nseq, int page_tokens,
-                            const float *q, float *out, int64_t rs_t, int64_t rs_h,
-                            float scale, void *stage, Workspace &ws, hipStream_t s,
-                            const float *k_new = nullptr, const float *v_new = nullptr,
-                            const NewRow *rows = nullptr);
 int launch_paged_decode_q8(const PagedSeg *segs, int nseg, int nseq, int page_tokens,
                            const float *q, float *out, int64_t rs_t, int64_t rs_h, float scale,
                            void *stage, Workspace &ws, hipStream_t s);

@@ -55,7 +55,8 @@ struct pkv_seq {
   pkv_pool *pool;
   std::vector<int32_t> pages;  // in token order
   int64_t len;
-  int32_t *d_pages;  // device copy of `pages` for the append kernel, n_pages entries
+  int32_t *d_pages;  // device copy of `pages` (append and decode kernels), n_pages entries
+  bool d_stale = true;  // `pages` changed since d_pages was last written
 };
 
 namespace pkv {
@@ -77,6 +78,7 @@ void release_tail(pkv_seq *s, size_t keep) {
   while (s->pages.size() > keep) {
     release_page(s->pool, s->pages.back());
     s->pages.pop_back();
+    s->d_stale = true;
   }
 }
 
@@ -115,16 +117,26 @@ int stage_release(pkv_pool *p, int slot) {
 }
 
 // The page table of s into its device copy, staged through a pinned slot.
-int upload_pages(pkv_seq *s) {
+// Bring d_pages up to date (a copy only when the page list changed since the last one).
+// The copy reads a pinned staging slot, so it cannot be captured in a HIP graph.
+int sync_pages(pkv_seq *s) {
   pkv_pool *p = s->pool;
   const size_t bytes = s->pages.size() * sizeof(int32_t);
-  if (bytes == 0) return PKV_OK;
+  if (!s->d_stale || bytes == 0) return PKV_OK;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  PKV_HIP(hipStreamIsCapturing(p->stream, &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return set_error(PKV_ERR_UNSUPPORTED,
+                     "a paged sequence whose page list changed cannot be captured in a graph");
   int slot = 0;
   int rc = stage_acquire(p, bytes, &slot);
   if (rc) return rc;
   memcpy(p->stage[slot], s->pages.data(), bytes);
   PKV_HIP(hipMemcpyAsync(s->d_pages, p->stage[slot], bytes, hipMemcpyHostToDevice, p->stream));
-  return stage_release(p, slot);
+  rc = stage_release(p, slot);
+  if (rc) return rc;
+  s->d_stale = false;
+  return PKV_OK;
 }
 
 // The rows of tokens [0, len) of s, contiguous ([token][head] rows) in p->gather: K at
@@ -182,8 +194,12 @@ int make_room(pkv_seq *s, int64_t n, size_t *reserved) {
                            p->stream));
     release_page(p, old);
     s->pages.back() = mine;
+    s->d_stale = true;
   }
-  while (s->pages.size() < need) s->pages.push_back(take_page(p));
+  while (s->pages.size() < need) {
+    s->pages.push_back(take_page(p));
+    s->d_stale = true;
+  }
   return PKV_OK;
 }
 
@@ -199,39 +215,35 @@ bool fast_decode_shape(const pkv_pool *p, int num_heads) {
 // to it, so sequence i sees len + 1 keys (the caller then advances len).
 int paged_decode(pkv_pool *p, pkv_seq *const *seqs, int n, const float *q, float scale,
                  float *out, const float *k = nullptr, const float *v = nullptr) {
+  if (p->quant == PKV_QUANT_Q4K) {
+    PagedSeqDesc d[kMaxPagedSeqs];
+    for (int i = 0; i < n; ++i) {
+      const int rc = sync_pages(seqs[i]);
+      if (rc) return rc;
+      d[i] = PagedSeqDesc{seqs[i]->d_pages, seqs[i]->len};
+    }
+    const PagedPoolDesc pd{p->k, p->v, (int64_t)p->page_bytes, p->page_lg};
+    return launch_paged_decode_q4k(d, n, pd, q, out, scale, p->ws, p->stream, k, v);
+  }
   std::vector<PagedSeg> segs;
-  std::vector<NewRow> rows;
-  const int64_t rs_t = (int64_t)p->n_kv_heads * (int64_t)p->bpr, rs_h = (int64_t)p->bpr;
   for (int i = 0; i < n; ++i) {
     const pkv_seq *s = seqs[i];
-    const size_t np = pages_for(p, s->len);
-    for (size_t j = 0; j < np; ++j) {
+    for (size_t j = 0; j < pages_for(p, s->len); ++j) {
       const int64_t t0 = (int64_t)j << p->page_lg;
       const int64_t m = s->len - t0 < p->page_tokens ? s->len - t0 : p->page_tokens;
       segs.push_back(PagedSeg{page_k(p, s->pages[j]), page_v(p, s->pages[j]), m, i});
     }
-    if (k != nullptr) {
-      const int64_t t = s->len;
-      const int32_t pg = s->pages[(size_t)(t >> p->page_lg)];
-      const int64_t off = (t & (p->page_tokens - 1)) * rs_t;
-      if (np == 0) segs.push_back(PagedSeg{page_k(p, pg), page_v(p, pg), 0, i});  // no keys yet
-      rows.push_back(NewRow{page_k(p, pg) + off, page_v(p, pg) + off});
-    }
   }
+  const int64_t rs_t = (int64_t)p->n_kv_heads * (int64_t)p->bpr, rs_h = (int64_t)p->bpr;
   int slot = -1;
   void *stage = nullptr;
-  if (k != nullptr || segs.size() > (size_t)kPagedArgSegs) {  // a device table, staged through a pinned slot
-    const int rc = stage_acquire(p, segs.size() * kPagedSegBytes + kPagedStageExtra, &slot);
+  if (segs.size() > (size_t)kPagedArgSegs) {  // a device table, staged through a pinned slot
+    const int rc = stage_acquire(p, segs.size() * kPagedSegBytes, &slot);
     if (rc) return rc;
     stage = p->stage[slot];
   }
-  const int rc =
-      p->quant == PKV_QUANT_Q4K
-          ? launch_paged_decode_q4k(segs.data(), (int)segs.size(), n, p->page_tokens, q, out,
-                                    rs_t, rs_h, scale, stage, p->ws, p->stream, k, v,
-                                    k != nullptr ? rows.data() : nullptr)
-          : launch_paged_decode_q8(segs.data(), (int)segs.size(), n, p->page_tokens, q, out,
-                                   rs_t, rs_h, scale, stage, p->ws, p->stream);
+  const int rc = launch_paged_decode_q8(segs.data(), (int)segs.size(), n, p->page_tokens, q, out,
+                                        rs_t, rs_h, scale, stage, p->ws, p->stream);
   if (slot >= 0) {
     const int rs = stage_release(p, slot);
     if (!rc && rs) return rs;
@@ -281,7 +293,7 @@ int pkv_pool_create(int quant, int n_kv_heads, int head_dim, int page_tokens, in
   }
   // the staging slots up front (pinned allocations can wait for the device): each holds a
   // segment table of every page of the pool, or a page table
-  const size_t stage_bytes = (size_t)n_pages * kPagedSegBytes + kPagedStageExtra;
+  const size_t stage_bytes = (size_t)n_pages * kPagedSegBytes + 4096;
   for (int i = 0; i < pkv_pool::kStages && e == hipSuccess; ++i) {
     e = hipHostMalloc(&p->stage[i], stage_bytes, hipHostMallocDefault);
     if (e == hipSuccess) p->stage_bytes[i] = stage_bytes;
@@ -397,7 +409,7 @@ int pkv_seq_append(pkv_seq *s, const float *k, const float *v, int64_t n, int64_
   if (n == 0) return PKV_OK;
   int rc = make_room(s, n, nullptr);
   if (rc) return rc;
-  rc = upload_pages(s);
+  rc = sync_pages(s);
   if (rc) return rc;
   rc = launch_append_paged(p->quant, k, v, p->k, p->v, s->d_pages, p->page_lg,
                            (int64_t)p->page_bytes, p->n_kv_heads, p->head_dim, n, s->len,

@@ -53,10 +53,9 @@ constexpr int kPieceGap = 6;   // virtual blocks before each segment after the f
 // common launch carries about 200 bytes of arguments instead of the 1.5 KB of the full
 // table.
 struct DecodeArgsBase {
-  int nseg, nwg;
-  int bpw, wps;  // fixed mode (wps > 0): blocks per workgroup, workgroups per segment
-  int vq, vr;    // stream mode: workgroup w's range on the virtual block line starts at
-                 // w vq + min(w, vr) and holds vq + (w < vr) blocks
+  int nseg, nwg;  // segments (or paged sequences), workgroups
+  int vq, vr;     // workgroup w's range on the virtual block line starts at
+                  // w vq + min(w, vr) and holds vq + (w < vr) blocks
   int64_t rs_t, rs_h;
   float sl2;                   // scale * log2(e)
   const float *q;              // [nseg][16][256]
@@ -69,20 +68,33 @@ struct DecodeArgsBase {
   DecodePrep prep;
   float *q_out;  // [nseg][16][256] prepared q, for the combine
   unsigned *status;  // the device status word (pkv_device_status)
-  // dseg non-null: the segment table lives in device memory (the seg array is unused);
-  // in stream mode wtab then holds, per workgroup, its first segment on the line and the
-  // slot of its first partial (its pieces take consecutive slots)
-  const DecodeSeg *dseg;
-  const int2 *wtab;
-  // Fused step: the new rows of nnew output rows (4 nnew rows: K and V of each KV head),
-  // written at newrows[i] (device table; the paged step) or, when null, at row t_new of
-  // segment i (nnew = nseg)
+  // Fused step: the new rows of nnew output rows (4 nnew rows: K and V of each KV
+  // head), at row t_new of segment i, or for paged sequences at row len of their page
   int nnew;
-  const NewRow *newrows;
 };
 template <int kSegs>
 struct DecodeArgsT : DecodeArgsBase {
   DecodeSeg seg[kSegs];
+};
+// Paged sequences with device page lists (kSegs == 0, the paged Q4K decode): output row i
+// attends to len keys held in pages[0..npg) of the pool's planes. Its segment j (page j)
+// sits on the virtual block line at vstart + j * pstride (pstride = blocks per page + the
+// gap), with the blocks of the keys it holds, or one virtual block for a sequence
+// without keys (a fused step's first token); kfirst numbers its segment 0 among all
+// segments of the launch. The fused step's new row of sequence i is row len of page
+// pages[len >> page_lg].
+struct PagedSeqArg {
+  const int32_t *pages;
+  int64_t len;
+  int vstart, npg, kfirst, pad;
+};
+template <>
+struct DecodeArgsT<0> : DecodeArgsBase {
+  PagedSeqArg pq[kMaxSegs];
+  uint8_t *kplane, *vplane;
+  int64_t page_bytes;
+  int page_lg, pstride;
+  int nsegs;  // segments of the launch
 };
 
 // Per-wave tables rebuilt for every 32-key block.
@@ -539,17 +551,57 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
   const uint32_t st_lds0 = __builtin_amdgcn_readfirstlane(
       (uint32_t)(size_t)((PKV_LDS void *)&sm.run.st[wave][0]));
 
-  // ---- pieces of this workgroup (wave-uniform): segment ps, its blocks [pb0, pb1), the
-  // partial slot. Fixed mode (wps > 0, paged segments): one piece, blocks
-  // [(wg - wg0) bpw, ..) of segment wg / wps, slot wg. Stream mode: the blocks of
-  // [V0, V1) on the launch's virtual block line, one piece per segment met, slot wg + s
-  // (distinct for every piece, consecutive for the pieces of one segment), or with a
-  // device table the slots from wtab (consecutive for the pieces of one output row).
+  // ---- pieces of this workgroup (wave-uniform): the blocks of [V0, V1) on the launch's
+  // virtual block line, one piece per segment met (its blocks [pb0, pb1)), each with its
+  // partial in slot wg + (the segment's index), distinct for every piece and
+  // consecutive for the pieces of one segment.
   const int V0 = wg * a.vq + (wg < a.vr ? wg : a.vr);
   const int V1 = V0 + a.vq + (wg < a.vr ? 1 : 0);
   int ps = -1, pb0 = 0, pb1 = 0, slot = wg;
   DecodeSeg sgv = {};  // read only while a piece is held
+  // paged device-list mode: (pi, pj) is the next segment the scan looks at
+  int pi = 0, pj = 0;
   auto next_piece = [&]() -> bool {
+    if constexpr (kSegs == 0) {
+      if (ps < 0) {  // the first segment that may meet [V0, V1): found by arithmetic
+        ps = 0;
+        while (pi + 1 < a.nseg && a.pq[pi + 1].vstart <= V0) ++pi;
+        const int rel = V0 - a.pq[pi].vstart;
+        pj = rel > 0 ? rel / a.pstride : 0;
+        if (pj >= a.pq[pi].npg) pj = a.pq[pi].npg - 1;
+      }
+      while (pi < a.nseg) {
+        const PagedSeqArg &sq = a.pq[pi];
+        const int64_t t0 = (int64_t)pj << a.page_lg, rest = sq.len - t0;
+        const int64_t keys = rest < ((int64_t)1 << a.page_lg) ? rest : ((int64_t)1 << a.page_lg);
+        const int nb = (int)((keys + kBlk - 1) / kBlk);
+        const int vs = sq.vstart + pj * a.pstride;
+        if (vs >= V1) return false;
+        const int ve = vs + (nb > 0 ? nb : 1);
+        const int k = sq.kfirst + pj, i = pi, j = pj;
+        if (++pj >= sq.npg) {
+          ++pi;
+          pj = 0;
+        }
+        if (ve > V0) {
+          const int64_t pg = sq.pages[j];
+          sgv.k = a.kplane + pg * a.page_bytes;
+          sgv.v = a.vplane + pg * a.page_bytes;
+          sgv.seq_k = keys;
+          sgv.t_new = 0;
+          sgv.nblk = nb;
+          sgv.wg0 = -1;
+          sgv.qi = i;
+          sgv.voff = vs;
+          pb0 = (V0 > vs ? V0 : vs) - vs;
+          const int e = (V1 < ve ? V1 : ve) - vs;
+          pb1 = e < nb ? e : nb;
+          slot = wg + k;
+          return true;
+        }
+      }
+      return false;
+    } else {
     if constexpr (kSegs == 1) {  // one segment at voff 0: the range is the piece
       if (ps >= 0) return false;
       ps = 0;
@@ -557,36 +609,6 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
       pb0 = V0;
       pb1 = V1 < sgv.nblk ? V1 : sgv.nblk;
       return V0 < (sgv.nblk > 0 ? sgv.nblk : 1);
-    }
-    if (a.wps > 0) {
-      if (ps >= 0) return false;
-      ps = wg / a.wps;
-      sgv = a.dseg != nullptr ? a.dseg[ps] : a.seg[ps];
-      pb0 = (wg - sgv.wg0) * a.bpw;
-      pb1 = pb0 + a.bpw < sgv.nblk ? pb0 + a.bpw : sgv.nblk;
-      return true;
-    }
-    if (a.dseg != nullptr) {
-      if (ps < 0) {
-        const int2 st = a.wtab[wg];
-        ps = st.x - 1;
-        slot = st.y - 1;
-      }
-      for (int s = ps + 1; s < a.nseg; ++s) {
-        const DecodeSeg e = a.dseg[s];
-        if (e.voff >= V1) return false;
-        const int ve = e.voff + (e.nblk > 0 ? e.nblk : 1);
-        if (ve > V0) {
-          ps = s;
-          sgv = e;
-          pb0 = (V0 > e.voff ? V0 : e.voff) - e.voff;
-          const int x = (V1 < ve ? V1 : ve) - e.voff;
-          pb1 = x < e.nblk ? x : e.nblk;
-          ++slot;
-          return true;
-        }
-      }
-      return false;
     }
     for (int s = ps + 1; s < a.nseg; ++s) {
       const int vs = a.seg[s].voff;
@@ -604,8 +626,37 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
       }
     }
     return false;
+    }
   };
   bool have = next_piece();
+  if constexpr (kSegs == 0) {
+    // The partial slots a workgroup owns run from wg + (segments ending at or before V0)
+    // to wg + (segments starting before V1); its pieces fill them, except the last one
+    // when its range does not end inside a segment: that slot gets an empty partial, so
+    // that every slot in an output row's range holds one. The last segment starting
+    // before V1 is (mi, mj).
+    int mi = 0;
+    while (mi + 1 < a.nseg && a.pq[mi + 1].vstart < V1) ++mi;
+    const PagedSeqArg &sq = a.pq[mi];
+    int mj = (V1 - 1 - sq.vstart) / a.pstride;
+    if (mj >= sq.npg) mj = sq.npg - 1;
+    const int64_t rest = sq.len - ((int64_t)mj << a.page_lg);
+    const int64_t keys = rest < ((int64_t)1 << a.page_lg) ? rest : ((int64_t)1 << a.page_lg);
+    const int nb = (int)((keys + kBlk - 1) / kBlk);
+    if (sq.vstart + mj * a.pstride + (nb > 0 ? nb : 1) <= V1) {
+      const int ms = wg + sq.kfirst + mj + 1;
+      static_assert(kThreads * 8 == 16 * kPartRow, "one partial: 8 floats per thread");
+      float *pz = a.part + ((int64_t)ms * 16 * kPartRow + 8 * tid);
+      const f4 z = {0.f, 0.f, 0.f, 0.f};
+      __builtin_nontemporal_store(z, reinterpret_cast<f4 *>(pz));
+      __builtin_nontemporal_store(z, reinterpret_cast<f4 *>(pz) + 1);
+      if (tid < 16) {
+        float *mlo = reinterpret_cast<float *>(a.ml + (ms * 16 + tid));
+        __builtin_nontemporal_store(-INFINITY, mlo);
+        __builtin_nontemporal_store(0.0f, mlo + 1);
+      }
+    }
+  }
 
   // Fused append: threads 0-255 (waves 0-3) of workgroup r quantize new row r (row
   // 4s + 2p + kv: segment s, K (p = 0) or V (p = 1), KV head kv; further rows go
@@ -618,7 +669,8 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
   PrepElem kpe[1] = {PrepElem{1.0f, 1.0f, 0.0f}};
   auto k_prep_elem = [&](int rs) {
     const int half = a.prep.n_rot >> 1;
-    const int64_t pos = a.seg[rs].t_new;
+    int64_t pos = 0;
+    if constexpr (kSegs != 0) pos = a.seg[rs].t_new;
     return load_prep_elem(a.prep.k_alpha, a.prep.cos_tab + pos * half,
                           a.prep.sin_tab + pos * half, tid, 256, a.prep.n_rot);
   };
@@ -656,9 +708,11 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
       const int rs = row >> 2, p = (row >> 1) & 1, kvr = row & 1;
       if (row != wg) xq = (p ? a.v_new : a.k_new)[((int64_t)rs * 2 + kvr) * 256 + tid];
       uint8_t *dst;
-      if (a.newrows != nullptr) {
-        const NewRow nr = a.newrows[rs];
-        dst = (p ? nr.v : nr.k) + kvr * a.rs_h;
+      if constexpr (kSegs == 0) {  // row len of the page that holds token len
+        const PagedSeqArg &sq = a.pq[rs];
+        const int64_t pg = sq.pages[sq.len >> a.page_lg];
+        dst = (p ? a.vplane : a.kplane) + pg * a.page_bytes +
+              (sq.len & (((int64_t)1 << a.page_lg) - 1)) * a.rs_t + kvr * a.rs_h;
       } else {
         const DecodeSeg &rg = a.seg[rs];
         dst = (p ? rg.v : rg.k) + rg.t_new * a.rs_t + kvr * a.rs_h;
@@ -1013,10 +1067,7 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
     d.seg[i].nblk = (int)((d.seg[i].seq_k + kBlk - 1) / kBlk);
     d.seg[i].qi = i;
   }
-  d.dseg = nullptr;
-  d.wtab = nullptr;
   d.nnew = n;
-  d.newrows = nullptr;
   // Stream-K plan: the segments' blocks on one virtual line (segment i from voff, an
   // empty segment as one block), with a gap of kPieceGap blocks before every segment
   // after the first, the estimated cost of one more pass (epilogue, q staging and the
@@ -1052,8 +1103,6 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
   const int wg = nwg + n - 1;  // partial slots
   d.nseg = n;
   d.nwg = nwg;
-  d.bpw = 0;
-  d.wps = 0;
   d.vq = vq;
   d.vr = vr;
   d.rs_t = rs_t;

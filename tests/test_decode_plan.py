@@ -102,79 +102,112 @@ def test_plan_random():
         check(nb)
 
 
-def paged_plan(nblks, qis):
-    """launch_paged_decode_q4k's stream plan (more than 32 pages): per workgroup its
-    first segment and first slot; slots numbered piece by piece in workgroup order."""
-    n, voff, V = len(nblks), [], 0
-    for i, nb in enumerate(nblks):
+def paged_plan(lens, fused, pblk):
+    """launch_paged_decode_q4k's plan over device page lists: per sequence its virtual
+    start, segment count (pages with keys; one virtual block for a fused step's sequence
+    without keys), first segment index, and the combine's slot range."""
+    pstride = pblk + GAP
+    ptok = 32 * pblk
+    pq, V, K = [], 0, 0
+    for i, n in enumerate(lens):
+        npg = -(-n // ptok) if n > 0 else 1
         if i > 0:
             V += GAP
-        voff.append(V)
-        V += max(nb, 1)
+        last = n - (npg - 1) * ptok
+        nb_last = -(-last // 32)
+        pq.append((n, V, npg, K))
+        V += (npg - 1) * pstride + max(nb_last, 1)
+        K += npg
+    vend = []
+    for i in range(len(lens)):
+        n, vs, npg, kf = pq[i]
+        last = n - (npg - 1) * ptok
+        vend.append(vs + (npg - 1) * pstride + max(-(-last // 32), 1))
     nwg = min(max((V + 3) // 4, 1), MAX_WGS)
     vq, vr = V // nwg, V % nwg
-    wt, slot, sfirst = [], 0, 0
-    nseq = max(qis) + 1
-    wg0, wg1 = [-1] * nseq, [-1] * nseq
-    for w in range(nwg):
-        V0 = w * vq + min(w, vr)
-        V1 = V0 + vq + (1 if w < vr else 0)
-        while sfirst < n and voff[sfirst] + max(nblks[sfirst], 1) <= V0:
-            sfirst += 1
-        wt.append((sfirst, slot))
-        i = sfirst
-        while i < n and voff[i] < V1:
-            if wg0[qis[i]] < 0:
-                wg0[qis[i]] = slot
-            slot += 1
-            wg1[qis[i]] = slot
-            i += 1
-    return voff, nwg, vq, vr, wt, slot, wg0, wg1
+
+    def wg_of(x):
+        big = vr * (vq + 1)
+        return x // (vq + 1) if x < big else vr + (x - big) // vq
+
+    wg0 = [wg_of(pq[i][1]) + pq[i][3] for i in range(len(lens))]
+    wg1 = [wg_of(vend[i] - 1) + pq[i][3] + pq[i][2] for i in range(len(lens))]
+    return pq, nwg, vq, vr, K, pstride, ptok, wg0, wg1
 
 
-def paged_pieces(nblks, voff, vq, vr, wt, w):
-    """The kernel's scan over the device table (next_piece, dseg branch)."""
+def seg_keys(n, j, ptok):
+    return min(n - j * ptok, ptok)
+
+
+def paged_pieces(pq, nwg, vq, vr, pstride, ptok, w):
+    """The kernel's scan (next_piece, kSegs == 0) and its empty-partial marker."""
     V0 = w * vq + min(w, vr)
     V1 = V0 + vq + (1 if w < vr else 0)
-    ps, slot = wt[w][0] - 1, wt[w][1] - 1
+    nseq = len(pq)
+    pi = 0
+    while pi + 1 < nseq and pq[pi + 1][1] <= V0:
+        pi += 1
+    rel = V0 - pq[pi][1]
+    pj = rel // pstride if rel > 0 else 0
+    pj = min(pj, pq[pi][2] - 1)
     out = []
-    while True:
-        for s in range(ps + 1, len(nblks)):
-            if voff[s] >= V1:
-                return out
-            nb = nblks[s]
-            ve = voff[s] + (nb if nb > 0 else 1)
-            if ve > V0:
-                ps, slot = s, slot + 1
-                out.append((s, max(V0, voff[s]) - voff[s], min(min(V1, ve) - voff[s], nb), slot))
-                break
-        else:
-            return out
+    while pi < nseq:
+        n, vst, npg, kf = pq[pi]
+        keys = seg_keys(n, pj, ptok)
+        nb = -(-keys // 32)
+        vs = vst + pj * pstride
+        if vs >= V1:
+            break
+        ve = vs + max(nb, 1)
+        k, i, j = kf + pj, pi, pj
+        pj += 1
+        if pj >= npg:
+            pi, pj = pi + 1, 0
+        if ve > V0:
+            out.append((i, j, max(V0, vs) - vs, min(min(V1, ve) - vs, nb), w + k))
+    # marker: the last segment starting before V1
+    mi = 0
+    while mi + 1 < nseq and pq[mi + 1][1] < V1:
+        mi += 1
+    n, vst, npg, kf = pq[mi]
+    mj = min((V1 - 1 - vst) // pstride, npg - 1)
+    nb = -(-seg_keys(n, mj, ptok) // 32)
+    marker = w + kf + mj + 1 if vst + mj * pstride + max(nb, 1) <= V1 else None
+    return out, marker
 
 
 def test_paged_plan_random():
     rng = random.Random(2)
-    for _ in range(1500):
+    for trial in range(1500):
         nseq = rng.randint(1, 32)
         pblk = rng.choice([1, 4, 32, 128, 512])
-        nblks, qis = [], []
-        for q in range(nseq):
-            for p in range(rng.randint(1, 12)):
-                nblks.append(pblk)
-                qis.append(q)
-            nblks[-1] = rng.randint(0, pblk)  # the last page of a sequence is partly full
-        if len(nblks) <= 32:
-            continue
-        voff, nwg, vq, vr, wt, nslots, wg0, wg1 = paged_plan(nblks, qis)
-        cover = [[0] * nb for nb in nblks]
-        seen = []
+        fused = rng.random() < 0.5
+        ptok = 32 * pblk
+        lens = []
+        for _ in range(nseq):
+            r = rng.random()
+            if r < 0.15 and fused:
+                lens.append(0)
+            elif r < 0.3:
+                lens.append(rng.choice([1, ptok - 1, ptok, ptok + 1, 3 * ptok]))
+            else:
+                lens.append(rng.randint(1, 12 * ptok))
+        pq, nwg, vq, vr, K, pstride, ptok, wg0, wg1 = paged_plan(lens, fused, pblk)
+        cover = [[0] * -(-n // 32) for n in lens]
+        written = {}
         for w in range(nwg):
-            for s, b0, b1, slot in paged_pieces(nblks, voff, vq, vr, wt, w):
-                seen.append((slot, qis[s]))
+            pieces, marker = paged_pieces(pq, nwg, vq, vr, pstride, ptok, w)
+            for i, j, b0, b1, slot in pieces:
+                assert slot not in written
+                written[slot] = i
                 for b in range(b0, b1):
-                    cover[s][b] += 1
-        assert all(c == 1 for row in cover for c in row)
-        slots = [x[0] for x in seen]
-        assert sorted(slots) == list(range(nslots))
-        for q in range(max(qis) + 1):
-            assert {sl for sl, qq in seen if qq == q} == set(range(wg0[q], wg1[q]))
+                    cover[i][j * pblk + b] += 1
+            if marker is not None:
+                assert marker not in written
+                written[marker] = None
+        assert all(c == 1 for row in cover for c in row), trial
+        assert all(0 <= sl < nwg + K for sl in written)
+        for i in range(nseq):  # the combine's range: this row's pieces and empty partials only
+            rng_slots = range(wg0[i], wg1[i])
+            assert all(sl in written and written[sl] in (i, None) for sl in rng_slots), (trial, i)
+            assert {sl for sl, q in written.items() if q == i} <= set(rng_slots)

@@ -206,6 +206,61 @@ def test_append_decode_batched(pk, orc, quant, page, nseq):
     assert pk.lib().pkv_device_status() == 0, pk.lib().pkv_last_error()
 
 
+def test_fused_step_graph_replay(pk, orc):
+    """A fused paged step whose sequences gain no page is captured in a HIP graph (Q4K
+    page lists live on the device): three replays, with other eager work on the pool in
+    between, each give the eager step's output bit for bit and leave the rows the oracle
+    holds."""
+    say("paged fused step, graph replay")
+    rng = np.random.default_rng(12)
+    lens = [100, 700, 33, 1500, 64 + 7]
+    pool = pk.PagedKvPool(2, 256, 64, 64, pk.KvCacheQuantization.Q4K)
+    seqs, caches = [], []
+    for n in lens:
+        s = pool.sequence()
+        c = orc.Cache(Q4K, 1, 2, 256, n + 1)
+        fill(pk, orc, s, c, rng, [n], 2, 256)
+        seqs.append(s)
+        caches.append(c)
+    kn = dev(rng.standard_normal((5, 2, 1, 256)).astype(np.float32))
+    vn = dev(rng.standard_normal((5, 2, 1, 256)).astype(np.float32))
+    q = dev(rng.standard_normal((5, 16, 256)).astype(np.float32))
+    outs = [None]
+
+    def step():
+        for s, n in zip(seqs, lens):
+            s.truncate(n)
+        outs[0] = pool.append_decode_batched(seqs, kn, vn, q, 1 / 16)
+
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()  # eager: sizes the workspace, syncs the page lists
+        torch.cuda.synchronize()
+        ref = host(outs[0])
+        with torch.cuda.graph(graph, stream=side):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    got_out = outs[0]
+    for i in range(3):
+        other = pool.sequence()  # eager work on the pool between the replays
+        other.append_quantized(kn[:1].repeat(1, 1, 3, 1), vn[:1].repeat(1, 1, 3, 1))
+        torch.cuda.synchronize()
+        del other
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(got_out), ref), f"replay {i}"
+    for i, (s, c) in enumerate(zip(seqs, caches)):
+        assert c.append(host(kn)[i][None], host(vn)[i][None]) == 0
+        ref_i = c.attend(host(q)[i][None, None], 1 / 16, c.seq_len - 1, True, mode="f64")[0, 0]
+        assert_attn_close(ref[i], ref_i, what=f"sequence {i}")
+        k, v = s.get_kv()
+        rk, rv = c.get_kv()
+        assert np.array_equal(host(k), rk) and np.array_equal(host(v), rv), f"sequence {i}"
+
+
 def test_append_decode_batched_all_or_nothing(pk, orc):
     """A pool one page short: PKV_ERR_OVERFLOW, no length or page changes."""
     say("paged fused step, pool overflow")
