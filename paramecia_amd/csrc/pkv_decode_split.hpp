@@ -1,12 +1,13 @@
 // Split-K decode plumbing shared by the decode kernels (Q4K MFMA, Q8_0): the segment
-// table of one launch, and the kernel that merges the per-workgroup partials of each
-// segment and adds the appended key of a fused decode step. Include-only; every
-// symbol has internal linkage.
+// table of one launch, and the kernel that merges the partials of each output row and
+// adds the appended key of a fused decode step. Include-only; every symbol has
+// internal linkage.
 //
-// Partial layout: part[wg][16 heads][256]: the un-normalised output in tile order (entry
-// 16 T + n holds element tile_e(T, n)); ml[wg][16 heads]: the running max m (log2 units)
-// and the sum l of 2^(score - m). A row is 1 KB, so the combine's 32-entry slices each
-// fill one 128-byte line, and a head's (m, l) pairs of all partials are contiguous.
+// Partial layout, one slot per piece of work (a workgroup's blocks of one segment):
+// part[slot][16 heads][256]: the un-normalised output in tile order (entry 16 T + n
+// holds element tile_e(T, n)); ml[slot][16 heads]: the running max m (log2 units) and the
+// sum l of 2^(score - m). A row is 1 KB, so the combine's 32-entry slices each fill one
+// 128-byte line, and a head's (m, l) pairs of all partials are contiguous.
 #pragma once
 #include <type_traits>
 
