@@ -12,6 +12,17 @@
 
 namespace pkv {
 
+// (nearest_int(v)).clamp(0, 15), nearest_int being candle's v.round() as i32 (half away
+// from zero, NaN -> 0), in two instructions. v_med3_f32 clamps to [0, 15] first; with a
+// NaN operand it returns the least of the other two, 0. v_cvt_rpi_i32_f32 then gives
+// floor(c + 0.5) without rounding the sum, which on [0, 15] is round half away from zero.
+__device__ __forceinline__ int32_t q4_level_i(float v) {
+  const float c = __builtin_amdgcn_fmed3f(v, 0.0f, 15.0f);
+  int32_t r;
+  asm("v_cvt_rpi_i32_f32 %0, %1" : "=v"(r) : "v"(c));
+  return r;
+}
+
 struct Q4kScratch {
   float scr[256];
   float red[2][8];
@@ -83,8 +94,7 @@ static __device__ __forceinline__ void q4k_quantize_superblock_lanes(float x, ui
     float iscale = 15.0f / (mx - fmin);
     scale = 1.0f / iscale;
     for (int t = 0; t < 5; ++t) {
-      int32_t li = nearest_int(iscale * (x - fmin));
-      li = li < 0 ? 0 : (li > 15 ? 15 : li);
+      const int32_t li = q4_level_i(iscale * (x - fmin));
       const bool changed = (uint32_t)li != L;
       L = (uint32_t)li;
       const float sumlx = q4k_chain_sum_32(mine, i, (x - fmin) * (float)li, 0.0f);
@@ -121,8 +131,7 @@ static __device__ __forceinline__ void q4k_quantize_superblock_lanes(float x, ui
   const float dd = f16_to_f32(dh) * (float)ls;
   if (dd != 0.0f) {
     const float dm = f16_to_f32(mh) * (float)lm;
-    const int32_t l = nearest_int((x + dm) / dd);
-    q = (uint32_t)(l < 0 ? 0 : (l > 15 ? 15 : l));
+    q = (uint32_t)q4_level_i((x + dm) / dd);
   }
   if (deq != nullptr) {  // to_float of this element: d * sc * q - dmin * m (two roundings)
     const float d1 = f16_to_f32(dh) * (float)ls, m1 = f16_to_f32(mh) * (float)lm;

@@ -56,18 +56,6 @@ __device__ __forceinline__ uint8_t *row_ptr(const AppendArgs &a, int p, int64_t 
   return a.dst[p] + dst_row(a, t, b, h) * a.bpr;
 }
 
-// clamp(nearest_int(v), 0, 15) as a float: nearest_int is candle's v.round() as i32
-// (half away from zero, NaN -> 0). rint rounds half to even; a tie it rounded down
-// (v - r == 0.5, exact: |v - r| <= 0.5 and r is v's nearest integer) goes up instead. A
-// tie below zero, a negative value, -0 and NaN all give +0 after the clamp, as the
-// integer path does.
-__device__ __forceinline__ float q4_level(float v) {
-  float r = __builtin_rintf(v);
-  r = (v - r == 0.5f) ? r + 1.0f : r;
-  r = (r > 0.0f) ? r : 0.0f;
-  return (r < 15.0f) ? r : 15.0f;
-}
-
 // candle make_qkx1_quants(nmax = 15, ntry = 5) over the 32 values of one sub-block.
 // The levels are kept as floats (small integers, exact), suml2 is summed in f32 (an
 // integer below 2^24, exact), and every other sum runs in the reference's order with one
@@ -96,7 +84,7 @@ __device__ void make_qkx1_quants_32(const float x[32], float &scale_out, float &
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
       const float d = x[i] - min;
-      const float li = q4_level(iscale * d);
+      const float li = (float)q4_level_i(iscale * d);
       did_change |= li != L[i];
       L[i] = li;
       sumlx += d * li;
@@ -201,8 +189,7 @@ __global__ __launch_bounds__(256) void q4k_append_kernel(AppendArgs a, int64_t u
 #pragma unroll
       for (int i = 0; i < 32; ++i) {
         if (slow & (1u << i)) {
-          int32_t l = nearest_int((x[i] + dm) / dd);
-          l = l < 0 ? 0 : (l > 15 ? 15 : l);
+          const int32_t l = q4_level_i((x[i] + dm) / dd);
           Lw[i >> 3] = (Lw[i >> 3] & ~(15u << (4 * (i & 7)))) | ((uint32_t)l << (4 * (i & 7)));
         }
       }

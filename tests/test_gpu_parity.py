@@ -100,6 +100,42 @@ def test_bulk_append_bitexact(pk, orc, quant):
     assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
 
 
+def nonfinite_rows(rng, n_rows, d):
+    """Random rows with NaN and infinities planted: one element, a whole 32-element
+    sub-block, every fifth element, both signs."""
+    x = rng.standard_normal((n_rows, d)).astype(np.float32)
+    plant = [lambda r: r.__setitem__(3, np.nan), lambda r: r.__setitem__(40, np.inf),
+             lambda r: r.__setitem__(70, -np.inf), lambda r: r.__setitem__(slice(0, 32), np.nan),
+             lambda r: r.__setitem__(slice(None, None, 5), np.inf),
+             lambda r: r.__setitem__(0, -np.nan), lambda r: None]
+    for i in range(n_rows):
+        plant[i % len(plant)](x[i])
+    return x
+
+
+@pytest.mark.parametrize("quant", [Q4K, Q8_0])
+def test_append_nonfinite_bitexact(pk, orc, quant):
+    """NaN and infinities quantize as the reference's integer conversions fix them (a NaN
+    level is 0), through the latency kernels (short appends) and the throughput kernels
+    (the 1500-token append)."""
+    say(f"non-finite append quant={quant}")
+    rng = np.random.default_rng(300 + quant)
+    g = pk.PreallocatedQuantizedKvCache(1, 2, 2048, 256, pk.KvCacheQuantization(quant))
+    c = orc.Cache(quant, 1, 2, 256, 2048)
+    for n in (7, 1500, 2):
+        k = nonfinite_rows(rng, 2 * n, 256).reshape(1, 2, n, 256)
+        v = nonfinite_rows(rng, 2 * n, 256).reshape(1, 2, n, 256)[:, :, ::-1].copy()
+        g.append_quantized(dev(k), dev(v))
+        assert c.append(k, v) == 0
+    gk, gv = g.raw_bytes()
+    ok, ov = c.valid_bytes()
+    assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
+    k, v = g.get_kv()
+    rk, rv = c.get_kv()
+    np.testing.assert_array_equal(host(k), rk)  # NaN matches NaN
+    np.testing.assert_array_equal(host(v), rv)
+
+
 def test_fill_normal_bitexact(pk, orc):
     say("fill_normal parity")
     t = torch.empty(1 << 20, dtype=torch.float32, device="cuda")
