@@ -56,60 +56,76 @@ __device__ __forceinline__ uint8_t *row_ptr(const AppendArgs &a, int p, int64_t 
   return a.dst[p] + dst_row(a, t, b, h) * a.bpr;
 }
 
-// candle make_qkx1_quants(nmax = 15, ntry = 5) over the 32 values of one sub-block.
-// The levels are kept as floats (small integers, exact), suml2 is summed in f32 (an
-// integer below 2^24, exact), and every other sum runs in the reference's order with one
-// rounding per operation.
-__device__ void make_qkx1_quants_32(const float x[32], float &scale_out, float &neg_min_out) {
-  float mn = x[0], mx = x[0];
-#pragma unroll
-  for (int i = 1; i < 32; ++i) {
-    if (total_key(x[i]) < total_key(mn)) mn = x[i];
-    if (total_key(x[i]) >= total_key(mx)) mx = x[i];
+// Lanes per Q4K sub-block in the throughput kernel (kL = 1, 2, 4) and the helpers that
+// join a sub-block's kL lanes: all moves within a quad of lanes (DPP), exact.
+template <int kL, int q>
+__device__ __forceinline__ float group_bcast(float v) {  // lane q of the group's value
+  if constexpr (kL == 1) {
+    return v;
+  } else {
+    constexpr int ctrl = kL == 2 ? (q | (q << 2) | ((2 + q) << 4) | ((2 + q) << 6)) : q * 0x55;
+    return u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(v), ctrl, 0xF, 0xF, false));
   }
-  if (mx == mn) {
-    scale_out = 0.0f;
-    neg_min_out = 0.0f;
-    return;
+}
+template <int kL, typename T, typename Op>
+__device__ __forceinline__ T group_allreduce(T v, Op op) {  // order-free ops only
+  if constexpr (kL >= 2) {
+    const int o = __builtin_amdgcn_update_dpp(0, (int)__builtin_bit_cast(uint32_t, v), 0xB1, 0xF,
+                                              0xF, false);  // quad_perm [1,0,3,2]
+    v = op(v, __builtin_bit_cast(T, o));
   }
-  float L[32];
-#pragma unroll
-  for (int i = 0; i < 32; ++i) L[i] = 0.0f;
-  float min = fmin_rs(mn, 0.0f);
-  float iscale = 15.0f / (mx - min);
-  float scale = 1.0f / iscale;
-  for (int t = 0; t < 5; ++t) {
-    float sumlx = 0.0f, suml2 = 0.0f;
-    bool did_change = false;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const float d = x[i] - min;
-      const float li = (float)q4_level_i(iscale * d);
-      did_change |= li != L[i];
-      L[i] = li;
-      sumlx += d * li;
-      suml2 = __builtin_fmaf(li, li, suml2);  // exact
-    }
-    scale = sumlx / suml2;
-    float sum = -0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) sum += x[i] - scale * L[i];
-    min = sum / 32.0f;
-    if (min > 0.0f) min = 0.0f;
-    iscale = 1.0f / scale;
-    if (!did_change) break;
+  if constexpr (kL >= 4) {
+    const int o = __builtin_amdgcn_update_dpp(0, (int)__builtin_bit_cast(uint32_t, v), 0x4E, 0xF,
+                                              0xF, false);  // quad_perm [2,3,0,1]
+    v = op(v, __builtin_bit_cast(T, o));
   }
-  scale_out = scale;
-  neg_min_out = -min;
+  return v;
+}
+// acc + term[0] + ... over the whole sub-block, in element order with one rounding per add:
+// lane q of the group adds its E terms to the running sum, which every lane then takes
+// from lane q (the other lanes' adds that step are discarded).
+template <int kL, int q = 0>
+struct GroupChain {
+  template <int E>
+  static __device__ __forceinline__ float run(const float (&term)[E], float acc) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int i = 0; i < E; ++i) acc += term[i];
+    acc = group_bcast<kL, q>(acc);
+    if constexpr (q + 1 < kL)
+      return GroupChain<kL, q + 1>::run(term, acc);
+    else
+      return acc;
+  }
+};
+template <int kL>
+__device__ __forceinline__ bool group_any(bool c) {
+  if constexpr (kL == 1) {
+    return c;
+  } else {
+    const uint64_t bal = __ballot(c);
+    const int base = (int)(threadIdx.x & 63) & ~(kL - 1);
+    return ((bal >> base) & ((1u << kL) - 1)) != 0;
+  }
 }
 
-// Q4K (BlockQ4K::from_float): 8 lanes per 256-element superblock, lane j owns
-// sub-block j. Cross-lane work is limited to exact max reductions and byte shuffles.
+// Q4K (BlockQ4K::from_float): 8 kL lanes per 256-element superblock. Lane (j, s) of the
+// superblock holds elements [32 j + s E, 32 j + (s + 1) E) of sub-block j, E = 32 / kL.
+// The sub-block fit is candle's make_qkx1_quants(nmax = 15, ntry = 5): levels are floats
+// (small integers, exact), suml2 an integer-valued f32 (exact, any order), and the two
+// other sums run in element order with one rounding per add, lane after lane through the
+// group. The element-wise work of a pass is split kL ways and the sums are not, so kL = 1
+// gives the fewest instructions per superblock (large appends) and kL = 2 or 4 the
+// shortest instruction stream per wave (appends with too few superblocks to fill the GPU).
+// Cross-lane work is limited to exact moves, max reductions and byte shuffles.
+template <int kL>
 __global__ __launch_bounds__(256) void q4k_append_kernel(AppendArgs a, int64_t units_per_tensor,
                                                          int nsb) {
+  constexpr int E = 32 / kL;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  int64_t unit = gid >> 3;
-  const int j = (int)(gid & 7);
+  int64_t unit = gid / (8 * kL);
+  const int r = (int)(gid & (8 * kL - 1));
+  const int j = r / kL, s = r & (kL - 1);
   const int64_t total = 2 * units_per_tensor;
   const bool active = unit < total;
   if (!active) unit = total - 1;  // compute redundantly, store nothing
@@ -122,14 +138,14 @@ __global__ __launch_bounds__(256) void q4k_append_kernel(AppendArgs a, int64_t u
   const int b = (int)(u % a.batch);
   const int64_t t = u / a.batch;
 
-  float x[32];
-  const int e0 = sb * 256 + 32 * j;
+  float x[E];
+  const int e0 = sb * 256 + 32 * j + s * E;
   const float *src = a.src[p];
-  if ((a.head_dim & 3) == 0 && e0 + 32 <= a.head_dim) {
+  if ((a.head_dim & 3) == 0 && e0 + E <= a.head_dim) {
     const float4 *s4 = reinterpret_cast<const float4 *>(
         src + (((int64_t)b * a.heads + h) * a.n + t) * a.head_dim + e0);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < E / 4; ++i) {
       float4 f = s4[i];
       x[4 * i] = f.x;
       x[4 * i + 1] = f.y;
@@ -138,17 +154,64 @@ __global__ __launch_bounds__(256) void q4k_append_kernel(AppendArgs a, int64_t u
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) x[i] = load_elem(src, a, t, b, h, e0 + i);
+    for (int i = 0; i < E; ++i) x[i] = load_elem(src, a, t, b, h, e0 + i);
   }
 
-  float scale, mins;
-  make_qkx1_quants_32(x, scale, mins);
+  // Sub-block min and max in f32::total_cmp order (exact integer keys)
+  int32_t kmin = total_key(x[0]), kmax = kmin;
+#pragma unroll
+  for (int i = 1; i < E; ++i) {
+    const int32_t k = total_key(x[i]);
+    kmin = k < kmin ? k : kmin;
+    kmax = k > kmax ? k : kmax;
+  }
+  kmin = group_allreduce<kL>(kmin, [](int32_t p, int32_t q) { return p < q ? p : q; });
+  kmax = group_allreduce<kL>(kmax, [](int32_t p, int32_t q) { return p > q ? p : q; });
+  const auto from_key = [](int32_t k) {
+    return u2f((uint32_t)(k ^ (int32_t)(((uint32_t)(k >> 31)) >> 1)));
+  };
+  const float mn = from_key(kmin), mx = from_key(kmax);
+
+  float scale = 0.0f, mins = 0.0f;
+  if (!(mx == mn)) {
+    float L[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) L[i] = 0.0f;
+    float min = fmin_rs(mn, 0.0f);
+    float iscale = 15.0f / (mx - min);
+    scale = 1.0f / iscale;
+    for (int it = 0; it < 5; ++it) {
+      float term[E];
+      float suml2 = 0.0f;
+      bool did_change = false;
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const float d = x[i] - min;
+        const float li = (float)q4_level_i(iscale * d);
+        did_change |= li != L[i];
+        L[i] = li;
+        term[i] = d * li;
+        suml2 = __builtin_fmaf(li, li, suml2);  // exact
+      }
+      suml2 = group_allreduce<kL>(suml2, [](float p, float q) { return p + q; });  // exact
+      const float sumlx = GroupChain<kL>::run(term, 0.0f);
+      scale = sumlx / suml2;
+#pragma unroll
+      for (int i = 0; i < E; ++i) term[i] = x[i] - scale * L[i];
+      const float sum = GroupChain<kL>::run(term, -0.0f);
+      min = sum / 32.0f;
+      if (min > 0.0f) min = 0.0f;
+      iscale = 1.0f / scale;
+      if (!group_any<kL>(did_change)) break;
+    }
+    mins = -min;
+  }
 
   float max_scale = scale, max_min = mins;
 #pragma unroll
-  for (int o = 1; o < 8; o <<= 1) {
-    max_scale = fmax_rs(max_scale, __shfl_xor(max_scale, o, 8));
-    max_min = fmax_rs(max_min, __shfl_xor(max_min, o, 8));
+  for (int o = kL; o < 8 * kL; o <<= 1) {
+    max_scale = fmax_rs(max_scale, __shfl_xor(max_scale, o, 8 * kL));
+    max_min = fmax_rs(max_min, __shfl_xor(max_min, o, 8 * kL));
   }
   max_scale = fmax_rs(max_scale, 0.0f);
   max_min = fmax_rs(max_min, 0.0f);
@@ -168,7 +231,10 @@ __global__ __launch_bounds__(256) void q4k_append_kernel(AppendArgs a, int64_t u
   // (v_rcp_f32 within 1 ulp), so rint(q) is its nearest integer unless q lies within
   // 2^-12 of a half-integer (a possible tie); those elements, and every element when
   // rcp(dd) is not finite, take the IEEE division.
-  uint32_t Lw[4] = {0u, 0u, 0u, 0u};
+  constexpr int NW = (E + 7) / 8;  // nibble words: element i at bits 4 (i % 8) of word i / 8
+  uint32_t Lw[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) Lw[w] = 0u;
   const float dd = f16_to_f32(dh) * (float)ls;
   if (dd != 0.0f) {
     const float dm = f16_to_f32(mh) * (float)lm;
@@ -176,7 +242,7 @@ __global__ __launch_bounds__(256) void q4k_append_kernel(AppendArgs a, int64_t u
     const bool exact_all = !(__builtin_fabsf(rdd) < 3.0e38f);
     uint32_t slow = 0u;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < E; ++i) {
       const float q = (x[i] + dm) * rdd;
       const float r = __builtin_rintf(q);
       const bool near_tie = __builtin_fabsf(q - r) > 0.5f - 0x1p-12f;
@@ -187,7 +253,7 @@ __global__ __launch_bounds__(256) void q4k_append_kernel(AppendArgs a, int64_t u
     }
     if (slow != 0u) {
 #pragma unroll
-      for (int i = 0; i < 32; ++i) {
+      for (int i = 0; i < E; ++i) {
         if (slow & (1u << i)) {
           const int32_t l = q4_level_i((x[i] + dm) / dd);
           Lw[i >> 3] = (Lw[i >> 3] & ~(15u << (4 * (i & 7)))) | ((uint32_t)l << (4 * (i & 7)));
@@ -196,11 +262,11 @@ __global__ __launch_bounds__(256) void q4k_append_kernel(AppendArgs a, int64_t u
     }
   }
 
-  // Header: d, dmin, and the 12 packed scale bytes, gathered from the 8 lanes.
+  // Header: d, dmin, and the 12 packed scale bytes, gathered from the 8 sub-blocks.
   uint32_t code = ls | (lm << 8);
   uint32_t codes[8];
 #pragma unroll
-  for (int jj = 0; jj < 8; ++jj) codes[jj] = __shfl(code, jj, 8);
+  for (int jj = 0; jj < 8; ++jj) codes[jj] = __shfl(code, jj * kL, 8 * kL);
   uint8_t sc[12];
 #pragma unroll
   for (int jj = 0; jj < 4; ++jj) {
@@ -211,30 +277,51 @@ __global__ __launch_bounds__(256) void q4k_append_kernel(AppendArgs a, int64_t u
     sc[jj + 8] = (uint8_t)((ls_hi & 0xF) | ((lm_hi & 0xF) << 4));
   }
 
-  // Nibbles: qs[32c + l] = L_{2c}[l] | L_{2c+1}[l] << 4. Lane j writes qs[16j, 16j+16).
+  // Nibbles: qs[32c + l] = L_{2c}[l] | L_{2c+1}[l] << 4. Lanes (2c, s) and (2c+1, s) own
+  // l in [sE, sE + E): the even lane writes the first E/2 bytes, the odd lane the rest,
+  // each taking the other half of its partner's nibbles (partner: lane ^ kL).
+  constexpr int H = E / 2;             // nibbles (= bytes written) per lane
+  constexpr int HW = (H + 7) / 8;      // words per half
   const bool odd = (j & 1) != 0;
-  uint32_t s0 = odd ? Lw[0] : Lw[2], s1 = odd ? Lw[1] : Lw[3];
-  uint32_t r0 = __shfl_xor(s0, 1, 8), r1 = __shfl_xor(s1, 1, 8);
-  uint32_t lo0 = odd ? r0 : Lw[0], lo1 = odd ? r1 : Lw[1];
-  uint32_t hi0 = odd ? Lw[2] : r0, hi1 = odd ? Lw[3] : r1;
-  uint32_t outw[4];
+  uint32_t lo[HW], hi[HW];
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const uint32_t lo = (w < 2) ? lo0 : lo1, hi = (w < 2) ? hi0 : hi1;
-    const int sh = (w & 1) * 16;
+  for (int w = 0; w < HW; ++w) {
+    uint32_t first, second;  // this lane's nibbles [0, H) and [H, E)
+    if constexpr (H >= 8) {
+      first = Lw[w];
+      second = Lw[HW + w];
+    } else {
+      first = Lw[0] & ((1u << (4 * H)) - 1u);
+      second = Lw[0] >> (4 * H);
+    }
+    const uint32_t recv = __shfl_xor(odd ? first : second, kL, 8 * kL);
+    lo[w] = odd ? recv : first;
+    hi[w] = odd ? second : recv;
+  }
+  constexpr int NB = H / 4;  // output words
+  uint32_t outw[NB];
+#pragma unroll
+  for (int w = 0; w < NB; ++w) {
+    const uint32_t l4 = lo[w / 2] >> (16 * (w & 1)), h4 = hi[w / 2] >> (16 * (w & 1));
     uint32_t v = 0;
 #pragma unroll
     for (int bb = 0; bb < 4; ++bb) {
-      uint32_t ln = (lo >> (sh + 4 * bb)) & 0xF, hn = (hi >> (sh + 4 * bb)) & 0xF;
+      const uint32_t ln = (l4 >> (4 * bb)) & 0xF, hn = (h4 >> (4 * bb)) & 0xF;
       v |= (ln | (hn << 4)) << (8 * bb);
     }
     outw[w] = v;
   }
   if (!active) return;
   uint8_t *blk = row_ptr(a, p, t, b, h) + (int64_t)sb * 144;
-  uint4 q4 = {outw[0], outw[1], outw[2], outw[3]};
-  *reinterpret_cast<uint4 *>(blk + 16 + 16 * j) = q4;
-  if (j == 0) {
+  uint8_t *qdst = blk + 16 + 32 * (j >> 1) + s * E + (odd ? H : 0);
+  if constexpr (NB == 4) {
+    *reinterpret_cast<uint4 *>(qdst) = uint4{outw[0], outw[1], outw[2], outw[3]};
+  } else if constexpr (NB == 2) {
+    *reinterpret_cast<uint2 *>(qdst) = uint2{outw[0], outw[1]};
+  } else {
+    *reinterpret_cast<uint32_t *>(qdst) = outw[0];
+  }
+  if (r == 0) {
     uint4 hd;
     hd.x = (uint32_t)dh | ((uint32_t)mh << 16);
     hd.y = (uint32_t)sc[0] | ((uint32_t)sc[1] << 8) | ((uint32_t)sc[2] << 16) | ((uint32_t)sc[3] << 24);
@@ -408,6 +495,10 @@ int launch_append_rows(int quant, const float *k, const float *v, uint8_t *kpool
   return launch_append_args(quant, a, s);
 }
 
+// Q4K superblocks (K and V) up to which the throughput kernel runs 4, then 2, lanes per
+// sub-block (1 above)
+constexpr int64_t kQ4kAppendLanes4Max = 2048, kQ4kAppendLanes2Max = 8192;
+
 static int launch_append_args(int quant, AppendArgs &a, hipStream_t s) {
   const int batch = a.batch, heads = a.heads;
   const int64_t n = a.n;
@@ -418,11 +509,19 @@ static int launch_append_args(int quant, AppendArgs &a, hipStream_t s) {
     hipLaunchKernelGGL(q4k_append_small_kernel, dim3((unsigned)(2 * rows * nsb)), dim3(256), 0,
                        s, a, nsb);
   } else if (quant == PKV_QUANT_Q4K) {
+    // 8 kL lanes per superblock: split each sub-block's fit over more lanes while the
+    // append has too few superblocks to give every SIMD a wave
     const int nsb = a.padded / 256;
     const int64_t units = rows * nsb;
-    const int64_t threads = 2 * units * 8;
-    hipLaunchKernelGGL(q4k_append_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                       s, a, units, nsb);
+    const int kl = 2 * units <= kQ4kAppendLanes4Max ? 4 : (2 * units <= kQ4kAppendLanes2Max ? 2 : 1);
+    const int64_t threads = 2 * units * 8 * kl;
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if (kl == 4)
+      hipLaunchKernelGGL(q4k_append_kernel<4>, grid, dim3(256), 0, s, a, units, nsb);
+    else if (kl == 2)
+      hipLaunchKernelGGL(q4k_append_kernel<2>, grid, dim3(256), 0, s, a, units, nsb);
+    else
+      hipLaunchKernelGGL(q4k_append_kernel<1>, grid, dim3(256), 0, s, a, units, nsb);
   } else if (quant == PKV_QUANT_Q8_0) {
     const int nblk = a.padded / 32;
     const int64_t units = rows * nblk;

@@ -100,6 +100,25 @@ def test_bulk_append_bitexact(pk, orc, quant):
     assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
 
 
+@pytest.mark.parametrize("D,n", [(256, 300), (320, 150), (256, 1500), (320, 700), (256, 2100),
+                                 (320, 1100)])
+def test_q4k_append_lane_splits_bitexact(pk, orc, D, n):
+    """The throughput kernel at each split of a sub-block's fit over lanes: K and V
+    superblocks 1200 (D 256) / 1200 (D 320, two superblocks per row, the second
+    zero-padded) run 4 lanes per sub-block, 6000 / 5600 run 2, 8400 / 8800 run 1."""
+    say(f"q4k lane-split append D={D} n={n}")
+    rng = np.random.default_rng(400 + D + n)
+    g = pk.PreallocatedQuantizedKvCache(1, 2, n + 8, D, pk.KvCacheQuantization.Q4K)
+    c = orc.Cache(Q4K, 1, 2, D, n + 8)
+    k = special_rows(rng, 2 * n, D).reshape(1, 2, n, D) * 3
+    v = special_rows(rng, 2 * n, D).reshape(1, 2, n, D)[:, :, ::-1].copy()
+    g.append_quantized(dev(k), dev(v))
+    assert c.append(k, v) == 0
+    gk, gv = g.raw_bytes()
+    ok, ov = c.valid_bytes()
+    assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
+
+
 def nonfinite_rows(rng, n_rows, d):
     """Random rows with NaN and infinities planted: one element, a whole 32-element
     sub-block, every fifth element, both signs."""
