@@ -71,6 +71,16 @@ def cpu_model() -> str:
         return "unknown"
 
 
+def append_roofline(kernel, bound, tokens, heads, us):
+    """Roofline entry of a quantize-append launch: f32 K and V in, packed Q4K rows out
+    (head_dim 256: 1024 B in and 144 B out per row and tensor)."""
+    nbytes = 2 * heads * tokens * (256 * 4 + Q4K_ROW)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"kernel": kernel, "bound": bound, "bytes_per_launch": nbytes,
+            "avg_launch_us": round(us, 2), "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def event_time(torch, fn, steps, warmup):
     """Milliseconds per call of fn: HIP events around `steps` calls after `warmup`."""
     for _ in range(warmup):
@@ -137,6 +147,9 @@ def run_config3(args):
         torch.cuda.synchronize()
         fill_s += time.perf_counter() - t0
         caches.append(c)
+    # the append alone, warm: the last layer's fill again at offset 0 (the same rows, so
+    # the cache is unchanged), HIP events around 5 calls
+    fill_ev_ms = event_time(torch, lambda: caches[-1].append_quantized(kbuf, vbuf, offset=0), 5, 2)
     del kbuf, vbuf
     q = torch.empty((L, 1, 1, W.NUM_HEADS, W.HEAD_DIM), dtype=torch.float32, device=dev)
     kn = torch.empty((L, 1, W.NUM_KV_HEADS, 1, W.HEAD_DIM), dtype=torch.float32, device=dev)
@@ -243,6 +256,9 @@ def run_config3(args):
             "traffic_source": MEASURED_TRAFFIC[3][1],
         },
         "append_tokens_per_s": round(L * S / fill_s, 1),
+        "append_roofline": append_roofline(
+            f"q4k_append_kernel<1> ({S}-token layer, one lane per sub-block fit)", "valu", S,
+            W.NUM_KV_HEADS, fill_ev_ms * 1000.0),
     }
     if args.prep:
         result["unprepared_us_per_step"] = round(
@@ -552,9 +568,13 @@ def run_config2(args):
         extra["prep_append_chunk_us"] = round(graph_time(
             torch, lambda: c.append_prep(qc, kcp, vcp, prep, offset=S), args.steps,
             args.warmup, reps) * 1000, 2)
-        extra["append_chunk_us"] = round(graph_time(
-            torch, lambda: c.append_quantized(kc, vc, offset=S), args.steps, args.warmup,
-            reps) * 1000, 2)
+    # 20 appends per graph replay: the 7 µs kernel, not the graph launch
+    app_ms = graph_time(torch, lambda: c.append_quantized(kc, vc, offset=S), args.steps,
+                        args.warmup, 20)
+    extra["append_chunk_us"] = round(app_ms * 1000, 2)
+    extra["append_roofline"] = append_roofline(
+        f"q4k_append_kernel<4> ({C}-token chunk, four lanes per sub-block fit)", "latency", C,
+        2, app_ms * 1000)
     if not args.no_cpu_baseline:
         extra["cpu_baseline"] = cpu_baseline_prefill(c, kc, vc, qc, k1, v1, q1, S, C,
                                                      args.cpu_threads)
@@ -620,6 +640,11 @@ def run_config4(args):
     ms_eager = event_time(torch, step, args.steps, args.warmup)
     ms_restore = graph_time(torch, restore, args.steps, args.warmup)
     ms = graph_time(torch, step, args.steps, args.warmup)
+
+    def suffix():
+        for l in full:
+            l.quantized_cache.append_quantized(ks, vs, offset=S)
+    ms_suffix = graph_time(torch, suffix, args.steps, args.warmup)
     full_bytes = len(full) * S * 2 * 2 * Q4K_ROW
     lin_bytes = (W.N_LAYERS - len(full)) * 4 * (W.DN_HEADS * W.DN_DK * W.DN_DV +
                                                 W.DN_CONV_DIM * (W.DN_CONV_K - 1) + W.DN_HEADS)
@@ -636,6 +661,11 @@ def run_config4(args):
                         "eager_restore_us": round(ms_restore_eager * 1000, 2),
                         "eager_restore_plus_suffix_us": round(ms_eager * 1000, 2),
                         "restored_bytes": full_bytes + lin_bytes,
+                        "suffix_appends_us": round(ms_suffix * 1000, 2),
+                        "append_roofline": append_roofline(
+                            f"q4k_append_kernel<2> ({SUF}-token suffix, one layer; two lanes "
+                            "per sub-block fit)", "latency", SUF, 2,
+                            ms_suffix * 1000 / len(full)),
                         "roofline": {"kernel": "copy_segments (restore)", "bound": "hbm",
                                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
