@@ -180,6 +180,10 @@ __global__ __launch_bounds__(256) void q4k_append_kernel(AppendArgs a, int64_t u
     float min = fmin_rs(mn, 0.0f);
     float iscale = 15.0f / (mx - min);
     scale = 1.0f / iscale;
+    // split fits unroll their passes (no level copies between passes); the one-lane fit
+    // stays rolled, unrolled it needs 130 VGPRs and loses a wave per SIMD
+    constexpr int kPassUnroll = kL > 1 ? 5 : 1;
+#pragma unroll kPassUnroll
     for (int it = 0; it < 5; ++it) {
       float term[E];
       float suml2 = 0.0f;
