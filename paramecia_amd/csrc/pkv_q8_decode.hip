@@ -10,8 +10,9 @@
 // Work split: a workgroup of 512 threads owns a contiguous key range of one segment
 // (one cache's batch row, or one sequence of a batched decode step) and both KV heads;
 // threads 0-255 take KV head 0, threads 256-511 head 1. The range streams through LDS
-// in chunks of 32 keys (K and V rows of both heads, 34.8 KB): QK with one thread per
-// (query head, key), an online softmax per query head over the chunk, then PV with one
+// in chunks of 32 keys (K and V rows of both heads, 34.8 KB; 16 keys up to 8192 cached
+// keys): QK with one or two threads per (query head, key), an online softmax per query
+// head over the chunk, then PV with one
 // thread per output element e for the group's 8 query heads. Each workgroup writes one
 // split-K partial in tile order; decode_combine_kernel merges them (and the new key of
 // a fused step). Dequantization is exact (int8 * d in f32, as the reference's to_float),
@@ -29,7 +30,7 @@ namespace pkv {
 namespace {
 
 constexpr int kQ8Row = 272;    // bytes of one head's row: 8 blocks x 34
-constexpr int kQ8Chunk = 32;   // keys per LDS chunk
+constexpr int kQ8Chunk = 32;   // keys per LDS chunk (16 for short caches)
 constexpr int kQ8Threads = 512;
 constexpr int kQ8RowWords = kQ8Row / 4;  // 68 dwords, 16-byte aligned rows (272 = 17 x 16)
 
@@ -49,12 +50,13 @@ struct Q8Args {
   int wps;
 };
 
+template <int kChunk>
 struct Q8Smem {
-  uint32_t k[2][kQ8Chunk][kQ8RowWords];  // [kv][key][dword]
-  uint32_t v[2][kQ8Chunk][kQ8RowWords];
+  uint32_t k[2][kChunk][kQ8RowWords];  // [kv][key][dword]
+  uint32_t v[2][kChunk][kQ8RowWords];
   float q[16][256];
-  float p[2][kQ8Chunk][8];  // weights [kv][key][head of the group]
-  float alpha[2][8];        // rescale of the running sums for this chunk
+  float p[2][kChunk][8];  // weights [kv][key][head of the group]
+  float alpha[2][8];      // rescale of the running sums for this chunk
 };
 
 // BlockQ8_0::from_float of one 256-element row by 256 threads (thread e owns element
@@ -86,8 +88,14 @@ __device__ __forceinline__ float h16(uint32_t w, int hi) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? (w >> 16) : (w & 0xFFFF)));
 }
 
+// kChunk keys per LDS chunk. 32: one QK thread per (query head, key) over all 256
+// dimensions. 16 (short caches, twice the workgroups): two threads per (query head, key),
+// each over four of the eight blocks, their sums added by a lane exchange; every
+// workgroup then does half the work of a 32-key one, so a launch with one chunk per
+// workgroup ends sooner.
+template <int kChunk>
 __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
-  __shared__ Q8Smem sm;
+  __shared__ Q8Smem<kChunk> sm;
   const int tid = threadIdx.x, half = tid >> 8, t = tid & 255;
   const int wg = blockIdx.x;
   int b = 0;
@@ -114,46 +122,55 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
     }
   }
 
-  // ---- q of the 16 heads into LDS
+  // ---- chunk staging: K and V rows of both heads, 2 x 2 x kChunk x 68 dwords, loaded
+  // into registers, then written to LDS
+  constexpr int kWords = 2 * kChunk * kQ8RowWords;  // per tensor
+  constexpr int kPer = (kWords + kQ8Threads - 1) / kQ8Threads;
+  uint32_t kv_[2][kPer];
+  const auto load_chunk = [&](int64_t c0, int nk) {
+#pragma unroll
+    for (int x = 0; x < kPer; ++x) {
+      const int i = tid + x * kQ8Threads;
+      const int kvh = i / (kChunk * kQ8RowWords), r = i % (kChunk * kQ8RowWords);
+      const int key = r / kQ8RowWords, w = r % kQ8RowWords;
+      const bool ok = i < kWords && key < nk;
+      const int64_t off = (c0 + (ok ? key : 0)) * a.rs_t + kvh * a.rs_h + 4 * w;
+      kv_[0][x] = ok ? *reinterpret_cast<const uint32_t *>(sg.k + off) : 0u;
+      kv_[1][x] = ok ? *reinterpret_cast<const uint32_t *>(sg.v + off) : 0u;
+    }
+  };
+  const auto chunk_keys = [&](int64_t c0) { return (int)(k1 - c0 < kChunk ? k1 - c0 : kChunk); };
+
+  // ---- q of the 16 heads into LDS; the first chunk's loads are issued behind q's, so
+  // that both are in flight together
   {
     const float4 *q4 = reinterpret_cast<const float4 *>(a.q + (int64_t)sg.qi * 16 * 256);
+    const float4 qa = q4[tid], qb = q4[tid + 512];
+    if (k0 < k1) load_chunk(k0, chunk_keys(k0));
     float4 *s4 = reinterpret_cast<float4 *>(&sm.q[0][0]);
-    s4[tid] = q4[tid];
-    s4[tid + 512] = q4[tid + 512];
+    s4[tid] = qa;
+    s4[tid + 512] = qb;
   }
 
-  // QK role: (head hh of the group, key kk of the chunk); PV role: element e = t
-  const int hh = t >> 5, kk = t & 31;
+  // QK role: (head hh of the group, key kk of the chunk[, block half dh]); PV role:
+  // element e = t
+  constexpr int kSplit = 32 / kChunk;  // threads per (head, key)
+  const int hh = t >> 5, kk = (t & 31) / kSplit, dh = t & (kSplit - 1);
   float m_run = -INFINITY, l_run = 0.0f;  // QK role: this thread's head
   float acc[8];
 #pragma unroll
   for (int h = 0; h < 8; ++h) acc[h] = 0.0f;
 
-  for (int64_t c0 = k0; c0 < k1; c0 += kQ8Chunk) {
-    const int nk = (int)(k1 - c0 < kQ8Chunk ? k1 - c0 : kQ8Chunk);
+  for (int64_t c0 = k0; c0 < k1; c0 += kChunk) {
+    const int nk = chunk_keys(c0);
     __syncthreads();  // the previous chunk's readers are done
-    // ---- stage the chunk: K and V rows of both heads, 2 x 2 x 32 x 68 dwords
-    {
-      constexpr int kWords = 2 * kQ8Chunk * kQ8RowWords;  // per tensor
-      constexpr int kPer = (kWords + kQ8Threads - 1) / kQ8Threads;
-      uint32_t kv_[2][kPer];
+    if (c0 != k0) load_chunk(c0, nk);
 #pragma unroll
-      for (int x = 0; x < kPer; ++x) {
-        const int i = tid + x * kQ8Threads;
-        const int kvh = i / (kQ8Chunk * kQ8RowWords), r = i % (kQ8Chunk * kQ8RowWords);
-        const int key = r / kQ8RowWords, w = r % kQ8RowWords;
-        const bool ok = i < kWords && key < nk;
-        const int64_t off = (c0 + (ok ? key : 0)) * a.rs_t + kvh * a.rs_h + 4 * w;
-        kv_[0][x] = ok ? *reinterpret_cast<const uint32_t *>(sg.k + off) : 0u;
-        kv_[1][x] = ok ? *reinterpret_cast<const uint32_t *>(sg.v + off) : 0u;
-      }
-#pragma unroll
-      for (int x = 0; x < kPer; ++x) {
-        const int i = tid + x * kQ8Threads;
-        if (i < kWords) {
-          (&sm.k[0][0][0])[i] = kv_[0][x];
-          (&sm.v[0][0][0])[i] = kv_[1][x];
-        }
+    for (int x = 0; x < kPer; ++x) {
+      const int i = tid + x * kQ8Threads;
+      if (i < kWords) {
+        (&sm.k[0][0][0])[i] = kv_[0][x];
+        (&sm.v[0][0][0])[i] = kv_[1][x];
       }
     }
     __syncthreads();
@@ -164,8 +181,9 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
       const float *qh = sm.q[8 * half + hh];
       float s = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int jj = 0; jj < 8 / kSplit; ++jj) {
         // block j: bytes 34 j .. 34 j + 33 of the row (d, then 32 int8)
+        const int j = jj + dh * (8 / kSplit);
         const int o = 34 * j;
         const float d = h16(krow[o >> 2], (o >> 1) & 1);
         float part = 0.0f;
@@ -177,22 +195,25 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
         }
         s += part * d;
       }
+      if constexpr (kSplit == 2) s += __shfl_xor(s, 1, 32);  // blocks 0-3 + blocks 4-7
       // log2 units, clamped at +-100 nats; keys past the chunk are masked
       float s2 = fminf(fmaxf(s * a.sl2, -kSplitClampL2), kSplitClampL2);
       if (kk >= nk) s2 = -INFINITY;
       float mc = s2;
 #pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) mc = fmaxf(mc, __shfl_xor(mc, o, 32));
+      for (int o = 16; o >= kSplit; o >>= 1) mc = fmaxf(mc, __shfl_xor(mc, o, 32));
       const float m_new = fmaxf(m_run, mc);
       const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
       const float p = (s2 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s2 - m_new);
       float ps = p;
 #pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) ps += __shfl_xor(ps, o, 32);
+      for (int o = 16; o >= kSplit; o >>= 1) ps += __shfl_xor(ps, o, 32);
       l_run = l_run * alpha + ps;
       m_run = m_new;
-      sm.p[half][kk][hh] = p;
-      if (kk == 0) sm.alpha[half][hh] = alpha;
+      if (dh == 0) {
+        sm.p[half][kk][hh] = p;
+        if (kk == 0) sm.alpha[half][hh] = alpha;
+      }
     }
     __syncthreads();
 
@@ -225,7 +246,7 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
   const int idx = tile_index(t);
 #pragma unroll
   for (int h = 0; h < 8; ++h) P[(8 * half + h) * kPartRow + idx] = acc[h];
-  if (kk == 0) a.ml[(int64_t)wg * 16 + 8 * half + hh] = float2{m_run, l_run};
+  if (kk == 0 && dh == 0) a.ml[(int64_t)wg * 16 + 8 * half + hh] = float2{m_run, l_run};
 }
 
 }  // namespace
@@ -248,11 +269,13 @@ static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, cons
   }
   d.dseg = nullptr;
   d.wps = 0;
-  // keys per workgroup: one 32-key chunk while that keeps <= 512 partials per
-  // segment, more chunks per workgroup for longer caches
+  // keys per workgroup: one chunk while that keeps <= 512 partials per segment (16-key
+  // chunks up to 8192 keys, 32-key chunks beyond), more chunks per workgroup for longer
+  // caches
   int64_t kpw = (longest + 511) / 512;
-  kpw = (kpw + kQ8Chunk - 1) / kQ8Chunk * kQ8Chunk;
-  if (kpw < kQ8Chunk) kpw = kQ8Chunk;
+  const int chunk = kpw <= 16 ? 16 : kQ8Chunk;
+  kpw = (kpw + chunk - 1) / chunk * chunk;
+  if (kpw < chunk) kpw = chunk;
   CombineArgs c;
   int wg = 0;
   for (int i = 0; i < n; ++i) {
@@ -278,7 +301,11 @@ static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, cons
   d.part = static_cast<float *>(ws.ptr);
   d.ml = reinterpret_cast<float2 *>(d.part + part_floats);
   d.dq = d.part + part_floats + ml_floats;
-  hipLaunchKernelGGL(q8_decode_kernel, dim3((unsigned)wg), dim3(kQ8Threads), 0, s, d);
+  if (chunk == 16)
+    hipLaunchKernelGGL(q8_decode_kernel<16>, dim3((unsigned)wg), dim3(kQ8Threads), 0, s, d);
+  else
+    hipLaunchKernelGGL(q8_decode_kernel<kQ8Chunk>, dim3((unsigned)wg), dim3(kQ8Threads), 0, s,
+                       d);
   PKV_HIP(hipGetLastError());
   c.part = d.part;
   c.ml = d.ml;
@@ -364,7 +391,8 @@ int launch_paged_decode_q8(const PagedSeg *segs, int nseg, int nseq, int page_to
     PKV_HIP(hipMemcpyAsync(dtab, stage, tab_bytes, hipMemcpyHostToDevice, s));
     d.dseg = dtab;
   }
-  hipLaunchKernelGGL(q8_decode_kernel, dim3((unsigned)nwg), dim3(kQ8Threads), 0, s, d);
+  hipLaunchKernelGGL(q8_decode_kernel<kQ8Chunk>, dim3((unsigned)nwg), dim3(kQ8Threads), 0, s,
+                     d);
   PKV_HIP(hipGetLastError());
   c.part = d.part;
   c.ml = d.ml;

@@ -251,7 +251,8 @@ def run_decode_q8(pk, orc, S, B=1, fused=True, seed=0, chans=None):
     return np.abs(got - ref).max()
 
 
-@pytest.mark.parametrize("S", [0, 1, 31, 32, 33, 511, 512, 513, 4096, 20000])
+@pytest.mark.parametrize("S", [0, 1, 15, 16, 17, 31, 32, 33, 511, 512, 513, 4096, 8192, 8193,
+                               20000])
 def test_q8_decode_fused(pk, orc, S):
     say(f"Q8_0 fused decode S={S}")
     run_decode_q8(pk, orc, S, fused=True, seed=300 + S)
