@@ -51,7 +51,7 @@ struct Q8Args {
 };
 
 template <int kChunk>
-struct Q8Smem {
+struct alignas(16) Q8Smem {
   uint32_t k[2][kChunk][kQ8RowWords];  // [kv][key][dword]
   uint32_t v[2][kChunk][kQ8RowWords];
   float q[16][256];
@@ -177,21 +177,31 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
 
     // ---- QK: score of (head 8 half + hh, key kk) = sum_j d_j sum_i q8 * q
     {
-      const uint32_t *krow = sm.k[half][kk];
-      const float *qh = sm.q[8 * half + hh];
+      // this thread's blocks start dh * 8 / kSplit blocks (34 dwords per 4 blocks) into
+      // the row, so every byte position below is a compile-time constant
+      constexpr int kBlk = 8 / kSplit;
+      const uint32_t *krow = sm.k[half][kk] + dh * (34 * kBlk / 4);
+      const float4 *qh4 = reinterpret_cast<const float4 *>(sm.q[8 * half + hh] + 32 * kBlk * dh);
       float s = 0.0f;
 #pragma unroll
-      for (int jj = 0; jj < 8 / kSplit; ++jj) {
-        // block j: bytes 34 j .. 34 j + 33 of the row (d, then 32 int8)
-        const int j = jj + dh * (8 / kSplit);
-        const int o = 34 * j;
-        const float d = h16(krow[o >> 2], (o >> 1) & 1);
+      for (int jj = 0; jj < kBlk; ++jj) {
+        // block: bytes o .. o + 33 past krow (f16 d, then 32 int8), within dwords o/4 .. o/4 + 8
+        const int o = 34 * jj;
+        uint32_t w[9];
+#pragma unroll
+        for (int x = 0; x < 9; ++x) w[x] = krow[(o >> 2) + x];
+        const float d = h16(w[0], (o >> 1) & 1);
         float part = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          const int ob = o + 2 + i;
-          const int8_t qb = (int8_t)(krow[ob >> 2] >> (8 * (ob & 3)));
-          part += (float)qb * qh[32 * j + i];
+        for (int i4 = 0; i4 < 8; ++i4) {
+          const float4 qv = qh4[8 * jj + i4];
+          const float qc[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int pos = (o & 3) + 2 + 4 * i4 + c;
+            const int8_t qb = (int8_t)(w[pos >> 2] >> (8 * (pos & 3)));
+            part += (float)qb * qc[c];
+          }
         }
         s += part * d;
       }
@@ -222,10 +232,11 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
       const int e = t, j = e >> 5, ob = 34 * j + 2 + (e & 31);
 #pragma unroll
       for (int h = 0; h < 8; ++h) acc[h] *= sm.alpha[half][h];
-      for (int key = 0; key < nk; ++key) {
+      const int wd = (34 * j) >> 2, hd = ((34 * j) >> 1) & 1, wq = ob >> 2, sq = 8 * (ob & 3);
+      const auto pv_key = [&](int key) {
         const uint32_t *vrow = sm.v[half][key];
-        const float d = h16(vrow[(34 * j) >> 2], ((34 * j) >> 1) & 1);
-        const int8_t qb = (int8_t)(vrow[ob >> 2] >> (8 * (ob & 3)));
+        const float d = h16(vrow[wd], hd);
+        const int8_t qb = (int8_t)(vrow[wq] >> sq);
         const float vv = (float)qb * d;
         const float4 p0 = *reinterpret_cast<const float4 *>(&sm.p[half][key][0]);
         const float4 p1 = *reinterpret_cast<const float4 *>(&sm.p[half][key][4]);
@@ -237,6 +248,12 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
         acc[5] += p1.y * vv;
         acc[6] += p1.z * vv;
         acc[7] += p1.w * vv;
+      };
+      if (nk == kChunk) {  // a full chunk: unrolled, its LDS reads issued ahead
+#pragma unroll
+        for (int key = 0; key < kChunk; ++key) pv_key(key);
+      } else {
+        for (int key = 0; key < nk; ++key) pv_key(key);
       }
     }
   }
