@@ -78,15 +78,19 @@ __device__ __forceinline__ float wave64_sum(float x) {
   return x;
 }
 
-// 6-bit scale and min codes of sub-block j from the 12 header bytes (get_scale_min_k4)
-__device__ __forceinline__ void q4k_scale_min(const uint8_t *s, int j, float &sc, float &m) {
-  if (j < 4) {
-    sc = (float)(s[j] & 63);
-    m = (float)(s[j + 4] & 63);
-  } else {
-    sc = (float)((s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4));
-    m = (float)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
-  }
+// 6-bit scale and min codes of sub-block j (get_scale_min_k4) from the 12 header bytes
+// held as three little-endian words (header byte i is byte i & 3 of word i >> 2). j may
+// differ between lanes: a shift by 8 (j & 3) reads bytes j & 3, 4 + (j & 3) and
+// 8 + (j & 3), where an indexed byte array would lower to compare-and-select chains.
+__device__ __forceinline__ void q4k_scale_min(uint32_t w0, uint32_t w1, uint32_t w2, int j,
+                                              float &sc, float &m) {
+  const int sh = 8 * (j & 3);
+  const uint32_t b0 = w0 >> sh, b1 = w1 >> sh, b2 = w2 >> sh;
+  const uint32_t lo_s = b0 & 63, lo_m = b1 & 63;
+  const uint32_t hi_s = (b2 & 0xF) | (((b0 >> 6) & 3) << 4);
+  const uint32_t hi_m = ((b2 >> 4) & 0xF) | (((b1 >> 6) & 3) << 4);
+  sc = (float)(j < 4 ? lo_s : hi_s);
+  m = (float)(j < 4 ? lo_m : hi_m);
 }
 
 // sigmoid(g) through v_exp_f32 and v_rcp_f32 (about 1 ulp each; the projection's
@@ -209,14 +213,10 @@ __global__ __launch_bounds__(256) void oproj_k45_kernel(OprojArgs a) {
         }
         // the chunk's two sub-blocks: (d * sc, dmin * m) from the superblock header
         const uint4 hd = hdr[r][ch];
-        uint8_t sbytes[12];
-        const uint32_t hw[3] = {hd.y, hd.z, hd.w};
-#pragma unroll
-        for (int i = 0; i < 12; ++i) sbytes[i] = (uint8_t)(hw[i >> 2] >> (8 * (i & 3)));
         const float d = f16_to_f32((uint16_t)(hd.x & 0xFFFF)), dmin = f16_to_f32((uint16_t)(hd.x >> 16));
         float sc0, m0, sc1, m1;
-        q4k_scale_min(sbytes, 2 * cc, sc0, m0);
-        q4k_scale_min(sbytes, 2 * cc + 1, sc1, m1);
+        q4k_scale_min(hd.y, hd.z, hd.w, 2 * cc, sc0, m0);
+        q4k_scale_min(hd.y, hd.z, hd.w, 2 * cc + 1, sc1, m1);
         acc[r] += (d * sc0) * (pl[0] + pl[1]) - (dmin * m0) * sl + (d * sc1) * (ph[0] + ph[1]) -
                   (dmin * m1) * sh;
       }
