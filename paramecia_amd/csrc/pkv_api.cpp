@@ -33,15 +33,37 @@ int Workspace::reserve(size_t need) {
                                       " bytes of scratch; the no-alloc scratch holds " +
                                       std::to_string(bytes));
   size_t grow = need + need / 4 + 4096;
-  if (ptr) {
-    // A kernel may still read the old buffer; growth is rare, so wait for the device.
-    PKV_HIP(hipDeviceSynchronize());
-    PKV_HIP(hipFree(ptr));
-    ptr = nullptr;
-    bytes = 0;
-  }
-  PKV_HIP(hipMalloc(&ptr, grow));
+  void *fresh = nullptr;
+  PKV_HIP(hipMalloc(&fresh, grow));
+  // queued kernels and captured graphs may still use the old buffer: retire it
+  if (ptr) retired.push_back(ptr);
+  ptr = fresh;
   bytes = grow;
+  return PKV_OK;
+}
+
+int Workspace::reserve_flags(hipStream_t s) {
+  if (flags) return PKV_OK;
+  if (fixed) return set_error(PKV_ERR_ARG, "no arrival flags in a no-alloc call");
+  void *f = nullptr;
+  PKV_HIP(hipMalloc(&f, (size_t)kFlagRows * kFlagCols * sizeof(uint32_t)));
+  const int rc = launch_zero_words(static_cast<uint32_t *>(f), (size_t)kFlagRows * kFlagCols, s);
+  if (rc) {
+    (void)hipFree(f);
+    return rc;
+  }
+  flags = static_cast<uint32_t *>(f);
+  return PKV_OK;
+}
+
+int refuse_under_capture(hipStream_t s, const char *what) {
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  PKV_HIP(hipStreamIsCapturing(s, &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return set_error(PKV_ERR_UNSUPPORTED,
+                     std::string(what) +
+                         " allocates or clears device memory, which a captured HIP graph "
+                         "cannot replay: call it before capturing");
   return PKV_OK;
 }
 
@@ -70,9 +92,11 @@ int Workspace::mark_host_used(hipStream_t s) {
 Workspace::~Workspace() {
   if (fixed) return;
   if (host_pending) (void)hipEventSynchronize(host_ev);
-  if (ptr) {
+  if (ptr || flags || !retired.empty()) {
     (void)hipDeviceSynchronize();
-    (void)hipFree(ptr);
+    if (ptr) (void)hipFree(ptr);
+    if (flags) (void)hipFree(flags);
+    for (void *r : retired) (void)hipFree(r);
   }
   if (host) (void)hipHostFree(host);
   if (host_ev) (void)hipEventDestroy(host_ev);
@@ -221,6 +245,7 @@ int pkv_create(int quant, int batch, int n_kv_heads, int head_dim, int64_t max_s
     return set_error(PKV_ERR_ARG, "unknown quantization");
   if (batch <= 0 || n_kv_heads <= 0 || head_dim <= 0 || max_seq_len < 0)
     return set_error(PKV_ERR_ARG, "batch, n_kv_heads, head_dim must be > 0, max_seq_len >= 0");
+  if (int rc = refuse_under_capture(static_cast<hipStream_t>(stream), "pkv_create")) return rc;
   pkv_cache *h = new pkv_cache();
   h->quant = quant;
   h->batch = batch;
@@ -308,6 +333,7 @@ int pkv_resize_batch(pkv_cache *h, int batch) {
   if (!h) return set_error(PKV_ERR_ARG, "null handle");
   if (batch <= 0) return set_error(PKV_ERR_ARG, "batch must be > 0");
   if (batch == h->batch) return PKV_OK;
+  if (int rc = refuse_under_capture(h->stream, "pkv_resize_batch")) return rc;
   const size_t total = (size_t)batch * h->n_kv_heads * (size_t)h->max_seq_len * h->bpr;
   const size_t alloc = total ? total : 256;
   uint8_t *k = nullptr, *v = nullptr;
@@ -330,7 +356,42 @@ int pkv_resize_batch(pkv_cache *h, int batch) {
   return PKV_OK;
 }
 
-// FullAttention offset rule (qwen3_next.rs:2430-2440) then the overflow rule (:435-441).
+// F16/BF16 caches grow instead of overflowing: the reference's float path concatenates
+// every append onto the cached rows (Tensor::cat) and sets max_seq_len to the new length
+// (qwen3_next.rs:2492-2516), so it has no capacity limit. Here the buffers are
+// reallocated to max(need, 2 x capacity) tokens (amortised O(1) per token), rows
+// [0, seq_len) copied on the handle's stream and the tail zeroed; the old buffers are
+// freed once the stream has passed the copy. Not under graph capture (it allocates).
+static int grow_float_cache(pkv_cache *h, int64_t need) {
+  if (int rc = refuse_under_capture(h->stream, "growing an F16/BF16 cache past its capacity"))
+    return rc;
+  int64_t cap = h->max_seq_len * 2;
+  if (cap < need) cap = need;
+  const size_t row = (size_t)h->batch * h->n_kv_heads * h->bpr;  // one token's rows
+  const size_t alloc = (size_t)cap * row, keep = (size_t)h->seq_len * row;
+  uint8_t *k = nullptr, *v = nullptr;
+  hipError_t e = hipMalloc(&k, alloc ? alloc : 256);
+  if (e == hipSuccess) e = hipMalloc(&v, alloc ? alloc : 256);
+  if (e == hipSuccess && keep) e = hipMemcpyAsync(k, h->k, keep, hipMemcpyDeviceToDevice, h->stream);
+  if (e == hipSuccess && keep) e = hipMemcpyAsync(v, h->v, keep, hipMemcpyDeviceToDevice, h->stream);
+  if (e == hipSuccess && alloc > keep) e = hipMemsetAsync(k + keep, 0, alloc - keep, h->stream);
+  if (e == hipSuccess && alloc > keep) e = hipMemsetAsync(v + keep, 0, alloc - keep, h->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
+  if (e != hipSuccess) {
+    if (k) (void)hipFree(k);
+    if (v) (void)hipFree(v);
+    return hip_error(e, "growing an F16/BF16 cache");
+  }
+  (void)hipFree(h->k);
+  (void)hipFree(h->v);
+  h->k = k;
+  h->v = v;
+  h->max_seq_len = cap;
+  return PKV_OK;
+}
+
+// FullAttention offset rule (qwen3_next.rs:2430-2440) then the overflow rule (:435-441);
+// F16/BF16 caches grow instead (grow_float_cache).
 static int position_for_append(pkv_cache *h, int64_t n, int64_t offset) {
   if (n < 0) return set_error(PKV_ERR_ARG, "n must be >= 0");
   if (offset >= 0 && offset != h->seq_len) {
@@ -341,6 +402,8 @@ static int position_for_append(pkv_cache *h, int64_t n, int64_t offset) {
                                            std::to_string(offset) + " but cache has " +
                                            std::to_string(h->seq_len) + " tokens");
   }
+  if (h->seq_len + n > h->max_seq_len && !pkv_quant_is_ggml(h->quant))
+    return grow_float_cache(h, h->seq_len + n);
   if (h->seq_len + n > h->max_seq_len)
     return set_error(PKV_ERR_OVERFLOW, "Quantized KV cache overflow: trying to store " +
                                            std::to_string(h->seq_len + n) +
@@ -728,6 +791,7 @@ int pkv_prefix_linear_sizes(const pkv_prefix *p, int layer, size_t *n_ssm, size_
 int pkv_prefix_save_full(pkv_prefix *p, int layer, const pkv_cache *h) {
   if (!p || !h || layer < 0 || layer >= (int)p->entries.size())
     return set_error(PKV_ERR_ARG, "bad argument");
+  if (int rc = refuse_under_capture(h->stream, "pkv_prefix_save_full")) return rc;
   Entry &e = p->entries[(size_t)layer];
   e.release();
   if (h->seq_len == 0) return PKV_OK;  // PrefixCacheEntry::Empty
@@ -761,6 +825,7 @@ int pkv_prefix_save_linear(pkv_prefix *p, int layer, const float *ssm, size_t n_
   if (!p || layer < 0 || layer >= (int)p->entries.size() || !ssm || !conv)
     return set_error(PKV_ERR_ARG, "bad argument");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (int rc = refuse_under_capture(s, "pkv_prefix_save_linear")) return rc;
   Entry &e = p->entries[(size_t)layer];
   e.release();
   hipError_t er = hipMalloc(&e.ssm, (n_ssm ? n_ssm : 1) * 4);

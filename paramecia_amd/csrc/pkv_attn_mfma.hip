@@ -123,6 +123,9 @@ int launch_paged_decode_q4k(const PagedSeqDesc *seqs, int nseq, const PagedPoolD
   d.k_new = k_new;
   d.v_new = v_new;
   d.nnew = fused ? nseq : 0;
+  d.ncomb = 0;  // several output rows: the separate combine kernel
+  d.flags = nullptr;
+  d.out = out;
   d.prep = DecodePrep{};
   d.q_out = nullptr;
   d.kplane = pool.k;

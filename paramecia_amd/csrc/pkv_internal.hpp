@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <vector>
 
 #include "../../include/pkv.h"
 
@@ -44,25 +45,40 @@ inline size_t row_bytes(int quant, int head_dim) {
 constexpr unsigned kStatusBarrierTimeout = 1u;  // the fused quantizer's barrier of waves 0-3
 int device_status_word(unsigned **out);
 
+// PKV_ERR_UNSUPPORTED when `s` is capturing a HIP graph: for calls that allocate device
+// memory or clear it with hipMemsetAsync, neither of which a replay can repeat.
+int refuse_under_capture(hipStream_t s, const char *what);
+
 // Byte addressing of packed rows: row(b, t, h) = base + b*sb + t*st + h*sh.
 struct RowStrides {
   int64_t b, t, h;
 };
 
 // Split-K scratch owned by a cache handle or by a stateless call.
-// Device scratch grows (hipMalloc) on demand, never inside a kernel. The pinned host
-// buffer stages small descriptor tables; an event guards its reuse.
-// A fixed workspace (fixed = true) wraps caller-provided device memory: reserve() never
-// allocates and refuses a need beyond `bytes` (PKV_ERR_ARG); nothing is freed.
+// Device scratch grows (hipMalloc) on demand, never inside a kernel. A buffer it grows
+// out of is retired, not freed: a HIP graph captured earlier keeps its address in its
+// kernel arguments and writes there on every replay, so retired buffers live until the
+// workspace is destroyed (growth is geometric: they add up to less than 4x the last
+// size). The pinned host buffer stages small descriptor tables; an event guards its
+// reuse. A fixed workspace (fixed = true) wraps caller-provided device memory: reserve()
+// never allocates and refuses a need beyond `bytes` (PKV_ERR_ARG); nothing is freed.
 struct Workspace {
   void *ptr = nullptr;
   size_t bytes = 0;
   bool fixed = false;
+  std::vector<void *> retired;
   void *host = nullptr;
   size_t host_bytes = 0;
   hipEvent_t host_ev = nullptr;
   bool host_pending = false;
+  // Arrival flags of a fused decode launch: kFlagRows x kFlagCols words, zeroed by a
+  // kernel on the stream when first allocated, and left zeroed by every launch that uses
+  // them (its combiners reset the words they consumed). Separate from `ptr`, which other
+  // calls on the same workspace reuse for partials.
+  static constexpr int kFlagRows = 128, kFlagCols = 256;
+  uint32_t *flags = nullptr;
   int reserve(size_t need);
+  int reserve_flags(hipStream_t s);  // allocates and zeroes `flags` once
   int reserve_host(size_t need);   // waits for the previous staged copy first
   int mark_host_used(hipStream_t s);
   ~Workspace();
@@ -218,6 +234,8 @@ int launch_scale_channels(float *x, size_t rows, int dim, const int *ch, int n_c
                           float factor, hipStream_t s);
 int launch_copy_segments(void *const *dst, const void *const *src, const size_t *bytes, int n,
                          Workspace &ws, hipStream_t s);
+// n words of dst set to zero by a kernel (capturable, unlike hipMemsetAsync).
+int launch_zero_words(uint32_t *dst, size_t n, hipStream_t s);
 int launch_oproj(const float *attn, const float *gate, const uint8_t *w, int w_type, float *out,
                  int batch, int in_dim, int out_dim, hipStream_t s);
 // ---- launcher (pkv_oproj_mfma.hip): the batched form, Q4K/Q5K/Q6K ----

@@ -167,40 +167,106 @@ int gather_rows(const pkv_seq *s, uint8_t **kc, uint8_t **vc) {
                               p->stream);
 }
 
-// Pages for n more tokens of s: a shared, partly filled last page is first copied into a
-// page of s's own, then fresh pages follow. PKV_ERR_OVERFLOW, with nothing changed, when
-// the pool lacks them (`reserved`: pages already promised to other sequences of the call).
-int make_room(pkv_seq *s, int64_t n, size_t *reserved) {
-  pkv_pool *p = s->pool;
+// What n more tokens of s need: `cow` when the page holding token len is shared and
+// partly filled (its rows are first copied into a page of s's own), `fresh` pages taken
+// from the pool in all (the copy's page included). Safe for any page list length.
+struct RoomPlan {
+  bool cow;
+  size_t fresh;
+};
+RoomPlan plan_room(const pkv_seq *s, int64_t n) {
+  const pkv_pool *p = s->pool;
   const size_t have = s->pages.size(), need = pages_for(p, s->len + n);
-  const bool cow = (s->len & (p->page_tokens - 1)) != 0 && p->refs[(size_t)s->pages.back()] > 1;
-  const size_t fresh = need - have + (cow ? 1 : 0);
+  const size_t cur = (size_t)(s->len >> p->page_lg);  // the page that holds token len
+  const bool cow = n > 0 && (s->len & (p->page_tokens - 1)) != 0 && cur < have &&
+                   p->refs[(size_t)s->pages[cur]] > 1;
+  return RoomPlan{cow, (need > have ? need - have : 0) + (cow ? 1 : 0)};
+}
+
+// A page list that changes (a copy on write, new pages) or that the device copy does not
+// yet hold must be copied to the device from pinned memory (sync_pages), which a HIP graph
+// cannot replay: refused under capture, before anything changes.
+int capture_guard(const pkv_seq *s, int64_t n) {
+  if (!s->d_stale && plan_room(s, n).fresh == 0) return PKV_OK;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  PKV_HIP(hipStreamIsCapturing(s->pool->stream, &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return set_error(PKV_ERR_UNSUPPORTED,
+                     "a paged sequence whose page list changes cannot be captured in a graph");
+  return PKV_OK;
+}
+
+// The state make_room changed, to put back when a later step of the same call fails.
+struct RoomUndo {
+  size_t size = 0;      // page list length before
+  size_t cow_idx = 0;   // the copied page's index
+  int32_t cow_old = -1; // the shared page it replaced (-1: no copy on write)
+  int32_t cow_new = -1;
+};
+
+// Pages for n more tokens of s: a shared, partly filled page is first copied into a page
+// of s's own, then fresh pages follow. PKV_ERR_OVERFLOW, with nothing changed, when the
+// pool lacks them (`reserved`: pages already promised to other sequences of the call; a
+// non-null `reserved` only counts). `undo` (optional) records the change for undo_room.
+int make_room(pkv_seq *s, int64_t n, size_t *reserved, RoomUndo *undo = nullptr) {
+  pkv_pool *p = s->pool;
+  const RoomPlan plan = plan_room(s, n);
+  const size_t need = pages_for(p, s->len + n);
   const size_t avail = p->free_list.size() - (reserved ? *reserved : 0);
-  if (fresh > avail)
-    return set_error(PKV_ERR_OVERFLOW, "Paged KV pool overflow: " + std::to_string(fresh) +
+  if (plan.fresh > avail)
+    return set_error(PKV_ERR_OVERFLOW, "Paged KV pool overflow: " + std::to_string(plan.fresh) +
                                            " more pages needed, " + std::to_string(avail) +
                                            " free");
   if (reserved) {  // a dry run: count only
-    *reserved += fresh;
+    *reserved += plan.fresh;
     return PKV_OK;
   }
-  if (cow) {
-    // the shared, partly filled last page: its rows into a page of this sequence's own
-    const int32_t old = s->pages.back(), mine = take_page(p);
+  if (undo) *undo = RoomUndo{s->pages.size(), 0, -1, -1};
+  if (plan.cow) {
+    // the shared, partly filled page: its rows into a page of this sequence's own
+    const size_t idx = (size_t)(s->len >> p->page_lg);
+    const int32_t old = s->pages[idx], mine = take_page(p);
     const size_t bytes = (size_t)(s->len & (p->page_tokens - 1)) * p->n_kv_heads * p->bpr;
-    PKV_HIP(hipMemcpyAsync(page_k(p, mine), page_k(p, old), bytes, hipMemcpyDeviceToDevice,
-                           p->stream));
-    PKV_HIP(hipMemcpyAsync(page_v(p, mine), page_v(p, old), bytes, hipMemcpyDeviceToDevice,
-                           p->stream));
+    hipError_t e = hipMemcpyAsync(page_k(p, mine), page_k(p, old), bytes,
+                                  hipMemcpyDeviceToDevice, p->stream);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(page_v(p, mine), page_v(p, old), bytes, hipMemcpyDeviceToDevice,
+                         p->stream);
+    if (e != hipSuccess) {
+      release_page(p, mine);
+      return hip_error(e, "copy on write of a shared page");
+    }
     release_page(p, old);
-    s->pages.back() = mine;
+    s->pages[idx] = mine;
     s->d_stale = true;
+    if (undo) {
+      undo->cow_idx = idx;
+      undo->cow_old = old;
+      undo->cow_new = mine;
+    }
   }
   while (s->pages.size() < need) {
     s->pages.push_back(take_page(p));
     s->d_stale = true;
   }
   return PKV_OK;
+}
+
+// Put s's page list back as it was before make_room (a later step of the call failed):
+// the pages it took return to the pool and a copied page gives way to the shared one
+// again. The device copy of the list may already hold the new one: it is marked stale.
+void undo_room(pkv_seq *s, const RoomUndo &u) {
+  pkv_pool *p = s->pool;
+  while (s->pages.size() > u.size) {
+    release_page(p, s->pages.back());
+    s->pages.pop_back();
+  }
+  if (u.cow_new >= 0) {
+    ++p->refs[(size_t)u.cow_old];
+    s->pages[u.cow_idx] = u.cow_old;
+    release_page(p, u.cow_new);
+  }
+  s->d_stale = true;
 }
 
 bool fast_decode_shape(const pkv_pool *p, int num_heads) {
@@ -267,6 +333,8 @@ int pkv_pool_create(int quant, int n_kv_heads, int head_dim, int page_tokens, in
     return set_error(PKV_ERR_ARG, "n_kv_heads, head_dim and n_pages must be > 0");
   if (page_tokens < 32 || page_tokens > (1 << 20) || (page_tokens & (page_tokens - 1)) != 0)
     return set_error(PKV_ERR_ARG, "page_tokens must be a power of two in [32, 2^20]");
+  if (int rc = refuse_under_capture(static_cast<hipStream_t>(stream), "pkv_pool_create"))
+    return rc;
   pkv_pool *p = new pkv_pool();
   p->quant = quant;
   p->n_kv_heads = n_kv_heads;
@@ -407,14 +475,20 @@ int pkv_seq_append(pkv_seq *s, const float *k, const float *v, int64_t n, int64_
     pkv_seq_truncate(s, offset);
   }
   if (n == 0) return PKV_OK;
-  int rc = make_room(s, n, nullptr);
+  int rc = capture_guard(s, n);
+  if (rc) return rc;
+  RoomUndo undo;
+  rc = make_room(s, n, nullptr, &undo);
   if (rc) return rc;
   rc = sync_pages(s);
-  if (rc) return rc;
-  rc = launch_append_paged(p->quant, k, v, p->k, p->v, s->d_pages, p->page_lg,
-                           (int64_t)p->page_bytes, p->n_kv_heads, p->head_dim, n, s->len,
-                           p->stream);
-  if (rc) return rc;
+  if (!rc)
+    rc = launch_append_paged(p->quant, k, v, p->k, p->v, s->d_pages, p->page_lg,
+                             (int64_t)p->page_bytes, p->n_kv_heads, p->head_dim, n, s->len,
+                             p->stream);
+  if (rc) {
+    undo_room(s, undo);
+    return rc;
+  }
   s->len += n;
   return PKV_OK;
 }
@@ -438,17 +512,23 @@ int pkv_seq_append_batched(pkv_seq *const *seqs, int n, const float *k, const fl
   for (int i0 = 0; i0 < n; i0 += kAppendSeqs) {
     const int m = n - i0 < kAppendSeqs ? n - i0 : kAppendSeqs;
     int64_t off[kAppendSeqs];
-    for (int i = 0; i < m; ++i) {
-      pkv_seq *s = seqs[i0 + i];
-      const int rc = make_room(s, 1, nullptr);
-      if (rc) return rc;
+    RoomUndo undo[kAppendSeqs];
+    int made = 0, rc = PKV_OK;
+    for (; made < m; ++made) {
+      pkv_seq *s = seqs[i0 + made];
+      rc = make_room(s, 1, nullptr, &undo[made]);
+      if (rc) break;
       const int64_t t = s->len;
-      off[i] = (int64_t)s->pages[(size_t)(t >> p->page_lg)] * (int64_t)p->page_bytes +
-               (t & (p->page_tokens - 1)) * (int64_t)p->n_kv_heads * (int64_t)p->bpr;
+      off[made] = (int64_t)s->pages[(size_t)(t >> p->page_lg)] * (int64_t)p->page_bytes +
+                  (t & (p->page_tokens - 1)) * (int64_t)p->n_kv_heads * (int64_t)p->bpr;
     }
-    const int rc = launch_append_rows(p->quant, k + i0 * per, v + i0 * per, p->k, p->v, off, m,
-                                      p->n_kv_heads, p->head_dim, p->stream);
-    if (rc) return rc;
+    if (!rc)
+      rc = launch_append_rows(p->quant, k + i0 * per, v + i0 * per, p->k, p->v, off, m,
+                              p->n_kv_heads, p->head_dim, p->stream);
+    if (rc) {  // this chunk queued nothing: its page lists go back (earlier chunks stay)
+      for (int i = made - 1; i >= 0; --i) undo_room(seqs[i0 + i], undo[i]);
+      return rc;
+    }
     for (int i = 0; i < m; ++i) ++seqs[i0 + i]->len;
   }
   return PKV_OK;
@@ -535,22 +615,26 @@ int pkv_seq_append_decode_batched(pkv_seq *const *seqs, int n, const float *k, c
     if (rc) return rc;
     return pkv_seq_decode_batched(seqs, n, q, num_heads, scale, out);
   }
-  // all or nothing: count the pages first
+  // all or nothing for every refusal: the pages are counted and the capture status
+  // checked for every sequence before any chunk changes a page list or queues work
   size_t reserved = 0;
   for (int i = 0; i < n; ++i) {
-    const int rc = make_room(seqs[i], 1, &reserved);
+    int rc = make_room(seqs[i], 1, &reserved);
+    if (!rc) rc = capture_guard(seqs[i], 1);
     if (rc) return rc;
   }
   const size_t per = (size_t)p->n_kv_heads * p->head_dim, qrow = (size_t)num_heads * p->head_dim;
   for (int i0 = 0; i0 < n; i0 += kMaxPagedSeqs) {
     const int m = n - i0 < kMaxPagedSeqs ? n - i0 : kMaxPagedSeqs;
-    int rc = PKV_OK;
-    for (int i = 0; i < m && !rc; ++i) rc = make_room(seqs[i0 + i], 1, nullptr);
+    RoomUndo undo[kMaxPagedSeqs];
+    int made = 0, rc = PKV_OK;
+    for (; made < m && !rc; ++made) rc = make_room(seqs[i0 + made], 1, nullptr, &undo[made]);
+    if (rc) --made;  // the failed one changed nothing
     if (!rc)
       rc = paged_decode(p, seqs + i0, m, q + i0 * qrow, scale, out + i0 * qrow, k + i0 * per,
                         v + i0 * per);
-    if (rc) {  // nothing of this chunk was queued: give back the pages taken for it
-      for (int i = 0; i < m; ++i) release_tail(seqs[i0 + i], pages_for(p, seqs[i0 + i]->len));
+    if (rc) {  // nothing of this chunk was queued: its page lists go back as they were
+      for (int i = made - 1; i >= 0; --i) undo_room(seqs[i0 + i], undo[i]);
       return rc;
     }
     for (int i = 0; i < m; ++i) ++seqs[i0 + i]->len;

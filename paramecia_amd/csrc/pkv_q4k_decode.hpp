@@ -33,6 +33,8 @@
 // Include-only: the kernel template and its launch plan, instantiated by
 // pkv_attn_mfma.hip (kPrep = false) and pkv_attn_mfma_prep.hip (kPrep = true).
 #pragma once
+#include <cstdlib>
+
 #include "pkv_decode_split.hpp"
 #include "pkv_mfma_common.hpp"
 #include "pkv_q4k_lanes.hpp"
@@ -71,6 +73,14 @@ struct DecodeArgsBase {
   // Fused step: the new rows of nnew output rows (4 nnew rows: K and V of each KV
   // head), at row t_new of segment i, or for paged sequences at row len of their page
   int nnew;
+  // In-launch combine (one segment): ncomb combiner workgroups follow the nwg decode
+  // workgroups in the grid and merge the partials as they arrive; 0 = the separate
+  // combine kernel. flags[c][w] (Workspace::kFlagCols words per row) is set by decode
+  // workgroup w once its partial (and new rows, prepared q) are stored, and cleared by
+  // combiner c after it has read them.
+  int ncomb;
+  uint32_t *flags;
+  float *out;  // [16][256]: the combiners' output row
 };
 template <int kSegs>
 struct DecodeArgsT : DecodeArgsBase {
@@ -536,9 +546,170 @@ __device__ __forceinline__ void issue_prep_consts(void *alpha_lds, void *tail_ld
       : "memory", "scc");
 }
 
+// ---- In-launch combine of a one-segment decode (the combiner workgroups).
+// Combiner c (grid index nwg + c) merges head c / 8, tile-order entries 32 (c % 8) ..
+// +31, as decode_combine_kernel does, but inside the decode launch: a combiner is
+// dispatched once a decode workgroup has left its CU (the decode workgroups come first
+// in the grid and never wait, so they all finish whatever the dispatch order), and each
+// of its threads waits for the arrival flags of the partials it merges, then loads them.
+// Cross-XCD visibility without cache maintenance: every word a combiner reads (partials,
+// (m, l) pairs, new rows, prepared q, flags) is written with agent-scope (sc1) stores and
+// read with agent-scope loads, and a decode workgroup sets its flags only after
+// s_waitcnt vmcnt(0) on those stores and a barrier. The waits are bounded (2^16 polls,
+// well under a second);
+// a combiner that gives up sets kStatusBarrierTimeout (pkv_device_status()).
+constexpr int kTailWGs = Workspace::kFlagRows;  // 16 heads x 8 slices of 32 entries
+constexpr int kFlagCols = Workspace::kFlagCols;
+static_assert(kTailWGs == 16 * 8 && kMainWGs <= kFlagCols && kCombSlices * kCombChunk == kMainWGs &&
+                  kCombSlices * 8 <= kThreads,
+              "combiner layout: one round of partial loads, threads 0-255 merge");
+constexpr int kSC1 = 16;  // buffer cache policy bit: agent-scope coherent access (sc1)
+
+__device__ __forceinline__ void store_sc1(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_sc1(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool flag_set(const uint32_t *p) {
+  return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+}
+
+struct TailSmem {
+  float dotp[4];
+  float mx[kCombSlices], ls[kCombSlices];
+  float4 accs[kCombSlices][8];
+};
+
+// The merge is decode_combine_kernel's, step for step (the same slices, partial order and
+// sums), so both forms give the same bits.
+template <bool kPrep, int kSegs>
+__device__ __forceinline__ void tail_combine(const DecodeArgsT<kSegs> &a, void *lds) {
+  TailSmem &t = *reinterpret_cast<TailSmem *>(lds);
+  const int c = blockIdx.x - a.nwg, nwg = a.nwg;
+  const int h = c >> 3, i0 = 32 * (c & 7), kvh = h >> 3;
+  const int tid = threadIdx.x, ps = tid >> 3, g4 = tid & 7;
+  const bool merger = tid < kCombSlices * 8;  // threads 0-255; waves 4-7 only wait
+  const int per = (nwg + kCombSlices - 1) / kCombSlices;  // <= kCombChunk
+  const int w0 = ps * per, w1 = w0 + per < nwg ? w0 + per : nwg;
+  const uint32_t *frow = a.flags + (int64_t)c * kFlagCols;
+  const bool fused = a.k_new != nullptr;
+  // Each merging wave waits, one load per lane and poll, for the flags of its 64 partials
+  // (lane (ps, g4) polls partial w0 + g4) and of the workgroups that wrote what all its
+  // lanes read: the new K and V rows of KV head kvh (rows kvh and 2 + kvh, quantized by
+  // workgroups row % nwg) and the prepared q (workgroup 0).
+  bool ok = true;
+  if (merger) {
+    const int mine = w0 + g4;
+    const uint32_t *fa = (g4 < per && mine < w1) ? frow + mine : nullptr;
+    const int lane = tid & 63;
+    const int xw = lane == 0 ? kvh % nwg : lane == 1 ? (2 + kvh) % nwg : 0;
+    const uint32_t *fb = ((lane < 2 && fused) || (lane == 2 && kPrep)) ? frow + xw : nullptr;
+    bool done = false;
+    for (int i = 0; i < (1 << 16) && !done; ++i) {  // each poll waits for uncached loads
+      const bool sa = fa == nullptr || flag_set(fa);
+      const bool sb = fb == nullptr || flag_set(fb);
+      done = __all(sa && sb);
+      if (!done) __builtin_amdgcn_s_sleep(2);
+    }
+    ok = done;
+  }
+  float2 mlv[kCombChunk];
+  float4 ov[kCombChunk];
+  float qv = 0.0f, kv = 0.0f;
+  if (merger) {
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        a.part, 0, nwg * 16 * kPartRow * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rm =
+        __builtin_amdgcn_make_buffer_rsrc(a.ml, 0, nwg * 16 * 8, 0x00020000);
+#pragma unroll
+    for (int x = 0; x < kCombChunk; ++x) {
+      const int w = w0 + x;
+      if (w < w1) {
+        mlv[x] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rm, (w * 16 + h) * 8, 0, kSC1));
+        ov[x] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rp, ((w * 16 + h) * kPartRow + i0 + 4 * g4) * 4, 0, kSC1));
+      } else {
+        mlv[x] = float2{-INFINITY, 0.0f};
+        ov[x] = float4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    if (fused) {
+      qv = kPrep ? load_sc1(a.q_out + h * 256 + tid) : a.q[h * 256 + tid];
+      kv = load_sc1(a.dq + kvh * 256 + tid);
+    }
+  }
+  float m_loc = -INFINITY, lacc = 0.0f;
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (merger) {
+    float mc = m_loc;
+#pragma unroll
+    for (int x = 0; x < kCombChunk; ++x) mc = fmaxf(mc, mlv[x].x);
+    if (mc != -INFINITY) {
+      const float r = (m_loc == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_loc - mc);
+      acc.x *= r;
+      acc.y *= r;
+      acc.z *= r;
+      acc.w *= r;
+      lacc *= r;
+#pragma unroll
+      for (int x = 0; x < kCombChunk; ++x) {
+        const float f = (mlv[x].x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mlv[x].x - mc);
+        acc.x += f * ov[x].x;
+        acc.y += f * ov[x].y;
+        acc.z += f * ov[x].z;
+        acc.w += f * ov[x].w;
+        lacc += f * mlv[x].y;
+      }
+      m_loc = mc;
+    }
+  }
+  const float d = wave_sum(qv * kv);
+  if (merger && (tid & 63) == 0) t.dotp[tid >> 6] = d;
+  if (merger && g4 == 0) t.mx[ps] = m_loc;
+  __syncthreads();
+  const float s_new = fused ? fminf(fmaxf((t.dotp[0] + t.dotp[1] + t.dotp[2] + t.dotp[3]) * a.sl2,
+                                          -kSplitClampL2), kSplitClampL2)
+                            : -INFINITY;
+  float M = s_new;
+#pragma unroll
+  for (int x = 0; x < kCombSlices; ++x) M = fmaxf(M, t.mx[x]);
+  const float f = (m_loc == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_loc - M);
+  if (merger) {
+    t.accs[ps][g4] = float4{acc.x * f, acc.y * f, acc.z * f, acc.w * f};
+    if (g4 == 0) t.ls[ps] = lacc * f;
+  }
+  __syncthreads();
+  // every merging wave is past its flag waits: the flags consumed go back to zero
+  if (tid < nwg)
+    __hip_atomic_store(const_cast<uint32_t *>(frow) + tid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (merger && !ok && (tid & 63) == 0)
+    __hip_atomic_fetch_or(a.status, kStatusBarrierTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid < 32) {
+    float sum = 0.0f, L = 0.0f;
+    const float *accf = reinterpret_cast<const float *>(&t.accs[0][0]);
+#pragma unroll
+    for (int x = 0; x < kCombSlices; ++x) {
+      sum += accf[32 * x + tid];
+      L += t.ls[x];
+    }
+    const int e = tile_e((i0 + tid) >> 4, (i0 + tid) & 15);
+    const float f_new = (s_new == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_new - M);
+    L += f_new;
+    if (fused) sum += f_new * load_sc1(a.dq + (2 + kvh) * 256 + e);
+    a.out[h * 256 + e] = L > 0.0f ? sum / L : 0.0f;
+  }
+}
+
 template <bool kPrep, int kSegs>
 __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs> a) {
   __shared__ Smem sm;
+  if constexpr (kSegs == 1) {
+    if ((int)blockIdx.x >= a.nwg) {  // a combiner workgroup (in-launch combine)
+      tail_combine<kPrep>(a, &sm);
+      return;
+    }
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kv = wave & 1, wsub = wave >> 1;
   const int wg = blockIdx.x;
@@ -729,9 +900,18 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
       float deq;
       q4k_quantize_superblock_lanes(xq, dst, &sm.run.t.quant.scr, tid, &deq, bar);
       bar.target += 12;  // the three barriers of that call
-      a.dq[(int64_t)row * 256 + tid] = deq;
+      store_sc1(a.dq + (int64_t)row * 256 + tid, deq);  // read by combiners on other XCDs
     }
     __builtin_amdgcn_s_setprio(0);
+  };
+  // In-launch combine: every store of this workgroup that a combiner reads has completed
+  // (each thread's vmcnt, then the barrier), then flag [c][slot] of every combiner c.
+  auto publish = [&](int pslot) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid < a.ncomb)
+      __hip_atomic_store(a.flags + (int64_t)tid * kFlagCols + pslot, 1u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
   };
   // One pass per piece; the fused append runs in the first. A workgroup without blocks
   // on its part of the line (have false) only quantizes, if it is a quantizing one.
@@ -873,10 +1053,17 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
         }
         if (wg == sg.wg0 && wsub == 0 && n < 8) {  // the combine's copy of the prepared q
           float *qo = a.q_out + ((int64_t)sg.qi * 16 + 8 * kvu + n) * 256 + 64 * g;
+          if (a.ncomb > 0) {  // read by combiners of this launch, on other XCDs
 #pragma unroll
-          for (int st = 0; st < 8; ++st) {
-            *reinterpret_cast<float4 *>(qo + 8 * st) = float4{v[st][0], v[st][1], v[st][2], v[st][3]};
-            *reinterpret_cast<float4 *>(qo + 8 * st + 4) = float4{v[st][4], v[st][5], v[st][6], v[st][7]};
+            for (int st = 0; st < 8; ++st)
+#pragma unroll
+              for (int k = 0; k < 8; ++k) store_sc1(qo + 8 * st + k, v[st][k]);
+          } else {
+#pragma unroll
+            for (int st = 0; st < 8; ++st) {
+              *reinterpret_cast<float4 *>(qo + 8 * st) = float4{v[st][0], v[st][1], v[st][2], v[st][3]};
+              *reinterpret_cast<float4 *>(qo + 8 * st + 4) = float4{v[st][4], v[st][5], v[st][6], v[st][7]};
+            }
           }
         }
 #pragma unroll
@@ -899,7 +1086,24 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
     static_assert(kLoadsPerStage == 12, "the vmcnt above counts one stage of loads");
 
     if (qnow) quantize_rows();
-    if (!have) return;
+    if (!have) {
+      if constexpr (kSegs == 1) {
+        // (the one-segment plan gives every workgroup a block; should it not, its slot
+        // holds an empty partial for the combiners)
+        if (a.ncomb > 0) {
+          float *pz = a.part + ((int64_t)slot * 16 * kPartRow + 8 * tid);
+#pragma unroll
+          for (int x = 0; x < 8; ++x) store_sc1(pz + x, 0.0f);
+          if (tid < 16) {
+            float *mlo = reinterpret_cast<float *>(a.ml + (slot * 16 + tid));
+            store_sc1(mlo, -INFINITY);
+            store_sc1(mlo + 1, 0.0f);
+          }
+          publish(slot);
+        }
+      }
+      return;
+    }
     build_q();
 
     WaveState S;
@@ -1021,10 +1225,17 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
       }
       // one 32-bit index (slot < 2^16), so that no per-lane address outlives the piece
       float *d0 = a.part + ((slot * 16 + 8 * kv2 + 4 * g2) * kPartRow + 16 * T2 + n2);
-      __builtin_nontemporal_store(acc.x, d0);
-      __builtin_nontemporal_store(acc.y, d0 + kPartRow);
-      __builtin_nontemporal_store(acc.z, d0 + 2 * kPartRow);
-      __builtin_nontemporal_store(acc.w, d0 + 3 * kPartRow);
+      if (a.ncomb > 0) {
+        store_sc1(d0, acc.x);
+        store_sc1(d0 + kPartRow, acc.y);
+        store_sc1(d0 + 2 * kPartRow, acc.z);
+        store_sc1(d0 + 3 * kPartRow, acc.w);
+      } else {
+        __builtin_nontemporal_store(acc.x, d0);
+        __builtin_nontemporal_store(acc.y, d0 + kPartRow);
+        __builtin_nontemporal_store(acc.z, d0 + 2 * kPartRow);
+        __builtin_nontemporal_store(acc.w, d0 + 3 * kPartRow);
+      }
     }
     if (tid < 16) {
       const int kv2 = tid >> 3, h = tid & 7;
@@ -1035,10 +1246,18 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
         L += sm.run.t.tab[2 * s4 + kv2].vmd[16 + h];
       }
       float *mlo = reinterpret_cast<float *>(a.ml + (slot * 16 + tid));
-      __builtin_nontemporal_store(M, mlo);
-      __builtin_nontemporal_store(L, mlo + 1);
+      if (a.ncomb > 0) {
+        store_sc1(mlo, M);
+        store_sc1(mlo + 1, L);
+      } else {
+        __builtin_nontemporal_store(M, mlo);
+        __builtin_nontemporal_store(L, mlo + 1);
+      }
     }
-    if constexpr (kSegs == 1) break;  // one segment: one piece
+    if constexpr (kSegs == 1) {  // one segment: one piece
+      if (a.ncomb > 0) publish(slot);
+      break;
+    }
     if (!next_piece()) break;
     // the next piece's q and blocks refill the stage buffers, the merge area until here
     __syncthreads();
@@ -1047,6 +1266,16 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
 
 
 }  // namespace
+
+// The in-launch combine of one-segment decodes is on unless PKV_DECODE_FUSE=0 (the
+// separate combine kernel, kept for comparison).
+static inline bool decode_fuse_enabled() {
+  static const bool on = [] {
+    const char *e = getenv("PKV_DECODE_FUSE");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
 
 // Plan and launch the decode and combine kernels over n <= kMaxSegs segments.
 // kPrep: q_norm / k_norm / rope of the step's q and new k run inside the kernels (prep
@@ -1124,11 +1353,25 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
   d.prep = kPrep ? *prep : DecodePrep{};
   rc = device_status_word(&d.status);
   if (rc) return rc;
+  // one output row: the combine runs inside the decode launch (combiner workgroups after
+  // the decode ones), unless the workspace cannot hold arrival flags (a no-alloc call)
+  d.ncomb = 0;
+  d.flags = nullptr;
+  d.out = out;
+  if (n == 1 && decode_fuse_enabled() && !ws.fixed) {
+    rc = ws.reserve_flags(s);
+    if (rc) return rc;
+    d.ncomb = kTailWGs;
+    d.flags = ws.flags;
+  }
   if (n == 1) {
     DecodeArgsT<1> d1;
     static_cast<DecodeArgsBase &>(d1) = d;
     d1.seg[0] = d.seg[0];
-    hipLaunchKernelGGL((q4k_decode_kernel<kPrep, 1>), dim3((unsigned)nwg), dim3(kThreads), 0, s, d1);
+    hipLaunchKernelGGL((q4k_decode_kernel<kPrep, 1>), dim3((unsigned)(nwg + d.ncomb)), dim3(kThreads),
+                       0, s, d1);
+    PKV_HIP(hipGetLastError());
+    if (d.ncomb > 0) return PKV_OK;
   } else {
     hipLaunchKernelGGL((q4k_decode_kernel<kPrep, kMaxSegs>), dim3((unsigned)nwg), dim3(kThreads), 0,
                        s, d);

@@ -109,7 +109,20 @@ __global__ __launch_bounds__(256) void copy_segments_kernel(Table tab, int n, ui
   }
 }
 
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t *dst, size_t n) {
+  for (size_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) dst[i] = 0u;
+}
+
 }  // namespace
+
+int launch_zero_words(uint32_t *dst, size_t n, hipStream_t s) {
+  if (n == 0) return PKV_OK;
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 1024) blocks = 1024;
+  hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)blocks), dim3(256), 0, s, dst, n);
+  PKV_HIP(hipGetLastError());
+  return PKV_OK;
+}
 
 int launch_fill_normal(float *dst, size_t n, uint64_t seed, uint64_t stream_id, float scale,
                        hipStream_t s) {

@@ -136,7 +136,6 @@ class PreallocatedQuantizedKvCache:
         self.quant = KvCacheQuantization(int(quant) or _lib.QUANT_F16)
         self.num_kv_heads = num_kv_heads
         self.head_dim = head_dim
-        self.max_seq_len = max_seq_len
         self.bytes_per_row = lib().pkv_bytes_per_row(int(quant), head_dim)
 
     def __del__(self):
@@ -152,6 +151,12 @@ class PreallocatedQuantizedKvCache:
     @property
     def seq_len(self) -> int:
         return lib().pkv_len(self._h)
+
+    @property
+    def max_seq_len(self) -> int:
+        """Capacity in tokens. Q8_0/Q4K caches keep it; F16/BF16 caches grow past it on an
+        append (the reference's float cache grows by Tensor::cat, qwen3_next.rs:2492-2516)."""
+        return lib().pkv_capacity(self._h)
 
     @property
     def batch_size(self) -> int:

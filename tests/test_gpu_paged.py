@@ -399,3 +399,104 @@ def test_append_batched_matches_single(pk, orc, quant):
         assert np.array_equal(host(k), rk) and np.array_equal(host(v), rv), i
     with pytest.raises(pk.KvCacheError):
         pool.append_batched([seqs[0], seqs[0]], dev(kn[:2]), dev(vn[:2]))
+
+
+def test_refused_append_under_capture_changes_nothing(pk, orc):
+    """An append whose page list would change (a copy on write of a shared, partly filled
+    page, or a new page) is refused under graph capture before anything changes: page
+    counts, free pages and lengths stay, and the next eager appends (a copy on write, then
+    a smaller append) hold exactly the oracle's rows."""
+    say("paged appends refused under capture")
+    rng = np.random.default_rng(17)
+    pool = pk.PagedKvPool(2, 256, 64, 8, pk.KvCacheQuantization.Q4K)
+    a = pool.sequence()
+    ca = orc.Cache(Q4K, 1, 2, 256, 400)
+    fill(pk, orc, a, ca, rng, [100], 2, 256)  # one full page, one with 36 rows
+    b = a.fork()
+    cb = orc.Cache(Q4K, 1, 2, 256, 400)
+    cb.load_bytes(*ca.valid_bytes(), 100)
+    free0 = pool.free_pages
+    k = rng.standard_normal((1, 2, 40, 256)).astype(np.float32)
+    kn = rng.standard_normal((2, 2, 1, 256)).astype(np.float32)
+    q = rng.standard_normal((2, 16, 256)).astype(np.float32)
+    dk, dkn, dq = dev(k), dev(kn), dev(q)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    x = torch.zeros(1, device="cuda")
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            x.add_(1.0)
+            with pytest.raises(pk.KvCacheError, match="graph"):
+                b.append_quantized(dk, dk)  # copy on write + a new page
+            with pytest.raises(pk.KvCacheError, match="graph"):
+                pool.append_decode_batched([a, b], dkn, dkn, dq, 1 / 16)
+    torch.cuda.synchronize()
+    assert (a.seq_len, b.seq_len, a.pages, b.pages, pool.free_pages) == (100, 100, 2, 2, free0)
+    b.append_quantized(dk, dk)  # eager: copies the shared page, takes a new one
+    assert cb.append(k, k) == 0
+    k2 = rng.standard_normal((1, 2, 3, 256)).astype(np.float32)
+    b.append_quantized(dev(k2), dev(k2))
+    assert cb.append(k2, k2) == 0
+    assert pool.free_pages == free0 - 2
+    for s, c in ((a, ca), (b, cb)):
+        gk, gv = s.get_kv()
+        rk, rv = c.get_kv()
+        assert np.array_equal(host(gk), rk) and np.array_equal(host(gv), rv)
+
+
+def test_graph_replay_survives_workspace_growth(pk, orc):
+    """A captured fused paged step keeps working after an eager call on the same pool
+    grows the pool's workspace (a 256-query prefill chunk needs far more split-K scratch
+    than the decode): the buffer the graph's kernels write is retired, not freed, so the
+    replays after the growth give the eager step's output bit for bit, and the chunk's
+    own output matches the oracle."""
+    say("paged graph replay after workspace growth")
+    rng = np.random.default_rng(23)
+    lens = [300, 1000]
+    pool = pk.PagedKvPool(2, 256, 256, 16, pk.KvCacheQuantization.Q4K)
+    seqs, caches = [], []
+    for n in lens:
+        s = pool.sequence()
+        c = orc.Cache(Q4K, 1, 2, 256, n + 1)
+        fill(pk, orc, s, c, rng, [n], 2, 256)
+        seqs.append(s)
+        caches.append(c)
+    kn = dev(rng.standard_normal((2, 2, 1, 256)).astype(np.float32))
+    q = dev(rng.standard_normal((2, 16, 256)).astype(np.float32))
+    outs = [None]
+
+    def step():
+        for s, n in zip(seqs, lens):
+            s.truncate(n)
+        outs[0] = pool.append_decode_batched(seqs, kn, kn, q, 1 / 16)
+
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+        torch.cuda.synchronize()
+        ref = host(outs[0])
+        with torch.cuda.graph(graph, stream=side):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    got = outs[0]
+    graph.replay()
+    assert np.array_equal(host(got), ref)
+    # eager prefill chunk over the longer sequence: grows the pool's workspace
+    s1, n1 = seqs[1], lens[1]
+    s1.truncate(n1)
+    qc = rng.standard_normal((1, 256, 16, 256)).astype(np.float32)
+    out_c = host(s1.attend(dev(qc), 1 / 16, n1 - 256))
+    c1 = orc.Cache(Q4K, 1, 2, 256, n1)
+    c1.load_bytes(*caches[1].valid_bytes(), n1)
+    ref_c = c1.attend(qc, 1 / 16, n1 - 256, True, mode="f64")
+    assert_attn_close(out_c, ref_c, what="prefill chunk after capture")
+    for i in range(2):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(got), ref), f"replay {i} after growth"
+    assert pk.lib().pkv_device_status() == 0, pk.lib().pkv_last_error()

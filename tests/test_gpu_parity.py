@@ -466,3 +466,84 @@ def test_batched_decode_matches_per_sequence(pk, orc):
         assert_attn_close(out[i], ref)
         assert g.seq_len == lens[i] + 1
         assert np.array_equal(host(g.raw_bytes()[0]), c.valid_bytes()[0])
+
+
+@pytest.mark.parametrize("quant", [F16, BF16])
+def test_float_cache_grows_past_capacity(pk, orc, quant):
+    """F16/BF16 caches grow instead of overflowing, as the reference's float cache grows by
+    Tensor::cat (qwen3_next.rs:2492-2516): appends past the capacity keep every row
+    already stored (bytes equal to an oracle cache with room for all of them), the
+    offset rule still rewinds, and attention over the grown cache matches the oracle."""
+    say(f"float cache growth quant={quant}")
+    rng = np.random.default_rng(31)
+    g = pk.PreallocatedQuantizedKvCache(1, 2, 4, 64, pk.KvCacheQuantization(quant))
+    c = orc.Cache(quant, 1, 2, 64, 64)
+    for n in (3, 5, 1, 20):  # 3 -> 8 -> 9 -> 29 tokens: capacity 4 -> 8 -> 16 -> 32
+        k = rng.standard_normal((1, 2, n, 64)).astype(np.float32)
+        v = rng.standard_normal((1, 2, n, 64)).astype(np.float32)
+        g.append_quantized(dev(k), dev(v))
+        assert c.append(k, v) == 0
+        assert g.seq_len == c.seq_len and g.max_seq_len >= g.seq_len
+    assert g.max_seq_len == 32
+    gk, gv = g.raw_bytes()
+    rk, rv = c.valid_bytes()
+    assert np.array_equal(host(gk), rk) and np.array_equal(host(gv), rv)
+    k = rng.standard_normal((1, 2, 2, 64)).astype(np.float32)
+    g.append_quantized(dev(k), dev(k), offset=25)  # rewinds to 25, then 27 tokens
+    c.truncate(25)
+    assert c.append(k, k) == 0 and g.seq_len == 27
+    q = rng.standard_normal((1, 1, 8, 64)).astype(np.float32)
+    out = host(g.attend(dev(q), 0.125, 26))
+    assert_attn_close(out, c.attend(q, 0.125, 26, True, mode="f64"))
+
+
+def test_allocating_calls_refused_under_capture(pk):
+    """Calls that allocate or clear device memory (pkv_create, pkv_resize_batch,
+    pkv_prefix_save_full / _linear, pkv_pool_create) return PKV_ERR_UNSUPPORTED on a
+    capturing stream, before anything is queued, and work again once the capture ends."""
+    say("allocating calls under capture")
+    import ctypes
+    L = pk.lib()
+    g = pk.PreallocatedQuantizedKvCache(1, 2, 64, 256, pk.KvCacheQuantization.Q4K)
+    g.append_quantized(torch.randn(1, 2, 8, 256, device="cuda"),
+                       torch.randn(1, 2, 8, 256, device="cuda"))
+    ssm = torch.zeros(32 * 128 * 128, device="cuda")
+    conv = torch.zeros(8192 * 3, device="cuda")
+    pre = ctypes.c_void_p()
+    assert L.pkv_prefix_create((ctypes.c_uint32 * 1)(7), 1, 2, ctypes.byref(pre)) == 0
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    x = torch.zeros(4, device="cuda")
+    torch.cuda.synchronize()
+    codes = {}
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            x.add_(1.0)
+            s = ctypes.c_void_p(side.cuda_stream)
+            h = ctypes.c_void_p()
+            codes["create"] = L.pkv_create(4, 1, 2, 256, 64, s, ctypes.byref(h))
+            assert not h.value
+            g.set_stream(side.cuda_stream)
+            codes["resize"] = L.pkv_resize_batch(g.handle, 2)
+            codes["save_full"] = L.pkv_prefix_save_full(pre, 0, g.handle)
+            codes["save_linear"] = L.pkv_prefix_save_linear(
+                pre, 1, ctypes.c_void_p(ssm.data_ptr()), ssm.numel(),
+                ctypes.c_void_p(conv.data_ptr()), conv.numel(), None, 32, s)
+            p = ctypes.c_void_p()
+            codes["pool"] = L.pkv_pool_create(4, 2, 256, 64, 4, s, ctypes.byref(p))
+            assert not p.value
+    torch.cuda.synchronize()
+    assert all(c == 8 for c in codes.values()), codes  # PKV_ERR_UNSUPPORTED
+    g.set_stream(torch.cuda.current_stream().cuda_stream)
+    assert g.batch_size == 1 and g.seq_len == 8
+    assert L.pkv_prefix_entry_kind(pre, 0) == 0 and L.pkv_prefix_entry_kind(pre, 1) == 0
+    graph.replay()  # the capture recorded the add only: one replay adds one
+    torch.cuda.synchronize()
+    assert float(x[0]) == 1.0
+    # eager again: every call works
+    assert L.pkv_prefix_save_full(pre, 0, g.handle) == 0
+    assert L.pkv_prefix_entry_kind(pre, 0) == 1
+    assert L.pkv_prefix_free(pre) == 0
+    g.resize_batch(2)
+    assert g.batch_size == 2
