@@ -81,10 +81,23 @@ def append_roofline(kernel, bound, tokens, heads, us):
             "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+WARM_S = 0.25  # --warm-seconds: the warm-up also lasts at least this long
+WARM_RUN = {"calls": 0}  # warm-up calls made by the last event_time (reported in lines)
+
+
 def event_time(torch, fn, steps, warmup):
-    """Milliseconds per call of fn: HIP events around `steps` calls after `warmup`."""
-    for _ in range(warmup):
+    """Milliseconds per call of fn: HIP events around `steps` calls after the warm-up.
+    The warm-up is at least `warmup` calls and lasts at least WARM_S seconds of wall time
+    (the GPU's clocks ramp up under sustained work; a short warm-up leaves the first
+    timed steps at lower clocks). Nothing of the timed calls changes."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t0 < WARM_S:
         fn()
+        n += 1
+        if n % 16 == 0:
+            torch.cuda.synchronize()
+    WARM_RUN["calls"] = n
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
@@ -107,18 +120,29 @@ def graph_time(torch, fn, steps, warmup, reps=1):
     work. With --no-graph the calls are timed eagerly instead."""
     if NO_GRAPH:
         return event_time(torch, fn, steps, warmup)
-    graph = torch.cuda.CUDAGraph()
+    # Two graphs of the same steps, replayed in turn: HIP submits a replay of a graph
+    # only once that graph's previous replay has finished, so with a single graph the GPU
+    # idles for a submission (about 10 us here) before every replay; with two, the next
+    # replay is always queued behind the running one, as in a serving loop.
+    graphs = [torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()]
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         fn()
         torch.cuda.synchronize()
-        with torch.cuda.graph(graph, stream=side):
-            for _ in range(reps):
-                fn()
+        for g in graphs:
+            with torch.cuda.graph(g, stream=side):
+                for _ in range(reps):
+                    fn()
     torch.cuda.current_stream().wait_stream(side)
+    turn = [0]
+
+    def replay():
+        graphs[turn[0] & 1].replay()
+        turn[0] += 1
+
     replays = max(1, steps // reps)  # steps timed: replays * reps (== steps when reps | steps)
-    return event_time(torch, graph.replay, replays, max(1, warmup // reps)) / reps
+    return event_time(torch, replay, replays, max(1, warmup // reps)) / reps
 
 
 # ------------------------------------------------------------------ config 3 (headline)
@@ -191,7 +215,8 @@ def run_config3(args):
     # serving-loop form), and a graph of a single step for reference
     reps = args.graph_reps if args.graph_reps > 0 else 1
     ms = graph_time(torch, step, args.steps, args.warmup, reps)
-    ms_1 = graph_time(torch, step, args.steps, args.warmup, 1)
+    warm_calls = WARM_RUN["calls"]
+    ms_1 = graph_time(torch, step, args.steps, args.warmup, 1) if reps > 1 else ms
 
     # Per-launch duration of a layer's kernels (decode + combine): the layer's share of
     # the graph-timed step, ms / L, which also holds the gaps between launches and agrees
@@ -225,6 +250,8 @@ def run_config3(args):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_calls_run": warm_calls,
+        "warm_seconds": WARM_S,
         "ms_per_step": round(ms, 4),
         "eager_us_per_step": round(eager_ms * 1000.0, 2),
         "graph_steps_per_replay": reps,
@@ -1039,11 +1066,15 @@ def main() -> int:
                          "counter passes, which do not support graph capture here)")
     ap.add_argument("--no-copy-ceiling", action="store_true",
                     help="skip the device-to-device copy ceiling measured after each config")
+    ap.add_argument("--warm-seconds", type=float, default=0.25,
+                    help="each timed run's warm-up lasts at least this long (and at least "
+                         "--warmup calls): the GPU clocks ramp up under sustained work")
     ap.add_argument("--headline-only", action="store_true",
                     help="default run: measure config 3 only, without configs 1, 2, 4 and 5")
     args = ap.parse_args()
-    global NO_GRAPH
+    global NO_GRAPH, WARM_S
     NO_GRAPH = args.no_graph
+    WARM_S = max(0.0, args.warm_seconds)
     if args.gpus != 1:
         print("bench.py measures the single-GPU path only: every GPU box in this build has "
               "one MI355X, and the KV-cache path needs no collectives (see DESIGN.md for how "

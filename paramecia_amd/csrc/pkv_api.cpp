@@ -42,17 +42,17 @@ int Workspace::reserve(size_t need) {
   return PKV_OK;
 }
 
-int Workspace::reserve_flags(hipStream_t s) {
-  if (flags) return PKV_OK;
-  if (fixed) return set_error(PKV_ERR_ARG, "no arrival flags in a no-alloc call");
+int Workspace::reserve_fused(hipStream_t s) {
+  if (fused) return PKV_OK;
+  if (fixed) return set_error(PKV_ERR_ARG, "no in-launch combine in a no-alloc call");
   void *f = nullptr;
-  PKV_HIP(hipMalloc(&f, (size_t)kFlagRows * kFlagCols * sizeof(uint32_t)));
-  const int rc = launch_zero_words(static_cast<uint32_t *>(f), (size_t)kFlagRows * kFlagCols, s);
+  PKV_HIP(hipMalloc(&f, kFusedBytes));
+  const int rc = launch_zero_words(static_cast<uint32_t *>(f), kFusedBytes / 4, s);
   if (rc) {
     (void)hipFree(f);
     return rc;
   }
-  flags = static_cast<uint32_t *>(f);
+  fused = f;
   return PKV_OK;
 }
 
@@ -92,10 +92,10 @@ int Workspace::mark_host_used(hipStream_t s) {
 Workspace::~Workspace() {
   if (fixed) return;
   if (host_pending) (void)hipEventSynchronize(host_ev);
-  if (ptr || flags || !retired.empty()) {
+  if (ptr || fused || !retired.empty()) {
     (void)hipDeviceSynchronize();
     if (ptr) (void)hipFree(ptr);
-    if (flags) (void)hipFree(flags);
+    if (fused) (void)hipFree(fused);
     for (void *r : retired) (void)hipFree(r);
   }
   if (host) (void)hipHostFree(host);

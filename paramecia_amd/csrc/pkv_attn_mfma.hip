@@ -124,7 +124,7 @@ int launch_paged_decode_q4k(const PagedSeqDesc *seqs, int nseq, const PagedPoolD
   d.v_new = v_new;
   d.nnew = fused ? nseq : 0;
   d.ncomb = 0;  // several output rows: the separate combine kernel
-  d.flags = nullptr;
+  d.words = nullptr;
   d.out = out;
   d.prep = DecodePrep{};
   d.q_out = nullptr;

@@ -79,6 +79,94 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// Sum (max) over the lanes l, l ^ 8, l ^ 16, l ^ 32 of a wave, every one of them getting it
+// (DPP row rotate by 8, then the row-pair and half swaps): the reduction over the 8 partial
+// slices a wave holds, with the lane's float4 of entries (l % 8) fixed. The tree order is
+// fixed, so the result does not depend on timing.
+__device__ __forceinline__ float slices_sum(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, x),
+                                                            __builtin_bit_cast(int, x), 0x128, 0xF,
+                                                            0xF, false));  // row_ror:8
+  {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    x = __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+  }
+  {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    x = __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+  }
+  return x;
+}
+__device__ __forceinline__ float slices_max(float x) {
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, x),
+                                                                    __builtin_bit_cast(int, x), 0x128,
+                                                                    0xF, 0xF, false)));
+  {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    x = fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+  }
+  {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    x = fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+  }
+  return x;
+}
+
+// The end of a (head, 32-entry slice) merge, shared by both combine forms so that they
+// give the same bits. 256 threads: thread (ps, g4) = (tid / 8, tid % 8) holds its slice
+// of partials' running max m_loc (log2 units), sums acc (entries 4 g4 .. 4 g4 + 3 of the
+// slice) and lacc, and qk, its term of the new key's q . k (0 without one). The new key's
+// score and weight join the max; threads 0-31 then hold entry tid of the slice: returns
+// sum / L for it (vnew: that entry of the new key's V row). Every thread of the workgroup
+// (256 or more) calls it: two barriers.
+struct FinishSmem {
+  float dotp[4], mw[4], lw[4];
+  float4 accw[4][8];
+};
+__device__ __forceinline__ float combine_finish(FinishSmem &t, int tid, bool merger, float m_loc,
+                                                float4 acc, float lacc, float qk, bool has_new,
+                                                float sl2, float vnew) {
+  const int w = tid >> 6, g4 = tid & 7;
+  const float d = wave_sum(qk);
+  const float mw = slices_max(m_loc);
+  if (merger && (tid & 63) == 0) {
+    t.dotp[w] = d;
+    t.mw[w] = mw;
+  }
+  __syncthreads();
+  const float s_new = has_new ? fminf(fmaxf((t.dotp[0] + t.dotp[1] + t.dotp[2] + t.dotp[3]) * sl2,
+                                            -kSplitClampL2), kSplitClampL2)
+                              : -INFINITY;
+  const float M = fmaxf(fmaxf(fmaxf(s_new, t.mw[0]), fmaxf(t.mw[1], t.mw[2])), t.mw[3]);
+  const float f = (m_loc == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_loc - M);
+  const float ax = slices_sum(acc.x * f), ay = slices_sum(acc.y * f), az = slices_sum(acc.z * f),
+              aw = slices_sum(acc.w * f), al = slices_sum(lacc * f);
+  if (merger && (tid & 63) < 8) {
+    t.accw[w][g4] = float4{ax, ay, az, aw};
+    if (g4 == 0) t.lw[w] = al;
+  }
+  __syncthreads();
+  float r = 0.0f;
+  if (tid < 32) {
+    const float *a0 = reinterpret_cast<const float *>(&t.accw[0][0]);
+    float sum = ((a0[tid] + a0[32 + tid]) + (a0[64 + tid] + a0[96 + tid]));
+    float L = ((t.lw[0] + t.lw[1]) + (t.lw[2] + t.lw[3]));
+    const float f_new = (s_new == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_new - M);
+    L += f_new;
+    if (has_new) sum += f_new * vnew;
+    r = L > 0.0f ? sum / L : 0.0f;
+  }
+  return r;
+}
+
 // out[b][h][e] = (sum_w o_w 2^(m_w - M) + [new key]) / (sum_w l_w 2^(m_w - M) + [new key]).
 // One workgroup per (head, 32-entry slice of the tile-order row, batch): thread (ps, g4)
 // reads a float4 of entries and the (m, l) pair of every partial in slice ps of the
@@ -104,9 +192,7 @@ struct CombineArgsT {
 using CombineArgs = CombineArgsT<kMaxSegs>;
 template <int kRows>
 __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgsT<kRows> c) {
-  __shared__ float dotp[4];
-  __shared__ float mx[kCombSlices], ls[kCombSlices];
-  __shared__ float4 accs[kCombSlices][8];
+  __shared__ FinishSmem fs;
   const int h = blockIdx.x >> 3, i0 = 32 * (blockIdx.x & 7), b = blockIdx.y;
   const int tid = threadIdx.x, ps = tid >> 3, g4 = tid & 7;
   const float *dq = c.dq;
@@ -160,36 +246,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgsT<kRows>
       m_loc = mc;
     }
   }
-  const float d = wave_sum(qv * kv);
-  if ((tid & 63) == 0) dotp[tid >> 6] = d;
-  if (g4 == 0) mx[ps] = m_loc;
-  __syncthreads();
-  // every thread: the new key's score and the overall max M; each slice then rescales
-  // its own sums to M, so that the final sum over slices is plain adds
-  const float s_new = dq != nullptr
-                          ? fminf(fmaxf((dotp[0] + dotp[1] + dotp[2] + dotp[3]) * sl2, -kSplitClampL2), kSplitClampL2)
-                          : -INFINITY;
-  float M = s_new;
-#pragma unroll
-  for (int x = 0; x < kCombSlices; ++x) M = fmaxf(M, mx[x]);
-  const float f = (m_loc == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_loc - M);
-  accs[ps][g4] = float4{acc.x * f, acc.y * f, acc.z * f, acc.w * f};
-  if (g4 == 0) ls[ps] = lacc * f;
-  __syncthreads();
-  if (tid < 32) {
-    float sum = 0.0f, L = 0.0f;
-    const float *accf = reinterpret_cast<const float *>(&accs[0][0]);
-#pragma unroll
-    for (int x = 0; x < kCombSlices; ++x) {
-      sum += accf[32 * x + tid];
-      L += ls[x];
-    }
-    const int e = tile_e((i0 + tid) >> 4, (i0 + tid) & 15);
-    const float f_new = (s_new == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_new - M);
-    L += f_new;
-    if (dq != nullptr) sum += f_new * dq[((int64_t)b * 4 + 2 + (h >> 3)) * 256 + e];
-    c.out[((int64_t)b * 16 + h) * 256 + e] = L > 0.0f ? sum / L : 0.0f;
-  }
+  const int e = tile_e((i0 + (tid & 31)) >> 4, (i0 + (tid & 31)) & 15);
+  const float vnew = (dq != nullptr && tid < 32) ? dq[((int64_t)b * 4 + 2 + (h >> 3)) * 256 + e] : 0.0f;
+  const float r = combine_finish(fs, tid, true, m_loc, acc, lacc, qv * kv, dq != nullptr, sl2, vnew);
+  if (tid < 32) c.out[((int64_t)b * 16 + h) * 256 + e] = r;
 }
 
 // Launch the combine over n output rows (grid: 128 (head, slice) workgroups per row).

@@ -71,14 +71,18 @@ struct Workspace {
   size_t host_bytes = 0;
   hipEvent_t host_ev = nullptr;
   bool host_pending = false;
-  // Arrival flags of a fused decode launch: kFlagRows x kFlagCols words, zeroed by a
-  // kernel on the stream when first allocated, and left zeroed by every launch that uses
-  // them (its combiners reset the words they consumed). Separate from `ptr`, which other
-  // calls on the same workspace reuse for partials.
-  static constexpr int kFlagRows = 128, kFlagCols = 256;
-  uint32_t *flags = nullptr;
+  // The partials and control words of one-row decodes whose combine runs inside the
+  // decode launch: kFusedSlots split-K partials ([slot][16][256] floats, then
+  // [slot][16] (m, l) pairs) and kFusedWords words, zeroed by a kernel on the stream when
+  // first allocated. Every launch leaves them in a state the next one relies on (each
+  // word's lowest bit holds the parity of the launch that wrote it), so nothing else may
+  // write them: separate from `ptr`, which other calls reuse.
+  static constexpr int kFusedSlots = 256, kFusedWords = 1024;
+  static constexpr size_t kFusedBytes =
+      ((size_t)kFusedSlots * 16 * 256 + (size_t)kFusedSlots * 16 * 2 + kFusedWords) * 4;
+  void *fused = nullptr;
   int reserve(size_t need);
-  int reserve_flags(hipStream_t s);  // allocates and zeroes `flags` once
+  int reserve_fused(hipStream_t s);  // allocates and zeroes `fused` once
   int reserve_host(size_t need);   // waits for the previous staged copy first
   int mark_host_used(hipStream_t s);
   ~Workspace();

@@ -75,11 +75,10 @@ struct DecodeArgsBase {
   int nnew;
   // In-launch combine (one segment): ncomb combiner workgroups follow the nwg decode
   // workgroups in the grid and merge the partials as they arrive; 0 = the separate
-  // combine kernel. flags[c][w] (Workspace::kFlagCols words per row) is set by decode
-  // workgroup w once its partial (and new rows, prepared q) are stored, and cleared by
-  // combiner c after it has read them.
+  // combine kernel. `words` are the control words of the workspace's fused region (see
+  // tail_combine), part / ml then point into that region.
   int ncomb;
-  uint32_t *flags;
+  uint32_t *words;
   float *out;  // [16][256]: the combiners' output row
 };
 template <int kSegs>
@@ -548,95 +547,129 @@ __device__ __forceinline__ void issue_prep_consts(void *alpha_lds, void *tail_ld
 
 // ---- In-launch combine of a one-segment decode (the combiner workgroups).
 // Combiner c (grid index nwg + c) merges head c / 8, tile-order entries 32 (c % 8) ..
-// +31, as decode_combine_kernel does, but inside the decode launch: a combiner is
-// dispatched once a decode workgroup has left its CU (the decode workgroups come first
-// in the grid and never wait, so they all finish whatever the dispatch order), and each
-// of its threads waits for the arrival flags of the partials it merges, then loads them.
-// Cross-XCD visibility without cache maintenance: every word a combiner reads (partials,
-// (m, l) pairs, new rows, prepared q, flags) is written with agent-scope (sc1) stores and
-// read with agent-scope loads, and a decode workgroup sets its flags only after
-// s_waitcnt vmcnt(0) on those stores and a barrier. The waits are bounded (2^16 polls,
-// well under a second);
-// a combiner that gives up sets kStatusBarrierTimeout (pkv_device_status()).
-constexpr int kTailWGs = Workspace::kFlagRows;  // 16 heads x 8 slices of 32 entries
-constexpr int kFlagCols = Workspace::kFlagCols;
-static_assert(kTailWGs == 16 * 8 && kMainWGs <= kFlagCols && kCombSlices * kCombChunk == kMainWGs &&
-                  kCombSlices * 8 <= kThreads,
+// +31, as decode_combine_kernel does, inside the decode launch: a combiner is dispatched
+// once a decode workgroup has left its CU (the decode workgroups come first in the grid
+// and never wait, so they all finish whatever the dispatch order).
+// Readiness without flags or cache maintenance: every word a decode workgroup writes for
+// the combiners carries the launch's parity in its lowest bit (partial values and (m, l)
+// lose that bit; both combine forms clear it, so they give the same bits), written with
+// agent-scope (sc1) stores, and each combiner thread polls the very words it merges with
+// agent-scope loads until their parity is the launch's. A slot holds either the previous
+// launch's words (the other parity) or this launch's: every launch writes every slot it
+// uses, and launches on a workspace are ordered on one stream. The launch parity: decode
+// workgroups read word kWordGen at their start and use its complement; combiner c keeps
+// its own copy in word kWordComb + c and flips it once its merge is done, and combiner 0
+// also flips kWordGen then, after every decode workgroup has read it (each one read it
+// before writing a partial that combiner 0 has merged). The new rows and the prepared q
+// are written early and flagged by words set to the parity after s_waitcnt vmcnt(0). The
+// waits are bounded (2^16 polls); a combiner that gives up sets kStatusBarrierTimeout
+// (pkv_device_status()), and the words must then be zeroed again (a new workspace).
+constexpr int kTailWGs = 128;  // 16 heads x 8 slices of 32 entries
+static_assert(kCombSlices * kCombChunk == kMainWGs && kCombSlices * 8 <= kThreads &&
+                  kMainWGs <= Workspace::kFusedSlots,
               "combiner layout: one round of partial loads, threads 0-255 merge");
+constexpr int kWordGen = 0;      // launch parity seen by the decode workgroups
+constexpr int kWordComb = 32;    // + c: combiner c's launch parity
+constexpr int kWordRow = 256;    // + r: parity of the launch whose new row r is stored
+constexpr int kWordQ = 288;      // + kv: parity of the launch whose prepared q rows are stored
+static_assert(kWordComb + kTailWGs <= kWordRow && kWordQ + 2 <= Workspace::kFusedWords, "words");
 constexpr int kSC1 = 16;  // buffer cache policy bit: agent-scope coherent access (sc1)
 
 __device__ __forceinline__ void store_sc1(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void store_sc1(uint32_t *p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ float load_sc1(const float *p) {
   return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ bool flag_set(const uint32_t *p) {
-  return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+__device__ __forceinline__ uint32_t load_sc1(const uint32_t *p) {
+  return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-
-struct TailSmem {
-  float dotp[4];
-  float mx[kCombSlices], ls[kCombSlices];
-  float4 accs[kCombSlices][8];
-};
+// a partial word with its lowest bit replaced by the launch parity, and back
+__device__ __forceinline__ float tag_par(float x, uint32_t par) {
+  return __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, x) & ~1u) | par);
+}
+__device__ __forceinline__ float untag(float x) {
+  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) & ~1u);
+}
+__device__ __forceinline__ uint32_t par_of(float x) { return __builtin_bit_cast(uint32_t, x) & 1u; }
 
 // The merge is decode_combine_kernel's, step for step (the same slices, partial order and
 // sums), so both forms give the same bits.
 template <bool kPrep, int kSegs>
 __device__ __forceinline__ void tail_combine(const DecodeArgsT<kSegs> &a, void *lds) {
-  TailSmem &t = *reinterpret_cast<TailSmem *>(lds);
+  FinishSmem &t = *reinterpret_cast<FinishSmem *>(lds);
   const int c = blockIdx.x - a.nwg, nwg = a.nwg;
   const int h = c >> 3, i0 = 32 * (c & 7), kvh = h >> 3;
   const int tid = threadIdx.x, ps = tid >> 3, g4 = tid & 7;
   const bool merger = tid < kCombSlices * 8;  // threads 0-255; waves 4-7 only wait
   const int per = (nwg + kCombSlices - 1) / kCombSlices;  // <= kCombChunk
   const int w0 = ps * per, w1 = w0 + per < nwg ? w0 + per : nwg;
-  const uint32_t *frow = a.flags + (int64_t)c * kFlagCols;
   const bool fused = a.k_new != nullptr;
-  // Each merging wave waits, one load per lane and poll, for the flags of its 64 partials
-  // (lane (ps, g4) polls partial w0 + g4) and of the workgroups that wrote what all its
-  // lanes read: the new K and V rows of KV head kvh (rows kvh and 2 + kvh, quantized by
-  // workgroups row % nwg) and the prepared q (workgroup 0).
-  bool ok = true;
-  if (merger) {
-    const int mine = w0 + g4;
-    const uint32_t *fa = (g4 < per && mine < w1) ? frow + mine : nullptr;
-    const int lane = tid & 63;
-    const int xw = lane == 0 ? kvh % nwg : lane == 1 ? (2 + kvh) % nwg : 0;
-    const uint32_t *fb = ((lane < 2 && fused) || (lane == 2 && kPrep)) ? frow + xw : nullptr;
-    bool done = false;
-    for (int i = 0; i < (1 << 16) && !done; ++i) {  // each poll waits for uncached loads
-      const bool sa = fa == nullptr || flag_set(fa);
-      const bool sb = fb == nullptr || flag_set(fb);
-      done = __all(sa && sb);
-      if (!done) __builtin_amdgcn_s_sleep(2);
-    }
-    ok = done;
-  }
+  const uint32_t par = (load_sc1(a.words + kWordComb + c) ^ 1u) & 1u;
   float2 mlv[kCombChunk];
   float4 ov[kCombChunk];
-  float qv = 0.0f, kv = 0.0f;
+  bool ok = true;
+  // the new key's q . k products and this thread's V value of it, loaded during the polls
+  // as soon as the wave has seen the new rows' (and prepared q's) words
+  const int e_out = tile_e((i0 + (tid & 31)) >> 4, (i0 + (tid & 31)) & 15);
+  float qv = 0.0f, kv = 0.0f, vnew = 0.0f;
   if (merger) {
+    // Poll the words this thread merges (and, on lanes 0-2, the new-row and prepared-q
+    // words every lane reads) until each has this launch's parity; a poll reloads only
+    // what is not there yet.
     const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
         a.part, 0, nwg * 16 * kPartRow * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t rm =
         __builtin_amdgcn_make_buffer_rsrc(a.ml, 0, nwg * 16 * 8, 0x00020000);
+    const int cnt = w1 > w0 ? w1 - w0 : 0;
+    uint32_t need = (1u << cnt) - 1u;
+    const int lane = tid & 63;
+    const uint32_t *xw = (lane < 2 && fused) ? a.words + kWordRow + 2 * lane + kvh
+                         : (lane == 2 && kPrep) ? a.words + kWordQ + kvh
+                                                : nullptr;
+    bool xok = xw == nullptr, have_new = !fused;
 #pragma unroll
     for (int x = 0; x < kCombChunk; ++x) {
-      const int w = w0 + x;
-      if (w < w1) {
-        mlv[x] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rm, (w * 16 + h) * 8, 0, kSC1));
-        ov[x] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                               rp, ((w * 16 + h) * kPartRow + i0 + 4 * g4) * 4, 0, kSC1));
-      } else {
-        mlv[x] = float2{-INFINITY, 0.0f};
-        ov[x] = float4{0.f, 0.f, 0.f, 0.f};
-      }
+      mlv[x] = float2{-INFINITY, 0.0f};
+      ov[x] = float4{0.f, 0.f, 0.f, 0.f};
     }
-    if (fused) {
-      qv = kPrep ? load_sc1(a.q_out + h * 256 + tid) : a.q[h * 256 + tid];
-      kv = load_sc1(a.dq + kvh * 256 + tid);
+    bool done = false;
+    for (int it = 0; it < (1 << 16) && !done; ++it) {
+#pragma unroll
+      for (int x = 0; x < kCombChunk; ++x)
+        if ((need >> x) & 1u) {
+          const int w = w0 + x;
+          mlv[x] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rm, (w * 16 + h) * 8, 0, kSC1));
+          ov[x] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rp, ((w * 16 + h) * kPartRow + i0 + 4 * g4) * 4, 0, kSC1));
+        }
+      if (!xok) xok = (load_sc1(xw) & 1u) == par;
+      if (!have_new && __all(xok)) {  // the new rows are stored: their values, once
+        qv = kPrep ? load_sc1(a.q_out + h * 256 + tid) : a.q[h * 256 + tid];
+        kv = load_sc1(a.dq + kvh * 256 + tid);
+        if (tid < 32) vnew = load_sc1(a.dq + (2 + kvh) * 256 + e_out);
+        have_new = true;
+      }
+#pragma unroll
+      for (int x = 0; x < kCombChunk; ++x)
+        if ((need >> x) & 1u) {
+          const uint32_t p = par_of(mlv[x].x) & par_of(mlv[x].y) & par_of(ov[x].x) & par_of(ov[x].y) &
+                             par_of(ov[x].z) & par_of(ov[x].w);
+          const uint32_t q = par_of(mlv[x].x) | par_of(mlv[x].y) | par_of(ov[x].x) | par_of(ov[x].y) |
+                             par_of(ov[x].z) | par_of(ov[x].w);
+          if ((par ? p : (q ^ 1u)) != 0u) need &= ~(1u << x);
+        }
+      done = __all(need == 0u && xok) && have_new;
+      if (!done) __builtin_amdgcn_s_sleep(2);
+    }
+    ok = done;
+#pragma unroll
+    for (int x = 0; x < kCombChunk; ++x) {
+      mlv[x] = float2{untag(mlv[x].x), untag(mlv[x].y)};
+      ov[x] = float4{untag(ov[x].x), untag(ov[x].y), untag(ov[x].z), untag(ov[x].w)};
     }
   }
   float m_loc = -INFINITY, lacc = 0.0f;
@@ -664,41 +697,16 @@ __device__ __forceinline__ void tail_combine(const DecodeArgsT<kSegs> &a, void *
       m_loc = mc;
     }
   }
-  const float d = wave_sum(qv * kv);
-  if (merger && (tid & 63) == 0) t.dotp[tid >> 6] = d;
-  if (merger && g4 == 0) t.mx[ps] = m_loc;
-  __syncthreads();
-  const float s_new = fused ? fminf(fmaxf((t.dotp[0] + t.dotp[1] + t.dotp[2] + t.dotp[3]) * a.sl2,
-                                          -kSplitClampL2), kSplitClampL2)
-                            : -INFINITY;
-  float M = s_new;
-#pragma unroll
-  for (int x = 0; x < kCombSlices; ++x) M = fmaxf(M, t.mx[x]);
-  const float f = (m_loc == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_loc - M);
-  if (merger) {
-    t.accs[ps][g4] = float4{acc.x * f, acc.y * f, acc.z * f, acc.w * f};
-    if (g4 == 0) t.ls[ps] = lacc * f;
+  // every merging wave has seen this launch's words: the launch parity flips (combiner 0
+  // also flips the decode workgroups' copy, which they have all read by now)
+  if (tid == 0) {
+    store_sc1(const_cast<uint32_t *>(a.words) + kWordComb + c, par);
+    if (c == 0) store_sc1(const_cast<uint32_t *>(a.words) + kWordGen, par);
   }
-  __syncthreads();
-  // every merging wave is past its flag waits: the flags consumed go back to zero
-  if (tid < nwg)
-    __hip_atomic_store(const_cast<uint32_t *>(frow) + tid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float r = combine_finish(t, tid, merger, m_loc, acc, lacc, qv * kv, fused, a.sl2, vnew);
   if (merger && !ok && (tid & 63) == 0)
     __hip_atomic_fetch_or(a.status, kStatusBarrierTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (tid < 32) {
-    float sum = 0.0f, L = 0.0f;
-    const float *accf = reinterpret_cast<const float *>(&t.accs[0][0]);
-#pragma unroll
-    for (int x = 0; x < kCombSlices; ++x) {
-      sum += accf[32 * x + tid];
-      L += t.ls[x];
-    }
-    const int e = tile_e((i0 + tid) >> 4, (i0 + tid) & 15);
-    const float f_new = (s_new == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_new - M);
-    L += f_new;
-    if (fused) sum += f_new * load_sc1(a.dq + (2 + kvh) * 256 + e);
-    a.out[h * 256 + e] = L > 0.0f ? sum / L : 0.0f;
-  }
+  if (tid < 32) a.out[h * 256 + e_out] = r;
 }
 
 template <bool kPrep, int kSegs>
@@ -711,6 +719,12 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
     }
   }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the launch parity of an in-launch combine (0 otherwise), in the lowest bit of every
+  // partial word this workgroup writes
+  uint32_t par = 0;
+  if constexpr (kSegs == 1) {
+    if (a.ncomb > 0) par = __builtin_amdgcn_readfirstlane((load_sc1(a.words + kWordGen) ^ 1u) & 1u);
+  }
   const int kv = wave & 1, wsub = wave >> 1;
   const int wg = blockIdx.x;
   const int n = lane & 15, g = lane >> 4;
@@ -901,17 +915,13 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
       q4k_quantize_superblock_lanes(xq, dst, &sm.run.t.quant.scr, tid, &deq, bar);
       bar.target += 12;  // the three barriers of that call
       store_sc1(a.dq + (int64_t)row * 256 + tid, deq);  // read by combiners on other XCDs
+      if (a.ncomb > 0) {  // the row's word once all 256 values are stored
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        bar();
+        if (tid == 0) store_sc1(a.words + kWordRow + row, par);
+      }
     }
     __builtin_amdgcn_s_setprio(0);
-  };
-  // In-launch combine: every store of this workgroup that a combiner reads has completed
-  // (each thread's vmcnt, then the barrier), then flag [c][slot] of every combiner c.
-  auto publish = [&](int pslot) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid < a.ncomb)
-      __hip_atomic_store(a.flags + (int64_t)tid * kFlagCols + pslot, 1u, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
   };
   // One pass per piece; the fused append runs in the first. A workgroup without blocks
   // on its part of the line (have false) only quantizes, if it is a quantizing one.
@@ -1058,6 +1068,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
             for (int st = 0; st < 8; ++st)
 #pragma unroll
               for (int k = 0; k < 8; ++k) store_sc1(qo + 8 * st + k, v[st][k]);
+            // (the wave's word follows below, once every lane's stores are done)
           } else {
 #pragma unroll
             for (int st = 0; st < 8; ++st) {
@@ -1065,6 +1076,10 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
               *reinterpret_cast<float4 *>(qo + 8 * st + 4) = float4{v[st][4], v[st][5], v[st][6], v[st][7]};
             }
           }
+        }
+        if (a.ncomb > 0 && wg == sg.wg0 && wsub == 0) {  // this wave's q rows are stored
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          if (lane == 0) store_sc1(a.words + kWordQ + kvu, par);
         }
 #pragma unroll
         for (int st = 0; st < 8; ++st) convert(st, v[st]);
@@ -1093,13 +1108,12 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
         if (a.ncomb > 0) {
           float *pz = a.part + ((int64_t)slot * 16 * kPartRow + 8 * tid);
 #pragma unroll
-          for (int x = 0; x < 8; ++x) store_sc1(pz + x, 0.0f);
+          for (int x = 0; x < 8; ++x) store_sc1(pz + x, tag_par(0.0f, par));
           if (tid < 16) {
             float *mlo = reinterpret_cast<float *>(a.ml + (slot * 16 + tid));
-            store_sc1(mlo, -INFINITY);
-            store_sc1(mlo + 1, 0.0f);
+            store_sc1(mlo, tag_par(-INFINITY, par));
+            store_sc1(mlo + 1, tag_par(0.0f, par));
           }
-          publish(slot);
         }
       }
       return;
@@ -1225,16 +1239,17 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
       }
       // one 32-bit index (slot < 2^16), so that no per-lane address outlives the piece
       float *d0 = a.part + ((slot * 16 + 8 * kv2 + 4 * g2) * kPartRow + 16 * T2 + n2);
+      // lowest bit: the launch parity (in-launch combine) or zero
       if (a.ncomb > 0) {
-        store_sc1(d0, acc.x);
-        store_sc1(d0 + kPartRow, acc.y);
-        store_sc1(d0 + 2 * kPartRow, acc.z);
-        store_sc1(d0 + 3 * kPartRow, acc.w);
+        store_sc1(d0, tag_par(acc.x, par));
+        store_sc1(d0 + kPartRow, tag_par(acc.y, par));
+        store_sc1(d0 + 2 * kPartRow, tag_par(acc.z, par));
+        store_sc1(d0 + 3 * kPartRow, tag_par(acc.w, par));
       } else {
-        __builtin_nontemporal_store(acc.x, d0);
-        __builtin_nontemporal_store(acc.y, d0 + kPartRow);
-        __builtin_nontemporal_store(acc.z, d0 + 2 * kPartRow);
-        __builtin_nontemporal_store(acc.w, d0 + 3 * kPartRow);
+        __builtin_nontemporal_store(untag(acc.x), d0);
+        __builtin_nontemporal_store(untag(acc.y), d0 + kPartRow);
+        __builtin_nontemporal_store(untag(acc.z), d0 + 2 * kPartRow);
+        __builtin_nontemporal_store(untag(acc.w), d0 + 3 * kPartRow);
       }
     }
     if (tid < 16) {
@@ -1247,17 +1262,14 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
       }
       float *mlo = reinterpret_cast<float *>(a.ml + (slot * 16 + tid));
       if (a.ncomb > 0) {
-        store_sc1(mlo, M);
-        store_sc1(mlo + 1, L);
+        store_sc1(mlo, tag_par(M, par));
+        store_sc1(mlo + 1, tag_par(L, par));
       } else {
-        __builtin_nontemporal_store(M, mlo);
-        __builtin_nontemporal_store(L, mlo + 1);
+        __builtin_nontemporal_store(untag(M), mlo);
+        __builtin_nontemporal_store(untag(L), mlo + 1);
       }
     }
-    if constexpr (kSegs == 1) {  // one segment: one piece
-      if (a.ncomb > 0) publish(slot);
-      break;
-    }
+    if constexpr (kSegs == 1) break;  // one segment: one piece
     if (!next_piece()) break;
     // the next piece's q and blocks refill the stage buffers, the merge area until here
     __syncthreads();
@@ -1353,16 +1365,20 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
   d.prep = kPrep ? *prep : DecodePrep{};
   rc = device_status_word(&d.status);
   if (rc) return rc;
-  // one output row: the combine runs inside the decode launch (combiner workgroups after
-  // the decode ones), unless the workspace cannot hold arrival flags (a no-alloc call)
   d.ncomb = 0;
-  d.flags = nullptr;
+  d.words = nullptr;
   d.out = out;
-  if (n == 1 && decode_fuse_enabled() && !ws.fixed) {
-    rc = ws.reserve_flags(s);
+  // one output row over a full grid: the combine runs inside the decode launch, on the
+  // workspace's fused region (every such launch writes all of its slots, which the
+  // parity protocol needs); a no-alloc call has no fused region
+  if (n == 1 && nwg == Workspace::kFusedSlots && decode_fuse_enabled() && !ws.fixed) {
+    rc = ws.reserve_fused(s);
     if (rc) return rc;
+    float *f = static_cast<float *>(ws.fused);
     d.ncomb = kTailWGs;
-    d.flags = ws.flags;
+    d.part = f;
+    d.ml = reinterpret_cast<float2 *>(f + (size_t)Workspace::kFusedSlots * 16 * kPartRow);
+    d.words = reinterpret_cast<uint32_t *>(f + (size_t)Workspace::kFusedSlots * 16 * (kPartRow + 2));
   }
   if (n == 1) {
     DecodeArgsT<1> d1;
