@@ -9,6 +9,7 @@
 // sum l of 2^(score - m). A row is 1 KB, so the combine's 32-entry slices each fill one
 // 128-byte line, and a head's (m, l) pairs of all partials are contiguous.
 #pragma once
+#include <cstdlib>
 #include <type_traits>
 
 #include "pkv_internal.hpp"
@@ -250,6 +251,194 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgsT<kRows>
   const float vnew = (dq != nullptr && tid < 32) ? dq[((int64_t)b * 4 + 2 + (h >> 3)) * 256 + e] : 0.0f;
   const float r = combine_finish(fs, tid, true, m_loc, acc, lacc, qv * kv, dq != nullptr, sl2, vnew);
   if (tid < 32) c.out[((int64_t)b * 16 + h) * 256 + e] = r;
+}
+
+// ---- In-launch combine of a one-row decode (the combiner workgroups of a decode launch
+// over Workspace::kFusedSlots workgroups).
+// Combiner c (grid index nwg + c) merges head c / 8, tile-order entries 32 (c % 8) ..
+// +31, as decode_combine_kernel does, inside the decode launch: a combiner is dispatched
+// once a decode workgroup has left its CU (the decode workgroups come first in the grid
+// and never wait, so they all finish whatever the dispatch order).
+// Readiness without flags or cache maintenance: every word a decode workgroup writes for
+// the combiners carries the launch's parity in its lowest bit (partial values and (m, l)
+// lose that bit; both combine forms clear it, so they give the same bits), written with
+// agent-scope (sc1) stores, and each combiner thread polls the very words it merges with
+// agent-scope loads until their parity is the launch's. A slot holds either the previous
+// launch's words (the other parity) or this launch's: every launch writes every slot it
+// uses, and launches on a workspace are ordered on one stream. The launch parity: decode
+// workgroups read word kWordGen at their start and use its complement; combiner c keeps
+// its own copy in word kWordComb + c and flips it once its merge is done, and combiner 0
+// also flips kWordGen then, after every decode workgroup has read it (each one read it
+// before writing a partial that combiner 0 has merged). The new rows and the prepared q
+// are written early and flagged by words set to the parity after s_waitcnt vmcnt(0). The
+// waits are bounded (2^16 polls); a combiner that gives up sets kStatusBarrierTimeout
+// (pkv_device_status()), and the words must then be zeroed again (a new workspace).
+constexpr int kTailWGs = 128;  // 16 heads x 8 slices of 32 entries
+constexpr int kTailThreads = 512;  // threads 0-255 merge, 256-511 only wait
+static_assert(kCombSlices * kCombChunk == Workspace::kFusedSlots && kCombSlices * 8 <= kTailThreads,
+              "combiner layout: one round of partial loads over the fused slots");
+constexpr int kWordGen = 0;      // launch parity seen by the decode workgroups
+constexpr int kWordComb = 32;    // + c: combiner c's launch parity
+constexpr int kWordRow = 256;    // + r: parity of the launch whose new row r is stored
+constexpr int kWordQ = 288;      // + kv: parity of the launch whose prepared q rows are stored
+static_assert(kWordComb + kTailWGs <= kWordRow && kWordQ + 2 <= Workspace::kFusedWords, "words");
+constexpr int kSC1 = 16;  // buffer cache policy bit: agent-scope coherent access (sc1)
+
+__device__ __forceinline__ void store_sc1(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_sc1(uint32_t *p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_sc1(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_sc1(const uint32_t *p) {
+  return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// a partial word with its lowest bit replaced by the launch parity, and back
+__device__ __forceinline__ float tag_par(float x, uint32_t par) {
+  return __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, x) & ~1u) | par);
+}
+__device__ __forceinline__ float untag(float x) {
+  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) & ~1u);
+}
+__device__ __forceinline__ uint32_t par_of(float x) { return __builtin_bit_cast(uint32_t, x) & 1u; }
+
+// The merge is decode_combine_kernel's, step for step (the same slices, partial order and
+// sums), so both forms give the same bits.
+// The fields a combiner reads: nwg partial slots at part / ml (the fused region), the
+// control words, q (or, with kPrep, the prepared q_out), the new rows dq (null without
+// a fused append), the output row and the status word.
+struct TailArgs {
+  int nwg;
+  uint32_t *words;
+  const float *part;
+  const float2 *ml;
+  const float *q, *q_out, *dq;
+  float *out;
+  float sl2;
+  unsigned *status;
+};
+template <bool kPrep>
+__device__ __forceinline__ void tail_combine(const TailArgs &a, int c, void *lds) {
+  FinishSmem &t = *reinterpret_cast<FinishSmem *>(lds);
+  const int nwg = a.nwg;
+  const int h = c >> 3, i0 = 32 * (c & 7), kvh = h >> 3;
+  const int tid = threadIdx.x, ps = tid >> 3, g4 = tid & 7;
+  const bool merger = tid < kCombSlices * 8;  // threads 0-255; waves 4-7 only wait
+  const int per = (nwg + kCombSlices - 1) / kCombSlices;  // <= kCombChunk
+  const int w0 = ps * per, w1 = w0 + per < nwg ? w0 + per : nwg;
+  const bool fused = a.dq != nullptr;
+  const uint32_t par = (load_sc1(a.words + kWordComb + c) ^ 1u) & 1u;
+  float2 mlv[kCombChunk];
+  float4 ov[kCombChunk];
+  bool ok = true;
+  // the new key's q . k products and this thread's V value of it, loaded during the polls
+  // as soon as the wave has seen the new rows' (and prepared q's) words
+  const int e_out = tile_e((i0 + (tid & 31)) >> 4, (i0 + (tid & 31)) & 15);
+  float qv = 0.0f, kv = 0.0f, vnew = 0.0f;
+  if (merger) {
+    // Poll the words this thread merges (and, on lanes 0-2, the new-row and prepared-q
+    // words every lane reads) until each has this launch's parity; a poll reloads only
+    // what is not there yet.
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.part), 0, nwg * 16 * kPartRow * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rm =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float2 *>(a.ml), 0, nwg * 16 * 8, 0x00020000);
+    const int cnt = w1 > w0 ? w1 - w0 : 0;
+    uint32_t need = (1u << cnt) - 1u;  // entries not merged yet
+    const int lane = tid & 63;
+    const uint32_t *xw = (lane < 2 && fused) ? a.words + kWordRow + 2 * lane + kvh
+                         : (lane == 2 && kPrep) ? a.words + kWordQ + kvh
+                                                : nullptr;
+    bool xok = xw == nullptr, have_new = !fused;
+#pragma unroll
+    for (int x = 0; x < kCombChunk; ++x) {
+      mlv[x] = float2{-INFINITY, 0.0f};
+      ov[x] = float4{0.f, 0.f, 0.f, 0.f};
+    }
+    bool done = false;
+    for (int it = 0; it < (1 << 16) && !done; ++it) {
+#pragma unroll
+      for (int x = 0; x < kCombChunk; ++x)
+        if ((need >> x) & 1u) {  // every word not there yet
+          const int w = w0 + x;
+          mlv[x] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rm, (w * 16 + h) * 8, 0, kSC1));
+          ov[x] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rp, ((w * 16 + h) * kPartRow + i0 + 4 * g4) * 4, 0, kSC1));
+        }
+      if (!xok) xok = (load_sc1(xw) & 1u) == par;
+      if (!have_new && __all(xok)) {  // the new rows are stored: their values, once
+        qv = kPrep ? load_sc1(a.q_out + h * 256 + tid) : a.q[h * 256 + tid];
+        kv = load_sc1(a.dq + kvh * 256 + tid);
+        if (tid < 32) vnew = load_sc1(a.dq + (2 + kvh) * 256 + e_out);
+        have_new = true;
+      }
+      const uint32_t pm = par ? 0u : 1u;  // a word is this launch's when its low bit ^ pm is 1
+#pragma unroll
+      for (int x = 0; x < kCombChunk; ++x)
+        if ((need >> x) & 1u) {
+          const uint32_t mok = (par_of(mlv[x].x) ^ pm) & (par_of(mlv[x].y) ^ pm);
+          const uint32_t ook = (par_of(ov[x].x) ^ pm) & (par_of(ov[x].y) ^ pm) &
+                               (par_of(ov[x].z) ^ pm) & (par_of(ov[x].w) ^ pm);
+          if (mok && ook) need &= ~(1u << x);
+        }
+      done = __all(need == 0u && xok) && have_new;
+      if (!done) __builtin_amdgcn_s_sleep(2);
+    }
+    ok = done;
+#pragma unroll
+    for (int x = 0; x < kCombChunk; ++x) {
+      mlv[x] = float2{untag(mlv[x].x), untag(mlv[x].y)};
+      ov[x] = float4{untag(ov[x].x), untag(ov[x].y), untag(ov[x].z), untag(ov[x].w)};
+    }
+  }
+  float m_loc = -INFINITY, lacc = 0.0f;
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (merger) {
+    float mc = m_loc;
+#pragma unroll
+    for (int x = 0; x < kCombChunk; ++x) mc = fmaxf(mc, mlv[x].x);
+    if (mc != -INFINITY) {
+      const float r = (m_loc == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_loc - mc);
+      acc.x *= r;
+      acc.y *= r;
+      acc.z *= r;
+      acc.w *= r;
+      lacc *= r;
+#pragma unroll
+      for (int x = 0; x < kCombChunk; ++x) {
+        const float f = (mlv[x].x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mlv[x].x - mc);
+        acc.x += f * ov[x].x;
+        acc.y += f * ov[x].y;
+        acc.z += f * ov[x].z;
+        acc.w += f * ov[x].w;
+        lacc += f * mlv[x].y;
+      }
+      m_loc = mc;
+    }
+  }
+  // every merging wave has seen this launch's words: the launch parity flips (combiner 0
+  // also flips the decode workgroups' copy, which they have all read by now)
+  if (tid == 0) {
+    store_sc1(a.words + kWordComb + c, par);
+    if (c == 0) store_sc1(a.words + kWordGen, par);
+  }
+  const float r = combine_finish(t, tid, merger, m_loc, acc, lacc, qv * kv, fused, a.sl2, vnew);
+  if (merger && !ok && (tid & 63) == 0)
+    __hip_atomic_fetch_or(a.status, kStatusBarrierTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid < 32) a.out[h * 256 + e_out] = r;
+}
+
+// The in-launch combine of one-row decodes is on unless PKV_DECODE_FUSE=0 (the separate
+// combine kernel, kept for comparison).
+static inline bool decode_fuse_enabled() {
+  static const bool on = [] {
+    const char *e = getenv("PKV_DECODE_FUSE");
+    return !(e && e[0] == '0');
+  }();
+  return on;
 }
 
 // Launch the combine over n output rows (grid: 128 (head, slice) workgroups per row).

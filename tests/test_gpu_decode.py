@@ -297,3 +297,63 @@ def test_q8_batched_varlen(pk, orc):
         gk, gv = g.raw_bytes()
         ok, ov = c.valid_bytes()
         assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
+
+
+def test_inlaunch_combine_replays_and_mixed_sizes(pk, orc):
+    """One-row decodes over 256 workgroups merge their partials inside the decode launch,
+    polling words that carry the launch parity (a per-handle region every such launch
+    rewrites). On one handle: eager fused steps, a captured step replayed three times with
+    other eager steps (which flip the parity) in between, and shorter decodes that take
+    the separate combine in between: every output equals the first eager output bit for
+    bit, or the oracle's for a different input."""
+    say("in-launch combine: graph replays, eager steps and short decodes interleaved")
+    S, Sshort = 40000, 3000
+    rng = np.random.default_rng(77)
+    g = pk.PreallocatedQuantizedKvCache(1, 2, S + 1, 256, pk.KvCacheQuantization.Q4K)
+    c = orc.Cache(Q4K, 1, 2, 256, S + 1)
+    k = rng.standard_normal((1, 2, S, 256)).astype(np.float32)
+    v = rng.standard_normal((1, 2, S, 256)).astype(np.float32)
+    g.append_quantized(dev(k), dev(v))
+    assert c.append(k, v) == 0
+    kn = rng.standard_normal((1, 2, 1, 256)).astype(np.float32)
+    vn = rng.standard_normal((1, 2, 1, 256)).astype(np.float32)
+    q = rng.standard_normal((1, 1, 16, 256)).astype(np.float32)
+    q2 = rng.standard_normal((1, 1, 16, 256)).astype(np.float32)
+    dkn, dvn, dq, dq2 = dev(kn), dev(vn), dev(q), dev(q2)
+    ref = host(g.append_attend(dkn, dvn, dq, 1 / 16, offset=S))
+    assert c.append(kn, vn) == 0
+    assert_attn_close(ref, c.attend(q, 1 / 16, S, True, mode="f64"), what="eager fused step")
+    ref2 = c.attend(q2, 1 / 16, S, True, mode="f64")
+    cs = orc.Cache(Q4K, 1, 2, 256, Sshort)
+    cs.load_bytes(*c.valid_bytes(), Sshort)
+    ref_short = cs.attend(q, 1 / 16, Sshort - 1, True, mode="f64")
+    outs = [None]
+
+    def step():
+        outs[0] = g.append_attend(dkn, dvn, dq, 1 / 16, offset=S)
+
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    got = outs[0]
+    for i in range(3):
+        for j in range(i + 1):  # eager fused steps with another query: the parity moves on
+            assert_attn_close(host(g.append_attend(dkn, dvn, dq2, 1 / 16, offset=S)), ref2,
+                              what=f"eager step {i}.{j}")
+        g.set_len(Sshort)  # a shorter decode: fewer workgroups, the separate combine
+        assert_attn_close(host(g.attend(dq, 1 / 16, Sshort - 1)), ref_short, what=f"short {i}")
+        g.set_len(S + 1)
+        graph.replay()
+        assert np.array_equal(host(got), ref), f"replay {i}"
+        assert np.array_equal(host(g.append_attend(dkn, dvn, dq, 1 / 16, offset=S)), ref), f"eager {i}"
+    gk, gv = g.raw_bytes()
+    ok, ov = c.valid_bytes()
+    assert np.array_equal(host(gk), ok) and np.array_equal(host(gv), ov)
+    assert pk.lib().pkv_device_status() == 0, pk.lib().pkv_last_error()
