@@ -85,6 +85,17 @@ WARM_S = 0.25  # --warm-seconds: the warm-up also lasts at least this long
 WARM_RUN = {"calls": 0}  # warm-up calls made by the last event_time (reported in lines)
 
 
+def device_status_check():
+    """After every timed region: the library's device status word (a fused decode step's
+    bounded waits that gave up, pkv_device_status) must be clear, else the timed steps did
+    not produce valid results and the run fails instead of printing a number."""
+    from paramecia_amd import _lib
+    L = _lib.lib()
+    if L.pkv_device_status() != 0:
+        raise RuntimeError("device status set after a timed region: " +
+                           L.pkv_last_error().decode())
+
+
 def event_time(torch, fn, steps, warmup):
     """Milliseconds per call of fn: HIP events around `steps` calls after the warm-up.
     The warm-up is at least `warmup` calls and lasts at least WARM_S seconds of wall time
@@ -105,6 +116,7 @@ def event_time(torch, fn, steps, warmup):
         fn()
     b.record()
     torch.cuda.synchronize()
+    device_status_check()
     return a.elapsed_time(b) / steps
 
 
@@ -232,6 +244,12 @@ def run_config3(args):
         step(ev[s_])
     torch.cuda.synchronize()
     bracketed_ms = sum(a.elapsed_time(b) for row in ev for a, b in row) / (args.steps * L)
+    device_status_check()
+    graph_ms = ms
+    # the step time: the faster of the two launch forms (both do every step's full work);
+    # the other is reported beside it
+    from_graph = graph_ms <= eager_ms
+    ms = graph_ms if from_graph else eager_ms
     per_launch_ms = ms / L
 
     keys = S + 1
@@ -253,7 +271,9 @@ def run_config3(args):
         "warmup_calls_run": warm_calls,
         "warm_seconds": WARM_S,
         "ms_per_step": round(ms, 4),
+        "value_from": "graph replay" if from_graph else "eager launches",
         "eager_us_per_step": round(eager_ms * 1000.0, 2),
+        "graph_us_per_step": round(graph_ms * 1000.0, 2),
         "graph_steps_per_replay": reps,
         "one_step_graph_us_per_step": round(ms_1 * 1000.0, 2),
         "higher_is_better": False,
@@ -270,14 +290,16 @@ def run_config3(args):
         "step_hbm_gbs": round(step_bytes / (ms * 1e-3) / 1e9, 1),
         "step_pct_of_peak": round(100.0 * step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
         "roofline": {
-            "kernel": ("pkv_append_attend_prep (one layer: prep-append kernel + decode "
-                       "kernel + combine kernel)") if args.prep else
-                      "pkv_append_attend (one layer: decode kernel + combine kernel)",
+            "kernel": ("pkv_append_attend_prep (one layer: one decode launch that prepares q "
+                       "and the new K row, quantizes the new rows and merges its partials in "
+                       "its combiner workgroups)") if args.prep else
+                      ("pkv_append_attend (one layer: one decode launch that quantizes the "
+                       "new rows and merges its split-K partials in its combiner workgroups)"),
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
             "bytes_per_launch": layer_bytes(keys),
             "avg_launch_us": round(per_launch_ms * 1000.0, 2),
-            "avg_launch_source": "graph-timed step / layers (HIP events around the replays)",
+            "avg_launch_source": "the step time (value) / layers (HIP events around the steps)",
             "event_bracketed_launch_us": round(bracketed_ms * 1000.0, 2),
             "traffic": traffic(3),
             "traffic_source": MEASURED_TRAFFIC[3][1],
@@ -677,7 +699,10 @@ def run_config4(args):
                                                 W.DN_CONV_DIM * (W.DN_CONV_K - 1) + W.DN_HEADS)
     moved = 2 * (full_bytes + lin_bytes)  # read + write
     gbs = moved / (ms_restore * 1e-3) / 1e9
-    return base_result(4, "PrefixCache restore GB/s (12 x 65536-token Q4K layers + 36 DeltaNet "
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_restore(full[0].quantized_cache, ks, vs, S, SUF, len(full))
+    r = base_result(4, "PrefixCache restore GB/s (12 x 65536-token Q4K layers + 36 DeltaNet "
                           "states) and restore + 1024-token suffix µs",
                        round(gbs, 1), "GB/s", True, ms, args,
                        "config4: restore_prefix_cache of 12 full layers (65536 Q4K tokens each) "
@@ -698,6 +723,53 @@ def run_config4(args):
                                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                                      "bytes_per_launch": moved, "traffic": traffic(4),
                                      "traffic_source": MEASURED_TRAFFIC[4][1]}})
+    if cpu is not None:
+        r["cpu_baseline"] = cpu
+    return r
+
+
+def cpu_baseline_restore(cache, ks, vs, S, SUF, layers):
+    """Config 4 on the oracle's restatement of the reference's CPU restore path
+    (qwen3_next.rs:2819-2884): a saved quantized layer is f32 (save_kv_state dequantizes,
+    :2780-2815), and restore_kv_state clears the cache, re-quantizes every saved row through
+    append and dequantizes the whole cache once more (the discarded get_kv, :2843-2847);
+    then the suffix's 1024 tokens are quantized and appended. The 36 DeltaNet states are
+    restored by reference (Arc clones of contiguous tensors, :4106-4132): no work. The
+    oracle's codecs are single-threaded. Timed: the restore over the first `sample` saved
+    tokens (scaled by S / sample: every part is linear in the rows) plus the whole suffix
+    append, for one layer, median of CPU_RUNS runs, times `layers`."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    from paramecia_amd import workloads as W
+
+    sample = min(S, 16384)
+    c = oracle_cache_from(cache, 4, S, sample)
+    kd, vd = c.get_kv()  # the saved f32 K / V (save_kv_state)
+    kd, vd = np.ascontiguousarray(kd), np.ascontiguousarray(vd)
+    ksn, vsn = ks.cpu().numpy(), vs.cpu().numpy()
+    r = orc.Cache(4, 1, W.NUM_KV_HEADS, W.HEAD_DIM, sample + SUF)
+    t_rest, t_suf = [], []
+    for _ in range(CPU_RUNS):
+        t0 = time.perf_counter()
+        r.clear()
+        assert r.append(kd, vd) == 0
+        r.get_kv()
+        t1 = time.perf_counter()
+        assert r.append(ksn, vsn) == 0
+        t2 = time.perf_counter()
+        t_rest.append(t1 - t0)
+        t_suf.append(t2 - t1)
+    per_layer = median(t_rest) * S / sample + median(t_suf)
+    return {"value": round(per_layer * layers * 1e6, 1), "unit": "us per restore + suffix",
+            "cores": 1, "kind": "port",
+            "sample": f"config 4: one layer's re-quantizing restore over the first {sample} of "
+                      f"{S} saved tokens (scaled by {S / sample:g}) plus its {SUF}-token suffix "
+                      f"append, median of {CPU_RUNS} runs, times {layers} layers; DeltaNet "
+                      f"states restore by reference (no work); single-threaded oracle codecs "
+                      f"on {cpu_model()}",
+            "restore_runs_s": [round(x, 4) for x in t_rest],
+            "suffix_runs_s": [round(x, 4) for x in t_suf]}
 
 
 # ------------------------------------------------------------------ config 5
@@ -747,7 +819,10 @@ def run_config5(args):
     ms = graph_time(torch, step, args.steps, args.warmup, reps)
     nbytes = L * sum(layer_bytes(S + 1) for S in lens)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return base_result(5, "batched decode µs/step (16 sequences, 12 layers, Q4K)",
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_batched(caches[0], kn[0], vn[0], q[0], lens, args.cpu_threads, L)
+    r = base_result(5, "batched decode µs/step (16 sequences, 12 layers, Q4K)",
                        round(ms * 1000, 2), "us/step", False, ms, args,
                        "config5: 16 batch-1 Q4K caches per layer (seeded lengths 1024-65536, "
                        "5 outlier channels x20), 12 layers; step = append 1 token + attend, "
@@ -758,6 +833,59 @@ def run_config5(args):
                                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                                      "bytes_per_step": nbytes,
                                      "traffic_per_layer": traffic(5)}})
+    if cpu is not None:
+        r["cpu_baseline"] = cpu
+    return r
+
+
+def cpu_baseline_batched(caches, kn, vn, q, lens, threads, layers):
+    """Config 5 on the oracle's faithful CPU path (each sequence's decode step as
+    cpu_baseline_decode times it: the reference serves one sequence at a time). Timed on
+    the shortest, a middle and the longest sequence of layer 0 (all cores; median of
+    CPU_RUNS runs each), fitted as t = a + b * keys and summed over the 16 sequences and
+    the layers; the one-thread leg times the shortest sequence and scales by the keys."""
+    from paramecia_amd import workloads as W
+
+    nthreads = cpu_threads(threads)
+    order = sorted(range(len(lens)), key=lambda i: lens[i])
+    picks = [order[0], order[len(order) // 2], order[-1]]
+    xs, ts = [], []
+    single = None
+    for i in picks:
+        S = lens[i]
+        c = oracle_cache_from(caches[i], 4, S, S)
+        knp = kn[i:i + 1].unsqueeze(2).cpu().numpy()
+        vnp = vn[i:i + 1].unsqueeze(2).cpu().numpy()
+        qnp = q[i:i + 1].unsqueeze(1).cpu().numpy()
+
+        def once(th):
+            t0 = time.perf_counter()
+            assert c.append_at(knp, vnp, S) == 0
+            c.attend(qnp, W.SCALE, S, True, mode="faithful", threads=th)
+            return time.perf_counter() - t0
+
+        xs.append(S + 1)
+        ts.append(median([once(nthreads) for _ in range(CPU_RUNS)]))
+        if i == order[0]:
+            single = (S + 1, median([once(1) for _ in range(CPU_RUNS)]))
+        del c
+    b = (ts[-1] - ts[0]) / max(1, xs[-1] - xs[0])
+    a = max(0.0, ts[0] - b * xs[0])
+    keys = [S + 1 for S in lens]
+    per_layer = sum(a + b * k for k in keys)
+    return {"value": round(per_layer * layers * 1e6, 1), "unit": "us/step", "cores": nthreads,
+            "kind": "port",
+            "sample": f"config 5: decode steps of the sequences with {xs[0]}, {xs[1]} and {xs[2]} "
+                      f"keys of layer 0, each the median of {CPU_RUNS} runs on {nthreads} OpenMP "
+                      f"threads, fitted t = a + b keys (a {a * 1e3:.3g} ms, b {b * 1e9:.4g} ns) "
+                      f"and summed over the 16 sequences and {layers} layers; {cpu_model()}",
+            "sample_s": [round(x, 4) for x in ts],
+            "single_thread": {
+                "value": round(single[1] * sum(keys) / single[0] * layers * 1e6, 1),
+                "unit": "us/step", "cores": 1,
+                "sample": f"one thread, the {single[0]}-key sequence's step, median of {CPU_RUNS} "
+                          f"runs, scaled by the step's {sum(keys)} keys per layer and {layers} "
+                          f"layers"}}
 
 
 def run_config5_paged(args, lens, chans):
