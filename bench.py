@@ -71,10 +71,10 @@ def cpu_model() -> str:
         return "unknown"
 
 
-def append_roofline(kernel, bound, tokens, heads, us):
-    """Roofline entry of a quantize-append launch: f32 K and V in, packed Q4K rows out
-    (head_dim 256: 1024 B in and 144 B out per row and tensor)."""
-    nbytes = 2 * heads * tokens * (256 * 4 + Q4K_ROW)
+def append_roofline(kernel, bound, tokens, heads, us, row=None):
+    """Roofline entry of a quantize-append launch: f32 K and V in, packed rows out
+    (head_dim 256: 1024 B in and `row` B out per row and tensor; Q4K 144 B, Q8_0 272 B)."""
+    nbytes = 2 * heads * tokens * (256 * 4 + (Q4K_ROW if row is None else row))
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"kernel": kernel, "bound": bound, "bytes_per_launch": nbytes,
             "avg_launch_us": round(us, 2), "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
@@ -403,7 +403,7 @@ def cpu_baseline_decode(cache, kn, vn, q, S, threads, config, quant, layers, sin
     }
 
 
-def cpu_baseline_prefill(cache, kc, vc, qc, k1, v1, q1, S, C, threads):
+def cpu_baseline_prefill(cache, kc, vc, qc, k1, v1, q1, S, C, threads, quant=4):
     """Config 2's step on the oracle's faithful CPU path: quantize-append the C-token chunk,
     causal attention of its C queries over S + C keys, then one decode step (append 1
     token, attend S + C + 1 keys). The chunk attention is timed on two samples of its last
@@ -417,7 +417,7 @@ def cpu_baseline_prefill(cache, kc, vc, qc, k1, v1, q1, S, C, threads):
     k1n, v1n, q1n = k1.cpu().numpy(), v1.cpu().numpy(), q1.cpu().numpy()
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
-    c = orc.Cache(4, 1, W.NUM_KV_HEADS, W.HEAD_DIM, S + C + 1)
+    c = orc.Cache(quant, 1, W.NUM_KV_HEADS, W.HEAD_DIM, S + C + 1)
     cache.truncate(S)
     kb, vb = cache.raw_bytes()
     c.load_bytes(kb.cpu().numpy(), vb.cpu().numpy(), S)
@@ -548,15 +548,18 @@ def run_config1(args):
 
 # ------------------------------------------------------------------ config 2
 def run_config2(args):
-    """Q4K, capacity 32768, 16384 cached: append a 512-token chunk and run its causal
-    attention over 16896 keys (q_offset 16384), as FullAttention::forward does for a
-    prefill chunk."""
+    """Q4K (or Q8_0 with --quant q8_0), capacity 32768, 16384 cached: append a 512-token
+    chunk and run its causal attention over 16896 keys (q_offset 16384), as
+    FullAttention::forward does for a prefill chunk."""
     import torch
     import paramecia_amd as pk
     from paramecia_amd import workloads as W
 
     S, C, cap = 16384, 512, 32768
-    c = pk.PreallocatedQuantizedKvCache(1, 2, cap, 256, pk.KvCacheQuantization.Q4K)
+    q8 = args.quant == "q8_0"
+    qname = "Q8_0" if q8 else "Q4K"
+    quant = pk.KvCacheQuantization.Q8_0 if q8 else pk.KvCacheQuantization.Q4K
+    c = pk.PreallocatedQuantizedKvCache(1, 2, cap, 256, quant)
     kb = torch.empty((1, 2, S, 256), device="cuda")
     vb = torch.empty_like(kb)
     pk.fill_normal(kb, W.SEED, W.stream_id(2, W.T_PREFILL_K))
@@ -604,7 +607,7 @@ def run_config2(args):
                          args.warmup, reps)
     flops = 16 * (C * S + C * (C + 1) // 2) * 256 * 2 * 2
     tf = flops / (ms_attn * 1e-3) / 1e12
-    workload = ("config2: Q4K cache with 16384 tokens; step = quantize-append a 512-token "
+    workload = (f"config2: {qname} cache with 16384 tokens; step = quantize-append a 512-token "
                 "chunk + causal attention of its 512 queries over 16896 keys + one decode "
                 "step (append 1 token, attend 16897 keys)")
     extra = {}
@@ -622,23 +625,25 @@ def run_config2(args):
                         args.warmup, 20)
     extra["append_chunk_us"] = round(app_ms * 1000, 2)
     extra["append_roofline"] = append_roofline(
-        f"q4k_append_kernel<4> ({C}-token chunk, four lanes per sub-block fit)", "latency", C,
-        2, app_ms * 1000)
+        (f"q8_0_append_kernel ({C}-token chunk)" if q8 else
+         f"q4k_append_kernel<4> ({C}-token chunk, four lanes per sub-block fit)"), "latency", C,
+        2, app_ms * 1000, row=272 if q8 else Q4K_ROW)
     if not args.no_cpu_baseline:
         extra["cpu_baseline"] = cpu_baseline_prefill(c, kc, vc, qc, k1, v1, q1, S, C,
-                                                     args.cpu_threads)
-    return base_result(2, "Q4K prefill chunk + decode µs (512-token append, 512 x 16896 causal "
-                       "attention, 1-token decode over 16897 keys)",
+                                                     args.cpu_threads, int(quant))
+    return base_result(2, f"{qname} prefill chunk + decode µs (512-token append, 512 x 16896 "
+                       "causal attention, 1-token decode over 16897 keys)",
                        round(ms * 1000, 2), "us/step", False, ms, args, workload,
                        {**extra, "graph_steps_per_replay": reps,
                         "one_step_graph_us_per_step": round(ms_1 * 1000, 2),
                         "prefill_attention_us": round(ms_attn * 1000, 2),
-                        "roofline": {"kernel": "pkv_attend prefill chunk (q4k_prefill_kernel + "
-                                     "split merge)",
+                        "roofline": {"kernel": "pkv_attend prefill chunk (%s + "
+                                     "prefill_merge_kernel)" % ("q8_prefill_kernel" if q8 else
+                                                                "q4k_prefill_kernel"),
                                      "bound": "mfma", "achieved": round(tf, 2),
                                      "peak": FP16_DENSE_TFLOPS, "unit": "TFLOP/s",
                                      "frac": round(tf / FP16_DENSE_TFLOPS, 5), "flops": flops,
-                                     "traffic": traffic(2)}})
+                                     "traffic": traffic("2q8" if q8 else 2)}})
 
 
 # ------------------------------------------------------------------ config 4
@@ -1174,6 +1179,8 @@ def main() -> int:
     ap.add_argument("--op-wtype", default="q4k", choices=["q4k", "q5k", "q6k", "q8_0"],
                     help="config 7: GGUF type of wo")
     ap.add_argument("--cached", type=int, default=131072, help="config 3: cached tokens")
+    ap.add_argument("--quant", default="q4k", choices=["q4k", "q8_0"],
+                    help="config 2: cache quantization")
     ap.add_argument("--paged", type=int, default=0,
                     help="config 5: run the workload on paged caches with this many tokens "
                          "per page (a power of two)")

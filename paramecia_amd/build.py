@@ -29,6 +29,7 @@ SOURCES = {
     "pkv_attn_mfma.hip": [],
     "pkv_attn_mfma_prep.hip": [],
     "pkv_prefill_mfma.hip": [],
+    "pkv_prefill_q8.hip": [],
     "pkv_q8_decode.hip": [],
     "pkv_util.hip": [],
     "pkv_deltanet.hip": [],

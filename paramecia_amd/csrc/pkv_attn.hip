@@ -30,6 +30,7 @@ int launch_append_attend_batched_q8(int quant, const SeqDesc *seqs, int n, const
                                     Workspace &ws, hipStream_t s);
 // Prefill chunk (l > 1) over Q4K rows of the Qwen3-Next shape (pkv_prefill_mfma.hip).
 int launch_prefill_mfma(const AttnArgs &a, Workspace &ws, hipStream_t s);
+int launch_prefill_q8_mfma(const AttnArgs &a, Workspace &ws, hipStream_t s);
 
 namespace {
 
@@ -230,6 +231,8 @@ int launch_attend(const AttnArgs &a, Workspace &ws, hipStream_t s) {
   rc = launch_attend_q8(a, nullptr, nullptr, nullptr, nullptr, -1, ws, s);
   if (rc != PKV_ERR_UNSUPPORTED) return rc;
   rc = launch_prefill_mfma(a, ws, s);
+  if (rc != PKV_ERR_UNSUPPORTED) return rc;
+  rc = launch_prefill_q8_mfma(a, ws, s);
   if (rc != PKV_ERR_UNSUPPORTED) return rc;
   return launch_attend_generic(a, ws, s);
 }

@@ -27,30 +27,11 @@
 //       the f32 rounding of a sum that long then grew with the keys of a split (row
 //       errors of 1e-4 of the row at 4k keys per split; about 5e-6 centred).
 #include "pkv_mfma_common.hpp"
+#include "pkv_prefill_common.hpp"
 
 namespace pkv {
 
 namespace {
-
-constexpr int kPfWaves = 8;
-constexpr int kPfThreads = 64 * kPfWaves;
-constexpr int kPosPerWG = 16;  // query positions per workgroup, two per wave
-constexpr int kRaw = 3;        // raw Q4K block stages in flight
-constexpr int kPfTargetWGs = 256;
-constexpr float kPfLazy = 8.0f;
-
-struct PrefillArgs {
-  const float *q;  // [B][l][16][256]
-  const uint8_t *k, *v;
-  int64_t rs_b, rs_t, rs_h;
-  int64_t seq_k;     // keys in the cache
-  int64_t q_offset;  // query i sees key j iff !causal || j <= i + q_offset
-  int l, causal;
-  int ntiles, nsplit, bps;  // position tiles, key splits, blocks per split
-  float sl2;                // scale * log2(e)
-  float *part;  // [B * nsplit][2][l * 8][258] partials in tile order (nsplit > 1)
-  float *out;   // [B][l][16][256] (nsplit == 1)
-};
 
 // Fp16 operand fragments and tables of one 32-key block of one KV head.
 struct DqBlock {
@@ -508,54 +489,6 @@ __global__ __launch_bounds__(kPfThreads) void q4k_prefill_kernel(PrefillArgs a) 
   }
 }
 
-// Merge the key splits: out[b][pos][8 kvg + hh][e] = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
-// One workgroup of 256 threads per 8 rows and batch: 32 threads per row, each taking 8
-// consecutive tile-order entries; every split's (m, l) and entries are loaded before any
-// is used (nsplit <= kMaxMergeSplits).
-constexpr int kMaxMergeSplits = 16;
-__global__ __launch_bounds__(256) void q4k_prefill_merge_kernel(const float *part, int nsplit,
-                                                                int l, float *out) {
-  const int r8 = threadIdx.x >> 5, j = threadIdx.x & 31;
-  const int row = blockIdx.x * 8 + r8, b = blockIdx.y;  // row = kvg * l * 8 + pos * 8 + hh
-  if (row >= 2 * l * 8) return;
-  const int kvg = row / (l * 8), rr = row % (l * 8), pos = rr >> 3, hh = rr & 7;
-  const int64_t split_stride = (int64_t)2 * l * 8 * 258;
-  const float *base = part + (((int64_t)(b * nsplit) * 2 + kvg) * l * 8 + rr) * 258;
-  float2 ml[kMaxMergeSplits], v[kMaxMergeSplits][4];
-#pragma unroll
-  for (int s = 0; s < kMaxMergeSplits; ++s) {
-    if (s < nsplit) {
-      const float *pr = base + s * split_stride;
-      ml[s] = *reinterpret_cast<const float2 *>(pr + 256);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) v[s][k] = *reinterpret_cast<const float2 *>(pr + 8 * j + 2 * k);
-    }
-  }
-  float M = -INFINITY;
-#pragma unroll
-  for (int s = 0; s < kMaxMergeSplits; ++s)
-    if (s < nsplit) M = fmaxf(M, ml[s].x);
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, L = 0.0f;
-#pragma unroll
-  for (int s = 0; s < kMaxMergeSplits; ++s) {
-    if (s < nsplit) {
-      const float f = (ml[s].x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ml[s].x - M);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        acc[2 * k] += f * v[s][k].x;
-        acc[2 * k + 1] += f * v[s][k].y;
-      }
-      L += f * ml[s].y;
-    }
-  }
-  float *orow = out + (((int64_t)b * l + pos) * 16 + 8 * kvg + hh) * 256;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int idx = 8 * j + k;
-    orow[tile_e(idx >> 4, idx & 15)] = L > 0.0f ? acc[k] / L : 0.0f;
-  }
-}
-
 }  // namespace
 
 int launch_prefill_mfma(const AttnArgs &a, Workspace &ws, hipStream_t s) {
@@ -566,44 +499,12 @@ int launch_prefill_mfma(const AttnArgs &a, Workspace &ws, hipStream_t s) {
       (uint64_t)a.seq_k * (uint64_t)a.rs.t >= (1ull << 32))
     return PKV_ERR_UNSUPPORTED;
   PrefillArgs d;
-  d.q = a.q;
-  d.k = a.k;
-  d.v = a.v;
-  d.rs_b = a.rs.b;
-  d.rs_t = a.rs.t;
-  d.rs_h = a.rs.h;
-  d.seq_k = a.seq_k;
-  d.q_offset = a.q_offset;
-  d.l = a.l;
-  d.causal = a.causal ? 1 : 0;
-  d.sl2 = a.scale * kLog2e;
-  d.ntiles = (a.l + kPosPerWG - 1) / kPosPerWG;
-  const int nblk = (int)((a.seq_k + kBlk - 1) / kBlk);
-  const int base = d.ntiles * 2 * a.batch;
-  int nsplit = (kPfTargetWGs + base - 1) / base;
-  if (nsplit > kMaxMergeSplits) nsplit = kMaxMergeSplits;
-  if (nsplit > nblk) nsplit = nblk > 0 ? nblk : 1;
-  if (nsplit < 1) nsplit = 1;
-  d.bps = (nblk + nsplit - 1) / nsplit;
-  if (d.bps < 1) d.bps = 1;
-  d.nsplit = nsplit;
-  d.out = a.out;
-  d.part = nullptr;
-  if (nsplit > 1) {
-    const size_t need = (size_t)a.batch * nsplit * 2 * a.l * 8 * 258 * sizeof(float);
-    const int rc = ws.reserve(need);
-    if (rc) return rc;
-    d.part = static_cast<float *>(ws.ptr);
-  }
-  hipLaunchKernelGGL(q4k_prefill_kernel, dim3((unsigned)d.ntiles, 2u, (unsigned)(nsplit * a.batch)),
+  const int rc = prefill_plan(a, a.scale * kLog2e, ws, d);
+  if (rc) return rc;
+  hipLaunchKernelGGL(q4k_prefill_kernel, dim3((unsigned)d.ntiles, 2u, (unsigned)(d.nsplit * a.batch)),
                      dim3(kPfThreads), 0, s, d);
   PKV_HIP(hipGetLastError());
-  if (nsplit > 1) {
-    hipLaunchKernelGGL(q4k_prefill_merge_kernel, dim3((unsigned)((2 * a.l * 8 + 7) / 8), (unsigned)a.batch),
-                       dim3(256), 0, s, d.part, nsplit, a.l, a.out);
-    PKV_HIP(hipGetLastError());
-  }
-  return PKV_OK;
+  return prefill_merge(d, a.batch, s);
 }
 
 }  // namespace pkv
