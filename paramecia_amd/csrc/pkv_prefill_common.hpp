@@ -29,10 +29,25 @@ struct PrefillArgs {
   int64_t q_offset;  // query i sees key j iff !causal || j <= i + q_offset
   int l, causal;
   int ntiles, nsplit, bps;  // position tiles, key splits, blocks per split
+  int ngroups;              // (batch, split, KV head) groups: 2 * nsplit * batch
   float sl2;                // scale * log2(e)
   float *part;  // [B * nsplit][2][l * 8][258] partials in tile order (nsplit > 1)
   float *out;   // [B][l][16][256] (nsplit == 1)
 };
+
+// A workgroup's tile, KV head, key split and batch row in the 1-D grid of ntiles *
+// ngroups workgroups: consecutive workgroups take consecutive (batch, split, KV head)
+// groups. The dispatcher deals workgroups to the 8 XCDs round-robin, so with 8 groups
+// (the 512-token chunk: 2 KV heads x 4 splits) every workgroup that streams one group's
+// key range runs on one XCD and the range is fetched into that XCD's L2 once, not by all
+// eight.
+struct PfWork {
+  int tile, kvg, split, b;
+};
+__device__ __forceinline__ PfWork prefill_work(const PrefillArgs &a) {
+  const int L = blockIdx.x, grp = L % a.ngroups, z = grp >> 1;
+  return PfWork{L / a.ngroups, grp & 1, z % a.nsplit, z / a.nsplit};
+}
 
 // Merge the key splits: out[b][pos][8 kvg + hh][e] = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
 // One workgroup of 256 threads per 8 rows and batch: 32 threads per row, each taking 8
@@ -107,6 +122,7 @@ static inline int prefill_plan(const AttnArgs &a, float sl2, Workspace &ws, Pref
   d.bps = (nblk + nsplit - 1) / nsplit;
   if (d.bps < 1) d.bps = 1;
   d.nsplit = nsplit;
+  d.ngroups = 2 * nsplit * a.batch;
   d.out = a.out;
   d.part = nullptr;
   if (nsplit > 1) {

@@ -225,8 +225,8 @@ __global__ __launch_bounds__(kPfThreads) void q4k_prefill_kernel(PrefillArgs a) 
   __shared__ PfSmem sm;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
-  const int tile = blockIdx.x, kvg = blockIdx.y;
-  const int split = blockIdx.z % a.nsplit, b = blockIdx.z / a.nsplit;
+  const PfWork wk = prefill_work(a);
+  const int tile = wk.tile, kvg = wk.kvg, split = wk.split, b = wk.b;
   const int p0 = tile * kPosPerWG;
   const int pw = p0 + 2 * wave;  // this wave's first position; row n -> pw + n / 8
 
@@ -501,7 +501,7 @@ int launch_prefill_mfma(const AttnArgs &a, Workspace &ws, hipStream_t s) {
   PrefillArgs d;
   const int rc = prefill_plan(a, a.scale * kLog2e, ws, d);
   if (rc) return rc;
-  hipLaunchKernelGGL(q4k_prefill_kernel, dim3((unsigned)d.ntiles, 2u, (unsigned)(d.nsplit * a.batch)),
+  hipLaunchKernelGGL(q4k_prefill_kernel, dim3((unsigned)(d.ntiles * d.ngroups)),
                      dim3(kPfThreads), 0, s, d);
   PKV_HIP(hipGetLastError());
   return prefill_merge(d, a.batch, s);

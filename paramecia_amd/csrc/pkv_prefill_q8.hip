@@ -11,10 +11,11 @@
 //
 // Work split (as the Q4K prefill kernel): a workgroup owns one KV head, 16 query
 // positions (128 rows = 16 positions x 8 heads of the group, 16 rows per wave) and one
-// split of the keys. Every 32-key block is staged raw in LDS by waves 5 and 6 (nine
+// split of the keys. Every 32-key block is staged raw in LDS by waves 6 and 7 (nine
 // 16-byte loads per tensor, lane-addressed) and dequantized ONCE into fp16 MFMA operand
-// fragments in LDS - K by waves 0-1, V by waves 2, 3, 4 and 7 - which all eight waves
-// then consume, so the dequantization is shared by 128 query rows.
+// fragments in LDS - K by waves 0-1, V by waves 2-5 - which all eight waves then
+// consume, so the dequantization is shared by 128 query rows. (Wave w runs on SIMD w % 4:
+// each SIMD holds one K or V dequantizing wave and one more.)
 //
 // Arithmetic (exact fp16 operands or hi + lo pairs, f32 accumulation):
 //   QK: per Q8 block j (32 elements, one MFMA K step), A[key][e] = int8 codes (exact in
@@ -23,7 +24,9 @@
 //   PV: B[key][e] = int8 * d (at most 18 significant bits) as an fp16 hi part and the
 //       exact lo remainder, A[row][key] = p as fp16 hi and lo parts: hi*hi + lo*hi +
 //       hi*lo in f32 (the dropped lo*lo is 2^-22 of a term). One fp16 rounding of V
-//       would put row errors near 3e-4 of the row.
+//       would put row errors near 3e-4 of the row. The output columns are in the
+//       decode kernels' tile order (column n of tile T is element tile_e(T, n)), so that
+//       a lane's four consecutive codes of one block feed four tiles.
 // Keys are permuted inside a block so that the QK result layout equals the PV
 // A-operand layout (lane (n, g) holds keys 8g..8g+7 of row n): the scores never leave
 // registers.
@@ -46,7 +49,7 @@ struct Q8Raw {
 struct Q8Dq {
   h8 ka[2][8][64];            // QK A: [tile][Q8 block j][lane]
   float kd[8][kBlk];          // d_j * scale * log2(e) per key
-  h8 vh[16][64], vl[16][64];  // PV B hi / lo: [16-element tile][lane]
+  h8 vh[16][64], vl[16][64];  // PV B hi / lo: [tile][lane]
 };
 struct Q8PfSmem {
   Q8Raw raw[kRaw];
@@ -98,38 +101,58 @@ __device__ __forceinline__ void q8_dq_keys(const Q8Raw &st, Q8Dq &D, float sl2, 
   }
 }
 
-// Waves 2, 3, 4, 7 (vw = 0..3): the PV B fragments of blocks 2 vw and 2 vw + 1 (tiles
-// 4 vw .. 4 vw + 3): lane (n, g) takes element 16 T + n of keys 8 g .. 8 g + 7.
-__device__ __forceinline__ void q8_dq_values(const Q8Raw &st, Q8Dq &D, int vw, int lane) {
+// {fp16(a0 - c0), fp16(a1 - c1)} for the fp16 halves c0, c1 of cw, each rounded once
+// from the exact f32 difference (v_fma_mix). The words are only stored to LDS (no MFMA
+// reads them), so no wait states follow.
+__device__ __forceinline__ uint32_t lo_pair(float a0, float a1, uint32_t cw) {
+  uint32_t d;
+  asm("v_fma_mixlo_f16 %0, %1, 1.0, -%3 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %0, %2, 1.0, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+      : "=&v"(d)
+      : "v"(a0), "v"(a1), "v"(cw));
+  return d;
+}
+
+// Waves 2-5 (vw = 0..3, kHl = vw & 1): the PV B fragments of the four tiles
+// T = 8 h + kHl + 2 b (h = vw >> 1, b = 0..3), whose columns follow the decode kernels'
+// tile order (column n of tile T is element tile_e(T, n)): lane (n, g) takes, for each
+// of keys 8 g .. 8 g + 7, the four codes 4 (n & 7) .. + 3 of block j = 4 h + 2 (n >> 3) +
+// kHl (one dword, two bytes past a dword boundary for even j), code b going to tile
+// 8 h + kHl + 2 b. Each value int8 * d (at most 18 significant bits, exact in f32: the
+// code + 128 times d, minus 128 d, in one fma) becomes an fp16 hi part and the exact lo
+// remainder.
+template <int kHl>
+__device__ __forceinline__ void q8_dq_values(const Q8Raw &st, Q8Dq &D, int h, int lane) {
   const int n = lane & 15, g = lane >> 4;
+  const int j = 4 * h + 2 * (n >> 3) + kHl;
+  const int cw = (34 * j + 2 + 4 * (n & 7)) >> 2;  // first dword of the four codes
+  const int dw = (34 * j) >> 2;                     // dword of d: low half (even j) or high
   const uint32_t *rows = reinterpret_cast<const uint32_t *>(st.v);
-#pragma unroll 1  // (unrolled, the dequantization's loads exceed the registers)
-  for (int jj = 0; jj < 2; ++jj) {
-    const int j = 2 * vw + jj;
-    float d[8];
+  uint32_t wh[4][4], wl[4][4];  // [b][key pair]: fp16 hi / lo words of keys 2p, 2p + 1
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t dw = rows[((8 * g + k) * kQ8RowB + 34 * j) >> 2];
-      d[k] = h2f((j & 1) ? (dw >> 16) : (dw & 0xFFFF));
+  for (int p = 0; p < 4; ++p) {
+    float v[2][4];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const uint32_t *row = rows + (8 * g + 2 * p + kk) * (kQ8RowB / 4);
+      uint32_t w = kHl ? row[cw] : __builtin_amdgcn_alignbyte(row[cw + 1], row[cw], 2);
+      w ^= 0x80808080u;  // code + 128 in each byte
+      const uint32_t dd = row[dw];
+      const float d = h2f(kHl ? (dd >> 16) : (dd & 0xFFFF)), nd = -128.0f * d;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) v[kk][b] = fmaf((float)((w >> (8 * b)) & 0xFFu), d, nd);
     }
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int T = 2 * j + tt;
-      const int e = 16 * T + n;
-      h8 hi8, lo8;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int byte = (8 * g + k) * kQ8RowB + 34 * j + 2 + (e & 31);
-        const uint32_t w = rows[byte >> 2];
-        const int32_t c = __builtin_amdgcn_sbfe(w, 8 * (byte & 3), 8);
-        const float v = (float)c * d[k];  // exact: 8 x 11 bits
-        const _Float16 h = (_Float16)v;
-        hi8[k] = h;
-        lo8[k] = (_Float16)(v - (float)h);  // the exact remainder (at most 7 bits)
-      }
-      D.vh[T][lane] = hi8;
-      D.vl[T][lane] = lo8;
+    for (int b = 0; b < 4; ++b) {
+      wh[b][p] = as_u(h2{(_Float16)v[0][b], (_Float16)v[1][b]});
+      wl[b][p] = lo_pair(v[0][b], v[1][b], wh[b][p]);
     }
+  }
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int T = 8 * h + kHl + 2 * b;
+    D.vh[T][lane] = __builtin_bit_cast(h8, u4{wh[b][0], wh[b][1], wh[b][2], wh[b][3]});
+    D.vl[T][lane] = __builtin_bit_cast(h8, u4{wl[b][0], wl[b][1], wl[b][2], wl[b][3]});
   }
 }
 
@@ -189,8 +212,8 @@ __global__ __launch_bounds__(kPfThreads) void q8_prefill_kernel(PrefillArgs a) {
   __shared__ Q8PfSmem sm;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
-  const int tile = blockIdx.x, kvg = blockIdx.y;
-  const int split = blockIdx.z % a.nsplit, b = blockIdx.z / a.nsplit;
+  const PfWork wk = prefill_work(a);
+  const int tile = wk.tile, kvg = wk.kvg, split = wk.split, b = wk.b;
   const int p0 = tile * kPosPerWG;
   const int pw = p0 + 2 * wave;  // this wave's first position; row n -> pw + n / 8
 
@@ -215,10 +238,10 @@ __global__ __launch_bounds__(kPfThreads) void q8_prefill_kernel(PrefillArgs a) {
   const u4s rk = make_rsrc(kbase, span), rv = make_rsrc(vbase, span);
   const Q8Plan P = make_q8_plan(lane, rs_t);
   const uint32_t bbytes = kBlk * rs_t;
-  const bool loader = wave == 5 || wave == 6;
+  const bool loader = wave >= 6;
   auto issue = [&](int i) {  // raw block i of this workgroup into stage i % kRaw
-    if (wave == 5) issue_q8_tensor(sm.raw[i % kRaw].k, P, rk, (uint32_t)(kb0 + i) * bbytes);
-    if (wave == 6) issue_q8_tensor(sm.raw[i % kRaw].v, P, rv, (uint32_t)(kb0 + i) * bbytes);
+    if (wave == 6) issue_q8_tensor(sm.raw[i % kRaw].k, P, rk, (uint32_t)(kb0 + i) * bbytes);
+    if (wave == 7) issue_q8_tensor(sm.raw[i % kRaw].v, P, rv, (uint32_t)(kb0 + i) * bbytes);
   };
   if (loader) {
     if (nb > 0) issue(0);
@@ -255,7 +278,7 @@ __global__ __launch_bounds__(kPfThreads) void q8_prefill_kernel(PrefillArgs a) {
   const int64_t myq = (int64_t)pw + (n >> 3);
   const int64_t klim = a.causal ? myq + a.q_offset : (int64_t)1 << 62;
 
-  // Waves 0-4 and 7 build the fp16 operands of block i + 1 while every wave runs the
+  // Waves 0-5 build the fp16 operands of block i + 1 while every wave runs the
   // MFMAs of block i: one barrier per block. Raw stages rotate over kRaw = 3 (blocks
   // i + 1 and i + 2 in flight or landed while block i + 3 is issued).
   auto dequant = [&](int blk) {
@@ -263,10 +286,13 @@ __global__ __launch_bounds__(kPfThreads) void q8_prefill_kernel(PrefillArgs a) {
     Q8Dq &Dn = sm.dq[blk & 1];
     if (wave < 2)
       q8_dq_keys(st, Dn, a.sl2, wave, lane);
-    else if (wave < 5)
-      q8_dq_values(st, Dn, wave - 2, lane);
-    else if (wave == 7)
-      q8_dq_values(st, Dn, 3, lane);
+    else if (wave < 6) {
+      const int vw = __builtin_amdgcn_readfirstlane(wave - 2);
+      if (vw & 1)
+        q8_dq_values<1>(st, Dn, vw >> 1, lane);
+      else
+        q8_dq_values<0>(st, Dn, vw >> 1, lane);
+    }
   };
   if (nb > 0) {
     if (loader) {  // block 0 landed (block 1 may still fly)
@@ -384,7 +410,7 @@ __global__ __launch_bounds__(kPfThreads) void q8_prefill_kernel(PrefillArgs a) {
       float *orow = a.out + (((int64_t)b * a.l + pos) * 16 + 8 * kvg + (row & 7)) * 256;
       const float inv = lrow[ii] > 0.0f ? 1.0f / lrow[ii] : 0.0f;
 #pragma unroll
-      for (int T = 0; T < 16; ++T) orow[16 * T + n] = acc[T][ii] * inv;
+      for (int T = 0; T < 16; ++T) orow[tile_e(T, n)] = acc[T][ii] * inv;
     }
   } else {
     float *pz = a.part + (((int64_t)(b * a.nsplit + split) * 2 + kvg) * a.l * 8) * 258;
@@ -395,7 +421,7 @@ __global__ __launch_bounds__(kPfThreads) void q8_prefill_kernel(PrefillArgs a) {
       if (pos >= a.l) continue;
       float *prow = pz + ((int64_t)pos * 8 + (row & 7)) * 258;
 #pragma unroll
-      for (int T = 0; T < 16; ++T) prow[tile_index(16 * T + n)] = acc[T][ii];
+      for (int T = 0; T < 16; ++T) prow[16 * T + n] = acc[T][ii];
       if (n == 0) {
         prow[256] = mrow[ii];
         prow[257] = lrow[ii];
@@ -418,7 +444,7 @@ int launch_prefill_q8_mfma(const AttnArgs &a, Workspace &ws, hipStream_t s) {
   PrefillArgs d;
   const int rc = prefill_plan(a, a.scale * kLog2e, ws, d);
   if (rc) return rc;
-  hipLaunchKernelGGL(q8_prefill_kernel, dim3((unsigned)d.ntiles, 2u, (unsigned)(d.nsplit * a.batch)),
+  hipLaunchKernelGGL(q8_prefill_kernel, dim3((unsigned)(d.ntiles * d.ngroups)),
                      dim3(kPfThreads), 0, s, d);
   PKV_HIP(hipGetLastError());
   return prefill_merge(d, a.batch, s);
