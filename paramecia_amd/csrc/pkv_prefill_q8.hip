@@ -306,6 +306,10 @@ __global__ __launch_bounds__(kPfThreads) void q8_prefill_kernel(PrefillArgs a) {
     dequant(0);
   }
   static_assert(kQ8Loads == 9, "the vmcnt waits count one tensor's loads");
+  // Waves 4 and 5 share SIMDs 0 and 1 with waves 0 and 1, which also dequantize: they
+  // build block i + 1's operands after block i's MFMAs instead of before, so that on each
+  // SIMD one wave's dequantization meets the other's MFMAs.
+  const bool late = wave == 4 || wave == 5;
   for (int i = 0; i < nb; ++i) {
     if (loader && i + 1 < nb) {  // block i + 1 landed (block i + 2 may still fly)
       if (i + 2 < nb)
@@ -317,7 +321,7 @@ __global__ __launch_bounds__(kPfThreads) void q8_prefill_kernel(PrefillArgs a) {
     // block i's raw stage no longer read
     __syncthreads();
     if (loader && i + 3 < nb) issue(i + 3);
-    if (i + 1 < nb) dequant(i + 1);
+    if (i + 1 < nb && !late) dequant(i + 1);
     const Q8Dq &D = sm.dq[i & 1];
 
     // ---- QK (two tiles of 16 keys); keys of the block at or past nlim are masked (past
@@ -390,6 +394,7 @@ __global__ __launch_bounds__(kPfThreads) void q8_prefill_kernel(PrefillArgs a) {
       acc[T] = mfma32(Al, Bh, acc[T]);
       acc[T] = mfma32(A, Bl, acc[T]);
     }
+    if (i + 1 < nb && late) dequant(i + 1);
   }
 
   // ---- epilogue: row sums, then the output or the split's partial
