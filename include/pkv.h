@@ -52,7 +52,8 @@ enum {
   PKV_ERR_EMPTY = 5,      /* "Cannot get storage from empty cache" (qn:583-585) */
   PKV_ERR_LAYERS = 6,     /* "Prefix cache layer count mismatch" (qn:5727-5733) */
   PKV_ERR_LAYOUT = 7,     /* snapshot does not fit the cache (quant/heads/dims) */
-  PKV_ERR_UNSUPPORTED = 8 /* combination with no kernel (e.g. head_dim > 512) */
+  PKV_ERR_UNSUPPORTED = 8 /* combination with no kernel (e.g. head_dim > 512), or a call that
+                             allocates, made on a capturing stream */
 };
 
 /* Entry kinds of a prefix cache layer (PrefixCacheEntry, qn:834-854). */
