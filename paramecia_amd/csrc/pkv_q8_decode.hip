@@ -227,9 +227,11 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
     }
     __syncthreads();
 
-    // ---- PV: element e = t of the 8 heads: acc = acc * alpha + sum_k p * (d_j * q8)
+    // ---- PV: element e = tile_e(t / 16, t % 16) of the 8 heads (thread t holds the
+    // partial's tile-order entry t, so that its stores are contiguous across lanes):
+    // acc = acc * alpha + sum_k p * (d_j * q8)
     {
-      const int e = t, j = e >> 5, ob = 34 * j + 2 + (e & 31);
+      const int e = tile_e(t >> 4, t & 15), j = e >> 5, ob = 34 * j + 2 + (e & 31);
 #pragma unroll
       for (int h = 0; h < 8; ++h) acc[h] *= sm.alpha[half][h];
       const int wd = (34 * j) >> 2, hd = ((34 * j) >> 1) & 1, wq = ob >> 2, sq = 8 * (ob & 3);
@@ -260,7 +262,7 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
 
   // ---- partial of this workgroup (tile order), m and l per head
   float *P = a.part + (int64_t)wg * 16 * kPartRow;
-  const int idx = tile_index(t);
+  const int idx = t;  // tile-order entry t (element tile_e(t / 16, t % 16))
 #pragma unroll
   for (int h = 0; h < 8; ++h) P[(8 * half + h) * kPartRow + idx] = acc[h];
   if (kk == 0 && dh == 0) a.ml[(int64_t)wg * 16 + 8 * half + hh] = float2{m_run, l_run};
