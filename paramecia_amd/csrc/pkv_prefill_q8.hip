@@ -32,12 +32,12 @@
 // registers.
 #include "pkv_mfma_common.hpp"
 #include "pkv_prefill_common.hpp"
+#include "pkv_q8_common.hpp"
 
 namespace pkv {
 
 namespace {
 
-constexpr int kQ8RowB = 272;        // bytes of one head's Q8_0 row (8 x 34)
 constexpr int kQ8Loads = 9;         // 16-byte loads per lane per tensor and block
 constexpr int kQ8StageB = 9216;     // 32 rows (8704 B) + the last load's overrun
 static_assert(kQ8Loads * 64 * 16 == kQ8StageB && 32 * kQ8RowB <= kQ8StageB, "stage size");
@@ -56,19 +56,6 @@ struct Q8PfSmem {
   Q8Dq dq[2];  // block i's operands in dq[i & 1] while block i + 1's are built
 };
 static_assert(sizeof(Q8PfSmem) <= 160 * 1024, "LDS budget of one workgroup");
-
-// Block-local key of row r of tile t (the QK A layout): lane (n, g) of the QK result
-// then holds keys 8g + 4t + i for row n.
-__device__ __forceinline__ int q8_key(int r, int t) { return 8 * (r >> 2) + 4 * t + (r & 3); }
-
-// Four int8 in a dword -> two dwords of two fp16 each, exactly: the bytes, offset by 128,
-// become the low bytes of fp16 1024 + u (exponent byte 0x64), then 1152 is subtracted.
-__device__ __forceinline__ void i8x4_to_h4(uint32_t w, h2 &lo, h2 &hi) {
-  const uint32_t u = w ^ 0x80808080u;
-  const h2 k = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-  lo = as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + k;
-  hi = as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + k;
-}
 
 // Waves 0-1: the QK A fragments of tile t: lane (r, g) takes key q8_key(r, t), elements
 // 32 j + 8 g .. + 7 of every block j; lanes g = 0 also store the key's d_j * sl2.
@@ -101,53 +88,11 @@ __device__ __forceinline__ void q8_dq_keys(const Q8Raw &st, Q8Dq &D, float sl2, 
   }
 }
 
-// {fp16(a0 - c0), fp16(a1 - c1)} for the fp16 halves c0, c1 of cw, each rounded once
-// from the exact f32 difference (v_fma_mix). The words are only stored to LDS (no MFMA
-// reads them), so no wait states follow.
-__device__ __forceinline__ uint32_t lo_pair(float a0, float a1, uint32_t cw) {
-  uint32_t d;
-  asm("v_fma_mixlo_f16 %0, %1, 1.0, -%3 op_sel_hi:[0,0,1]\n\t"
-      "v_fma_mixhi_f16 %0, %2, 1.0, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
-      : "=&v"(d)
-      : "v"(a0), "v"(a1), "v"(cw));
-  return d;
-}
-
-// Waves 2-5 (vw = 0..3, kHl = vw & 1): the PV B fragments of the four tiles
-// T = 8 h + kHl + 2 b (h = vw >> 1, b = 0..3), whose columns follow the decode kernels'
-// tile order (column n of tile T is element tile_e(T, n)): lane (n, g) takes, for each
-// of keys 8 g .. 8 g + 7, the four codes 4 (n & 7) .. + 3 of block j = 4 h + 2 (n >> 3) +
-// kHl (one dword, two bytes past a dword boundary for even j), code b going to tile
-// 8 h + kHl + 2 b. Each value int8 * d (at most 18 significant bits, exact in f32: the
-// code + 128 times d, minus 128 d, in one fma) becomes an fp16 hi part and the exact lo
-// remainder.
+// Waves 2-5 (vw = 0..3): the PV B fragments of unit vw (q8_v_words), into LDS.
 template <int kHl>
 __device__ __forceinline__ void q8_dq_values(const Q8Raw &st, Q8Dq &D, int h, int lane) {
-  const int n = lane & 15, g = lane >> 4;
-  const int j = 4 * h + 2 * (n >> 3) + kHl;
-  const int cw = (34 * j + 2 + 4 * (n & 7)) >> 2;  // first dword of the four codes
-  const int dw = (34 * j) >> 2;                     // dword of d: low half (even j) or high
-  const uint32_t *rows = reinterpret_cast<const uint32_t *>(st.v);
-  uint32_t wh[4][4], wl[4][4];  // [b][key pair]: fp16 hi / lo words of keys 2p, 2p + 1
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    float v[2][4];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const uint32_t *row = rows + (8 * g + 2 * p + kk) * (kQ8RowB / 4);
-      uint32_t w = kHl ? row[cw] : __builtin_amdgcn_alignbyte(row[cw + 1], row[cw], 2);
-      w ^= 0x80808080u;  // code + 128 in each byte
-      const uint32_t dd = row[dw];
-      const float d = h2f(kHl ? (dd >> 16) : (dd & 0xFFFF)), nd = -128.0f * d;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) v[kk][b] = fmaf((float)((w >> (8 * b)) & 0xFFu), d, nd);
-    }
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      wh[b][p] = as_u(h2{(_Float16)v[0][b], (_Float16)v[1][b]});
-      wl[b][p] = lo_pair(v[0][b], v[1][b], wh[b][p]);
-    }
-  }
+  uint32_t wh[4][4], wl[4][4];
+  q8_v_words<kHl>(reinterpret_cast<const uint32_t *>(st.v), kQ8RowB / 4, h, lane, wh, wl);
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     const int T = 8 * h + kHl + 2 * b;

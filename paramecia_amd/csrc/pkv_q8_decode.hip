@@ -24,6 +24,7 @@
 #include <vector>
 
 #include "pkv_decode_split.hpp"
+#include "pkv_q8_common.hpp"
 #include "pkv_scalar.hpp"
 
 namespace pkv {
@@ -268,6 +269,294 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
   if (kk == 0 && dh == 0) a.ml[(int64_t)wg * 16 + 8 * half + hh] = float2{m_run, l_run};
 }
 
+// ---- MFMA decode over 32-key blocks (caches up to 32k keys per segment)
+//
+// A workgroup of 4 waves owns a key range of one segment (kpw keys, a multiple of 32) and
+// one KV head: workgroup w serves partial slot w / 2 and KV head w % 2. Per 32-key block
+// the head's K and V rows are staged in LDS; wave qd builds the QK A fragments of blocks
+// j = 2 qd, 2 qd + 1 of both 16-key tiles into LDS (int8 codes, exact in fp16) and the PV
+// B fragments of its four 16-column tiles into registers (int8 * d as an exact fp16 hi/lo
+// pair, q8_v_words). Every wave then runs the head's QK: per tile and block j one MFMA
+// with q as B (columns 0-7 the fp16 hi parts of the group's 8 heads, 8-15 the lo
+// remainders, converted once per workgroup), scaled by d_j * scale * log2(e) of its key
+// in f32; the hi and lo columns are summed across lanes n and n ^ 8. The softmax weights
+// enter PV as A rows 0-7 (fp16 hi) and 8-15 (lo remainder): two MFMAs per tile (V hi and
+// lo), rows h and h + 8 summed at the end. The partial goes out in tile order, as the
+// other decode kernels write it, for decode_combine_kernel.
+constexpr int kQ8mThreads = 256;
+struct Q8mSmem {
+  h8 qf[8][64];                      // QK B operands: [block j][lane]
+  uint32_t raw[2][32][kQ8RowWords];  // [K / V][key][row]
+  float kd[8][32];                   // [block j][key]: d_j * sl2
+  float4 sp[4][2][64];               // each wave's partial scores: [wave][tile][lane]
+};
+
+// The MFMA decode is on unless PKV_Q8_MFMA=0 (the VALU kernel, kept for comparison).
+static inline bool q8_mfma_enabled() {
+  static const bool on = [] {
+    const char *e = getenv("PKV_Q8_MFMA");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
+__device__ __forceinline__ float xsum16(float x) {  // x of lanes l and l ^ 16, summed
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
+
+__global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
+  __shared__ Q8mSmem sm;
+  const int tid = threadIdx.x, lane = tid & 63, qd = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int wg = blockIdx.x, slot = wg >> 1, kv = wg & 1;
+  int b = 0;
+  while (b + 1 < a.nseg && slot >= a.seg[b + 1].wg0) ++b;
+  const DecodeSeg sg = a.seg[b];
+  const int64_t k0 = (int64_t)(slot - sg.wg0) * a.kpw;
+  const int64_t k1 = k0 + a.kpw < sg.seq_k ? k0 + a.kpw : sg.seq_k;
+  const uint8_t *kbase = sg.k + kv * a.rs_h, *vbase = sg.v + kv * a.rs_h;
+
+  // ---- fused append: new row r = 4 s + 2 p + kv (K p = 0, V p = 1) by workgroup r; the
+  // first row's input is loaded ahead of q and the first block, and quantized while those
+  // loads are in flight
+  const bool quant = a.k_new != nullptr && wg < 4 * a.nseg;
+  float xq = 0.0f;
+  if (quant) {
+    const int p = (wg >> 1) & 1, kvr = wg & 1;
+    xq = (p ? a.v_new : a.k_new)[((int64_t)(wg >> 2) * 2 + kvr) * 256 + tid];
+    asm volatile("" : "+v"(xq));
+  }
+
+  // head kv's K and V rows (272 bytes per key) of the block at c0, keys past nk as 0:
+  // every load is issued before the first LDS store
+  constexpr int kPieces = 2 * 32 * (kQ8RowB / 16);  // 16-byte pieces of a staged block
+  constexpr int kPer = (kPieces + kQ8mThreads - 1) / kQ8mThreads;
+  uint4 w[kPer];
+  auto load_block = [&](int64_t c0, int nk) {
+#pragma unroll
+    for (int x = 0; x < kPer; ++x) {
+      const int c = tid + x * kQ8mThreads;
+      const int tn = c / (kPieces / 2), r = c % (kPieces / 2);
+      const int key = r / 17, piece = r % 17;
+      w[x] = uint4{0u, 0u, 0u, 0u};
+      if (c < kPieces && key < nk)
+        w[x] = *reinterpret_cast<const uint4 *>((tn ? vbase : kbase) + (c0 + key) * a.rs_t + 16 * piece);
+    }
+  };
+  auto store_block = [&]() {
+#pragma unroll
+    for (int x = 0; x < kPer; ++x) {
+      const int c = tid + x * kQ8mThreads;
+      const int tn = c / (kPieces / 2), r = c % (kPieces / 2);
+      if (c < kPieces) *reinterpret_cast<uint4 *>(&sm.raw[tn][r / 17][4 * (r % 17)]) = w[x];
+    }
+  };
+  // ---- q of the head group as QK B operands, built once: fragment (j, lane (n, g)) holds
+  // elements 32 j + 8 g .. + 7 of head 8 kv + n % 8, as the fp16 hi part (n < 8) or the
+  // lo remainder (n >= 8); thread t builds fragments t and t + 256
+  {
+    float4 qv[2][2];
+#pragma unroll
+    for (int f2 = 0; f2 < 2; ++f2) {
+      const int f = tid + f2 * kQ8mThreads, j = f >> 6, fl = f & 63;
+      const float *qrow = a.q + ((int64_t)sg.qi * 16 + 8 * kv + (fl & 7)) * 256 + 32 * j + 8 * (fl >> 4);
+      qv[f2][0] = *reinterpret_cast<const float4 *>(qrow);
+      qv[f2][1] = *reinterpret_cast<const float4 *>(qrow + 4);
+    }
+    if (k0 < k1) load_block(k0, (int)(k1 - k0 < kBlk ? k1 - k0 : kBlk));
+    if (quant) {
+      for (int row = wg; row < 4 * a.nseg; row += a.nwg) {
+        const int rs = row >> 2, p = (row >> 1) & 1, kvr = row & 1;
+        if (row != wg) xq = (p ? a.v_new : a.k_new)[((int64_t)rs * 2 + kvr) * 256 + tid];
+        const DecodeSeg &rg = a.seg[rs];
+        uint8_t *dst = (p ? rg.v : rg.k) + rg.t_new * a.rs_t + kvr * a.rs_h;
+        a.dq[(int64_t)row * 256 + tid] = q8_quantize_row_lanes(xq, dst, tid);
+      }
+    }
+#pragma unroll
+    for (int f2 = 0; f2 < 2; ++f2) {
+      const int f = tid + f2 * kQ8mThreads, fl = f & 63;
+      const bool lo = (fl & 15) >= 8;
+      const float v8[8] = {qv[f2][0].x, qv[f2][0].y, qv[f2][0].z, qv[f2][0].w,
+                           qv[f2][1].x, qv[f2][1].y, qv[f2][1].z, qv[f2][1].w};
+      h8 fr;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const _Float16 hi = (_Float16)v8[k];
+        fr[k] = lo ? (_Float16)(v8[k] - (float)hi) : hi;
+      }
+      sm.qf[f >> 6][fl] = fr;
+    }
+  }
+
+  f4 acc[4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x) acc[x] = f4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;  // head n % 8 (the same in lanes n, n ^ 8 and every g)
+
+  for (int64_t c0 = k0; c0 < k1; c0 += kBlk) {
+    const int nk = (int)(k1 - c0 < kBlk ? k1 - c0 : kBlk);
+    if (c0 != k0) {
+      __syncthreads();  // the previous block's readers are done
+      load_block(c0, nk);
+    }
+    store_block();
+    __syncthreads();
+    // ---- QK over blocks j = 2 qd, 2 qd + 1, A fragments in registers (lane (r, g): key
+    // q8_key(r, t), elements 32 j + 8 g .. + 7); lanes g = 0 store d_j * sl2 of their key,
+    // read back by this wave's lanes only
+    h8 ka[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int kk = q8_key(n, t);
+      const uint32_t *row = &sm.raw[0][kk][0];
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * qd + jj;  // j & 1 == jj
+        const int w0i = (34 * j + 2 + 8 * g) >> 2;
+        uint32_t w0, w1;
+        if (jj) {
+          w0 = row[w0i];
+          w1 = row[w0i + 1];
+        } else {
+          const uint32_t x0 = row[w0i], x1 = row[w0i + 1], x2 = row[w0i + 2];
+          w0 = __builtin_amdgcn_alignbyte(x1, x0, 2);
+          w1 = __builtin_amdgcn_alignbyte(x2, x1, 2);
+        }
+        h2 a0, a1, a2, a3;
+        i8x4_to_h4(w0, a0, a1);
+        i8x4_to_h4(w1, a2, a3);
+        ka[t][jj] = h8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+        if (g == 0) {
+          const uint32_t dw = row[(34 * j) >> 2];
+          sm.kd[j][kk] = h2f(jj ? (dw >> 16) : (dw & 0xFFFF)) * a.sl2;
+        }
+      }
+    }
+    f4 cq[2][2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const h8 qbj = sm.qf[2 * qd + jj][lane];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) cq[t][jj] = mfma32(ka[t][jj], qbj, f4{0.f, 0.f, 0.f, 0.f});
+    }
+    // ---- PV B fragments of this wave's four tiles, in registers (while the MFMAs run)
+    uint32_t wh[4][4], wl[4][4];
+    if (qd & 1)
+      q8_v_words<1>(&sm.raw[1][0][0], kQ8RowWords, qd >> 1, lane, wh, wl);
+    else
+      q8_v_words<0>(&sm.raw[1][0][0], kQ8RowWords, qd >> 1, lane, wh, wl);
+    // this wave's part of the scores, scaled by its keys' d_j, to LDS
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float4 part = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const float4 dk = *reinterpret_cast<const float4 *>(&sm.kd[2 * qd + jj][8 * g + 4 * t]);
+        part.x = fmaf(dk.x, cq[t][jj][0], part.x);
+        part.y = fmaf(dk.y, cq[t][jj][1], part.y);
+        part.z = fmaf(dk.z, cq[t][jj][2], part.z);
+        part.w = fmaf(dk.w, cq[t][jj][3], part.w);
+      }
+      sm.sp[qd][t][lane] = part;
+    }
+    __syncthreads();  // every wave's part of the scores is in LDS
+
+    // ---- the scores: sc[4 t + i] of key 8 g + 4 t + i for column n, summed over the
+    // waves' blocks in block order (blocks 0-1, 2-3, 4-5, 6-7)
+    float sc[8];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float4 tot = sm.sp[0][t][lane];
+#pragma unroll
+      for (int w2 = 1; w2 < 4; ++w2) {
+        const float4 pw = sm.sp[w2][t][lane];
+        tot.x += pw.x;
+        tot.y += pw.y;
+        tot.z += pw.z;
+        tot.w += pw.w;
+      }
+      sc[4 * t + 0] = tot.x;
+      sc[4 * t + 1] = tot.y;
+      sc[4 * t + 2] = tot.z;
+      sc[4 * t + 3] = tot.w;
+    }
+    // hi + lo columns (lanes n and n ^ 8), clamp, mask the keys past the range
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float s = sc[k] + ror8(sc[k]);
+      sc[k] = 8 * g + k < nk ? fminf(fmaxf(s, -kSplitClampL2), kSplitClampL2) : -INFINITY;
+    }
+    // ---- online softmax of head n % 8 over the block (lanes n, n + 16, n + 32, n + 48)
+    float bm = sc[0];
+#pragma unroll
+    for (int k = 1; k < 8; ++k) bm = fmaxf(bm, sc[k]);
+    bm = xmax32(xmax16(bm));
+    const float m_new = fmaxf(m_run, bm);
+    if (__any(m_new != m_run)) {  // some head's max rose: rescale its sums (rows by head)
+      const float alpha = (m_new == m_run) ? 1.0f
+                          : (m_run == -INFINITY) ? 0.0f
+                                                 : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+      float ai[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ai[i] = __shfl(alpha, (4 * g + i) & 7);  // row 4 g + i
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[x][i] *= ai[i];
+    }
+    m_run = m_new;
+    float p[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      p[k] = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sc[k] - m_run);
+      l_run += p[k];
+    }
+    // A rows: n < 8 the fp16 hi parts of head n's weights, n >= 8 the lo remainders
+    uint32_t wa[4];
+#pragma unroll
+    for (int k2 = 0; k2 < 4; ++k2) {
+      const uint32_t hw = as_u(h2{(_Float16)p[2 * k2], (_Float16)p[2 * k2 + 1]});
+      const uint32_t lw = fp16_sub2(p[2 * k2], p[2 * k2 + 1], hw);
+      wa[k2] = n < 8 ? hw : lw;
+    }
+    const h8 A = __builtin_bit_cast(h8, u4{wa[0], wa[1], wa[2], wa[3]});
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      acc[x] = mfma32(A, __builtin_bit_cast(h8, u4{wh[x][0], wh[x][1], wh[x][2], wh[x][3]}), acc[x]);
+      acc[x] = mfma32(A, __builtin_bit_cast(h8, u4{wl[x][0], wl[x][1], wl[x][2], wl[x][3]}), acc[x]);
+    }
+  }
+
+  // ---- partial: rows h (hi weights) and h + 8 (lo) summed (lanes g and g + 2), tile T =
+  // 8 (qd >> 1) + (qd & 1) + 2 x, entry 16 T + n of head 8 kv + 4 g + i (lanes 0-31)
+  float *P = a.part + (int64_t)slot * 16 * kPartRow;
+  float r[4][4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[x][i] = xsum32(acc[x][i]);
+  if (g < 2) {
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int T = 8 * (qd >> 1) + (qd & 1) + 2 * x;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) P[(8 * kv + 4 * g + i) * kPartRow + 16 * T + n] = r[x][i];
+    }
+  }
+  // the weights' sum of head n % 8 over the lanes g (each holds its 8 keys)
+  float lt = xsum16(l_run);
+  lt = xsum32(lt);
+  if (qd == 0 && g == 0 && n < 8) a.ml[(int64_t)slot * 16 + 8 * kv + n] = float2{m_run, lt};
+}
+
 }  // namespace
 
 // Plan and launch the Q8_0 decode and the combine over n <= kMaxSegs segments.
@@ -288,13 +577,27 @@ static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, cons
   }
   d.dseg = nullptr;
   d.wps = 0;
-  // keys per workgroup: one chunk while that keeps <= 512 partials per segment (16-key
-  // chunks up to 8192 keys, 32-key chunks beyond), more chunks per workgroup for longer
-  // caches
-  int64_t kpw = (longest + 511) / 512;
-  const int chunk = kpw <= 16 ? 16 : kQ8Chunk;
-  kpw = (kpw + chunk - 1) / chunk * chunk;
-  if (kpw < chunk) kpw = chunk;
+  // The MFMA kernel for caches up to 32768 keys in the standard row layout (both heads'
+  // 272-byte rows adjacent, 16-byte aligned): 32-key blocks, one to four per workgroup
+  // (up to 256 workgroups per segment). Otherwise the VALU kernel: one chunk per
+  // workgroup while that keeps <= 512 partials per segment (16-key chunks up to 8192
+  // keys, 32-key chunks beyond), more chunks per workgroup for longer caches.
+  bool mfma = longest <= 32768 && rs_h == kQ8Row && rs_t % 16 == 0 && q8_mfma_enabled();
+  for (int i = 0; i < n && mfma; ++i)
+    mfma = (reinterpret_cast<uintptr_t>(in[i].k) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(in[i].v) & 15) == 0;
+  int64_t kpw;
+  int chunk;
+  if (mfma) {
+    chunk = kBlk;
+    kpw = kBlk * ((longest + 256 * kBlk - 1) / (256 * kBlk));
+    if (kpw < kBlk) kpw = kBlk;
+  } else {
+    kpw = (longest + 511) / 512;
+    chunk = kpw <= 16 ? 16 : kQ8Chunk;
+    kpw = (kpw + chunk - 1) / chunk * chunk;
+    if (kpw < chunk) kpw = chunk;
+  }
   CombineArgs c;
   int wg = 0;
   for (int i = 0; i < n; ++i) {
@@ -320,11 +623,16 @@ static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, cons
   d.part = static_cast<float *>(ws.ptr);
   d.ml = reinterpret_cast<float2 *>(d.part + part_floats);
   d.dq = d.part + part_floats + ml_floats;
-  if (chunk == 16)
+  if (mfma) {  // two workgroups (KV heads) per slot
+    d.nwg = 2 * wg;
+    hipLaunchKernelGGL(q8_decode_mfma_kernel, dim3((unsigned)(2 * wg)), dim3(kQ8mThreads), 0, s,
+                       d);
+  } else if (chunk == 16) {
     hipLaunchKernelGGL(q8_decode_kernel<16>, dim3((unsigned)wg), dim3(kQ8Threads), 0, s, d);
-  else
+  } else {
     hipLaunchKernelGGL(q8_decode_kernel<kQ8Chunk>, dim3((unsigned)wg), dim3(kQ8Threads), 0, s,
                        d);
+  }
   PKV_HIP(hipGetLastError());
   c.part = d.part;
   c.ml = d.ml;

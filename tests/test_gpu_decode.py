@@ -251,11 +251,22 @@ def run_decode_q8(pk, orc, S, B=1, fused=True, seed=0, chans=None):
     return np.abs(got - ref).max()
 
 
+# The MFMA kernel takes caches up to 32768 keys (one 32-key block per workgroup up to
+# 8192, two up to 16384, ...: 8223 and 16385 end in a partial block of a workgroup's last
+# pass); 32769 and 40000 take the VALU kernel's 32-key chunks.
 @pytest.mark.parametrize("S", [0, 1, 15, 16, 17, 31, 32, 33, 511, 512, 513, 4096, 8192, 8193,
-                               20000])
+                               8223, 16385, 20000, 32768, 32769, 40000])
 def test_q8_decode_fused(pk, orc, S):
     say(f"Q8_0 fused decode S={S}")
     run_decode_q8(pk, orc, S, fused=True, seed=300 + S)
+
+
+def test_q8_decode_outliers_multiblock(pk, orc):
+    """Outlier channels (x20) over 20000 keys: three 32-key blocks per MFMA workgroup, so
+    the running max rises between blocks and the sums are rescaled."""
+    say("Q8_0 decode outlier channels, 20000 keys")
+    from paramecia_amd import workloads as W
+    run_decode_q8(pk, orc, 20000, seed=501, chans=W.c5_channels())
 
 
 @pytest.mark.parametrize("S", [1, 64, 4097])
