@@ -312,23 +312,23 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
   const int tid = threadIdx.x, lane = tid & 63, qd = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int wg = blockIdx.x, slot = wg >> 1, kv = wg & 1;
+  // ---- fused append: the 4 n workgroups after the a.nwg decode ones quantize new row
+  // r = 4 s + 2 p + kv (K p = 0, V p = 1) each, so that no decode workgroup ends later
+  // for it
+  if (wg >= a.nwg) {
+    const int row = wg - a.nwg, rs = row >> 2, p = (row >> 1) & 1, kvr = row & 1;
+    const float x = (p ? a.v_new : a.k_new)[((int64_t)rs * 2 + kvr) * 256 + tid];
+    const DecodeSeg &rg = a.seg[rs];
+    uint8_t *dst = (p ? rg.v : rg.k) + rg.t_new * a.rs_t + kvr * a.rs_h;
+    a.dq[(int64_t)row * 256 + tid] = q8_quantize_row_lanes(x, dst, tid);
+    return;
+  }
   int b = 0;
   while (b + 1 < a.nseg && slot >= a.seg[b + 1].wg0) ++b;
   const DecodeSeg sg = a.seg[b];
   const int64_t k0 = (int64_t)(slot - sg.wg0) * a.kpw;
   const int64_t k1 = k0 + a.kpw < sg.seq_k ? k0 + a.kpw : sg.seq_k;
   const uint8_t *kbase = sg.k + kv * a.rs_h, *vbase = sg.v + kv * a.rs_h;
-
-  // ---- fused append: new row r = 4 s + 2 p + kv (K p = 0, V p = 1) by workgroup r; the
-  // first row's input is loaded ahead of q and the first block, and quantized while those
-  // loads are in flight
-  const bool quant = a.k_new != nullptr && wg < 4 * a.nseg;
-  float xq = 0.0f;
-  if (quant) {
-    const int p = (wg >> 1) & 1, kvr = wg & 1;
-    xq = (p ? a.v_new : a.k_new)[((int64_t)(wg >> 2) * 2 + kvr) * 256 + tid];
-    asm volatile("" : "+v"(xq));
-  }
 
   // head kv's K and V rows (272 bytes per key) of the block at c0, keys past nk as 0:
   // every load is issued before the first LDS store
@@ -356,40 +356,24 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
   };
   // ---- q of the head group as QK B operands, built once: fragment (j, lane (n, g)) holds
   // elements 32 j + 8 g .. + 7 of head 8 kv + n % 8, as the fp16 hi part (n < 8) or the
-  // lo remainder (n >= 8); thread t builds fragments t and t + 256
+  // lo remainder (n >= 8); thread t = 32 j + 8 g + h loads those of head h once and builds
+  // both fragments
   {
-    float4 qv[2][2];
-#pragma unroll
-    for (int f2 = 0; f2 < 2; ++f2) {
-      const int f = tid + f2 * kQ8mThreads, j = f >> 6, fl = f & 63;
-      const float *qrow = a.q + ((int64_t)sg.qi * 16 + 8 * kv + (fl & 7)) * 256 + 32 * j + 8 * (fl >> 4);
-      qv[f2][0] = *reinterpret_cast<const float4 *>(qrow);
-      qv[f2][1] = *reinterpret_cast<const float4 *>(qrow + 4);
-    }
+    const int j = tid >> 5, gq = (tid >> 3) & 3, hq = tid & 7;
+    const float *qrow = a.q + ((int64_t)sg.qi * 16 + 8 * kv + hq) * 256 + 32 * j + 8 * gq;
+    const float4 q0 = *reinterpret_cast<const float4 *>(qrow);
+    const float4 q1 = *reinterpret_cast<const float4 *>(qrow + 4);
     if (k0 < k1) load_block(k0, (int)(k1 - k0 < kBlk ? k1 - k0 : kBlk));
-    if (quant) {
-      for (int row = wg; row < 4 * a.nseg; row += a.nwg) {
-        const int rs = row >> 2, p = (row >> 1) & 1, kvr = row & 1;
-        if (row != wg) xq = (p ? a.v_new : a.k_new)[((int64_t)rs * 2 + kvr) * 256 + tid];
-        const DecodeSeg &rg = a.seg[rs];
-        uint8_t *dst = (p ? rg.v : rg.k) + rg.t_new * a.rs_t + kvr * a.rs_h;
-        a.dq[(int64_t)row * 256 + tid] = q8_quantize_row_lanes(xq, dst, tid);
-      }
-    }
+    const float v8[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    h8 fh, fl;
 #pragma unroll
-    for (int f2 = 0; f2 < 2; ++f2) {
-      const int f = tid + f2 * kQ8mThreads, fl = f & 63;
-      const bool lo = (fl & 15) >= 8;
-      const float v8[8] = {qv[f2][0].x, qv[f2][0].y, qv[f2][0].z, qv[f2][0].w,
-                           qv[f2][1].x, qv[f2][1].y, qv[f2][1].z, qv[f2][1].w};
-      h8 fr;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const _Float16 hi = (_Float16)v8[k];
-        fr[k] = lo ? (_Float16)(v8[k] - (float)hi) : hi;
-      }
-      sm.qf[f >> 6][fl] = fr;
+    for (int k = 0; k < 8; ++k) {
+      const _Float16 hi = (_Float16)v8[k];
+      fh[k] = hi;
+      fl[k] = (_Float16)(v8[k] - (float)hi);
     }
+    sm.qf[j][16 * gq + hq] = fh;
+    sm.qf[j][16 * gq + 8 + hq] = fl;
   }
 
   f4 acc[4];
@@ -623,10 +607,11 @@ static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, cons
   d.part = static_cast<float *>(ws.ptr);
   d.ml = reinterpret_cast<float2 *>(d.part + part_floats);
   d.dq = d.part + part_floats + ml_floats;
-  if (mfma) {  // two workgroups (KV heads) per slot
+  if (mfma) {  // two workgroups (KV heads) per slot, then one per new row
     d.nwg = 2 * wg;
-    hipLaunchKernelGGL(q8_decode_mfma_kernel, dim3((unsigned)(2 * wg)), dim3(kQ8mThreads), 0, s,
-                       d);
+    const int nq = fused ? 4 * n : 0;
+    hipLaunchKernelGGL(q8_decode_mfma_kernel, dim3((unsigned)(2 * wg + nq)), dim3(kQ8mThreads),
+                       0, s, d);
   } else if (chunk == 16) {
     hipLaunchKernelGGL(q8_decode_kernel<16>, dim3((unsigned)wg), dim3(kQ8Threads), 0, s, d);
   } else {
