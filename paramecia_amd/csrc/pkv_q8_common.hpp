@@ -42,17 +42,18 @@ __device__ __forceinline__ uint32_t lo_pair(float a0, float a1, uint32_t cw) {
 // block j = 4 h + 2 (n >> 3) + kHl (one dword, two bytes past a dword boundary for even
 // j), code b going to tile 8 h + kHl + 2 b. Each value int8 * d (at most 18 significant
 // bits, exact in f32: the code + 128 times d, minus 128 d, in one fma) becomes an fp16 hi
-// part and the exact lo remainder: wh[b][p] / wl[b][p] hold keys 8 g + 2 p, + 1.
-template <int kHl>
+// part and the exact lo remainder: wh[b - kB0][p] / wl[b - kB0][p] hold keys 8 g + 2 p,
+// + 1, for the codes b = kB0 .. kB0 + kNB - 1 (all four by default).
+template <int kHl, int kB0 = 0, int kNB = 4>
 __device__ __forceinline__ void q8_v_words(const uint32_t *rows, int row_words, int h, int lane,
-                                           uint32_t (&wh)[4][4], uint32_t (&wl)[4][4]) {
+                                           uint32_t (&wh)[kNB][4], uint32_t (&wl)[kNB][4]) {
   const int n = lane & 15, g = lane >> 4;
   const int j = 4 * h + 2 * (n >> 3) + kHl;
   const int cw = (34 * j + 2 + 4 * (n & 7)) >> 2;  // first dword of the four codes
   const int dw = (34 * j) >> 2;                     // dword of d: low half (even j) or high
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    float v[2][4];
+    float v[2][kNB];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const uint32_t *row = rows + (8 * g + 2 * p + kk) * row_words;
@@ -61,10 +62,11 @@ __device__ __forceinline__ void q8_v_words(const uint32_t *rows, int row_words, 
       const uint32_t dd = row[dw];
       const float d = h2f(kHl ? (dd >> 16) : (dd & 0xFFFF)), nd = -128.0f * d;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) v[kk][b] = fmaf((float)((w >> (8 * b)) & 0xFFu), d, nd);
+      for (int b = 0; b < kNB; ++b)
+        v[kk][b] = fmaf((float)((w >> (8 * (b + kB0))) & 0xFFu), d, nd);
     }
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
+    for (int b = 0; b < kNB; ++b) {
       wh[b][p] = as_u(h2{(_Float16)v[0][b], (_Float16)v[1][b]});
       wl[b][p] = lo_pair(v[0][b], v[1][b], wh[b][p]);
     }

@@ -271,24 +271,24 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
 
 // ---- MFMA decode over 32-key blocks (caches up to 32k keys per segment)
 //
-// A workgroup of 4 waves owns a key range of one segment (kpw keys, a multiple of 32) and
+// A workgroup of 8 waves owns a key range of one segment (kpw keys, a multiple of 32) and
 // one KV head: workgroup w serves partial slot w / 2 and KV head w % 2. Per 32-key block
-// the head's K and V rows are staged in LDS; wave qd builds the QK A fragments of blocks
-// j = 2 qd, 2 qd + 1 of both 16-key tiles into LDS (int8 codes, exact in fp16) and the PV
-// B fragments of its four 16-column tiles into registers (int8 * d as an exact fp16 hi/lo
-// pair, q8_v_words). Every wave then runs the head's QK: per tile and block j one MFMA
-// with q as B (columns 0-7 the fp16 hi parts of the group's 8 heads, 8-15 the lo
-// remainders, converted once per workgroup), scaled by d_j * scale * log2(e) of its key
-// in f32; the hi and lo columns are summed across lanes n and n ^ 8. The softmax weights
+// the head's K and V rows are staged in LDS; wave w builds, in registers, the QK A
+// fragments of tile t = w / 4 and blocks j = 2 (w % 4), + 1 (int8 codes, exact in fp16)
+// and the PV B fragments of its two 16-column tiles (int8 * d as an exact fp16 hi/lo
+// pair, q8_v_words). Its QK MFMAs (q as B: columns 0-7 the fp16 hi parts of the group's
+// 8 heads, 8-15 the lo remainders, converted once per workgroup) are scaled by
+// d_j * scale * log2(e) of their keys in f32, and the waves' parts are summed through
+// LDS; the hi and lo columns are summed across lanes n and n ^ 8. The softmax weights
 // enter PV as A rows 0-7 (fp16 hi) and 8-15 (lo remainder): two MFMAs per tile (V hi and
 // lo), rows h and h + 8 summed at the end. The partial goes out in tile order, as the
 // other decode kernels write it, for decode_combine_kernel.
-constexpr int kQ8mThreads = 256;
+constexpr int kQ8mThreads = 512;
 struct Q8mSmem {
   h8 qf[8][64];                      // QK B operands: [block j][lane]
   uint32_t raw[2][32][kQ8RowWords];  // [K / V][key][row]
   float kd[8][32];                   // [block j][key]: d_j * sl2
-  float4 sp[4][2][64];               // each wave's partial scores: [wave][tile][lane]
+  float4 sp[8][64];                  // each wave's part of its tile's scores: [wave][lane]
 };
 
 // The MFMA decode is on unless PKV_Q8_MFMA=0 (the VALU kernel, kept for comparison).
@@ -309,13 +309,14 @@ __device__ __forceinline__ float xsum16(float x) {  // x of lanes l and l ^ 16, 
 
 __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
   __shared__ Q8mSmem sm;
-  const int tid = threadIdx.x, lane = tid & 63, qd = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int wg = blockIdx.x, slot = wg >> 1, kv = wg & 1;
   // ---- fused append: the 4 n workgroups after the a.nwg decode ones quantize new row
   // r = 4 s + 2 p + kv (K p = 0, V p = 1) each, so that no decode workgroup ends later
   // for it
   if (wg >= a.nwg) {
+    if (tid >= 256) return;
     const int row = wg - a.nwg, rs = row >> 2, p = (row >> 1) & 1, kvr = row & 1;
     const float x = (p ? a.v_new : a.k_new)[((int64_t)rs * 2 + kvr) * 256 + tid];
     const DecodeSeg &rg = a.seg[rs];
@@ -359,26 +360,33 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
   // lo remainder (n >= 8); thread t = 32 j + 8 g + h loads those of head h once and builds
   // both fragments
   {
-    const int j = tid >> 5, gq = (tid >> 3) & 3, hq = tid & 7;
+    const int tq = tid & 255, j = tq >> 5, gq = (tq >> 3) & 3, hq = tq & 7;
     const float *qrow = a.q + ((int64_t)sg.qi * 16 + 8 * kv + hq) * 256 + 32 * j + 8 * gq;
-    const float4 q0 = *reinterpret_cast<const float4 *>(qrow);
-    const float4 q1 = *reinterpret_cast<const float4 *>(qrow + 4);
-    if (k0 < k1) load_block(k0, (int)(k1 - k0 < kBlk ? k1 - k0 : kBlk));
-    const float v8[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    h8 fh, fl;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const _Float16 hi = (_Float16)v8[k];
-      fh[k] = hi;
-      fl[k] = (_Float16)(v8[k] - (float)hi);
+    float4 q0 = {0.f, 0.f, 0.f, 0.f}, q1 = q0;
+    if (tid < 256) {
+      q0 = *reinterpret_cast<const float4 *>(qrow);
+      q1 = *reinterpret_cast<const float4 *>(qrow + 4);
     }
-    sm.qf[j][16 * gq + hq] = fh;
-    sm.qf[j][16 * gq + 8 + hq] = fl;
+    if (k0 < k1) load_block(k0, (int)(k1 - k0 < kBlk ? k1 - k0 : kBlk));
+    if (tid < 256) {
+      const float v8[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+      h8 fh, fl;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const _Float16 hi = (_Float16)v8[k];
+        fh[k] = hi;
+        fl[k] = (_Float16)(v8[k] - (float)hi);
+      }
+      sm.qf[j][16 * gq + hq] = fh;
+      sm.qf[j][16 * gq + 8 + hq] = fl;
+    }
   }
 
-  f4 acc[4];
+  const int tw = wv >> 2, qd = wv & 3;  // QK: tile tw, blocks 2 qd, 2 qd + 1
+  const int vu = wv >> 1, vb = wv & 1;  // PV: unit vu, codes 2 vb, 2 vb + 1 (two tiles)
+  f4 acc[2];
 #pragma unroll
-  for (int x = 0; x < 4; ++x) acc[x] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int x = 0; x < 2; ++x) acc[x] = f4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;  // head n % 8 (the same in lanes n, n ^ 8 and every g)
 
   for (int64_t c0 = k0; c0 < k1; c0 += kBlk) {
@@ -389,13 +397,12 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
     }
     store_block();
     __syncthreads();
-    // ---- QK over blocks j = 2 qd, 2 qd + 1, A fragments in registers (lane (r, g): key
-    // q8_key(r, t), elements 32 j + 8 g .. + 7); lanes g = 0 store d_j * sl2 of their key,
-    // read back by this wave's lanes only
-    h8 ka[2][2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int kk = q8_key(n, t);
+    // ---- QK of tile tw over blocks j = 2 qd, 2 qd + 1, A fragments in registers (lane
+    // (r, g): key q8_key(r, tw), elements 32 j + 8 g .. + 7); lanes g = 0 store d_j * sl2
+    // of their key, read back by this wave's lanes only
+    f4 cq[2];
+    {
+      const int kk = q8_key(n, tw);
       const uint32_t *row = &sm.raw[0][kk][0];
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
@@ -413,42 +420,38 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
         h2 a0, a1, a2, a3;
         i8x4_to_h4(w0, a0, a1);
         i8x4_to_h4(w1, a2, a3);
-        ka[t][jj] = h8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+        const h8 ka = h8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
         if (g == 0) {
           const uint32_t dw = row[(34 * j) >> 2];
           sm.kd[j][kk] = h2f(jj ? (dw >> 16) : (dw & 0xFFFF)) * a.sl2;
         }
+        cq[jj] = mfma32(ka, sm.qf[j][lane], f4{0.f, 0.f, 0.f, 0.f});
       }
     }
-    f4 cq[2][2];
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const h8 qbj = sm.qf[2 * qd + jj][lane];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) cq[t][jj] = mfma32(ka[t][jj], qbj, f4{0.f, 0.f, 0.f, 0.f});
+    // ---- PV B fragments of this wave's two tiles, in registers (while the MFMAs run)
+    uint32_t wh[2][4], wl[2][4];
+    if (vu & 1) {
+      if (vb) q8_v_words<1, 2, 2>(&sm.raw[1][0][0], kQ8RowWords, vu >> 1, lane, wh, wl);
+      else q8_v_words<1, 0, 2>(&sm.raw[1][0][0], kQ8RowWords, vu >> 1, lane, wh, wl);
+    } else {
+      if (vb) q8_v_words<0, 2, 2>(&sm.raw[1][0][0], kQ8RowWords, vu >> 1, lane, wh, wl);
+      else q8_v_words<0, 0, 2>(&sm.raw[1][0][0], kQ8RowWords, vu >> 1, lane, wh, wl);
     }
-    // ---- PV B fragments of this wave's four tiles, in registers (while the MFMAs run)
-    uint32_t wh[4][4], wl[4][4];
-    if (qd & 1)
-      q8_v_words<1>(&sm.raw[1][0][0], kQ8RowWords, qd >> 1, lane, wh, wl);
-    else
-      q8_v_words<0>(&sm.raw[1][0][0], kQ8RowWords, qd >> 1, lane, wh, wl);
-    // this wave's part of the scores, scaled by its keys' d_j, to LDS
+    // this wave's part of its tile's scores, scaled by its keys' d_j, to LDS
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    {
       float4 part = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        const float4 dk = *reinterpret_cast<const float4 *>(&sm.kd[2 * qd + jj][8 * g + 4 * t]);
-        part.x = fmaf(dk.x, cq[t][jj][0], part.x);
-        part.y = fmaf(dk.y, cq[t][jj][1], part.y);
-        part.z = fmaf(dk.z, cq[t][jj][2], part.z);
-        part.w = fmaf(dk.w, cq[t][jj][3], part.w);
+        const float4 dk = *reinterpret_cast<const float4 *>(&sm.kd[2 * qd + jj][8 * g + 4 * tw]);
+        part.x = fmaf(dk.x, cq[jj][0], part.x);
+        part.y = fmaf(dk.y, cq[jj][1], part.y);
+        part.z = fmaf(dk.z, cq[jj][2], part.z);
+        part.w = fmaf(dk.w, cq[jj][3], part.w);
       }
-      sm.sp[qd][t][lane] = part;
+      sm.sp[wv][lane] = part;
     }
     __syncthreads();  // every wave's part of the scores is in LDS
 
@@ -457,10 +460,10 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
     float sc[8];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      float4 tot = sm.sp[0][t][lane];
+      float4 tot = sm.sp[4 * t][lane];
 #pragma unroll
       for (int w2 = 1; w2 < 4; ++w2) {
-        const float4 pw = sm.sp[w2][t][lane];
+        const float4 pw = sm.sp[4 * t + w2][lane];
         tot.x += pw.x;
         tot.y += pw.y;
         tot.z += pw.z;
@@ -492,7 +495,7 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) ai[i] = __shfl(alpha, (4 * g + i) & 7);  // row 4 g + i
 #pragma unroll
-      for (int x = 0; x < 4; ++x)
+      for (int x = 0; x < 2; ++x)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[x][i] *= ai[i];
     }
@@ -513,24 +516,24 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
     }
     const h8 A = __builtin_bit_cast(h8, u4{wa[0], wa[1], wa[2], wa[3]});
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
+    for (int x = 0; x < 2; ++x) {
       acc[x] = mfma32(A, __builtin_bit_cast(h8, u4{wh[x][0], wh[x][1], wh[x][2], wh[x][3]}), acc[x]);
       acc[x] = mfma32(A, __builtin_bit_cast(h8, u4{wl[x][0], wl[x][1], wl[x][2], wl[x][3]}), acc[x]);
     }
   }
 
   // ---- partial: rows h (hi weights) and h + 8 (lo) summed (lanes g and g + 2), tile T =
-  // 8 (qd >> 1) + (qd & 1) + 2 x, entry 16 T + n of head 8 kv + 4 g + i (lanes 0-31)
+  // 8 (vu >> 1) + (vu & 1) + 2 (2 vb + x), entry 16 T + n of head 8 kv + 4 g + i (lanes 0-31)
   float *P = a.part + (int64_t)slot * 16 * kPartRow;
-  float r[4][4];
+  float r[2][4];
 #pragma unroll
-  for (int x = 0; x < 4; ++x)
+  for (int x = 0; x < 2; ++x)
 #pragma unroll
     for (int i = 0; i < 4; ++i) r[x][i] = xsum32(acc[x][i]);
   if (g < 2) {
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int T = 8 * (qd >> 1) + (qd & 1) + 2 * x;
+    for (int x = 0; x < 2; ++x) {
+      const int T = 8 * (vu >> 1) + (vu & 1) + 2 * (2 * vb + x);
 #pragma unroll
       for (int i = 0; i < 4; ++i) P[(8 * kv + 4 * g + i) * kPartRow + 16 * T + n] = r[x][i];
     }
@@ -538,7 +541,7 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
   // the weights' sum of head n % 8 over the lanes g (each holds its 8 keys)
   float lt = xsum16(l_run);
   lt = xsum32(lt);
-  if (qd == 0 && g == 0 && n < 8) a.ml[(int64_t)slot * 16 + 8 * kv + n] = float2{m_run, lt};
+  if (wv == 0 && g == 0 && n < 8) a.ml[(int64_t)slot * 16 + 8 * kv + n] = float2{m_run, lt};
 }
 
 }  // namespace
