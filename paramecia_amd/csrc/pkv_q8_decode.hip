@@ -35,11 +35,12 @@ constexpr int kQ8Chunk = 32;   // keys per LDS chunk (16 for short caches)
 constexpr int kQ8Threads = 512;
 constexpr int kQ8RowWords = kQ8Row / 4;  // 68 dwords, 16-byte aligned rows (272 = 17 x 16)
 
+// The scalar fields come first: the kernels read them through the scalar cache, and
+// ahead of the segment table they share its first lines with segment 0.
 struct Q8Args {
-  DecodeSeg seg[kMaxSegs];
   int nseg, nwg, kpw;  // segments, workgroups, keys per workgroup (a multiple of 32)
-  int64_t rs_t, rs_h;
   float sl2;
+  int64_t rs_t, rs_h;
   const float *q;              // [nseg][16][256]
   const float *k_new, *v_new;  // [nseg][2][256] or null
   float *part;                 // [nwg][16][kPartRow]
@@ -49,6 +50,7 @@ struct Q8Args {
   // owning workgroups [s * wps, (s + 1) * wps); the seg array is unused
   const DecodeSeg *dseg;
   int wps;
+  DecodeSeg seg[kMaxSegs];
 };
 
 template <int kChunk>
@@ -287,7 +289,8 @@ constexpr int kQ8mThreads = 512;
 struct Q8mSmem {
   h8 qf[8][64];                      // QK B operands: [block j][lane]
   uint32_t raw[2][32][kQ8RowWords];  // [K / V][key][row]
-  float kd[8][32];                   // [block j][key]: d_j * sl2
+  float kd[8][32];                   // [block j][key]: K's d_j * sl2 (written when staged)
+  float vd[8][32];                   // [block j][key]: V's d_j (written when staged)
   float4 sp[8][64];                  // each wave's part of its tile's scores: [wave][lane]
 };
 
@@ -307,52 +310,109 @@ __device__ __forceinline__ float xsum16(float x) {  // x of lanes l and l ^ 16, 
   return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
 }
 
+// q8_v_words for two codes b = kB0, kB0 + 1 of a staged 32-key block, with the d of
+// each key and block taken from the staged vd[j][key]: every LDS read of a lane (the
+// code dwords of its 8 keys, their 8 d) is issued before the first wait.
+template <int kHl, int kB0>
+__device__ __forceinline__ void q8_v_words_dec(const uint32_t (*rows)[kQ8RowWords],
+                                               const float (*vd)[32], int h, int lane,
+                                               uint32_t (&wh)[2][4], uint32_t (&wl)[2][4]) {
+  const int n = lane & 15, g = lane >> 4;
+  const int j = 4 * h + 2 * (n >> 3) + kHl;
+  const int cw = (34 * j + 2 + 4 * (n & 7)) >> 2;  // first dword of the four codes
+  uint32_t c0[8], c1[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    c0[k] = rows[8 * g + k][cw];
+    if (!kHl) c1[k] = rows[8 * g + k][cw + 1];
+  }
+  const float4 d0 = *reinterpret_cast<const float4 *>(&vd[j][8 * g]);
+  const float4 d1 = *reinterpret_cast<const float4 *>(&vd[j][8 * g + 4]);
+  __builtin_amdgcn_sched_barrier(0);
+  const float dk[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    float v[2][2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int k = 2 * p + kk;
+      const uint32_t w = (kHl ? c0[k] : __builtin_amdgcn_alignbyte(c1[k], c0[k], 2)) ^ 0x80808080u;
+      const float d = dk[k], nd = -128.0f * d;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) v[kk][b] = fmaf((float)((w >> (8 * (b + kB0))) & 0xFFu), d, nd);
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      wh[b][p] = as_u(h2{(_Float16)v[0][b], (_Float16)v[1][b]});
+      wl[b][p] = lo_pair(v[0][b], v[1][b], wh[b][p]);
+    }
+  }
+}
+
+// kOne: a one-segment launch; kFused: the launch appends the new rows. Neither needs a
+// kernel argument to tell a workgroup its role, so the decode workgroups' first scalar
+// loads (segment 0 and the scalars) go out together.
+template <bool kOne, bool kFused>
 __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
   __shared__ Q8mSmem sm;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
-  const int wg = blockIdx.x, slot = wg >> 1, kv = wg & 1;
-  // ---- fused append: the 4 n workgroups after the a.nwg decode ones quantize new row
-  // r = 4 s + 2 p + kv (K p = 0, V p = 1) each, so that no decode workgroup ends later
-  // for it
-  if (wg >= a.nwg) {
+  // ---- fused append: the first 4 n workgroups quantize new row r = 4 s + 2 p + kv (K
+  // p = 0, V p = 1) each; the decode workgroups follow
+  const int nq = kFused ? (kOne ? 4 : 4 * a.nseg) : 0;
+  const int wg = (int)blockIdx.x - nq, slot = wg >> 1, kv = wg & 1;
+  if (kFused && wg < 0) {
     if (tid >= 256) return;
-    const int row = wg - a.nwg, rs = row >> 2, p = (row >> 1) & 1, kvr = row & 1;
+    const int row = wg + nq, rs = row >> 2, p = (row >> 1) & 1, kvr = row & 1;
     const float x = (p ? a.v_new : a.k_new)[((int64_t)rs * 2 + kvr) * 256 + tid];
     const DecodeSeg &rg = a.seg[rs];
     uint8_t *dst = (p ? rg.v : rg.k) + rg.t_new * a.rs_t + kvr * a.rs_h;
     a.dq[(int64_t)row * 256 + tid] = q8_quantize_row_lanes(x, dst, tid);
     return;
   }
+  // a one-segment launch (kOne) reads segment 0 without waiting for nseg
   int b = 0;
-  while (b + 1 < a.nseg && slot >= a.seg[b + 1].wg0) ++b;
+  if (!kOne)
+    while (b + 1 < a.nseg && slot >= a.seg[b + 1].wg0) ++b;
   const DecodeSeg sg = a.seg[b];
   const int64_t k0 = (int64_t)(slot - sg.wg0) * a.kpw;
   const int64_t k1 = k0 + a.kpw < sg.seq_k ? k0 + a.kpw : sg.seq_k;
   const uint8_t *kbase = sg.k + kv * a.rs_h, *vbase = sg.v + kv * a.rs_h;
 
-  // head kv's K and V rows (272 bytes per key) of the block at c0, keys past nk as 0:
-  // every load is issued before the first LDS store
+  // head kv's K and V rows (272 bytes per key) of the block at c0: every load is issued
+  // before the first LDS store, unconditionally (pieces past the block and keys past nk
+  // read the last piece / key again, and are dropped or stored as 0), so that no load
+  // waits for another. The K pieces 2 j (j < 8), whose halfword j is d_j, also store
+  // d_j * sl2 for the QK scaling, the V pieces 2 j d_j for the PV operands.
   constexpr int kPieces = 2 * 32 * (kQ8RowB / 16);  // 16-byte pieces of a staged block
   constexpr int kPer = (kPieces + kQ8mThreads - 1) / kQ8mThreads;
   uint4 w[kPer];
   auto load_block = [&](int64_t c0, int nk) {
 #pragma unroll
     for (int x = 0; x < kPer; ++x) {
-      const int c = tid + x * kQ8mThreads;
+      const int c = min(tid + x * kQ8mThreads, kPieces - 1);
       const int tn = c / (kPieces / 2), r = c % (kPieces / 2);
-      const int key = r / 17, piece = r % 17;
-      w[x] = uint4{0u, 0u, 0u, 0u};
-      if (c < kPieces && key < nk)
-        w[x] = *reinterpret_cast<const uint4 *>((tn ? vbase : kbase) + (c0 + key) * a.rs_t + 16 * piece);
+      const int key = min(r / 17, nk - 1), piece = r % 17;
+      w[x] = *reinterpret_cast<const uint4 *>((tn ? vbase : kbase) + (c0 + key) * a.rs_t + 16 * piece);
     }
   };
-  auto store_block = [&]() {
+  auto store_block = [&](int nk) {
 #pragma unroll
     for (int x = 0; x < kPer; ++x) {
       const int c = tid + x * kQ8mThreads;
       const int tn = c / (kPieces / 2), r = c % (kPieces / 2);
-      if (c < kPieces) *reinterpret_cast<uint4 *>(&sm.raw[tn][r / 17][4 * (r % 17)]) = w[x];
+      const int key = r / 17, piece = r % 17;
+      if (c < kPieces) {
+        const uint4 v = key < nk ? w[x] : uint4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<uint4 *>(&sm.raw[tn][key][4 * piece]) = v;
+        if (piece < 16 && (piece & 1) == 0) {
+          const int j = piece >> 1;
+          const uint32_t dw = (j >> 1) == 0 ? v.x : (j >> 1) == 1 ? v.y : (j >> 1) == 2 ? v.z : v.w;
+          const float d = h2f((j & 1) ? (dw >> 16) : (dw & 0xFFFF));
+          if (tn == 0) sm.kd[j][key] = d * a.sl2;
+          else sm.vd[j][key] = d;
+        }
+      }
     }
   };
   // ---- q of the head group as QK B operands, built once: fragment (j, lane (n, g)) holds
@@ -362,11 +422,8 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
   {
     const int tq = tid & 255, j = tq >> 5, gq = (tq >> 3) & 3, hq = tq & 7;
     const float *qrow = a.q + ((int64_t)sg.qi * 16 + 8 * kv + hq) * 256 + 32 * j + 8 * gq;
-    float4 q0 = {0.f, 0.f, 0.f, 0.f}, q1 = q0;
-    if (tid < 256) {
-      q0 = *reinterpret_cast<const float4 *>(qrow);
-      q1 = *reinterpret_cast<const float4 *>(qrow + 4);
-    }
+    const float4 q0 = *reinterpret_cast<const float4 *>(qrow);  // threads >= 256 load again
+    const float4 q1 = *reinterpret_cast<const float4 *>(qrow + 4);
     if (k0 < k1) load_block(k0, (int)(k1 - k0 < kBlk ? k1 - k0 : kBlk));
     if (tid < 256) {
       const float v8[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
@@ -395,52 +452,41 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
       __syncthreads();  // the previous block's readers are done
       load_block(c0, nk);
     }
-    store_block();
+    store_block(nk);
     __syncthreads();
     // ---- QK of tile tw over blocks j = 2 qd, 2 qd + 1, A fragments in registers (lane
-    // (r, g): key q8_key(r, tw), elements 32 j + 8 g .. + 7); lanes g = 0 store d_j * sl2
-    // of their key, read back by this wave's lanes only
+    // (r, g): key q8_key(r, tw), elements 32 j + 8 g .. + 7)
     f4 cq[2];
     {
-      const int kk = q8_key(n, tw);
-      const uint32_t *row = &sm.raw[0][kk][0];
+      const h8 qb0 = sm.qf[2 * qd][lane], qb1 = sm.qf[2 * qd + 1][lane];
+      const uint32_t *row = &sm.raw[0][q8_key(n, tw)][0];
+      const int w0i = (68 * qd + 2 + 8 * g) >> 2;  // block 2 qd: two bytes past w0i
+      uint32_t x[5];
+#pragma unroll
+      for (int i = 0; i < 5; ++i) x[i] = row[w0i + (i < 3 ? i : 6 + i)];  // block 2 qd + 1 at w0i + 9
+      __builtin_amdgcn_sched_barrier(0);  // every read above is issued before the first wait
+      const uint32_t kw[2][2] = {{__builtin_amdgcn_alignbyte(x[1], x[0], 2),
+                                  __builtin_amdgcn_alignbyte(x[2], x[1], 2)},
+                                 {x[3], x[4]}};
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        const int j = 2 * qd + jj;  // j & 1 == jj
-        const int w0i = (34 * j + 2 + 8 * g) >> 2;
-        uint32_t w0, w1;
-        if (jj) {
-          w0 = row[w0i];
-          w1 = row[w0i + 1];
-        } else {
-          const uint32_t x0 = row[w0i], x1 = row[w0i + 1], x2 = row[w0i + 2];
-          w0 = __builtin_amdgcn_alignbyte(x1, x0, 2);
-          w1 = __builtin_amdgcn_alignbyte(x2, x1, 2);
-        }
         h2 a0, a1, a2, a3;
-        i8x4_to_h4(w0, a0, a1);
-        i8x4_to_h4(w1, a2, a3);
+        i8x4_to_h4(kw[jj][0], a0, a1);
+        i8x4_to_h4(kw[jj][1], a2, a3);
         const h8 ka = h8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
-        if (g == 0) {
-          const uint32_t dw = row[(34 * j) >> 2];
-          sm.kd[j][kk] = h2f(jj ? (dw >> 16) : (dw & 0xFFFF)) * a.sl2;
-        }
-        cq[jj] = mfma32(ka, sm.qf[j][lane], f4{0.f, 0.f, 0.f, 0.f});
+        cq[jj] = mfma32(ka, jj ? qb1 : qb0, f4{0.f, 0.f, 0.f, 0.f});
       }
     }
     // ---- PV B fragments of this wave's two tiles, in registers (while the MFMAs run)
     uint32_t wh[2][4], wl[2][4];
     if (vu & 1) {
-      if (vb) q8_v_words<1, 2, 2>(&sm.raw[1][0][0], kQ8RowWords, vu >> 1, lane, wh, wl);
-      else q8_v_words<1, 0, 2>(&sm.raw[1][0][0], kQ8RowWords, vu >> 1, lane, wh, wl);
+      if (vb) q8_v_words_dec<1, 2>(sm.raw[1], sm.vd, vu >> 1, lane, wh, wl);
+      else q8_v_words_dec<1, 0>(sm.raw[1], sm.vd, vu >> 1, lane, wh, wl);
     } else {
-      if (vb) q8_v_words<0, 2, 2>(&sm.raw[1][0][0], kQ8RowWords, vu >> 1, lane, wh, wl);
-      else q8_v_words<0, 0, 2>(&sm.raw[1][0][0], kQ8RowWords, vu >> 1, lane, wh, wl);
+      if (vb) q8_v_words_dec<0, 2>(sm.raw[1], sm.vd, vu >> 1, lane, wh, wl);
+      else q8_v_words_dec<0, 0>(sm.raw[1], sm.vd, vu >> 1, lane, wh, wl);
     }
     // this wave's part of its tile's scores, scaled by its keys' d_j, to LDS
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     {
       float4 part = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -458,12 +504,16 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
     // ---- the scores: sc[4 t + i] of key 8 g + 4 t + i for column n, summed over the
     // waves' blocks in block order (blocks 0-1, 2-3, 4-5, 6-7)
     float sc[8];
+    float4 sp8[8];
+#pragma unroll
+    for (int w2 = 0; w2 < 8; ++w2) sp8[w2] = sm.sp[w2][lane];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      float4 tot = sm.sp[4 * t][lane];
+      float4 tot = sp8[4 * t];
 #pragma unroll
       for (int w2 = 1; w2 < 4; ++w2) {
-        const float4 pw = sm.sp[4 * t + w2][lane];
+        const float4 pw = sp8[4 * t + w2];
         tot.x += pw.x;
         tot.y += pw.y;
         tot.z += pw.z;
@@ -486,14 +536,24 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
     for (int k = 1; k < 8; ++k) bm = fmaxf(bm, sc[k]);
     bm = xmax32(xmax16(bm));
     const float m_new = fmaxf(m_run, bm);
-    if (__any(m_new != m_run)) {  // some head's max rose: rescale its sums (rows by head)
+    // some head's max rose after the first block: rescale its sums (rows by head; on the
+    // first block they are still 0)
+    if (c0 != k0 && __any(m_new != m_run)) {
       const float alpha = (m_new == m_run) ? 1.0f
                           : (m_run == -INFINITY) ? 0.0f
                                                  : __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= alpha;
+      // row 4 g + i is head (4 g + i) % 8, whose alpha lane (4 g + i) % 8 holds
+      const auto lane_alpha = [&](int k) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), k));
+      };
+      const bool odd = (g & 1) != 0;
       float ai[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ai[i] = __shfl(alpha, (4 * g + i) & 7);  // row 4 g + i
+      for (int i = 0; i < 4; ++i) {
+        const float lo = lane_alpha(i), hi = lane_alpha(i + 4);
+        ai[i] = odd ? hi : lo;
+      }
 #pragma unroll
       for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -610,11 +670,18 @@ static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, cons
   d.part = static_cast<float *>(ws.ptr);
   d.ml = reinterpret_cast<float2 *>(d.part + part_floats);
   d.dq = d.part + part_floats + ml_floats;
-  if (mfma) {  // two workgroups (KV heads) per slot, then one per new row
+  if (mfma) {  // one workgroup per new row, then two (KV heads) per slot
     d.nwg = 2 * wg;
     const int nq = fused ? 4 * n : 0;
-    hipLaunchKernelGGL(q8_decode_mfma_kernel, dim3((unsigned)(2 * wg + nq)), dim3(kQ8mThreads),
-                       0, s, d);
+    const dim3 grid((unsigned)(2 * wg + nq)), block(kQ8mThreads);
+    if (n == 1 && fused)
+      hipLaunchKernelGGL((q8_decode_mfma_kernel<true, true>), grid, block, 0, s, d);
+    else if (n == 1)
+      hipLaunchKernelGGL((q8_decode_mfma_kernel<true, false>), grid, block, 0, s, d);
+    else if (fused)
+      hipLaunchKernelGGL((q8_decode_mfma_kernel<false, true>), grid, block, 0, s, d);
+    else
+      hipLaunchKernelGGL((q8_decode_mfma_kernel<false, false>), grid, block, 0, s, d);
   } else if (chunk == 16) {
     hipLaunchKernelGGL(q8_decode_kernel<16>, dim3((unsigned)wg), dim3(kQ8Threads), 0, s, d);
   } else {
