@@ -274,17 +274,18 @@ __global__ __launch_bounds__(kQ8Threads) void q8_decode_kernel(Q8Args a) {
 // ---- MFMA decode over 32-key blocks (caches up to 32k keys per segment)
 //
 // A workgroup of 8 waves owns a key range of one segment (kpw keys, a multiple of 32) and
-// one KV head: workgroup w serves partial slot w / 2 and KV head w % 2. Per 32-key block
-// the head's K and V rows are staged in LDS; wave w builds, in registers, the QK A
-// fragments of tile t = w / 4 and blocks j = 2 (w % 4), + 1 (int8 codes, exact in fp16)
-// and the PV B fragments of its two 16-column tiles (int8 * d as an exact fp16 hi/lo
-// pair, q8_v_words). Its QK MFMAs (q as B: columns 0-7 the fp16 hi parts of the group's
-// 8 heads, 8-15 the lo remainders, converted once per workgroup) are scaled by
-// d_j * scale * log2(e) of their keys in f32, and the waves' parts are summed through
-// LDS; the hi and lo columns are summed across lanes n and n ^ 8. The softmax weights
-// enter PV as A rows 0-7 (fp16 hi) and 8-15 (lo remainder): two MFMAs per tile (V hi and
-// lo), rows h and h + 8 summed at the end. The partial goes out in tile order, as the
-// other decode kernels write it, for decode_combine_kernel.
+// one KV head: decode workgroup w (after the quantizing ones) serves partial slot w / 2
+// and KV head w % 2. Per 32-key block the head's K and V rows are staged in LDS (with
+// the d_j of both); wave w builds, in registers, the QK A fragments of tile t = w / 4 and
+// blocks j = 2 (w % 4), + 1 (int8 codes, exact in fp16) and the PV B fragments of block
+// j = w (its codes, exact in fp16: two 16-column tiles, q8_v_codes_dec). Its QK MFMAs (q
+// as B: columns 0-7 the fp16 hi parts of the group's 8 heads, 8-15 the lo remainders,
+// converted once per workgroup) are scaled by d_j * scale * log2(e) of their keys in
+// f32, and the waves' parts are summed through LDS; the hi and lo columns are summed
+// across lanes n and n ^ 8. The softmax weights times the V d_j of their keys enter PV
+// as A rows 0-7 (fp16 hi) and 8-15 (lo remainder): one MFMA per tile, rows h and h + 8
+// summed at the end. The partial goes out in tile order, as the other decode kernels
+// write it, for decode_combine_kernel.
 constexpr int kQ8mThreads = 512;
 struct Q8mSmem {
   h8 qf[8][64];                      // QK B operands: [block j][lane]
@@ -310,42 +311,35 @@ __device__ __forceinline__ float xsum16(float x) {  // x of lanes l and l ^ 16, 
   return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
 }
 
-// q8_v_words for two codes b = kB0, kB0 + 1 of a staged 32-key block, with the d of
-// each key and block taken from the staged vd[j][key]: every LDS read of a lane (the
-// code dwords of its 8 keys, their 8 d) is issued before the first wait.
-template <int kHl, int kB0>
-__device__ __forceinline__ void q8_v_words_dec(const uint32_t (*rows)[kQ8RowWords],
-                                               const float (*vd)[32], int h, int lane,
-                                               uint32_t (&wh)[2][4], uint32_t (&wl)[2][4]) {
+// PV B fragments of the two tiles x = 0, 1 of block j of a staged 32-key block, the
+// codes themselves as fp16 (exact; d_j goes into the weights): column n of tile x is
+// element 32 j + 4 (n & 7) + 2 x + (n >> 3), so lane (n, g) reads, for each of keys
+// 8 g .. + 7, the one dword holding codes 4 (n & 7) .. + 3 of block j (two bytes past a
+// dword boundary for even j) and keeps bytes n >> 3 (tile 0) and 2 + (n >> 3) (tile 1).
+// v_perm gathers those bytes of two keys into one dword, which i8x4_to_h4 turns into
+// the fp16 pairs of both tiles. Every LDS read is issued before the first wait.
+__device__ __forceinline__ void q8_v_codes_dec(const uint32_t (*rows)[kQ8RowWords], int j,
+                                               int lane, uint32_t (&wb)[2][4]) {
   const int n = lane & 15, g = lane >> 4;
-  const int j = 4 * h + 2 * (n >> 3) + kHl;
-  const int cw = (34 * j + 2 + 4 * (n & 7)) >> 2;  // first dword of the four codes
+  const int cb = 34 * j + 2 + 4 * (n & 7), cw = cb >> 2;  // byte / dword of the four codes
+  const int sh = cb & 3;  // 0 (odd j: the codes are one dword) or 2 (even j: two)
   uint32_t c0[8], c1[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     c0[k] = rows[8 * g + k][cw];
-    if (!kHl) c1[k] = rows[8 * g + k][cw + 1];
+    c1[k] = sh ? rows[8 * g + k][cw + 1] : 0u;
   }
-  const float4 d0 = *reinterpret_cast<const float4 *>(&vd[j][8 * g]);
-  const float4 d1 = *reinterpret_cast<const float4 *>(&vd[j][8 * g + 4]);
   __builtin_amdgcn_sched_barrier(0);
-  const float dk[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+  const uint32_t b0 = n >> 3, b1 = 2 + b0;
+  const uint32_t sel = b0 | ((4 + b0) << 8) | (b1 << 16) | ((4 + b1) << 24);
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    float v[2][2];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int k = 2 * p + kk;
-      const uint32_t w = (kHl ? c0[k] : __builtin_amdgcn_alignbyte(c1[k], c0[k], 2)) ^ 0x80808080u;
-      const float d = dk[k], nd = -128.0f * d;
-#pragma unroll
-      for (int b = 0; b < 2; ++b) v[kk][b] = fmaf((float)((w >> (8 * (b + kB0))) & 0xFFu), d, nd);
-    }
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      wh[b][p] = as_u(h2{(_Float16)v[0][b], (_Float16)v[1][b]});
-      wl[b][p] = lo_pair(v[0][b], v[1][b], wh[b][p]);
-    }
+    const uint32_t w0 = __builtin_amdgcn_alignbyte(c1[2 * p], c0[2 * p], sh);
+    const uint32_t w1 = __builtin_amdgcn_alignbyte(c1[2 * p + 1], c0[2 * p + 1], sh);
+    h2 lo, hi;  // keys 8 g + 2 p, + 1 of tile 0 (lo) and tile 1 (hi)
+    i8x4_to_h4(__builtin_amdgcn_perm(w1, w0, sel), lo, hi);
+    wb[0][p] = as_u(lo);
+    wb[1][p] = as_u(hi);
   }
 }
 
@@ -440,7 +434,7 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
   }
 
   const int tw = wv >> 2, qd = wv & 3;  // QK: tile tw, blocks 2 qd, 2 qd + 1
-  const int vu = wv >> 1, vb = wv & 1;  // PV: unit vu, codes 2 vb, 2 vb + 1 (two tiles)
+  // PV: block j = wv (two tiles), its d_j folded into the weights
   f4 acc[2];
 #pragma unroll
   for (int x = 0; x < 2; ++x) acc[x] = f4{0.f, 0.f, 0.f, 0.f};
@@ -477,15 +471,12 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
         cq[jj] = mfma32(ka, jj ? qb1 : qb0, f4{0.f, 0.f, 0.f, 0.f});
       }
     }
-    // ---- PV B fragments of this wave's two tiles, in registers (while the MFMAs run)
-    uint32_t wh[2][4], wl[2][4];
-    if (vu & 1) {
-      if (vb) q8_v_words_dec<1, 2>(sm.raw[1], sm.vd, vu >> 1, lane, wh, wl);
-      else q8_v_words_dec<1, 0>(sm.raw[1], sm.vd, vu >> 1, lane, wh, wl);
-    } else {
-      if (vb) q8_v_words_dec<0, 2>(sm.raw[1], sm.vd, vu >> 1, lane, wh, wl);
-      else q8_v_words_dec<0, 0>(sm.raw[1], sm.vd, vu >> 1, lane, wh, wl);
-    }
+    // ---- PV B fragments of this wave's two tiles and the d_j of its keys 8 g .. + 7,
+    // in registers (while the MFMAs run)
+    uint32_t wb[2][4];
+    q8_v_codes_dec(sm.raw[1], wv, lane, wb);
+    const float4 vd0 = *reinterpret_cast<const float4 *>(&sm.vd[wv][8 * g]);
+    const float4 vd1 = *reinterpret_cast<const float4 *>(&sm.vd[wv][8 * g + 4]);
     // this wave's part of its tile's scores, scaled by its keys' d_j, to LDS
     {
       float4 part = {0.f, 0.f, 0.f, 0.f};
@@ -566,24 +557,26 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
       p[k] = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sc[k] - m_run);
       l_run += p[k];
     }
-    // A rows: n < 8 the fp16 hi parts of head n's weights, n >= 8 the lo remainders
+    // A rows: n < 8 the fp16 hi parts of head n's weights times d_j of their keys, n >= 8
+    // the lo remainders
+    const float dv[8] = {vd0.x, vd0.y, vd0.z, vd0.w, vd1.x, vd1.y, vd1.z, vd1.w};
     uint32_t wa[4];
 #pragma unroll
     for (int k2 = 0; k2 < 4; ++k2) {
-      const uint32_t hw = as_u(h2{(_Float16)p[2 * k2], (_Float16)p[2 * k2 + 1]});
-      const uint32_t lw = fp16_sub2(p[2 * k2], p[2 * k2 + 1], hw);
+      const float p0 = p[2 * k2] * dv[2 * k2], p1 = p[2 * k2 + 1] * dv[2 * k2 + 1];
+      const uint32_t hw = as_u(h2{(_Float16)p0, (_Float16)p1});
+      const uint32_t lw = fp16_sub2(p0, p1, hw);
       wa[k2] = n < 8 ? hw : lw;
     }
     const h8 A = __builtin_bit_cast(h8, u4{wa[0], wa[1], wa[2], wa[3]});
 #pragma unroll
-    for (int x = 0; x < 2; ++x) {
-      acc[x] = mfma32(A, __builtin_bit_cast(h8, u4{wh[x][0], wh[x][1], wh[x][2], wh[x][3]}), acc[x]);
-      acc[x] = mfma32(A, __builtin_bit_cast(h8, u4{wl[x][0], wl[x][1], wl[x][2], wl[x][3]}), acc[x]);
-    }
+    for (int x = 0; x < 2; ++x)
+      acc[x] = mfma32(A, __builtin_bit_cast(h8, u4{wb[x][0], wb[x][1], wb[x][2], wb[x][3]}), acc[x]);
   }
 
-  // ---- partial: rows h (hi weights) and h + 8 (lo) summed (lanes g and g + 2), tile T =
-  // 8 (vu >> 1) + (vu & 1) + 2 (2 vb + x), entry 16 T + n of head 8 kv + 4 g + i (lanes 0-31)
+  // ---- partial: rows h (hi weights) and h + 8 (lo) summed (lanes g and g + 2); element
+  // 32 wv + 4 (n & 7) + 2 x + (n >> 3) of head 8 kv + 4 g + i (lanes 0-31) goes to its
+  // tile-order entry (8 consecutive entries per 8 lanes)
   float *P = a.part + (int64_t)slot * 16 * kPartRow;
   float r[2][4];
 #pragma unroll
@@ -593,9 +586,9 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
   if (g < 2) {
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
-      const int T = 8 * (vu >> 1) + (vu & 1) + 2 * (2 * vb + x);
+      const int ent = tile_index(32 * wv + 4 * (n & 7) + 2 * x + (n >> 3));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) P[(8 * kv + 4 * g + i) * kPartRow + 16 * T + n] = r[x][i];
+      for (int i = 0; i < 4; ++i) P[(8 * kv + 4 * g + i) * kPartRow + ent] = r[x][i];
     }
   }
   // the weights' sum of head n % 8 over the lanes g (each holds its 8 keys)
