@@ -215,11 +215,14 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgsT<kRows>
     }
   };
   load_round(w0);
-  // the new key's q . k_new products, loaded after the partials (reduced further down)
-  float qv = 0.0f, kv = 0.0f;
+  // the new key's q . k_new products and this thread's V value of it, loaded after the
+  // partials (reduced further down)
+  const int e = tile_e((i0 + (tid & 31)) >> 4, (i0 + (tid & 31)) & 15);
+  float qv = 0.0f, kv = 0.0f, vnew = 0.0f;
   if (dq != nullptr) {
     qv = c.q[((int64_t)b * 16 + h) * 256 + tid];
     kv = dq[((int64_t)b * 4 + (h >> 3)) * 256 + tid];
+    if (tid < 32) vnew = dq[((int64_t)b * 4 + 2 + (h >> 3)) * 256 + e];
   }
   float m_loc = -INFINITY, lacc = 0.0f;
   float4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -247,8 +250,6 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgsT<kRows>
       m_loc = mc;
     }
   }
-  const int e = tile_e((i0 + (tid & 31)) >> 4, (i0 + (tid & 31)) & 15);
-  const float vnew = (dq != nullptr && tid < 32) ? dq[((int64_t)b * 4 + 2 + (h >> 3)) * 256 + e] : 0.0f;
   const float r = combine_finish(fs, tid, true, m_loc, acc, lacc, qv * kv, dq != nullptr, sl2, vnew);
   if (tid < 32) c.out[((int64_t)b * 16 + h) * 256 + e] = r;
 }
