@@ -576,7 +576,9 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
 
   // ---- partial: rows h (hi weights) and h + 8 (lo) summed (lanes g and g + 2); element
   // 32 wv + 4 (n & 7) + 2 x + (n >> 3) of head 8 kv + 4 g + i (lanes 0-31) goes to its
-  // tile-order entry (8 consecutive entries per 8 lanes)
+  // tile-order entry (8 consecutive entries per 8 lanes). Agent-scope (write-through)
+  // stores: the combine launch reads them from another XCD's L2 misses anyway, and the
+  // launch's end then has fewer dirty lines to write back.
   float *P = a.part + (int64_t)slot * 16 * kPartRow;
   float r[2][4];
 #pragma unroll
@@ -588,13 +590,17 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
     for (int x = 0; x < 2; ++x) {
       const int ent = tile_index(32 * wv + 4 * (n & 7) + 2 * x + (n >> 3));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) P[(8 * kv + 4 * g + i) * kPartRow + ent] = r[x][i];
+      for (int i = 0; i < 4; ++i) store_sc1(P + (8 * kv + 4 * g + i) * kPartRow + ent, r[x][i]);
     }
   }
   // the weights' sum of head n % 8 over the lanes g (each holds its 8 keys)
   float lt = xsum16(l_run);
   lt = xsum32(lt);
-  if (wv == 0 && g == 0 && n < 8) a.ml[(int64_t)slot * 16 + 8 * kv + n] = float2{m_run, lt};
+  if (wv == 0 && g == 0 && n < 8) {
+    float *mlo = reinterpret_cast<float *>(a.ml + ((int64_t)slot * 16 + 8 * kv + n));
+    store_sc1(mlo, m_run);
+    store_sc1(mlo + 1, lt);
+  }
 }
 
 }  // namespace
