@@ -21,6 +21,9 @@ COMMON = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     # Packed FP32 VOP3P forms are kept out of every kernel.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Leading scalar kernel arguments arrive in SGPRs at wave launch (gfx950 kernarg
+    # preload); a kernel whose only argument is a struct is unaffected.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall", "-Wno-unused-function", "-Wno-unused-result",
 ]
 SOURCES = {

@@ -191,16 +191,14 @@ struct CombineArgsT {
   int wg1[kRows];
 };
 using CombineArgs = CombineArgsT<kMaxSegs>;
-template <int kRows>
-__global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgsT<kRows> c) {
-  __shared__ FinishSmem fs;
-  const int h = blockIdx.x >> 3, i0 = 32 * (blockIdx.x & 7), b = blockIdx.y;
+// The merge of output row b from partials [wbeg, wbeg + nwg).
+__device__ __forceinline__ void combine_row(FinishSmem &fs, const float *part, const float2 *ml,
+                                            const float *q, const float *dq, float *out, float sl2,
+                                            int wbeg, int nwg, int b) {
+  const int h = blockIdx.x >> 3, i0 = 32 * (blockIdx.x & 7);
   const int tid = threadIdx.x, ps = tid >> 3, g4 = tid & 7;
-  const float *dq = c.dq;
-  const float sl2 = c.sl2;
-  const int wbeg = c.wg0[b], nwg = c.wg1[b] - wbeg;
-  const float *P = c.part + ((int64_t)wbeg * 16 + h) * kPartRow + i0 + 4 * g4;
-  const float2 *ML = c.ml + (int64_t)wbeg * 16 + h;
+  const float *P = part + ((int64_t)wbeg * 16 + h) * kPartRow + i0 + 4 * g4;
+  const float2 *ML = ml + (int64_t)wbeg * 16 + h;
   const int per = (nwg + kCombSlices - 1) / kCombSlices;
   const int w0 = ps * per, w1 = w0 + per < nwg ? w0 + per : nwg;
   float2 mlv[kCombChunk];
@@ -220,7 +218,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgsT<kRows>
   const int e = tile_e((i0 + (tid & 31)) >> 4, (i0 + (tid & 31)) & 15);
   float qv = 0.0f, kv = 0.0f, vnew = 0.0f;
   if (dq != nullptr) {
-    qv = c.q[((int64_t)b * 16 + h) * 256 + tid];
+    qv = q[((int64_t)b * 16 + h) * 256 + tid];
     kv = dq[((int64_t)b * 4 + (h >> 3)) * 256 + tid];
     if (tid < 32) vnew = dq[((int64_t)b * 4 + 2 + (h >> 3)) * 256 + e];
   }
@@ -251,7 +249,22 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgsT<kRows>
     }
   }
   const float r = combine_finish(fs, tid, true, m_loc, acc, lacc, qv * kv, dq != nullptr, sl2, vnew);
-  if (tid < 32) c.out[((int64_t)b * 16 + h) * 256 + e] = r;
+  if (tid < 32) out[((int64_t)b * 16 + h) * 256 + e] = r;
+}
+template <int kRows>
+__global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgsT<kRows> c) {
+  __shared__ FinishSmem fs;
+  const int b = blockIdx.y;
+  combine_row(fs, c.part, c.ml, c.q, c.dq, c.out, c.sl2, c.wg0[b], c.wg1[b] - c.wg0[b], b);
+}
+// One output row, every argument a scalar: the leading kernel arguments are preloaded into
+// SGPRs where the build asks for it, so the first loads wait for no kernel-argument fetch.
+__global__ __launch_bounds__(256) void decode_combine1_kernel(const float *part, const float2 *ml,
+                                                              const float *q, const float *dq,
+                                                              float *out, float sl2, int wbeg,
+                                                              int nwg) {
+  __shared__ FinishSmem fs;
+  combine_row(fs, part, ml, q, dq, out, sl2, wbeg, nwg, 0);
 }
 
 // ---- In-launch combine of a one-row decode (the combiner workgroups of a decode launch
@@ -445,16 +458,8 @@ static inline bool decode_fuse_enabled() {
 // Launch the combine over n output rows (grid: 128 (head, slice) workgroups per row).
 static inline int launch_combine(const CombineArgs &c, int n, hipStream_t s) {
   if (n == 1) {
-    CombineArgsT<1> c1;
-    c1.part = c.part;
-    c1.ml = c.ml;
-    c1.q = c.q;
-    c1.dq = c.dq;
-    c1.out = c.out;
-    c1.sl2 = c.sl2;
-    c1.wg0[0] = c.wg0[0];
-    c1.wg1[0] = c.wg1[0];
-    hipLaunchKernelGGL(decode_combine_kernel<1>, dim3(16 * 8, 1u), dim3(256), 0, s, c1);
+    hipLaunchKernelGGL(decode_combine1_kernel, dim3(16 * 8, 1u), dim3(256), 0, s, c.part, c.ml,
+                       c.q, c.dq, c.out, c.sl2, c.wg0[0], c.wg1[0] - c.wg0[0]);
   } else {
     hipLaunchKernelGGL(decode_combine_kernel<kMaxSegs>, dim3(16 * 8, (unsigned)n), dim3(256), 0,
                        s, c);

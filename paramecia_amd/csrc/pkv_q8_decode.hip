@@ -344,10 +344,14 @@ __device__ __forceinline__ void q8_v_codes_dec(const uint32_t (*rows)[kQ8RowWord
 }
 
 // kOne: a one-segment launch; kFused: the launch appends the new rows. Neither needs a
-// kernel argument to tell a workgroup its role, so the decode workgroups' first scalar
-// loads (segment 0 and the scalars) go out together.
+// kernel argument to tell a workgroup its role. The leading scalar arguments repeat what
+// the decode workgroups need first (segment 0's rows and key count, q, the partial
+// buffers, the row stride, kpw, sl2): the build preloads them into SGPRs, so the first
+// loads of a one-segment launch wait for no kernel-argument fetch.
 template <bool kOne, bool kFused>
-__global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
+__global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(
+    const uint8_t *k_0, const uint8_t *v_0, const float *q, float *part, float2 *mlb, int rs_t,
+    int kpw, int seq_k0, float sl2, Q8Args a) {
   __shared__ Q8mSmem sm;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
@@ -364,14 +368,24 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
     a.dq[(int64_t)row * 256 + tid] = q8_quantize_row_lanes(x, dst, tid);
     return;
   }
-  // a one-segment launch (kOne) reads segment 0 without waiting for nseg
-  int b = 0;
-  if (!kOne)
+  // the segment of this workgroup (segment 0 of a one-segment launch from the scalar
+  // arguments)
+  const uint8_t *sk = k_0, *sv = v_0;
+  int64_t seq_k = seq_k0;
+  int wg0 = 0, qi = 0;
+  if (!kOne) {
+    int b = 0;
     while (b + 1 < a.nseg && slot >= a.seg[b + 1].wg0) ++b;
-  const DecodeSeg sg = a.seg[b];
-  const int64_t k0 = (int64_t)(slot - sg.wg0) * a.kpw;
-  const int64_t k1 = k0 + a.kpw < sg.seq_k ? k0 + a.kpw : sg.seq_k;
-  const uint8_t *kbase = sg.k + kv * a.rs_h, *vbase = sg.v + kv * a.rs_h;
+    const DecodeSeg sg = a.seg[b];
+    sk = sg.k;
+    sv = sg.v;
+    seq_k = sg.seq_k;
+    wg0 = sg.wg0;
+    qi = sg.qi;
+  }
+  const int64_t k0 = (int64_t)(slot - wg0) * kpw;
+  const int64_t k1 = k0 + kpw < seq_k ? k0 + kpw : seq_k;
+  const uint8_t *kbase = sk + kv * kQ8Row, *vbase = sv + kv * kQ8Row;
 
   // head kv's K and V rows (272 bytes per key) of the block at c0: every load is issued
   // before the first LDS store, unconditionally (pieces past the block and keys past nk
@@ -387,7 +401,7 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
       const int c = min(tid + x * kQ8mThreads, kPieces - 1);
       const int tn = c / (kPieces / 2), r = c % (kPieces / 2);
       const int key = min(r / 17, nk - 1), piece = r % 17;
-      w[x] = *reinterpret_cast<const uint4 *>((tn ? vbase : kbase) + (c0 + key) * a.rs_t + 16 * piece);
+      w[x] = *reinterpret_cast<const uint4 *>((tn ? vbase : kbase) + (c0 + key) * rs_t + 16 * piece);
     }
   };
   auto store_block = [&](int nk) {
@@ -403,7 +417,7 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
           const int j = piece >> 1;
           const uint32_t dw = (j >> 1) == 0 ? v.x : (j >> 1) == 1 ? v.y : (j >> 1) == 2 ? v.z : v.w;
           const float d = h2f((j & 1) ? (dw >> 16) : (dw & 0xFFFF));
-          if (tn == 0) sm.kd[j][key] = d * a.sl2;
+          if (tn == 0) sm.kd[j][key] = d * sl2;
           else sm.vd[j][key] = d;
         }
       }
@@ -415,7 +429,7 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
   // both fragments
   {
     const int tq = tid & 255, j = tq >> 5, gq = (tq >> 3) & 3, hq = tq & 7;
-    const float *qrow = a.q + ((int64_t)sg.qi * 16 + 8 * kv + hq) * 256 + 32 * j + 8 * gq;
+    const float *qrow = q + ((int64_t)qi * 16 + 8 * kv + hq) * 256 + 32 * j + 8 * gq;
     const float4 q0 = *reinterpret_cast<const float4 *>(qrow);  // threads >= 256 load again
     const float4 q1 = *reinterpret_cast<const float4 *>(qrow + 4);
     if (k0 < k1) load_block(k0, (int)(k1 - k0 < kBlk ? k1 - k0 : kBlk));
@@ -579,7 +593,7 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
   // tile-order entry (8 consecutive entries per 8 lanes). Agent-scope (write-through)
   // stores: the combine launch reads them from another XCD's L2 misses anyway, and the
   // launch's end then has fewer dirty lines to write back.
-  float *P = a.part + (int64_t)slot * 16 * kPartRow;
+  float *P = part + (int64_t)slot * 16 * kPartRow;
   float r[2][4];
 #pragma unroll
   for (int x = 0; x < 2; ++x)
@@ -597,7 +611,7 @@ __global__ __launch_bounds__(kQ8mThreads) void q8_decode_mfma_kernel(Q8Args a) {
   float lt = xsum16(l_run);
   lt = xsum32(lt);
   if (wv == 0 && g == 0 && n < 8) {
-    float *mlo = reinterpret_cast<float *>(a.ml + ((int64_t)slot * 16 + 8 * kv + n));
+    float *mlo = reinterpret_cast<float *>(mlb + ((int64_t)slot * 16 + 8 * kv + n));
     store_sc1(mlo, m_run);
     store_sc1(mlo + 1, lt);
   }
@@ -628,7 +642,8 @@ static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, cons
   // (up to 256 workgroups per segment). Otherwise the VALU kernel: one chunk per
   // workgroup while that keeps <= 512 partials per segment (16-key chunks up to 8192
   // keys, 32-key chunks beyond), more chunks per workgroup for longer caches.
-  bool mfma = longest <= 32768 && rs_h == kQ8Row && rs_t % 16 == 0 && q8_mfma_enabled();
+  bool mfma = longest <= 32768 && rs_h == kQ8Row && rs_t % 16 == 0 && rs_t < (1 << 24) &&
+              q8_mfma_enabled();
   for (int i = 0; i < n && mfma; ++i)
     mfma = (reinterpret_cast<uintptr_t>(in[i].k) & 15) == 0 &&
            (reinterpret_cast<uintptr_t>(in[i].v) & 15) == 0;
@@ -673,14 +688,14 @@ static int launch_q8_segments(const DecodeSegIn *in, int n, const float *q, cons
     d.nwg = 2 * wg;
     const int nq = fused ? 4 * n : 0;
     const dim3 grid((unsigned)(2 * wg + nq)), block(kQ8mThreads);
-    if (n == 1 && fused)
-      hipLaunchKernelGGL((q8_decode_mfma_kernel<true, true>), grid, block, 0, s, d);
-    else if (n == 1)
-      hipLaunchKernelGGL((q8_decode_mfma_kernel<true, false>), grid, block, 0, s, d);
-    else if (fused)
-      hipLaunchKernelGGL((q8_decode_mfma_kernel<false, true>), grid, block, 0, s, d);
-    else
-      hipLaunchKernelGGL((q8_decode_mfma_kernel<false, false>), grid, block, 0, s, d);
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, grid, block, 0, s, d.seg[0].k, d.seg[0].v, q, d.part, d.ml,
+                         (int)rs_t, d.kpw, (int)d.seg[0].seq_k, d.sl2, d);
+    };
+    if (n == 1 && fused) go(q8_decode_mfma_kernel<true, true>);
+    else if (n == 1) go(q8_decode_mfma_kernel<true, false>);
+    else if (fused) go(q8_decode_mfma_kernel<false, true>);
+    else go(q8_decode_mfma_kernel<false, false>);
   } else if (chunk == 16) {
     hipLaunchKernelGGL(q8_decode_kernel<16>, dim3((unsigned)wg), dim3(kQ8Threads), 0, s, d);
   } else {
