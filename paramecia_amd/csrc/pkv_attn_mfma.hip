@@ -143,7 +143,8 @@ int launch_paged_decode_q4k(const PagedSeqDesc *seqs, int nseq, const PagedPoolD
   d.dq = fused ? d.part + part_floats + ml_floats : nullptr;
   rc = device_status_word(&d.status);
   if (rc) return rc;
-  hipLaunchKernelGGL((q4k_decode_kernel<false, 0>), dim3((unsigned)nwg), dim3(kThreads), 0, s, d);
+  hipLaunchKernelGGL((q4k_decode_kernel<false, 0>), dim3((unsigned)nwg), dim3(kThreads), 0, s,
+                     nullptr, nullptr, q, nullptr, k_new, decode_strides(rs_t, rs_h), 0, nwg, d);
   PKV_HIP(hipGetLastError());
   c.part = d.part;
   c.ml = d.ml;

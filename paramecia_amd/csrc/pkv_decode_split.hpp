@@ -474,5 +474,11 @@ static inline int launch_combine(const CombineArgs &c, int n, hipStream_t s) {
 static inline bool decode_rows_fit(int64_t seq_k, int64_t rs_t) {
   return rs_t < (1 << 24) && seq_k < (1 << 24) && (uint64_t)seq_k * (uint64_t)rs_t < (1ull << 32);
 }
+// The decode kernels' packed row strides: rs_t (< 2^24, decode_rows_fit) | rs_h << 24
+// (rs_h < 2^40, decode_head_stride_fits).
+static inline bool decode_head_stride_fits(int64_t rs_h) { return rs_h >= 0 && rs_h < (1ll << 40); }
+static inline uint64_t decode_strides(int64_t rs_t, int64_t rs_h) {
+  return (uint64_t)rs_t | ((uint64_t)rs_h << 24);
+}
 
 }  // namespace pkv

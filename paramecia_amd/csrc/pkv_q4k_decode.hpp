@@ -545,11 +545,18 @@ __device__ __forceinline__ void issue_prep_consts(void *alpha_lds, void *tail_ld
       : "memory", "scc");
 }
 
+// The leading scalar arguments repeat what a workgroup needs before its first loads
+// (segment 0's rows and key count for a one-segment launch, q, the fused region's words,
+// k_new, the row strides rs_t | rs_h << 24, nwg): the build preloads them into SGPRs,
+// so those loads wait for no kernel-argument fetch.
 template <bool kPrep, int kSegs>
-__global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs> a) {
+__global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
+    const uint8_t *k_0, const uint8_t *v_0, const float *q_0, uint32_t *words_0,
+    const float *knew_0, uint64_t strides, int seq_k0, int nwg_0, DecodeArgsT<kSegs> a) {
   __shared__ Smem sm;
-  if constexpr (kSegs == 1) {
-    if ((int)blockIdx.x >= a.nwg) {  // a combiner workgroup (in-launch combine)
+  constexpr bool kOne = kSegs == 1;
+  if constexpr (kOne) {
+    if ((int)blockIdx.x >= nwg_0) {  // a combiner workgroup (in-launch combine)
       const TailArgs t{a.nwg, a.words, a.part, a.ml, a.q, a.q_out,
                        a.k_new != nullptr ? a.dq : nullptr, a.out, a.sl2, a.status};
       tail_combine<kPrep>(t, (int)blockIdx.x - a.nwg, &sm);
@@ -559,15 +566,23 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // the launch parity of an in-launch combine (0 otherwise), in the lowest bit of every
   // partial word this workgroup writes
-  uint32_t par = 0;
+  // (a one-segment launch has its words exactly when it combines in-launch). The word is
+  // read without a branch (an empty buffer range reads 0) and the parity is formed where
+  // it is stored, so the load is waited for at the first store, not here.
+  uint32_t par_raw = 0u, par_on = 0u;
   if constexpr (kSegs == 1) {
-    if (a.ncomb > 0) par = __builtin_amdgcn_readfirstlane((load_sc1(a.words + kWordGen) ^ 1u) & 1u);
+    par_on = words_0 != nullptr ? 1u : 0u;
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(words_0, 0, par_on ? 4 * Workspace::kFusedWords : 0, 0x00020000);
+    par_raw = __builtin_amdgcn_raw_buffer_load_b32(rw, 4 * kWordGen, 0, kSC1);
   }
+  const auto parity = [&]() { return (par_raw ^ par_on) & par_on; };
   const int kv = wave & 1, wsub = wave >> 1;
   const int wg = blockIdx.x;
   const int n = lane & 15, g = lane >> 4;
   const int kvu = __builtin_amdgcn_readfirstlane(kv);
-  const uint32_t rs_t = (uint32_t)a.rs_t;
+  const uint32_t rs_t = (uint32_t)(strides & 0xFFFFFFu);
+  const int64_t rs_h = (int64_t)(strides >> 24);
   const LoadPlan P = make_plan(lane, rs_t);
   const uint32_t bstep = 4u * kBlk * rs_t;  // byte distance between a wave's blocks
   // LDS byte addresses of this wave's two stages
@@ -578,8 +593,12 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
   // virtual block line, one piece per segment met (its blocks [pb0, pb1)), each with its
   // partial in slot wg + (the segment's index), distinct for every piece and
   // consecutive for the pieces of one segment.
-  const int V0 = wg * a.vq + (wg < a.vr ? wg : a.vr);
-  const int V1 = V0 + a.vq + (wg < a.vr ? 1 : 0);
+  // (one segment: its blocks, or one virtual block for an empty one, split over nwg)
+  const int nblk0 = (int)((seq_k0 + kBlk - 1) / kBlk);
+  const int vq = kOne ? (nblk0 > 0 ? nblk0 : 1) / nwg_0 : a.vq;
+  const int vr = kOne ? (nblk0 > 0 ? nblk0 : 1) % nwg_0 : a.vr;
+  const int V0 = wg * vq + (wg < vr ? wg : vr);
+  const int V1 = V0 + vq + (wg < vr ? 1 : 0);
   int ps = -1, pb0 = 0, pb1 = 0, slot = wg;
   DecodeSeg sgv = {};  // read only while a piece is held
   // paged device-list mode: (pi, pj) is the next segment the scan looks at
@@ -628,7 +647,14 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
     if constexpr (kSegs == 1) {  // one segment at voff 0: the range is the piece
       if (ps >= 0) return false;
       ps = 0;
-      sgv = a.seg[0];
+      sgv.k = const_cast<uint8_t *>(k_0);
+      sgv.v = const_cast<uint8_t *>(v_0);
+      sgv.seq_k = seq_k0;
+      sgv.t_new = a.seg[0].t_new;
+      sgv.nblk = nblk0;
+      sgv.wg0 = 0;
+      sgv.qi = 0;
+      sgv.voff = 0;
       pb0 = V0;
       pb1 = V1 < sgv.nblk ? V1 : sgv.nblk;
       return V0 < (sgv.nblk > 0 ? sgv.nblk : 1);
@@ -687,7 +713,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
   // step, which attends to the new key. This runs while the first block streams in.
   // The row is read before any staging load is issued, so the compiler's wait for it
   // does not wait for the stage too.
-  const bool quant = a.k_new != nullptr && wg < 4 * a.nnew && tid < 256;
+  const bool quant = knew_0 != nullptr && wg < 4 * (kOne ? 1 : a.nnew) && tid < 256;
   float xq = 0.0f;
   PrepElem kpe[1] = {PrepElem{1.0f, 1.0f, 0.0f}};
   auto k_prep_elem = [&](int rs) {
@@ -705,7 +731,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
   float rcos = 1.0f, rsin = 0.0f;
   if (quant) {
     const int p = (wg >> 1) & 1, kvr = wg & 1;
-    xq = (p ? a.v_new : a.k_new)[((int64_t)(wg >> 2) * 2 + kvr) * 256 + tid];
+    xq = (p ? a.v_new : knew_0)[((int64_t)(wg >> 2) * 2 + kvr) * 256 + tid];
     if constexpr (kPrep) {
       if (p == 0) kpe[0] = k_prep_elem(wg >> 2);
       qa4 = reinterpret_cast<const f4 *>(a.prep.q_alpha)[lane];
@@ -735,10 +761,10 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
         const PagedSeqArg &sq = a.pq[rs];
         const int64_t pg = sq.pages[sq.len >> a.page_lg];
         dst = (p ? a.vplane : a.kplane) + pg * a.page_bytes +
-              (sq.len & (((int64_t)1 << a.page_lg) - 1)) * a.rs_t + kvr * a.rs_h;
+              (sq.len & (((int64_t)1 << a.page_lg) - 1)) * rs_t + kvr * rs_h;
       } else {
         const DecodeSeg &rg = a.seg[rs];
-        dst = (p ? rg.v : rg.k) + rg.t_new * a.rs_t + kvr * a.rs_h;
+        dst = (p ? rg.v : rg.k) + rg.t_new * rs_t + kvr * rs_h;
       }
       if constexpr (kPrep) {
         if (p == 0) {  // k_norm and rope of the new K row (bit-exact), then its quantization
@@ -756,7 +782,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
       if (a.ncomb > 0) {  // the row's word once all 256 values are stored
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         bar();
-        if (tid == 0) store_sc1(a.words + kWordRow + row, par);
+        if (tid == 0) store_sc1(a.words + kWordRow + row, parity());
       }
     }
     __builtin_amdgcn_s_setprio(0);
@@ -771,8 +797,8 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
     const int first = __builtin_amdgcn_readfirstlane(pb0 + wsub);
     const int nmine =
         __builtin_amdgcn_readfirstlane(have && first < pb1 ? (pb1 - first + 3) / 4 : 0);
-    const uint8_t *kbase = sg.k + kvu * a.rs_h;
-    const uint8_t *vbase = sg.v + kvu * a.rs_h;
+    const uint8_t *kbase = sg.k + kvu * rs_h;
+    const uint8_t *vbase = sg.v + kvu * rs_h;
     const int64_t seq_k = sg.seq_k;
     // rows of keys [0, seq_k) of this head; loads past them return zeros (masked keys)
     const uint32_t span = seq_k > 0 ? (uint32_t)(seq_k - 1) * rs_t + 144u : 0u;
@@ -793,7 +819,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
                             make_rsrc(a.prep.sin_tab + ro, (uint32_t)half * 4u), (uint32_t)lane);
         }
       }
-      const u4s rq = make_rsrc(a.q + ((int64_t)sg.qi * 16 + 8 * kvu) * 256, 8 * 256 * 4);
+      const u4s rq = make_rsrc(q_0 + ((int64_t)sg.qi * 16 + 8 * kvu) * 256, 8 * 256 * 4);
       issue_q(&sm.run.st[wave][1], rq, 16u * lane);
     }
     __syncthreads();
@@ -917,7 +943,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
         }
         if (a.ncomb > 0 && wg == sg.wg0 && wsub == 0) {  // this wave's q rows are stored
           asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-          if (lane == 0) store_sc1(a.words + kWordQ + kvu, par);
+          if (lane == 0) store_sc1(a.words + kWordQ + kvu, parity());
         }
 #pragma unroll
         for (int st = 0; st < 8; ++st) convert(st, v[st]);
@@ -946,11 +972,11 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
         if (a.ncomb > 0) {
           float *pz = a.part + ((int64_t)slot * 16 * kPartRow + 8 * tid);
 #pragma unroll
-          for (int x = 0; x < 8; ++x) store_sc1(pz + x, tag_par(0.0f, par));
+          for (int x = 0; x < 8; ++x) store_sc1(pz + x, tag_par(0.0f, parity()));
           if (tid < 16) {
             float *mlo = reinterpret_cast<float *>(a.ml + (slot * 16 + tid));
-            store_sc1(mlo, tag_par(-INFINITY, par));
-            store_sc1(mlo + 1, tag_par(0.0f, par));
+            store_sc1(mlo, tag_par(-INFINITY, parity()));
+            store_sc1(mlo + 1, tag_par(0.0f, parity()));
           }
         }
       }
@@ -1079,10 +1105,10 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
       float *d0 = a.part + ((slot * 16 + 8 * kv2 + 4 * g2) * kPartRow + 16 * T2 + n2);
       // lowest bit: the launch parity (in-launch combine) or zero
       if (a.ncomb > 0) {
-        store_sc1(d0, tag_par(acc.x, par));
-        store_sc1(d0 + kPartRow, tag_par(acc.y, par));
-        store_sc1(d0 + 2 * kPartRow, tag_par(acc.z, par));
-        store_sc1(d0 + 3 * kPartRow, tag_par(acc.w, par));
+        store_sc1(d0, tag_par(acc.x, parity()));
+        store_sc1(d0 + kPartRow, tag_par(acc.y, parity()));
+        store_sc1(d0 + 2 * kPartRow, tag_par(acc.z, parity()));
+        store_sc1(d0 + 3 * kPartRow, tag_par(acc.w, parity()));
       } else {
         __builtin_nontemporal_store(untag(acc.x), d0);
         __builtin_nontemporal_store(untag(acc.y), d0 + kPartRow);
@@ -1100,8 +1126,8 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(DecodeArgsT<kSegs>
       }
       float *mlo = reinterpret_cast<float *>(a.ml + (slot * 16 + tid));
       if (a.ncomb > 0) {
-        store_sc1(mlo, tag_par(M, par));
-        store_sc1(mlo + 1, tag_par(L, par));
+        store_sc1(mlo, tag_par(M, parity()));
+        store_sc1(mlo + 1, tag_par(L, parity()));
       } else {
         __builtin_nontemporal_store(untag(M), mlo);
         __builtin_nontemporal_store(untag(L), mlo + 1);
@@ -1126,6 +1152,7 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
                                   const float *k_new, const float *v_new, float *out,
                                   int64_t rs_t, int64_t rs_h, float scale, Workspace &ws,
                                   hipStream_t s, const DecodePrep *prep = nullptr) {
+  if (!decode_head_stride_fits(rs_h)) return PKV_ERR_UNSUPPORTED;
   DecodeArgsT<kMaxSegs> d;
   const bool fused = k_new != nullptr;
   for (int i = 0; i < n; ++i) {
@@ -1213,12 +1240,14 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
     static_cast<DecodeArgsBase &>(d1) = d;
     d1.seg[0] = d.seg[0];
     hipLaunchKernelGGL((q4k_decode_kernel<kPrep, 1>), dim3((unsigned)(nwg + d.ncomb)), dim3(kThreads),
-                       0, s, d1);
+                       0, s, d.seg[0].k, d.seg[0].v, q, d.words, k_new,
+                       decode_strides(rs_t, rs_h), (int)d.seg[0].seq_k, nwg, d1);
     PKV_HIP(hipGetLastError());
     if (d.ncomb > 0) return PKV_OK;
   } else {
     hipLaunchKernelGGL((q4k_decode_kernel<kPrep, kMaxSegs>), dim3((unsigned)nwg), dim3(kThreads), 0,
-                       s, d);
+                       s, d.seg[0].k, d.seg[0].v, q, d.words, k_new, decode_strides(rs_t, rs_h),
+                       (int)d.seg[0].seq_k, nwg, d);
   }
   PKV_HIP(hipGetLastError());
   c.part = d.part;
