@@ -42,9 +42,9 @@ Q8_ROW = 272
 # rocprofv3 --pmc runs (FETCH_SIZE x2.0, WRITE_SIZE x1.0) summarised in profiles/; the
 # profiling step cannot run inside bench.py itself. Refreshed with the profiles.
 MEASURED_TRAFFIC = {
-    3: (85_016_473, "profiles/q4k_decode_config3.md: the decode launch with its in-launch "
+    3: (85_000_000, "profiles/q4k_decode_config3.md: the decode launch with its in-launch "
                     "combine, per layer"),
-    1: (11_460_000, "profiles/q8_decode_config1.md: decode + combine"),
+    1: (11_130_572, "profiles/q8_decode_config1.md: decode + combine"),
     2: (170_260_000, "profiles/q4k_prefill_config2.md: prefill kernel + split merge"),
     "2q8": (136_320_102, "profiles/q8_prefill_config2.md: prefill kernel + split merge"),
     4: (1_064_255_795, "profiles/prefix_restore_config4.md: copy_segments_kernel read + "
