@@ -529,8 +529,13 @@ def run_config1(args):
     pk.fill_normal(vn, W.SEED, W.stream_id(1, W.T_NEW_V))
     step = lambda: c.append_attend(kn, vn, q, W.SCALE, offset=S)
     reps = args.graph_reps if args.graph_reps > 0 else 20
-    ms = graph_time(torch, step, args.steps, args.warmup, reps)
-    ms_1 = graph_time(torch, step, args.steps, args.warmup, 1)
+    # A step is ~8 us: at least 10 replays of 20 steps are timed (200 steps, 1.6 ms of
+    # GPU time), so that one replay's submission gap is not what a short --steps measures
+    sub = argparse.Namespace(**vars(args))
+    sub.steps = max(args.steps, 10 * reps)
+    ms = graph_time(torch, step, sub.steps, args.warmup, reps)
+    ms_1 = graph_time(torch, step, sub.steps, args.warmup, 1)
+    args = sub
     nbytes = layer_bytes(S + 1, Q8_ROW)
     gbs = nbytes / (ms * 1e-3) / 1e9
     r = base_result(1, "Q8_0 decode-attn µs/step @4097 keys, 1 layer", round(ms * 1000, 2),
