@@ -2,9 +2,9 @@
 // make_qkx1_quants(15, 5), restated; reference call site
 // paramecia-model/src/qwen3_next.rs:486-487): 256 threads per 256-element superblock,
 // one element per lane, 32 lanes per sub-block. The two f32 sums of make_qkx1_quants
-// accumulate in element order in the reference, so every lane of a sub-block stages
-// its term in LDS and replays the 32-term chain in order; the element-wise work
-// (rounding, clamping, products, the final division) runs in parallel. The bytes
+// accumulate in element order in the reference, so each sub-block's 32-term chain is
+// replayed in order, moving across its lanes; the element-wise work (rounding,
+// clamping, products, the final division) runs in parallel. The bytes
 // equal those of the 8-lane throughput kernel and of the CPU oracle.
 // Include-only; every function keeps a*b+c as two roundings (contraction off).
 #pragma once
@@ -24,28 +24,28 @@ __device__ __forceinline__ int32_t q4_level_i(float v) {
 }
 
 struct Q4kScratch {
-  float scr[256];
   float red[2][8];
   uint32_t codes[8];
   uint8_t nib[256];
 };
 
-__device__ __forceinline__ float q4k_chain_sum_32(float *scr, int i, float term, float init) {
+// The 32-term sum of each half-wave's terms (lane i of the half holds term i) in element
+// order, init first, in registers: the running sum moves up one lane per step (DPP
+// wave_shr:1), so after step k lane i holds ((init + t[i-k]) + ...) + t[i]. Lanes 31 and
+// 63 end with their half's sum (lane 32 starts its chain from init at step 0, like lane
+// 0), which is then read out and given to every lane of the half. No LDS round trip: the
+// other waves' block traffic makes those long.
+__device__ __forceinline__ float q4k_chain_sum_32(float term, float init) {
 #pragma clang fp contract(off)
-  scr[i] = term;
-  __builtin_amdgcn_wave_barrier();
-  const float4 *s4 = reinterpret_cast<const float4 *>(scr);
-  float acc = init;
+  float acc = init + term;
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const float4 t = s4[q];
-    acc += t.x;
-    acc += t.y;
-    acc += t.z;
-    acc += t.w;
+  for (int k = 1; k < 32; ++k) {
+    const int prev = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x138, 0xF, 0xF, false);
+    acc = __builtin_bit_cast(float, prev) + term;
   }
-  __builtin_amdgcn_wave_barrier();
-  return acc;
+  const int lo = __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 31);
+  const int hi = __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 63);
+  return __builtin_bit_cast(float, (__lane_id() < 32) ? lo : hi);
 }
 
 // All-reduce over the 32 lanes of each half-wave with DPP moves (within 16-lane rows)
@@ -77,7 +77,6 @@ static __device__ __forceinline__ void q4k_quantize_superblock_lanes(float x, ui
                                                                    Barrier bar = Barrier()) {
 #pragma clang fp contract(off)
   const int j = tid >> 5, i = tid & 31;
-  float *mine = S->scr + 32 * j;
   const auto imin = [](int32_t p, int32_t q) { return p < q ? p : q; };
   const auto imax = [](int32_t p, int32_t q) { return p > q ? p : q; };
   const auto iadd = [](int32_t p, int32_t q) { return p + q; };
@@ -97,10 +96,10 @@ static __device__ __forceinline__ void q4k_quantize_superblock_lanes(float x, ui
       const int32_t li = q4_level_i(iscale * (x - fmin));
       const bool changed = (uint32_t)li != L;
       L = (uint32_t)li;
-      const float sumlx = q4k_chain_sum_32(mine, i, (x - fmin) * (float)li, 0.0f);
+      const float sumlx = q4k_chain_sum_32((x - fmin) * (float)li, 0.0f);
       const int32_t l2 = halfwave_allreduce(li * li, iadd);
       scale = sumlx / (float)l2;
-      const float sum = q4k_chain_sum_32(mine, i, x - scale * (float)L, -0.0f);
+      const float sum = q4k_chain_sum_32(x - scale * (float)L, -0.0f);
       fmin = sum / 32.0f;
       if (fmin > 0.0f) fmin = 0.0f;
       iscale = 1.0f / scale;
@@ -116,11 +115,27 @@ static __device__ __forceinline__ void q4k_quantize_superblock_lanes(float x, ui
     S->red[1][j] = neg_min;
   }
   bar();
+  // The 16 values come into registers first (four LDS reads, one wait): read inside the
+  // fold, each read followed the previous step's uniform branch on a NaN, one LDS round
+  // trip per value.
+  float rv[2][8];
+  {
+    const float4 *r4 = reinterpret_cast<const float4 *>(&S->red[0][0]);
+    const float4 t0 = r4[0], t1 = r4[1], t2 = r4[2], t3 = r4[3];
+    rv[0][0] = t0.x; rv[0][1] = t0.y; rv[0][2] = t0.z; rv[0][3] = t0.w;
+    rv[0][4] = t1.x; rv[0][5] = t1.y; rv[0][6] = t1.z; rv[0][7] = t1.w;
+    rv[1][0] = t2.x; rv[1][1] = t2.y; rv[1][2] = t2.z; rv[1][3] = t2.w;
+    rv[1][4] = t3.x; rv[1][5] = t3.y; rv[1][6] = t3.z; rv[1][7] = t3.w;
+    asm volatile("" : "+v"(rv[0][0]), "+v"(rv[0][1]), "+v"(rv[0][2]), "+v"(rv[0][3]),
+                 "+v"(rv[0][4]), "+v"(rv[0][5]), "+v"(rv[0][6]), "+v"(rv[0][7]),
+                 "+v"(rv[1][0]), "+v"(rv[1][1]), "+v"(rv[1][2]), "+v"(rv[1][3]),
+                 "+v"(rv[1][4]), "+v"(rv[1][5]), "+v"(rv[1][6]), "+v"(rv[1][7]));
+  }
   float max_scale = 0.0f, max_min = 0.0f;  // fold from +0, NaN-dropping maxNum
 #pragma unroll
   for (int jj = 0; jj < 8; ++jj) {
-    max_scale = fmax_rs(S->red[0][jj], max_scale);
-    max_min = fmax_rs(S->red[1][jj], max_min);
+    max_scale = fmax_rs(rv[0][jj], max_scale);
+    max_min = fmax_rs(rv[1][jj], max_min);
   }
   const float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
   const float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
