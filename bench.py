@@ -225,9 +225,10 @@ def run_config3(args):
 
     # eager: 12 ctypes launches per step from Python (host overhead included)
     eager_ms = event_time(torch, step, args.steps, args.warmup)
-    # HIP graph of args.graph_reps 12-layer steps (default one), replayed (the
-    # serving-loop form), and a graph of a single step for reference
-    reps = args.graph_reps if args.graph_reps > 0 else 1
+    # HIP graph of args.graph_reps 12-layer steps (default ten), replayed (the
+    # serving-loop form, whose graph holds the whole forward pass: a replay's submission
+    # gap is shared by ten steps), and a graph of a single step for reference
+    reps = args.graph_reps if args.graph_reps > 0 else 10
     ms = graph_time(torch, step, args.steps, args.warmup, reps)
     warm_calls = WARM_RUN["calls"]
     ms_1 = graph_time(torch, step, args.steps, args.warmup, 1) if reps > 1 else ms
