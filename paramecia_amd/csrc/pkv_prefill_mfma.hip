@@ -304,7 +304,8 @@ __global__ __launch_bounds__(kPfThreads) void q4k_prefill_kernel(PrefillArgs a) 
   const int64_t klim = a.causal ? myq + a.q_offset : (int64_t)1 << 62;
 
   // Waves 0-4 build the fp16 operands of block i + 1 while every wave runs the MFMAs of
-  // block i: one barrier per block. Raw stages rotate over kRaw = 3 (blocks i + 1 and
+  // block i (waves 0-3 before them, wave 4 right after issuing its QK MFMAs): one
+  // barrier per block. Raw stages rotate over kRaw = 3 (blocks i + 1 and
   // i + 2 in flight or landed while block i + 3 is issued).
   auto dequant = [&](int blk) {
     const Stage &st = sm.raw[blk % kRaw];
@@ -313,8 +314,14 @@ __global__ __launch_bounds__(kPfThreads) void q4k_prefill_kernel(PrefillArgs a) 
       dq_keys(st, Dn, a.sl2, MK, wave, lane);
     else if (wave < 4)
       dq_values(st, Dn, MK, wave - 2, lane);
-    else if (wave == 4)
-      dq_value_mins(st, Dn, lane);
+  };
+  // Wave 4 builds the small min tables of block i + 1 (a few LDS round trips, little
+  // VALU) while its QK MFMAs of block i run, ahead of wave 0, which shares its SIMD: at
+  // the top of the block they put this wave's MFMAs after wave 0's dequantization.
+  auto dequant_mins = [&](int blk) {
+    __builtin_amdgcn_s_setprio(2);
+    dq_value_mins(sm.raw[blk % kRaw], sm.dq[blk & 1], lane);
+    __builtin_amdgcn_s_setprio(0);
   };
   if (nb > 0) {
     if (loader) {  // block 0 landed (block 1 may still fly)
@@ -326,6 +333,7 @@ __global__ __launch_bounds__(kPfThreads) void q4k_prefill_kernel(PrefillArgs a) 
     __syncthreads();
     if (loader && nb > 2) issue(2);
     dequant(0);
+    if (wave == 4) dequant_mins(0);
   }
   for (int i = 0; i < nb; ++i) {
     if (loader && i + 1 < nb) {  // block i + 1 landed (block i + 2 may still fly)
@@ -366,6 +374,10 @@ __global__ __launch_bounds__(kPfThreads) void q4k_prefill_kernel(PrefillArgs a) 
       const h4 A2 = D.ka2[t][lane];
       s2[t] = mfma16(A2, q2h, f4{0.f, 0.f, 0.f, 0.f});
       s2[t] = mfma16(A2, q2l, s2[t]);
+    }
+    if (wave == 4 && i + 1 < nb) {
+      __builtin_amdgcn_sched_barrier(0);  // the MFMAs above go out first
+      dequant_mins(i + 1);
     }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
