@@ -354,53 +354,78 @@ __device__ __forceinline__ void tail_combine(const TailArgs &a, int c, void *lds
   float qv = 0.0f, kv = 0.0f, vnew = 0.0f;
   if (merger) {
     // Poll the words this thread merges (and, on lanes 0-2, the new-row and prepared-q
-    // words every lane reads) until each has this launch's parity; a poll reloads only
-    // what is not there yet.
+    // words every lane reads) until each has this launch's parity.
     const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(a.part), 0, nwg * 16 * kPartRow * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t rm =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float2 *>(a.ml), 0, nwg * 16 * 8, 0x00020000);
-    const int cnt = w1 > w0 ? w1 - w0 : 0;
-    uint32_t need = (1u << cnt) - 1u;  // entries not merged yet
+    const int cnt = w1 > w0 ? w1 - w0 : 0;  // entries of this thread's slice
     const int lane = tid & 63;
     const uint32_t *xw = (lane < 2 && fused) ? a.words + kWordRow + 2 * lane + kvh
                          : (lane == 2 && kPrep) ? a.words + kWordQ + kvh
                                                 : nullptr;
     bool xok = xw == nullptr, have_new = !fused;
+    // Two poll rounds in flight: round r + 1's loads go out before round r's words are
+    // checked, so a word that lands during a round is seen about half a round trip
+    // sooner. Every round reloads every entry (a word, once this launch's, stays so).
+    float2 mlb[kCombChunk];
+    float4 ovb[kCombChunk];
+    uint32_t xa = 0u, xb = 0u;  // each round's copy of the lane's new-row / q word
+    const uint32_t *xw_any = xw != nullptr ? xw : a.words;  // (a load with no branch)
+    auto issue = [&](float2 (&m)[kCombChunk], float4 (&o)[kCombChunk], uint32_t &xv) {
+      xv = load_sc1(xw_any);
 #pragma unroll
-    for (int x = 0; x < kCombChunk; ++x) {
-      mlv[x] = float2{-INFINITY, 0.0f};
-      ov[x] = float4{0.f, 0.f, 0.f, 0.f};
-    }
-    bool done = false;
-    for (int it = 0; it < (1 << 16) && !done; ++it) {
+      for (int x = 0; x < kCombChunk; ++x) {
+        const int w = x < cnt ? w0 + x : w0;  // (past cnt: a copy of the first, unused)
+        m[x] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rm, (w * 16 + h) * 8, 0, kSC1));
+        o[x] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rp, ((w * 16 + h) * kPartRow + i0 + 4 * g4) * 4, 0, kSC1));
+      }
+    };
+    const uint32_t pm = par ? 0u : 1u;  // a word is this launch's when its low bit ^ pm is 1
+    auto check = [&](const float2 (&m)[kCombChunk], const float4 (&o)[kCombChunk],
+                     uint32_t xv) -> bool {
+      uint32_t miss = 0u;
 #pragma unroll
-      for (int x = 0; x < kCombChunk; ++x)
-        if ((need >> x) & 1u) {  // every word not there yet
-          const int w = w0 + x;
-          mlv[x] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rm, (w * 16 + h) * 8, 0, kSC1));
-          ov[x] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                 rp, ((w * 16 + h) * kPartRow + i0 + 4 * g4) * 4, 0, kSC1));
-        }
-      if (!xok) xok = (load_sc1(xw) & 1u) == par;
+      for (int x = 0; x < kCombChunk; ++x) {
+        const uint32_t mok = (par_of(m[x].x) ^ pm) & (par_of(m[x].y) ^ pm);
+        const uint32_t ook = (par_of(o[x].x) ^ pm) & (par_of(o[x].y) ^ pm) &
+                             (par_of(o[x].z) ^ pm) & (par_of(o[x].w) ^ pm);
+        if (x < cnt && !(mok && ook)) miss |= 1u << x;
+      }
+      if (!xok) xok = (xv & 1u) == par;
       if (!have_new && __all(xok)) {  // the new rows are stored: their values, once
         qv = kPrep ? load_sc1(a.q_out + h * 256 + tid) : a.q[h * 256 + tid];
         kv = load_sc1(a.dq + kvh * 256 + tid);
         if (tid < 32) vnew = load_sc1(a.dq + (2 + kvh) * 256 + e_out);
         have_new = true;
       }
-      const uint32_t pm = par ? 0u : 1u;  // a word is this launch's when its low bit ^ pm is 1
+      return __all(miss == 0u && xok) && have_new;
+    };
+    bool done = false;
+    issue(mlv, ov, xa);
+    for (int it = 0; it < (1 << 15) && !done; ++it) {
+      issue(mlb, ovb, xb);
+      if (check(mlv, ov, xa)) {
+        done = true;
+        break;
+      }
+      issue(mlv, ov, xa);
+      if (check(mlb, ovb, xb)) {
 #pragma unroll
-      for (int x = 0; x < kCombChunk; ++x)
-        if ((need >> x) & 1u) {
-          const uint32_t mok = (par_of(mlv[x].x) ^ pm) & (par_of(mlv[x].y) ^ pm);
-          const uint32_t ook = (par_of(ov[x].x) ^ pm) & (par_of(ov[x].y) ^ pm) &
-                               (par_of(ov[x].z) ^ pm) & (par_of(ov[x].w) ^ pm);
-          if (mok && ook) need &= ~(1u << x);
+        for (int x = 0; x < kCombChunk; ++x) {
+          mlv[x] = mlb[x];
+          ov[x] = ovb[x];
         }
-      done = __all(need == 0u && xok) && have_new;
-      if (!done) __builtin_amdgcn_s_sleep(2);
+        done = true;
+      }
     }
+#pragma unroll
+    for (int x = 0; x < kCombChunk; ++x)
+      if (x >= cnt) {  // no partial: an empty entry
+        mlv[x] = float2{-INFINITY, 0.0f};
+        ov[x] = float4{0.f, 0.f, 0.f, 0.f};
+      }
     ok = done;
 #pragma unroll
     for (int x = 0; x < kCombChunk; ++x) {
