@@ -108,7 +108,7 @@ struct DecodeArgsT<0> : DecodeArgsBase {
 
 // Per-wave tables rebuilt for every 32-key block.
 struct WaveTab {
-  float kd[kBlk], kdm[kBlk];                        // epilogue exchange (cmin)
+  float kd[kBlk], kdm[kBlk];                        // epilogue exchange (cmin); see below
   float vmd[kBlk], vmdm[kBlk];                      // V: mantissas of d and dmin
   _Float16 vsc[8][kBlk], vc[8][kBlk], vm[8][kBlk];  // V: fp16 constants [j][key]
 };
@@ -116,7 +116,8 @@ struct WaveTab {
 // LDS of one workgroup. Each wave owns stage buffers st[w][0], st[w][1] (adjacent, so
 // both are reached from one base register with immediate offsets) and a table area;
 // before its first refill of st[w][1] a wave stages its KV head's q rows there, and the
-// quantizer scratch of the quantizing waves 0-3 overlaps their tables. The merge area
+// quantizer scratch of the quantizing waves 0-3 overlaps their tables (used before their
+// block loops or once all four have left them). The merge area
 // reuses the first stage buffers once every wave has left the loop. Stages are always addressed by
 // indexing this array: a pointer chosen at run time between two stages loses its LDS
 // address space, and the generic (flat) loads it then compiles to wait on every
@@ -129,7 +130,6 @@ struct Smem {
         WaveTab tab[kWaves];
         struct {
           Q4kScratch scr;
-          uint32_t arrivals;  // barrier counter of the quantizing waves 0-3
           __attribute__((aligned(16))) float prow[256];  // k_norm / rope of a K row
           float pm;
         } quant;
@@ -140,7 +140,11 @@ struct Smem {
     } merge;
   };
 };
-static_assert(offsetof(decltype(Smem{}.run.t.quant), prow) >= sizeof(Q4kScratch) + 4 &&
+// The quantizing waves' barrier counter is tab[1].kd[0]: no wave writes a kd table
+// before the epilogue's first workgroup barrier (the prepared-q constants are staged in
+// vc / vm), and the quantizer scratch stays within tab[0].
+static_assert(sizeof(Smem{}.run.t.quant) <= sizeof(WaveTab), "quantizer scratch within tab[0]");
+static_assert(offsetof(decltype(Smem{}.run.t.quant), prow) >= sizeof(Q4kScratch) &&
                   sizeof(Smem{}.run.t.quant) <= 4 * sizeof(WaveTab),
               "quantizer scratch within the tables of the quantizing waves 0-3");
 static_assert(sizeof(float4[kWaves][16][2][16]) <= sizeof(Stage[kWaves]),
@@ -710,9 +714,14 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
   // Fused append: threads 0-255 (waves 0-3) of workgroup r quantize new row r (row
   // 4s + 2p + kv: segment s, K (p = 0) or V (p = 1), KV head kv; further rows go
   // round-robin when the grid is smaller) and publish it dequantized for the combine
-  // step, which attends to the new key. This runs while the first block streams in.
-  // The row is read before any staging load is issued, so the compiler's wait for it
-  // does not wait for the stage too.
+  // step, which attends to the new key. The row is read before any staging load.
+  // One output row (kOne): the quantization (about 3.5 us, a latency chain) runs first,
+  // while the first blocks stream in (the row is waited for here, so that the compiler's
+  // wait for it does not wait for a stage too), and the combiners have the new key's rows
+  // early. Batched launches quantize after their block loops (kQuantLate): there the
+  // rows go to a separate combine kernel, and a quantizing workgroup whose blocks start
+  // late ends last (measured: config 5 1098.5 -> 1093.3 us/step, config 3 294 -> 311).
+  constexpr bool kQuantLate = !kOne;
   const bool quant = knew_0 != nullptr && wg < 4 * (kOne ? 1 : a.nnew) && tid < 256;
   float xq = 0.0f;
   PrepElem kpe[1] = {PrepElem{1.0f, 1.0f, 0.0f}};
@@ -723,10 +732,10 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
     return load_prep_elem(a.prep.k_alpha, a.prep.cos_tab + pos * half,
                           a.prep.sin_tab + pos * half, tid, 256, a.prep.n_rot);
   };
-  // (kPrep) the quantizing waves, whose table areas hold the quantizer's scratch until
-  // it is done, load the q preparation constants (q_norm alphas 4 lane .. 4 lane + 3 and
-  // one rope cos / sin entry) with the new row and stage them in LDS after quantizing;
-  // the other waves stage them by DMA below
+  // (kPrep, quantizing first) the quantizing waves, whose table areas hold the quantizer's
+  // scratch until it is done, load the q preparation constants (q_norm alphas 4 lane ..
+  // 4 lane + 3 and one rope cos / sin entry) with the new row and stage them in LDS after
+  // quantizing; every other wave stages them by DMA below
   f4 qa4 = {1.0f, 1.0f, 1.0f, 1.0f};
   float rcos = 1.0f, rsin = 0.0f;
   if (quant) {
@@ -734,25 +743,29 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
     xq = (p ? a.v_new : knew_0)[((int64_t)(wg >> 2) * 2 + kvr) * 256 + tid];
     if constexpr (kPrep) {
       if (p == 0) kpe[0] = k_prep_elem(wg >> 2);
-      qa4 = reinterpret_cast<const f4 *>(a.prep.q_alpha)[lane];
-      const int half = a.prep.n_rot >> 1;
-      if (have) {  // the first piece's q position (a workgroup without blocks has none)
-        rcos = a.prep.cos_tab[sgv.t_new * half + (lane & (half - 1))];
-        rsin = a.prep.sin_tab[sgv.t_new * half + (lane & (half - 1))];
+      if constexpr (!kQuantLate) {
+        qa4 = reinterpret_cast<const f4 *>(a.prep.q_alpha)[lane];
+        const int half = a.prep.n_rot >> 1;
+        if (have) {  // the first piece's q position (a workgroup without blocks has none)
+          rcos = a.prep.cos_tab[sgv.t_new * half + (lane & (half - 1))];
+          rsin = a.prep.sin_tab[sgv.t_new * half + (lane & (half - 1))];
+        }
+        asm volatile("" : "+v"(xq), "+v"(kpe[0].alpha), "+v"(kpe[0].c), "+v"(kpe[0].s),
+                     "+v"(rcos), "+v"(rsin), "+v"(qa4));
       }
-      asm volatile("" : "+v"(xq), "+v"(kpe[0].alpha), "+v"(kpe[0].c), "+v"(kpe[0].s),
-                   "+v"(rcos), "+v"(rsin), "+v"(qa4));
-    } else {
+    } else if constexpr (!kQuantLate) {
       asm volatile("" : "+v"(xq));
     }
   }
-  if (tid == 0) sm.run.t.quant.arrivals = 0u;
+  uint32_t *const qarrive = reinterpret_cast<uint32_t *>(&sm.run.t.tab[1].kd[0]);
+  if (tid == 0) *qarrive = 0u;
   // Fused append (waves 0-3 of the quantizing workgroups, once): the rows, as above.
   auto quantize_rows = [&]() {
-    // the quantization delays this workgroup's blocks: it outranks the block loops of
-    // the waves sharing its SIMDs
+    // the quantization delays this workgroup's blocks or its partial: it outranks the
+    // block loops of the waves sharing its SIMDs
     __builtin_amdgcn_s_setprio(3);
-    QuantWavesBarrier bar{&sm.run.t.quant.arrivals, 0u, a.status};
+    QuantWavesBarrier bar{qarrive, 0u, a.status};
+    if constexpr (kQuantLate) bar();  // all four are done with their tables (the scratch)
     for (int row = wg; row < 4 * a.nnew; row += a.nwg) {
       const int rs = row >> 2, p = (row >> 1) & 1, kvr = row & 1;
       if (row != wg) xq = (p ? a.v_new : a.k_new)[((int64_t)rs * 2 + kvr) * 256 + tid];
@@ -809,10 +822,10 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
     // before any stage load (one barrier), so q returns ahead of the block data.
     if (have) {
       if constexpr (kPrep) {
-        if (!qnow) {
+        if (kQuantLate || !qnow) {
           const int half = a.prep.n_rot >> 1;
           const int64_t ro = sg.t_new * half;
-          issue_prep_consts(&sm.run.t.tab[wave],
+          issue_prep_consts(&sm.run.t.tab[wave].vc[0][0],
                             reinterpret_cast<uint8_t *>(&sm.run.st[wave][1]) + 8 * kQRow,
                             make_rsrc(a.prep.q_alpha, 1024u),
                             make_rsrc(a.prep.cos_tab + ro, (uint32_t)half * 4u),
@@ -839,10 +852,10 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
         asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
       else
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      if constexpr (kPrep) {
-        if (qnow) {  // after quantizing: the constants into this wave's table area and tail
+      if constexpr (kPrep && !kQuantLate) {
+        if (qnow) {  // after quantizing: the constants into this wave's vc / vm and tail
           float *tail = reinterpret_cast<float *>(&sm.run.st[wave][1]) + 8 * (kQRow / 4);
-          reinterpret_cast<f4 *>(&sm.run.t.tab[wave])[lane] = qa4;
+          reinterpret_cast<f4 *>(&sm.run.t.tab[wave].vc[0][0])[lane] = qa4;
           tail[lane] = lane < 32 ? rcos : 0.0f;
           tail[64 + lane] = lane < 32 ? rsin : 0.0f;
           __builtin_amdgcn_wave_barrier();
@@ -898,7 +911,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
           ss = __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
         }
         const float inv = 1.0f / __builtin_sqrtf(ss * (1.0f / 256.0f) + a.prep.eps);
-        const float *al = reinterpret_cast<const float *>(&sm.run.t.tab[wave]) + 64 * g;
+        const float *al = reinterpret_cast<const float *>(&sm.run.t.tab[wave].vc[0][0]) + 64 * g;
 #pragma unroll
         for (int st = 0; st < 8; ++st) {
           const float4 a0 = *reinterpret_cast<const float4 *>(al + 8 * st);
@@ -964,7 +977,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
     };
     static_assert(kLoadsPerStage == 12, "the vmcnt above counts one stage of loads");
 
-    if (qnow) quantize_rows();
+    if (qnow && (!kQuantLate || !have)) quantize_rows();
     if (!have) {
       if constexpr (kSegs == 1) {
         // (the one-segment plan gives every workgroup a block; should it not, its slot
@@ -1030,6 +1043,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
       }
       __builtin_amdgcn_s_setprio(0);
     }
+    if (kQuantLate && qnow) quantize_rows();
     // ---- epilogue: per-wave reductions, then the four waves of each KV head merged into
     // this workgroup's partial
     S.lsum += __shfl_xor(S.lsum, 16);
