@@ -47,6 +47,11 @@ namespace {
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;  // two waves per SIMD
 constexpr int kMainWGs = 256;
+// Quantize-only workgroups in front of a one-row fused launch of nwg decode workgroups
+// (the in-launch combine's full grid has none): 4 when the CUs have room for them.
+__host__ __device__ constexpr int kQuantFront(bool one, bool fused, int nwg) {
+  return one && fused && nwg <= kMainWGs - 4 ? 4 : 0;
+}
 constexpr float kLazy = 8.0f;  // log2 headroom of the running max before a rescale
 constexpr int kPieceGap = 6;   // virtual blocks before each segment after the first
 
@@ -560,7 +565,8 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
   __shared__ Smem sm;
   constexpr bool kOne = kSegs == 1;
   if constexpr (kOne) {
-    if ((int)blockIdx.x >= nwg_0) {  // a combiner workgroup (in-launch combine)
+    if ((int)blockIdx.x >= nwg_0 + kQuantFront(true, knew_0 != nullptr, nwg_0)) {
+      // a combiner workgroup (in-launch combine)
       const TailArgs t{a.nwg, a.words, a.part, a.ml, a.q, a.q_out,
                        a.k_new != nullptr ? a.dq : nullptr, a.out, a.sl2, a.status};
       tail_combine<kPrep>(t, (int)blockIdx.x - a.nwg, &sm);
@@ -582,7 +588,12 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
   }
   const auto parity = [&]() { return (par_raw ^ par_on) & par_on; };
   const int kv = wave & 1, wsub = wave >> 1;
-  const int wg = blockIdx.x;
+  // A one-row fused launch over fewer workgroups than CUs puts 4 workgroups in front that
+  // only quantize the new rows (qx; the host sizes the grid by the same rule), so that no
+  // decode workgroup's blocks wait behind the quantization.
+  const int qx = kQuantFront(kOne, knew_0 != nullptr, nwg_0);
+  const int wg = (int)blockIdx.x - qx;
+  const int qwg = qx > 0 ? (int)blockIdx.x : wg;  // the first new row this workgroup quantizes
   const int n = lane & 15, g = lane >> 4;
   const int kvu = __builtin_amdgcn_readfirstlane(kv);
   const uint32_t rs_t = (uint32_t)(strides & 0xFFFFFFu);
@@ -681,7 +692,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
     return false;
     }
   };
-  bool have = next_piece();
+  bool have = wg >= 0 && next_piece();
   if constexpr (kSegs == 0) {
     // The partial slots a workgroup owns run from wg + (segments ending at or before V0)
     // to wg + (segments starting before V1); its pieces fill them, except the last one
@@ -722,7 +733,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
   // rows go to a separate combine kernel, and a quantizing workgroup whose blocks start
   // late ends last (measured: config 5 1098.5 -> 1093.3 us/step, config 3 294 -> 311).
   constexpr bool kQuantLate = !kOne;
-  const bool quant = knew_0 != nullptr && wg < 4 * (kOne ? 1 : a.nnew) && tid < 256;
+  const bool quant = knew_0 != nullptr && (qx > 0 ? wg < 0 : wg < 4 * (kOne ? 1 : a.nnew)) && tid < 256;
   float xq = 0.0f;
   PrepElem kpe[1] = {PrepElem{1.0f, 1.0f, 0.0f}};
   auto k_prep_elem = [&](int rs) {
@@ -739,10 +750,10 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
   f4 qa4 = {1.0f, 1.0f, 1.0f, 1.0f};
   float rcos = 1.0f, rsin = 0.0f;
   if (quant) {
-    const int p = (wg >> 1) & 1, kvr = wg & 1;
-    xq = (p ? a.v_new : knew_0)[((int64_t)(wg >> 2) * 2 + kvr) * 256 + tid];
+    const int p = (qwg >> 1) & 1, kvr = qwg & 1;
+    xq = (p ? a.v_new : knew_0)[((int64_t)(qwg >> 2) * 2 + kvr) * 256 + tid];
     if constexpr (kPrep) {
-      if (p == 0) kpe[0] = k_prep_elem(wg >> 2);
+      if (p == 0) kpe[0] = k_prep_elem(qwg >> 2);
       if constexpr (!kQuantLate) {
         qa4 = reinterpret_cast<const f4 *>(a.prep.q_alpha)[lane];
         const int half = a.prep.n_rot >> 1;
@@ -766,9 +777,9 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
     __builtin_amdgcn_s_setprio(3);
     QuantWavesBarrier bar{qarrive, 0u, a.status};
     if constexpr (kQuantLate) bar();  // all four are done with their tables (the scratch)
-    for (int row = wg; row < 4 * a.nnew; row += a.nwg) {
+    for (int row = qwg; row < 4 * a.nnew; row += a.nwg) {
       const int rs = row >> 2, p = (row >> 1) & 1, kvr = row & 1;
-      if (row != wg) xq = (p ? a.v_new : a.k_new)[((int64_t)rs * 2 + kvr) * 256 + tid];
+      if (row != qwg) xq = (p ? a.v_new : a.k_new)[((int64_t)rs * 2 + kvr) * 256 + tid];
       uint8_t *dst;
       if constexpr (kSegs == 0) {  // row len of the page that holds token len
         const PagedSeqArg &sq = a.pq[rs];
@@ -781,7 +792,7 @@ __global__ __launch_bounds__(kThreads) void q4k_decode_kernel(
       }
       if constexpr (kPrep) {
         if (p == 0) {  // k_norm and rope of the new K row (bit-exact), then its quantization
-          if (row != wg) kpe[0] = k_prep_elem(rs);
+          if (row != qwg) kpe[0] = k_prep_elem(rs);
           float xx[1] = {xq};
           prep_row<1>(xx, kpe, 256, a.prep.eps, a.prep.n_rot, sm.run.t.quant.prow,
                       &sm.run.t.quant.pm, tid, bar);
@@ -1253,7 +1264,8 @@ static int launch_decode_segments(const DecodeSegIn *in, int n, const float *q,
     DecodeArgsT<1> d1;
     static_cast<DecodeArgsBase &>(d1) = d;
     d1.seg[0] = d.seg[0];
-    hipLaunchKernelGGL((q4k_decode_kernel<kPrep, 1>), dim3((unsigned)(nwg + d.ncomb)), dim3(kThreads),
+    const int qx = kQuantFront(true, fused, nwg);
+    hipLaunchKernelGGL((q4k_decode_kernel<kPrep, 1>), dim3((unsigned)(qx + nwg + d.ncomb)), dim3(kThreads),
                        0, s, d.seg[0].k, d.seg[0].v, q, d.words, k_new,
                        decode_strides(rs_t, rs_h), (int)d.seg[0].seq_k, nwg, d1);
     PKV_HIP(hipGetLastError());
